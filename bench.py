@@ -1,0 +1,260 @@
+"""Throughput of the scan! / mapreduce hot path on one MI355X.
+
+A step is one pass of the path over one batch of synthetic Float32 data at
+n = 2^28 (BASELINE.json's headline configuration):
+    scan!(+, dst, src)                 inclusive, 2*4*n bytes
+    mapreduce!(identity, +, out, src)  full reduction, 4*n bytes
+Inputs are resident in HBM before timing starts. `value` is algorithmic GB/s
+of the whole step (12*n bytes / step time). The JSON line also carries the
+per-kernel roofline of the dominant kernel (the scan), measured with HIP
+events on the stream the kernels run on, the measured copy ceiling, and the
+CPU baseline (the oracle's restatement of Base.accumulate! / Base.mapreduce,
+timed on this host).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--all]
+  --all   also time every BASELINE.json configuration (stderr table and
+          gpurun_out/bench_all.json).
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, REPO)
+
+PEAK_HBM_GBPS = 8000.0
+N = 2**28
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def time_calls(fn, reps, batches=5):
+    """Average seconds per call: `batches` event-timed batches of `reps`
+    back-to-back calls on the current stream; returns the median batch."""
+    s = torch.cuda.current_stream()
+    out = []
+    for _ in range(batches):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for _ in range(reps):
+            fn()
+        e1.record(s)
+        e1.synchronize()
+        out.append(e0.elapsed_time(e1) / 1e3 / reps)
+    return float(np.median(out))
+
+
+def load_traffic():
+    """HBM bytes per scan launch measured with rocprofv3 --pmc (FETCH_SIZE +
+    WRITE_SIZE, scaled by the copy-kernel calibration), if recorded."""
+    p = os.path.join(REPO, "profiles", "traffic_scan_f32_2p28.json")
+    if os.path.exists(p):
+        with open(p) as fh:
+            return json.load(fh).get("hbm_bytes_per_launch")
+    return None
+
+
+def cpu_baseline(oracle, budget_s=12.0):
+    threads = max(1, min(16, os.cpu_count() or 1))
+    n = N
+    x = np.random.default_rng(20261201).random(n, dtype=np.float32)
+    y = np.empty_like(x)
+    oracle.baseline_scan_add_f32(x[: 1 << 20], y[: 1 << 20], threads)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        oracle.baseline_scan_add_f32(x, y, threads)
+        oracle.baseline_sum_f32(x, threads)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or reps >= 50:
+            break
+    gbps = reps * 12 * n / el / 1e9
+    return {"value": round(gbps, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{reps} steps of the same workload (2^28 F32 two-pass chunked scan + chunked sum, "
+                      f"Float32 arithmetic, OpenMP) on {threads} host threads, {el:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--all", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: the scan/mapreduce path here is single-GPU "
+              "(multi-GPU sharding is a design note only); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import __graft_entry__
+    kf = __graft_entry__.load_package()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    g = torch.Generator(device=dev).manual_seed(20261201)
+    src = torch.rand(N, device=dev, generator=g, dtype=torch.float32)
+    dst = torch.empty_like(src)
+    out = torch.empty(1, device=dev, dtype=torch.float32)
+    tmp_scan = kf.get_allocation(kf.Scan1D, kf.identity, "+", src)
+    tmp_red = kf.get_allocation(kf.MapReduce1D, kf.identity, "+", src)
+
+    def do_scan():
+        kf.scan_("+", dst, src, tmp=tmp_scan)
+
+    def do_reduce():
+        kf.mapreduce_(kf.identity, "+", out, src, tmp=tmp_red)
+
+    def step():
+        do_scan()
+        do_reduce()
+
+    log(f"bench: warmup {args.warmup} steps")
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    log(f"bench: timing {args.steps} steps")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    step_s = e0.elapsed_time(e1) / 1e3 / args.steps
+    value = 12 * N / step_s / 1e9
+
+    # per-kernel averages over the timed pattern (events on the launch stream)
+    scan_s = time_calls(do_scan, 20)
+    red_s = time_calls(do_reduce, 20)
+    cbuf = torch.empty_like(src)
+
+    def do_copy():
+        kf.vcopy_(cbuf, src)
+
+    def do_dtod():
+        cbuf.copy_(src)
+
+    copy_s = time_calls(do_copy, 20)
+    dtod_s = time_calls(do_dtod, 20)
+    copy_gbps = 8 * N / copy_s / 1e9
+    dtod_gbps = 8 * N / dtod_s / 1e9
+    ceiling = max(copy_gbps, dtod_gbps)
+    scan_gbps = 8 * N / scan_s / 1e9
+    red_gbps = 4 * N / red_s / 1e9
+    log(f"scan {scan_s*1e6:.1f} us {scan_gbps:.0f} GB/s | reduce {red_s*1e6:.1f} us {red_gbps:.0f} GB/s | "
+        f"copy kernel {copy_gbps:.0f} GB/s, hipMemcpyDtoD {dtod_gbps:.0f} GB/s")
+
+    cpu = None
+    if not args.no_cpu:
+        from oracle import oracle
+        log("bench: cpu baseline")
+        cpu = cpu_baseline(oracle)
+
+    line = {
+        "metric": "scan!/mapreduce GB/s and % HBM roofline at n=2^28 Float32, 1xMI355X",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_s * 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: U[0,1) Float32, torch.Generator seed 20261201, resident in HBM",
+        "config": {"workload": "scan!(+, dst, src) inclusive + mapreduce!(identity, +, out, src), "
+                               "Float32 n=2^28 (BASELINE.json configs[1] size, Float32 as in the metric)",
+                   "n": N, "bytes_per_step": 12 * N},
+        "roofline": {"bound": "hbm", "kernel": "scan_kernel<float,OpAdd,MapIdentity>",
+                     "achieved": round(scan_gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                     "frac": round(scan_gbps / PEAK_HBM_GBPS, 4), "traffic": load_traffic(),
+                     "avg_launch_us": round(scan_s * 1e6, 2), "algorithmic_bytes_per_launch": 8 * N},
+        "kernels": {
+            "scan_gbps": round(scan_gbps, 1), "scan_frac_of_copy": round(scan_gbps / ceiling, 4),
+            "mapreduce_gbps": round(red_gbps, 1), "mapreduce_frac_of_copy": round(red_gbps / ceiling, 4),
+            "mapreduce_frac_of_peak": round(red_gbps / PEAK_HBM_GBPS, 4), "mapreduce_avg_launch_us": round(red_s * 1e6, 2),
+            "copy_kernel_gbps": round(copy_gbps, 1), "hipMemcpyDtoD_gbps": round(dtod_gbps, 1),
+            "copy_ceiling_gbps": round(ceiling, 1),
+        },
+        "cpu_baseline": cpu,
+        "wall_s_timed": round(wall, 4),
+    }
+    if args.all:
+        line["all_configs"] = bench_all(kf, dev, ceiling)
+    print(json.dumps(line), flush=True)
+
+
+def bench_all(kf, dev, ceiling):
+    """Every BASELINE.json configuration: GB/s, % of peak, % of the copy ceiling."""
+    rows = []
+    g = torch.Generator(device=dev).manual_seed(20261201)
+
+    def rec(name, bytes_, fn, reps=20):
+        fn()
+        torch.cuda.synchronize()
+        s = time_calls(fn, reps)
+        gb = bytes_ / s / 1e9
+        rows.append({"config": name, "us": round(s * 1e6, 2), "gbps": round(gb, 1),
+                     "frac_peak": round(gb / PEAK_HBM_GBPS, 4), "frac_copy": round(gb / ceiling, 4)})
+        log(f"  {name:48s} {s*1e6:10.1f} us {gb:8.0f} GB/s  {gb/ceiling*100:5.1f}% of copy")
+
+    x = torch.rand(10**6, device=dev, generator=g)
+    y = torch.empty_like(x)
+    rec("C1 scan F32 incl n=1e6", 8e6, lambda: kf.scan_("+", y, x))
+    del x, y
+    xi = torch.randint(0, 16, (2**28,), device=dev, generator=g, dtype=torch.int32)
+    yi = torch.empty_like(xi)
+    rec("C2 scan Int32 incl n=2^28", 8 * 2**28, lambda: kf.scan_("+", yi, xi))
+    rec("C2 scan Int32 excl n=2^28", 8 * 2**28, lambda: kf.scan_("+", yi, xi, exclusive=True))
+    o = torch.empty(1, device=dev, dtype=torch.int32)
+    xr = torch.randint(-2**31, 2**31 - 1, (2**28,), device=dev, generator=g, dtype=torch.int32)
+    rec("C3c mapreduce max Int32 n=2^28", 4 * 2**28, lambda: kf.mapreduce_(kf.identity, max, o, xr))
+    del xi, yi, xr
+    xf = torch.randn(2**30, device=dev, generator=g)
+    of = torch.empty(1, device=dev)
+    rec("C3a mapreduce abs2,+ F32 n=2^30", 4 * 2**30, lambda: kf.mapreduce_(kf.abs2, "+", of, xf), reps=10)
+    del xf
+    xd = torch.randn(2**28, device=dev, generator=g, dtype=torch.float64)
+    od = torch.empty(1, device=dev, dtype=torch.float64)
+    rec("C3b mapreduce abs2,+ F64 n=2^28", 8 * 2**28, lambda: kf.mapreduce_(kf.abs2, "+", od, xd))
+    del xd
+    ab = torch.empty(2**26, 2, device=dev)
+    ab[:, 0].uniform_(0.9, 1.0, generator=g)
+    ab[:, 1].normal_(generator=g)
+    yab = torch.empty_like(ab)
+    rec("C4 affine scan n=2^26", 16 * 2**26, lambda: kf.scan_(kf.affine, yab, ab))
+    del ab, yab
+    t = torch.rand(2**28, device=dev, generator=g) * 2 - 1
+    A1 = t.as_strided((4096, 65536), (1, 4096))
+    d1 = torch.empty(65536, device=dev)
+    rec("C5a dims=1 4096x65536", 4 * 2**28 + 4 * 65536, lambda: kf.mapreduce_(kf.identity, "+", d1, A1, dims=1))
+    A2 = t.as_strided((65536, 4096), (1, 65536))
+    d2 = torch.empty(65536, device=dev)
+    rec("C5b dims=2 65536x4096", 4 * 2**28 + 4 * 65536, lambda: kf.mapreduce_(kf.identity, "+", d2, A2, dims=2))
+    V1 = A1[:, ::2]
+    d1v = torch.empty(32768, device=dev)
+    rec("C5c dims=1 view 4096x(65536/2)", 4 * 2**27 + 4 * 32768,
+        lambda: kf.mapreduce_(kf.identity, "+", d1v, V1, dims=1))
+    V2 = A2[:, ::2]
+    rec("C5d dims=2 view 65536x(4096/2)", 4 * 2**27 + 4 * 65536,
+        lambda: kf.mapreduce_(kf.identity, "+", d2, V2, dims=2))
+    os.makedirs(os.path.join(REPO, "gpurun_out"), exist_ok=True)
+    with open(os.path.join(REPO, "gpurun_out", "bench_all.json"), "w") as fh:
+        json.dump({"copy_ceiling_gbps": ceiling, "rows": rows}, fh, indent=1)
+    return rows
+
+
+if __name__ == "__main__":
+    main()

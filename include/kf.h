@@ -1,0 +1,145 @@
+/*
+ * kf.h — C ABI of libkfhip.so, the gfx950 (MI355X) implementation of
+ * KernelForge.jl's scan / mapreduce hot path.
+ *
+ * Every entry point takes plain device pointers, element counts and strides
+ * (in elements), and a hipStream_t (passed as void*; NULL = default stream).
+ * Calls are stream-ordered and non-blocking; the library never allocates
+ * device memory and never synchronises. Scratch memory is caller-owned:
+ * size it with the matching *_scratch_bytes query and zero-fill it ONCE
+ * before its first use (kf_scratch_reset does that on a stream). After that
+ * the kernels keep it valid themselves (epoch-tagged tile descriptors and
+ * self-resetting counters), so one scratch buffer may be reused across calls,
+ * dtypes, operators and sizes without clearing. Calls that share a scratch
+ * buffer must be ordered on one stream; concurrent calls need distinct
+ * buffers.
+ *
+ * Return codes: KF_OK, KF_EINVAL (bad enum, shape, stride or alignment),
+ * KF_ENOSCRATCH (scratch missing or too small), KF_EHIP (a HIP error; the
+ * text is in kf_last_error()). n == 0 is a successful no-op.
+ *
+ * Semantics follow Julia Base, as the reference's tests require
+ * (reference test/tests/scan/scan_test.jl:1-125 compares against
+ * `accumulate`, the test/tests/mapreduce files against `mapreduce`/`sum`).
+ */
+#ifndef KF_H
+#define KF_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KF_VERSION 100 /* 1.0.0 */
+
+typedef enum {
+  KF_OK = 0,
+  KF_EINVAL = 1,
+  KF_ENOSCRATCH = 2,
+  KF_EHIP = 3
+} kf_status;
+
+/* Binary operator `op` of scan!/mapreduce. KF_OP_AFFINE is the
+ * non-commutative composition (a1,b1) o (a2,b2) = (a2*a1, a2*b1 + b2) on
+ * KF_F32X2 pairs; it is accepted by kf_scan only. */
+typedef enum {
+  KF_OP_ADD = 0,
+  KF_OP_MAX = 1,
+  KF_OP_MIN = 2,
+  KF_OP_AFFINE = 3
+} kf_op;
+
+/* Element map `f` (applied to each element before `op`). */
+typedef enum {
+  KF_MAP_IDENTITY = 0,
+  KF_MAP_ABS2 = 1
+} kf_map;
+
+/* Element types. KF_F32X2 is an interleaved (a, b) pair of float32. */
+typedef enum {
+  KF_F32 = 0,
+  KF_F64 = 1,
+  KF_I32 = 2,
+  KF_I64 = 3,
+  KF_U8 = 4,
+  KF_F32X2 = 5
+} kf_dtype;
+
+int kf_version(void);
+
+/* Text of the last error raised on the calling host thread ("" if none). */
+const char* kf_last_error(void);
+
+/* Zero-fill `bytes` of scratch on `stream` with a fill kernel (no memset
+ * node, so it is safe inside captured graphs). */
+int kf_scratch_reset(void* scratch, size_t bytes, void* stream);
+
+/* ---------------------------------------------------------------- scan ----
+ * dst[i] = f(src[0]) op ... op f(src[i])              (exclusive = 0)
+ * dst[0] = identity(op); dst[i] = incl[i-1]            (exclusive = 1)
+ * Strides are in elements (1 = contiguous). src and dst may alias only
+ * exactly (in-place scan, same pointer and stride).
+ *
+ * Replaces the reference's
+ *   scan!(f, op, dst, src; g, tmp, Nitem, workgroup, family, arch)
+ *     src/scan/scan.jl:251-284 (host) -> _scan_impl! src/scan/scan.jl:414-479
+ *     -> scan_kernel_packed! / scan_kernel! src/scan/scan_kernel.jl:94-478
+ * and get_allocation(Scan1D, ...) src/scan/scan.jl:156-211 (scratch size).
+ * The exclusive variant has no reference counterpart (CUB/rocPRIM
+ * ExclusiveSum semantics, used by the reference's vendor benchmarks
+ * perfs/rocm_cpp/hipcub_hipcc/rocprim_scan_benchmark.cpp). */
+size_t kf_scan_scratch_bytes(kf_dtype dt, kf_op op, int64_t n);
+
+int kf_scan(kf_op op, kf_map f, kf_dtype dt, int exclusive,
+            const void* src, int64_t src_stride,
+            void* dst, int64_t dst_stride, int64_t n,
+            void* scratch, size_t scratch_bytes, void* stream);
+
+/* -------------------------------------------------------------- reduce ----
+ * dst[0] = f(src[0]) op f(src[stride]) op ... (n terms), written on device.
+ * op must be commutative (ADD, MAX, MIN). The result is deterministic: the
+ * combine tree depends only on n and the pointer alignment.
+ *
+ * Replaces the reference's mapreduce1d!(f, op, dst, src; tmp, ...)
+ *   src/mapreduce/1D/mapreduce1d.jl:259-345 -> mapreduce1d_kernel!
+ *   src/mapreduce/1D/mapreduce1d_kernel.jl:5-93, and
+ * get_allocation(MapReduce1D, ...) src/mapreduce/1D/mapreduce1d.jl:140-170. */
+size_t kf_reduce_scratch_bytes(kf_dtype dt, int64_t n);
+
+int kf_reduce(kf_op op, kf_map f, kf_dtype dt,
+              const void* src, int64_t n, int64_t stride,
+              void* dst, void* scratch, size_t scratch_bytes, void* stream);
+
+/* ---------------------------------------------------------- reduce_dim ----
+ * A is a column-major rows x cols matrix: A[i, j] at A + i + j*col_stride
+ * (col_stride >= rows; col_stride = 2*rows is the view A[:, 1:2:end]).
+ *   dim = 1: dst[j * dst_stride] = op_i f(A[i, j])   (cols outputs)
+ *   dim = 2: dst[i * dst_stride] = op_j f(A[i, j])   (rows outputs)
+ * op must be commutative (ADD, MAX, MIN).
+ *
+ * Replaces the reference's mapreduce2d!(f, op, dst, src, dim)
+ *   src/mapreduce/2D/mapreduce2d.jl:111-126, which routes dim=1 to
+ *   vecmat! (src/mapreduce/2D/vecmat.jl:411-531, vecmat_kernel.jl:1-169)
+ *   and dim=2 to matvec! (src/mapreduce/2D/matvec.jl:480-611,
+ *   matvec_kernel.jl:1-239). */
+size_t kf_reduce_dim_scratch_bytes(kf_dtype dt, int64_t rows, int64_t cols, int dim);
+
+int kf_reduce_dim(kf_op op, kf_map f, kf_dtype dt,
+                  const void* A, int64_t rows, int64_t cols, int64_t col_stride,
+                  int dim, void* dst, int64_t dst_stride,
+                  void* scratch, size_t scratch_bytes, void* stream);
+
+/* ---------------------------------------------------------------- copy ----
+ * dst[0:bytes] = src[0:bytes] with 16-byte streaming loads/stores: the
+ * bandwidth ceiling the scan/reduce kernels are measured against.
+ * Replaces the reference's vcopy! src/copy/copy.jl:24-28 /
+ * copy_kernel! src/copy/copy_kernel.jl:3-18. */
+int kf_copy(void* dst, const void* src, size_t bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KF_H */

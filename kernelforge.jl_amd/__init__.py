@@ -1,0 +1,486 @@
+"""kernelforge_amd — host side of the MI355X scan / mapreduce path.
+
+A Python mirror of KernelForge.jl's operator interface for this path, over
+the C ABI of libkfhip.so (include/kf.h). Names follow the reference with
+Julia's `!` spelled as a trailing underscore:
+
+    scan_(op, dst, src)            KernelForge.scan!(op, dst, src)
+    scan_(f, op, dst, src)         KernelForge.scan!(f, op, dst, src)
+    scan(op, src) / scan(f, op, src)
+    mapreduce(f, op, src, dims=None)   -> scalar (dims=None) or tensor
+    mapreduce_(f, op, dst, src, dims=None)
+    get_allocation(kind, f, op, src)   -> KernelBuffer (the reference's `tmp`)
+    vcopy_(dst, src)
+
+(reference src/scan/scan.jl:218-284, src/mapreduce/mapreduce.jl:51-212,
+src/allocations.jl:16-41, src/copy/copy.jl:24-28).
+
+Arrays are torch tensors on a ROCm device, read with Julia's conventions:
+tensor dim k is Julia dim k+1, `dims` are 1-based, and a Julia column-major
+matrix is a tensor whose first dim has stride 1 (e.g. `torch.empty(n, m).T`
+is an m x n column-major matrix; `A[:, ::2]` is `view(A, :, 1:2:end)`).
+Affine pairs are float32 tensors of shape (n, 2) holding (a, b).
+
+Operators: `+` (operator.add or "+"), `max`, `min`, `affine` (scan only);
+maps: `identity`, `abs2`. Anything else raises ArgumentError, as does a
+shape/dtype mismatch. Tuning keywords of the reference (Nitem, workgroup,
+blocks, family, arch) are accepted and ignored: launch shapes are fixed for
+gfx950. Calls are asynchronous on torch's current stream except the full
+`mapreduce`, which returns a host scalar (like the reference's
+`Array(dst)[1]`, src/mapreduce/1D/mapreduce1d.jl:203).
+"""
+import operator
+
+import torch
+
+from . import _lib as _L
+
+__all__ = [
+    "ArgumentError", "KernelBuffer", "AffineOp", "affine", "identity", "abs2",
+    "scan", "scan_", "mapreduce", "mapreduce_", "get_allocation", "vcopy_",
+    "Scan1D", "MapReduce1D", "MapReduce2D",
+]
+
+
+class ArgumentError(ValueError):
+    """Invalid argument (Julia's ArgumentError)."""
+
+
+def identity(x):
+    return x
+
+
+def abs2(x):
+    return x * x
+
+
+class AffineOp:
+    """(a1, b1) o (a2, b2) = (a2*a1, a2*b1 + b2): composition of the maps
+    x -> a*x + b, older map first. Scanning it solves x_t = a_t x_{t-1} + b_t."""
+
+    def __call__(self, p, q):
+        return (q[0] * p[0], q[0] * p[1] + q[1])
+
+    def __repr__(self):
+        return "affine"
+
+
+affine = AffineOp()
+
+# Allocation kinds (reference src/algorithms.jl:16-31 tags).
+Scan1D, MapReduce1D, MapReduce2D = "Scan1D", "MapReduce1D", "MapReduce2D"
+
+_OPS = {"+": _L.OP_ADD, "max": _L.OP_MAX, "min": _L.OP_MIN, "affine": _L.OP_AFFINE}
+_MAPS = {"identity": _L.MAP_IDENTITY, "abs2": _L.MAP_ABS2}
+_DTYPES = {torch.float32: _L.F32, torch.float64: _L.F64, torch.int32: _L.I32,
+           torch.int64: _L.I64, torch.uint8: _L.U8}
+
+
+def _op_code(op):
+    if op is operator.add or op is operator.iadd or op is sum:
+        return _L.OP_ADD
+    if op is max:
+        return _L.OP_MAX
+    if op is min:
+        return _L.OP_MIN
+    if isinstance(op, AffineOp):
+        return _L.OP_AFFINE
+    if isinstance(op, str) and op in _OPS:
+        return _OPS[op]
+    raise ArgumentError(f"unsupported operator {op!r}: expected +, max, min or affine")
+
+
+def _map_code(f):
+    if f is None or f is identity:
+        return _L.MAP_IDENTITY
+    if f is abs2:
+        return _L.MAP_ABS2
+    if isinstance(f, str) and f in _MAPS:
+        return _MAPS[f]
+    raise ArgumentError(f"unsupported map {f!r}: expected identity or abs2")
+
+
+def _stream_ptr(t):
+    return ctypes_void(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def ctypes_void(x):
+    import ctypes
+    return ctypes.c_void_p(x)
+
+
+def _require_device(*ts):
+    for t in ts:
+        if not isinstance(t, torch.Tensor):
+            raise ArgumentError(f"expected a torch.Tensor, got {type(t).__name__}")
+        if t.device.type != "cuda":
+            raise ArgumentError("kernelforge_amd operates on GPU tensors (device 'cuda'); "
+                                f"got a tensor on {t.device}")
+    dev = ts[0].device
+    for t in ts[1:]:
+        if t.device != dev:
+            raise ArgumentError(f"tensors on different devices: {dev} and {t.device}")
+
+
+# ---------------------------------------------------------------------------
+# Scratch buffers (the reference's `tmp` KernelBuffer)
+# ---------------------------------------------------------------------------
+class KernelBuffer:
+    """Caller-owned scratch for one kind of call. Zero-filled at creation;
+    the kernels keep it valid across calls, so it can be reused with
+    different data (reference test/tests/scan/scan_test.jl:103-125)."""
+
+    def __init__(self, kind, nbytes, device):
+        self.kind = kind
+        self.nbytes = int(max(nbytes, 256))
+        raw = torch.zeros(self.nbytes + 256, dtype=torch.uint8, device=device)
+        off = (-raw.data_ptr()) % 256
+        self._raw = raw
+        self.arr = raw[off:off + self.nbytes]
+
+    @property
+    def ptr(self):
+        return self.arr.data_ptr()
+
+    def __repr__(self):
+        return f"KernelBuffer({self.kind}, {self.nbytes} bytes, {self.arr.device})"
+
+
+_default_tmp = {}
+
+
+def _scratch(kind, need, device, tmp):
+    if tmp is not None:
+        if not isinstance(tmp, KernelBuffer):
+            raise ArgumentError(f"tmp must be a KernelBuffer, got {type(tmp).__name__}")
+        if tmp.nbytes < need:
+            raise ArgumentError(f"tmp holds {tmp.nbytes} bytes, this call needs {need}")
+        return tmp
+    key = (kind, device, torch.cuda.current_stream(device).cuda_stream)
+    buf = _default_tmp.get(key)
+    if buf is None or buf.nbytes < need:
+        buf = KernelBuffer(kind, max(need, 2 * (buf.nbytes if buf else 0)), device)
+        _default_tmp[key] = buf
+    return buf
+
+
+# ---------------------------------------------------------------------------
+# scan! (reference src/scan/scan.jl:218-284)
+# ---------------------------------------------------------------------------
+def _scan_operand(t, op):
+    """(dtype code, n, element stride) of a scan operand."""
+    if op == _L.OP_AFFINE:
+        if t.dtype != torch.float32 or t.dim() != 2 or t.shape[1] != 2:
+            raise ArgumentError("the affine scan takes float32 (a, b) pairs of shape (n, 2)")
+        if t.shape[0] > 0 and (t.stride(1) != 1 or t.stride(0) % 2 != 0):
+            raise ArgumentError("affine pairs must be stored as adjacent (a, b) float32 values")
+        return _L.F32X2, t.shape[0], max(t.stride(0) // 2, 1)
+    if t.dim() != 1:
+        raise ArgumentError(f"scan! takes vectors; got a {t.dim()}-d tensor")
+    if t.dtype not in _DTYPES:
+        raise ArgumentError(f"unsupported element type {t.dtype}")
+    return _DTYPES[t.dtype], t.shape[0], t.stride(0) if t.shape[0] > 1 else 1
+
+
+def _split_f_op(args, n_arrays, name):
+    if len(args) == n_arrays + 1:
+        return identity, args[0], args[1:]
+    if len(args) == n_arrays + 2:
+        return args[0], args[1], args[2:]
+    raise ArgumentError(f"{name} takes ([f,] op, {', '.join(['array'] * n_arrays)})")
+
+
+def scan_(*args, exclusive=False, tmp=None, g=None, **tuning):
+    """scan!([f,] op, dst, src; exclusive=False, tmp=None) -> dst.
+
+    dst[i] = f(src[1]) op ... op f(src[i]) (inclusive, the reference's only
+    mode), or the exclusive variant dst[1] = identity(op),
+    dst[i] = inclusive[i-1]. In place (dst is src) is allowed."""
+    f, op, (dst, src) = _split_f_op(args, 2, "scan!")
+    if g is not None and g is not identity:
+        raise ArgumentError("scan!: only g = identity is supported")
+    opc, fc = _op_code(op), _map_code(f)
+    _require_device(dst, src)
+    dt, n, ss = _scan_operand(src, opc)
+    ddt, dn, ds = _scan_operand(dst, opc)
+    if ddt != dt:
+        raise ArgumentError(f"dst eltype {dst.dtype} differs from src eltype {src.dtype}")
+    if dn != n:
+        raise ArgumentError(f"dst has length {dn}, src has length {n}")
+    if n == 0:
+        return dst
+    L = _L.lib()
+    need = L.kf_scan_scratch_bytes(dt, opc, n)
+    buf = _scratch(Scan1D, need, src.device, tmp)
+    with torch.cuda.device(src.device):
+        rc = L.kf_scan(opc, fc, dt, int(bool(exclusive)), ctypes_void(src.data_ptr()), ss,
+                       ctypes_void(dst.data_ptr()), ds, n, ctypes_void(buf.ptr), buf.nbytes, _stream_ptr(src))
+    _L.check(rc, "scan!")
+    return dst
+
+
+def scan(*args, exclusive=False, tmp=None, g=None, **tuning):
+    """scan([f,] op, src) -> new dst (reference src/scan/scan.jl:218-244)."""
+    f, op, (src,) = _split_f_op(args, 1, "scan")
+    _require_device(src)
+    dst = torch.empty_like(src, memory_format=torch.contiguous_format)
+    return scan_(f, op, dst, src, exclusive=exclusive, tmp=tmp, g=g, **tuning)
+
+
+# ---------------------------------------------------------------------------
+# mapreduce (reference src/mapreduce/mapreduce.jl:51-298)
+# ---------------------------------------------------------------------------
+def _normalize_dims(dims, nd):
+    if isinstance(dims, int):
+        dims = (dims,)
+    try:
+        dims = tuple(int(d) for d in dims)
+    except TypeError:
+        raise ArgumentError(f"dims must be an int or a tuple of ints, got {dims!r}")
+    for d in dims:
+        if not 1 <= d <= nd:
+            raise ArgumentError(f"dimension {d} out of range for {nd}-dimensional array")
+    if len(set(dims)) != len(dims):
+        raise ArgumentError(f"duplicate dimensions in dims={dims}")
+    return tuple(sorted(dims))
+
+
+def _classify_dims(dims, nd):
+    """(lead_end, tail_start) with the reference's meaning
+    (src/mapreduce/mapreduce.jl:272-298): dims[:lead_end] are 1..lead_end,
+    dims[tail_start-1:] are the last dims; (0, N+1) = general layout."""
+    N = len(dims)
+    lead_end = 0
+    for k in range(1, N + 1):
+        if dims[k - 1] == k:
+            lead_end = k
+        else:
+            break
+    tail_start = N + 1
+    for k in range(N, 0, -1):
+        if dims[k - 1] == nd - (N - k):
+            tail_start = k
+        else:
+            break
+    if lead_end > 0 and tail_start <= N:
+        if all(dims[i + 1] == dims[i] + 1 for i in range(N - 1)):
+            return lead_end, N + 1
+    n_tail = N - tail_start + 1 if tail_start <= N else 0
+    if lead_end + n_tail != N:
+        return 0, N + 1
+    return lead_end, tail_start
+
+
+def _merge(sizes, strides):
+    """Single (count, stride) for a run of dims in column-major order, or None."""
+    count, stride, expect = 1, None, None
+    for s, st in zip(sizes, strides):
+        if s == 1:
+            continue
+        if stride is None:
+            stride, expect = st, st * s
+        elif st != expect:
+            return None
+        else:
+            expect = st * s
+        count *= s
+    return count, (stride if stride is not None else 1)
+
+
+def _as_matrix(t, k):
+    """View dims [0, k) as rows and [k, nd) as columns of a column-major
+    matrix: (rows, cols, col_stride). Rows must be unit-stride."""
+    sizes, strides = list(t.shape), list(t.stride())
+    r = _merge(sizes[:k], strides[:k])
+    c = _merge(sizes[k:], strides[k:])
+    if r is None or c is None or (r[0] > 1 and r[1] != 1):
+        raise NotImplementedError(
+            f"layout with shape {tuple(sizes)} and strides {tuple(strides)} cannot be viewed as a "
+            "column-major matrix split at dim {k}")
+    rows, cols = r[0], c[0]
+    col_stride = c[1] if cols > 1 else max(rows, 1)
+    if cols > 1 and col_stride < rows:
+        raise NotImplementedError("overlapping or row-major layout is not supported")
+    return rows, cols, col_stride
+
+
+def _colmajor_empty(shape, dtype, device):
+    nd = len(shape)
+    if nd == 0:
+        return torch.empty((), dtype=dtype, device=device)
+    return torch.empty(tuple(reversed(shape)), dtype=dtype, device=device).permute(*reversed(range(nd)))
+
+
+def _check_reducible(src, opc, fc):
+    if opc == _L.OP_AFFINE:
+        raise ArgumentError("mapreduce needs a commutative operator; the affine operator is scan-only")
+    if src.dtype not in _DTYPES:
+        raise ArgumentError(f"unsupported element type {src.dtype}")
+
+
+def _reduce_full_into(fc, opc, dst, src, tmp):
+    """dst[0] = mapreduce(f, op, src) for any layout expressible as a
+    column-major matrix (1-D strided views included)."""
+    L = _L.lib()
+    dt = _DTYPES[src.dtype]
+    n = src.numel()
+    if n == 0:
+        raise ArgumentError("reducing over an empty collection is not allowed")
+    merged = _merge(list(src.shape), list(src.stride()))
+    stream = _stream_ptr(src)
+    with torch.cuda.device(src.device):
+        if merged is not None:
+            need = L.kf_reduce_scratch_bytes(dt, n)
+            buf = _scratch(MapReduce1D, need, src.device, tmp)
+            rc = L.kf_reduce(opc, fc, dt, ctypes_void(src.data_ptr()), n, merged[1], ctypes_void(dst.data_ptr()),
+                             ctypes_void(buf.ptr), buf.nbytes, stream)
+            _L.check(rc, "mapreduce")
+            return
+        # two passes: columns of the first-dim-contiguous matrix, then the column results
+        rows, cols, cs = _as_matrix(src, 1)
+        part = torch.empty(cols, dtype=src.dtype, device=src.device)
+        _reduce_dim_into(fc, opc, part, 1, src, rows, cols, cs, 1, None)
+        need = L.kf_reduce_scratch_bytes(dt, cols)
+        buf = _scratch(MapReduce1D, need, src.device, tmp)
+        rc = L.kf_reduce(opc, _L.MAP_IDENTITY, dt, ctypes_void(part.data_ptr()), cols, 1,
+                         ctypes_void(dst.data_ptr()), ctypes_void(buf.ptr), buf.nbytes, stream)
+        _L.check(rc, "mapreduce")
+
+
+def _reduce_dim_into(fc, opc, dst, dst_stride, src, rows, cols, cs, dim, tmp, base_ptr=None):
+    L = _L.lib()
+    dt = _DTYPES[src.dtype]
+    need = L.kf_reduce_dim_scratch_bytes(dt, rows, cols, dim)
+    buf = _scratch(MapReduce2D, need, src.device, tmp)
+    ptr = src.data_ptr() if base_ptr is None else base_ptr
+    with torch.cuda.device(src.device):
+        rc = L.kf_reduce_dim(opc, fc, dt, ctypes_void(ptr), rows, cols, cs, dim, ctypes_void(dst.data_ptr()),
+                             dst_stride, ctypes_void(buf.ptr), buf.nbytes, _stream_ptr(src))
+    _L.check(rc, f"mapreduce(dims={dim})")
+
+
+def _to_scalar(t):
+    return t.item()
+
+
+def mapreduce(f, op, src, dims=None, g=None, tmp=None, **tuning):
+    """mapreduce(f, op, src; dims=None) (reference src/mapreduce/mapreduce.jl:51-120).
+
+    dims=None or ":" -> host scalar; otherwise a tensor with size 1 along the
+    reduced dims, laid out column-major. `g` (post-map) is supported for the
+    full reduction, where it is applied to the returned scalar."""
+    fc, opc = _map_code(f), _op_code(op)
+    _require_device(src)
+    _check_reducible(src, opc, fc)
+    if dims is None or dims == ":" or dims is Ellipsis:
+        out = torch.empty(1, dtype=src.dtype, device=src.device)
+        _reduce_full_into(fc, opc, out, src, tmp)
+        val = _to_scalar(out)
+        return g(val) if g is not None else val
+    if g is not None and g is not identity:
+        raise ArgumentError("mapreduce with dims: only g = identity is supported")
+    nd = src.dim()
+    dims_t = _normalize_dims(dims, nd)
+    shape = list(src.shape)
+    out_shape = [1 if (i + 1) in dims_t else s for i, s in enumerate(shape)]
+    dst = _colmajor_empty(out_shape, src.dtype, src.device)
+    mapreduce_(f, op, dst, src, dims=dims_t, tmp=tmp)
+    return dst
+
+
+def mapreduce_(f, op, dst, src, dims=None, g=None, tmp=None, **tuning):
+    """mapreduce!(f, op, dst, src; dims=None) (reference src/mapreduce/mapreduce.jl:151-212)."""
+    fc, opc = _map_code(f), _op_code(op)
+    _require_device(dst, src)
+    _check_reducible(src, opc, fc)
+    if g is not None and g is not identity:
+        raise ArgumentError("mapreduce!: only g = identity is supported")
+    if dst.dtype != src.dtype:
+        raise ArgumentError(f"dst eltype {dst.dtype} differs from src eltype {src.dtype}")
+    if dims is None or dims == ":" or dims is Ellipsis:
+        if dst.numel() < 1:
+            raise ArgumentError("dst must hold at least one element")
+        _reduce_full_into(fc, opc, dst.as_strided((1,), (1,)), src, tmp)
+        return dst
+    nd = src.dim()
+    dims_t = _normalize_dims(dims, nd)
+    shape = list(src.shape)
+    keep = [s for i, s in enumerate(shape) if (i + 1) not in dims_t]
+    nkeep = 1
+    for s in keep:
+        nkeep *= s
+    if dst.numel() != nkeep:
+        raise ArgumentError(f"dst has {dst.numel()} elements, the reduction produces {nkeep}")
+    dflat = _merge(list(dst.shape), list(dst.stride()))
+    if dflat is None:
+        raise ArgumentError("dst must be expressible as a strided vector")
+    dst_stride = dflat[1]
+    if src.numel() == 0:
+        if nkeep:
+            raise ArgumentError("reducing over an empty dimension is not allowed")
+        return dst
+    if len(dims_t) == nd:  # every dim: a full reduction into a (1,...,1) array
+        _reduce_full_into(fc, opc, dst, src, tmp)
+        return dst
+    lead_end, tail_start = _classify_dims(dims_t, nd)
+    leading, trailing = lead_end > 0, tail_start <= len(dims_t)
+    if leading and not trailing:
+        rows, cols, cs = _as_matrix(src, lead_end)
+        _reduce_dim_into(fc, opc, dst, dst_stride, src, rows, cols, cs, 1, tmp)
+        return dst
+    if trailing and not leading:
+        k = dims_t[tail_start - 1] - 1
+        rows, cols, cs = _as_matrix(src, k)
+        _reduce_dim_into(fc, opc, dst, dst_stride, src, rows, cols, cs, 2, tmp)
+        return dst
+    if leading and trailing:
+        # trailing block first (no map afterwards), then the leading block
+        k = dims_t[tail_start - 1] - 1
+        rows, cols, cs = _as_matrix(src, k)
+        mid = torch.empty(rows, dtype=src.dtype, device=src.device)
+        _reduce_dim_into(fc, opc, mid, 1, src, rows, cols, cs, 2, tmp)
+        lead = 1
+        for s in shape[:lead_end]:
+            lead *= s
+        _reduce_dim_into(_L.MAP_IDENTITY, opc, dst, dst_stride, mid, lead, rows // lead, lead, 1, tmp)
+        return dst
+    raise NotImplementedError(
+        f"dims={dims_t} on a {nd}-d array needs the general-dims kernel (reference mapreducedims), "
+        "which this build does not provide yet")
+
+
+def get_allocation(kind, f, op, src, *args, **kwargs):
+    """Scratch for a later call with the same operands
+    (reference src/scan/scan.jl:156-211, src/mapreduce/1D/mapreduce1d.jl:140-170).
+    kind: Scan1D, MapReduce1D or MapReduce2D (then pass dims=1 or 2)."""
+    L = _L.lib()
+    opc = _op_code(op)
+    _map_code(f)
+    _require_device(src)
+    if kind == Scan1D:
+        dt, n, _ = _scan_operand(src, opc)
+        need = L.kf_scan_scratch_bytes(dt, opc, n)
+    elif kind == MapReduce1D:
+        need = L.kf_reduce_scratch_bytes(_DTYPES[src.dtype], src.numel())
+    elif kind == MapReduce2D:
+        dim = int(kwargs.get("dims", args[0] if args else 1))
+        rows, cols, _ = _as_matrix(src, 1) if src.dim() == 2 else (src.numel(), 1, src.numel())
+        need = L.kf_reduce_dim_scratch_bytes(_DTYPES[src.dtype], rows, cols, dim)
+    else:
+        raise ArgumentError(f"unknown allocation kind {kind!r}")
+    return KernelBuffer(kind, need, src.device)
+
+
+def vcopy_(dst, src):
+    """vcopy!(dst, src) (reference src/copy/copy.jl:24-28): dst .= src for
+    contiguous tensors of equal size in bytes."""
+    _require_device(dst, src)
+    if not (dst.is_contiguous() and src.is_contiguous()):
+        raise ArgumentError("vcopy! needs contiguous tensors")
+    nb = src.numel() * src.element_size()
+    if dst.numel() * dst.element_size() != nb:
+        raise ArgumentError("vcopy!: size mismatch")
+    with torch.cuda.device(src.device):
+        rc = _L.lib().kf_copy(ctypes_void(dst.data_ptr()), ctypes_void(src.data_ptr()), nb, _stream_ptr(src))
+    _L.check(rc, "vcopy!")
+    return dst

@@ -1,0 +1,68 @@
+"""ctypes binding of libkfhip.so (the C ABI declared in include/kf.h).
+
+The library must have been built (kernelforge.jl_amd/build.py); there is no
+fallback: a missing library raises at first use.
+"""
+import ctypes
+import os
+import threading
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libkfhip.so")
+
+# enums mirrored from include/kf.h
+KF_OK, KF_EINVAL, KF_ENOSCRATCH, KF_EHIP = 0, 1, 2, 3
+OP_ADD, OP_MAX, OP_MIN, OP_AFFINE = 0, 1, 2, 3
+MAP_IDENTITY, MAP_ABS2 = 0, 1
+F32, F64, I32, I64, U8, F32X2 = 0, 1, 2, 3, 4, 5
+
+# Every symbol include/kf.h declares, with its ctypes signature.
+_P, _I, _I64, _SZ = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_size_t
+SIGNATURES = {
+    "kf_version": ([], _I),
+    "kf_last_error": ([], ctypes.c_char_p),
+    "kf_scratch_reset": ([_P, _SZ, _P], _I),
+    "kf_scan_scratch_bytes": ([_I, _I, _I64], _SZ),
+    "kf_scan": ([_I, _I, _I, _I, _P, _I64, _P, _I64, _I64, _P, _SZ, _P], _I),
+    "kf_reduce_scratch_bytes": ([_I, _I64], _SZ),
+    "kf_reduce": ([_I, _I, _I, _P, _I64, _I64, _P, _P, _SZ, _P], _I),
+    "kf_reduce_dim_scratch_bytes": ([_I, _I64, _I64, _I], _SZ),
+    "kf_reduce_dim": ([_I, _I, _I, _P, _I64, _I64, _I64, _I, _P, _I64, _P, _SZ, _P], _I),
+    "kf_copy": ([_P, _P, _SZ, _P], _I),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+class KernelForgeError(RuntimeError):
+    """A HIP-level failure reported by libkfhip (KF_EHIP)."""
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        with _lock:
+            if _lib is None:
+                if not os.path.exists(LIB_PATH):
+                    raise RuntimeError(
+                        f"{LIB_PATH} is not built; run kernelforge.jl_amd/build.py "
+                        "(or __graft_entry__.build()) first")
+                L = ctypes.CDLL(LIB_PATH)
+                for name, (args, res) in SIGNATURES.items():
+                    fn = getattr(L, name)
+                    fn.argtypes = args
+                    fn.restype = res
+                _lib = L
+    return _lib
+
+
+def check(rc, what):
+    """Translate a kf_status into the exception the reference raises."""
+    if rc == KF_OK:
+        return
+    msg = lib().kf_last_error().decode(errors="replace")
+    if rc in (KF_EINVAL, KF_ENOSCRATCH):
+        from . import ArgumentError
+        raise ArgumentError(f"{what}: {msg}")
+    raise KernelForgeError(f"{what}: {msg}")

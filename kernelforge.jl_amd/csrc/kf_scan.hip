@@ -1,0 +1,356 @@
+// Single-pass decoupled-lookback prefix scan for gfx950.
+//
+// Follows the algorithm of the reference's scan_kernel_packed! /
+// scan_kernel! (reference src/scan/scan_kernel.jl:94-478): per-tile
+// thread/wave/block scan, publish the tile aggregate (PARTIAL), look back
+// over predecessor descriptors until an inclusive prefix (PREFIX) is found,
+// publish the tile's own PREFIX, apply the prefix and store. The MI355X
+// design differs from the reference in these ways:
+//
+//  * Tile = 256 threads x 64 bytes per lane = 16 KiB. Each wave loads its
+//    4 KiB chunk with 16-byte streaming loads in striped order (fully
+//    coalesced), transposes it through a bank-padded LDS region into a
+//    per-lane blocked run, and transposes back for 16-byte stores.
+//  * Wave scans use DPP row shifts and row broadcasts (no LDS, no
+//    ds_bpermute). The lookback window is one wave: lane j reads the
+//    descriptor of tile (t - 64 + j) so lane order is tile order and a DPP
+//    scan combines the window in the order a non-commutative op needs.
+//  * Descriptors are W 64-bit words per tile (W = sizeof(T)/4, at least 1).
+//    Every word carries a 32-bit tag {epoch:30, state:2} next to 32 bits of
+//    the value, and is written/read with relaxed device-scope atomics, so a
+//    reader either sees all W words with one tag (a consistent value) or
+//    retries; no fences are needed for any element size (the reference uses
+//    one packed word for <= 4-byte types and a split flag/partial layout
+//    with fences otherwise, scan_kernel.jl:24-58, :94-299).
+//  * Tiles are numbered by an atomic ticket, not by workgroup id, so a tile
+//    only ever waits on tiles that already started. The ticket counter and
+//    the epoch share one 64-bit word; the block holding the last ticket
+//    advances the epoch and clears the counter. Descriptors of earlier calls
+//    carry older epochs and read as INVALID, so the scratch buffer needs no
+//    clearing between calls (the reference fill!s its descriptors before
+//    every launch, src/scan/scan.jl:444-470).
+#include "kf_common.h"
+
+namespace kf {
+
+constexpr int kScanBlock = 256;
+constexpr int kScanWaves = kScanBlock / kWave;
+constexpr int kLaneBytes = 64;                         // bytes of the tile each lane owns
+constexpr int kWaveSlots = 256 + 32;                   // 16-byte LDS slots per wave, incl. padding
+constexpr uint32_t kStatePartial = 1, kStatePrefix = 2;
+constexpr size_t kScanHeaderBytes = 256;
+constexpr uint32_t kSpinLimit = 1u << 24;  // lookback polls before giving up (seconds)
+
+template <class T> struct ScanShape {
+  static constexpr int ITEMS = kLaneBytes / (int)sizeof(T);
+  static constexpr int TILE = kScanBlock * ITEMS;
+  static constexpr int W = Words<T>::W;
+};
+
+// One 16-byte pad slot after every 8 slots: both the striped pattern
+// (consecutive lanes -> consecutive slots) and the blocked pattern
+// (lane l -> slots 4l..4l+3) hit distinct 16-byte bank groups.
+__device__ inline int pad_slot(int s) { return s + (s >> 3); }
+
+template <class T> __device__ inline int pad_elem(int e) {
+  constexpr int per_slot = 16 / (int)sizeof(T);
+  const int s = e / per_slot;
+  return pad_slot(s) * per_slot + (e - s * per_slot);
+}
+
+template <class T>
+__device__ inline void publish(uint64_t* desc, int64_t tile, uint32_t tag, T v) {
+  const Words<T> w = to_words(v);
+#pragma unroll
+  for (int i = 0; i < ScanShape<T>::W; ++i)
+    st_agent(desc + tile * ScanShape<T>::W + i, ((uint64_t)tag << 32) | w.w[i]);
+}
+
+// Decoupled lookback, executed by one full wave. Returns the combination of
+// every tile before `tile` (tile > 0), in tile order.
+template <class T, class Op>
+__device__ inline T lookback(const uint64_t* desc, int64_t tile, uint32_t epoch30) {
+  constexpr int W = ScanShape<T>::W;
+  const int lane = lane_id();
+  const T id = Op::template identity<T>();
+  T run = id;
+  int64_t newest = tile - 1;  // the window's lane 63
+  for (uint32_t polls = 0;; ++polls) {
+    if (polls == kSpinLimit) {
+      // A predecessor never published: impossible unless the scratch buffer
+      // was corrupted or shared by concurrent calls. Record it in header word
+      // 1 and finish the grid (results are then invalid) instead of hanging.
+      __hip_atomic_fetch_or(const_cast<uint64_t*>(desc) - kScanHeaderBytes / sizeof(uint64_t) + 1,
+                            (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return run;
+    }
+    const int64_t t = newest - (kWave - 1) + lane;
+    T v = id;
+    uint32_t state = kStatePrefix;  // tiles before 0: an identity prefix
+    if (t >= 0) {
+      uint64_t d[W];
+#pragma unroll
+      for (int i = 0; i < W; ++i) d[i] = ld_agent(desc + t * W + i);
+      const uint32_t tag = (uint32_t)(d[0] >> 32);
+      bool ok = (tag >> 2) == epoch30;
+#pragma unroll
+      for (int i = 1; i < W; ++i) ok &= (uint32_t)(d[i] >> 32) == tag;
+      state = ok ? (tag & 3u) : 0u;
+      Words<T> w;
+#pragma unroll
+      for (int i = 0; i < W; ++i) w.w[i] = (uint32_t)d[i];
+      v = from_words<T>(w);
+    }
+    const uint64_t invalid = __builtin_amdgcn_ballot_w64(state == 0);
+    const uint64_t prefix = __builtin_amdgcn_ballot_w64(state == kStatePrefix);
+    if (prefix != 0) {
+      const int m = 63 - __builtin_clzll(prefix);
+      if ((invalid >> m) == 0) {
+        const T tot = wave_reduce<Op>(lane >= m ? v : id);
+        return Op::combine(tot, run);
+      }
+    } else if (invalid == 0) {
+      const T tot = wave_reduce<Op>(v);
+      run = Op::combine(tot, run);
+      newest -= kWave;
+      continue;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+template <class T, class Op> __device__ inline T exclusive_first() {
+  if constexpr (__is_same(Op, OpAdd) && (__is_same(T, float) || __is_same(T, double)))
+    return T(0);  // +0.0, as Julia / CUB produce for the first exclusive sum
+  else
+    return Op::template identity<T>();
+}
+
+template <class T, class Op, class Map>
+__global__ __launch_bounds__(kScanBlock) void scan_kernel(
+    const T* src, int64_t src_stride, T* dst, int64_t dst_stride, int64_t n,
+    int64_t ntiles, uint64_t* scratch, int exclusive, int vec) {
+  constexpr int ITEMS = ScanShape<T>::ITEMS;
+  constexpr int TILE = ScanShape<T>::TILE;
+  __shared__ uint4 lds[kScanWaves * kWaveSlots];
+  __shared__ T wave_agg[kScanWaves];
+  __shared__ T block_excl;
+  __shared__ uint64_t s_ticket;
+
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int wave = tid / kWave;
+  const T id = Op::template identity<T>();
+
+  if (tid == 0) {
+    const uint64_t tk = __hip_atomic_fetch_add(scratch, (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_ticket = tk;
+    if ((int64_t)(uint32_t)tk == ntiles - 1)  // every ticket is out: next call's epoch
+      st_agent(scratch, ((tk >> 32) + 1) << 32);
+  }
+  __syncthreads();
+  const uint64_t tk = s_ticket;
+  const int64_t tile = (int64_t)(uint32_t)tk;
+  const uint32_t epoch30 = (uint32_t)(tk >> 32) & 0x3fffffffu;
+  uint64_t* desc = scratch + kScanHeaderBytes / sizeof(uint64_t);
+
+  const int64_t wbase = tile * TILE + (int64_t)wave * kWave * ITEMS;  // first element of this wave's chunk
+  const bool full = vec && (tile + 1) * TILE <= n;
+  uint4* wl = lds + wave * kWaveSlots;
+  T* wlt = reinterpret_cast<T*>(wl);
+
+  // ---- load: striped global -> LDS -> blocked registers -------------------
+  T items[ITEMS];
+  if (full) {
+    const uint4* g = reinterpret_cast<const uint4*>(src + wbase);
+    uint4 r[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) r[j] = ld_stream(g + j * kWave + lane);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) wl[pad_slot(j * kWave + lane)] = r[j];
+  } else {
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) {
+      const int e = i * kWave + lane;
+      const int64_t idx = wbase + e;
+      wlt[pad_elem<T>(e)] = idx < n ? Map::apply(src[idx * src_stride]) : id;
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  {
+    uint4 q[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) q[k] = wl[pad_slot(lane * 4 + k)];
+    __builtin_memcpy(items, q, sizeof(items));
+  }
+  if (full) {
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) items[i] = Map::apply(items[i]);
+  }
+
+  // ---- thread, wave and block scans ---------------------------------------
+#pragma unroll
+  for (int i = 1; i < ITEMS; ++i) items[i] = Op::combine(items[i - 1], items[i]);
+  const T lane_incl = wave_inclusive_scan<Op>(items[ITEMS - 1]);
+  const T lane_excl = wave_shift_right<Op>(lane_incl);
+  if (lane == kWave - 1) wave_agg[wave] = lane_incl;
+  __syncthreads();
+
+  if (wave == 0) {
+    T agg = wave_agg[0];
+#pragma unroll
+    for (int w = 1; w < kScanWaves; ++w) agg = Op::combine(agg, wave_agg[w]);
+    T excl = id;
+    if (tile == 0) {
+      if (lane == 0) publish(desc, tile, (epoch30 << 2) | kStatePrefix, agg);
+    } else {
+      if (lane == 0) publish(desc, tile, (epoch30 << 2) | kStatePartial, agg);
+      excl = lookback<T, Op>(desc, tile, epoch30);
+      if (lane == 0) publish(desc, tile, (epoch30 << 2) | kStatePrefix, Op::combine(excl, agg));
+    }
+    if (lane == 0) block_excl = excl;
+  }
+  __syncthreads();
+
+  T prefix = block_excl;
+  for (int w = 0; w < wave; ++w) prefix = Op::combine(prefix, wave_agg[w]);
+  prefix = Op::combine(prefix, lane_excl);
+
+  if (exclusive) {
+#pragma unroll
+    for (int i = ITEMS - 1; i > 0; --i) items[i] = Op::combine(prefix, items[i - 1]);
+    items[0] = (tile == 0 && tid == 0) ? exclusive_first<T, Op>() : prefix;
+  } else {
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) items[i] = Op::combine(prefix, items[i]);
+  }
+
+  // ---- store: blocked registers -> LDS -> striped global ------------------
+  {
+    uint4 q[4];
+    __builtin_memcpy(q, items, sizeof(items));
+#pragma unroll
+    for (int k = 0; k < 4; ++k) wl[pad_slot(lane * 4 + k)] = q[k];
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  if (full) {
+    uint4* g = reinterpret_cast<uint4*>(dst + wbase);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) st_stream(g + j * kWave + lane, wl[pad_slot(j * kWave + lane)]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) {
+      const int e = i * kWave + lane;
+      const int64_t idx = wbase + e;
+      if (idx < n) dst[idx * dst_stride] = wlt[pad_elem<T>(e)];
+    }
+  }
+}
+
+template <class T> int64_t scan_tiles(int64_t n) {
+  return (n + ScanShape<T>::TILE - 1) / ScanShape<T>::TILE;
+}
+
+template <class T> size_t scan_scratch(int64_t n) {
+  return kScanHeaderBytes + (size_t)scan_tiles<T>(n) * ScanShape<T>::W * sizeof(uint64_t);
+}
+
+template <class T, class Op, class Map>
+int launch_scan(const void* src, int64_t ss, void* dst, int64_t ds, int64_t n, int excl,
+                void* scratch, hipStream_t stream) {
+  const int64_t ntiles = scan_tiles<T>(n);
+  const bool vec = ss == 1 && ds == 1 && ((uintptr_t)src % 16 == 0) && ((uintptr_t)dst % 16 == 0);
+  hipLaunchKernelGGL((scan_kernel<T, Op, Map>), dim3((unsigned)ntiles), dim3(kScanBlock), 0, stream,
+                     (const T*)src, ss, (T*)dst, ds, n, ntiles, (uint64_t*)scratch, excl, (int)vec);
+  return kf_check_launch("scan_kernel");
+}
+
+template <class T, class Op>
+int scan_map(kf_map f, const void* src, int64_t ss, void* dst, int64_t ds, int64_t n, int excl,
+             void* scratch, hipStream_t stream) {
+  if constexpr (__is_same(T, f32x2)) {
+    return launch_scan<T, Op, MapIdentity>(src, ss, dst, ds, n, excl, scratch, stream);
+  } else {
+    if (f == KF_MAP_ABS2) return launch_scan<T, Op, MapAbs2>(src, ss, dst, ds, n, excl, scratch, stream);
+    return launch_scan<T, Op, MapIdentity>(src, ss, dst, ds, n, excl, scratch, stream);
+  }
+}
+
+template <class T>
+int scan_op(kf_op op, kf_map f, const void* src, int64_t ss, void* dst, int64_t ds, int64_t n,
+            int excl, void* scratch, hipStream_t stream) {
+  if constexpr (__is_same(T, f32x2)) {
+    return scan_map<T, OpAffine>(f, src, ss, dst, ds, n, excl, scratch, stream);
+  } else {
+    switch (op) {
+      case KF_OP_ADD: return scan_map<T, OpAdd>(f, src, ss, dst, ds, n, excl, scratch, stream);
+      case KF_OP_MAX: return scan_map<T, OpMax>(f, src, ss, dst, ds, n, excl, scratch, stream);
+      default: return scan_map<T, OpMin>(f, src, ss, dst, ds, n, excl, scratch, stream);
+    }
+  }
+}
+
+}  // namespace kf
+
+using namespace kf;
+
+extern "C" size_t kf_scan_scratch_bytes(kf_dtype dt, kf_op op, int64_t n) {
+  (void)op;
+  if (n < 0) n = 0;
+  switch (dt) {
+    case KF_F32: return scan_scratch<float>(n);
+    case KF_F64: return scan_scratch<double>(n);
+    case KF_I32: return scan_scratch<int32_t>(n);
+    case KF_I64: return scan_scratch<int64_t>(n);
+    case KF_U8: return scan_scratch<uint8_t>(n);
+    case KF_F32X2: return scan_scratch<f32x2>(n);
+  }
+  return 0;
+}
+
+extern "C" int kf_scan(kf_op op, kf_map f, kf_dtype dt, int exclusive, const void* src,
+                       int64_t src_stride, void* dst, int64_t dst_stride, int64_t n, void* scratch,
+                       size_t scratch_bytes, void* stream) {
+  int rc = kf_validate_op(op, f, dt, /*allow_affine=*/1);
+  if (rc) return rc;
+  if (n < 0) return kf_set_error(KF_EINVAL, "kf_scan: n = %lld < 0", (long long)n);
+  if (n == 0) return KF_OK;
+  if (!src || !dst) return kf_set_error(KF_EINVAL, "kf_scan: null src or dst");
+  if (src_stride < 1 || dst_stride < 1)
+    return kf_set_error(KF_EINVAL, "kf_scan: strides must be >= 1 (got %lld, %lld)",
+                        (long long)src_stride, (long long)dst_stride);
+  const size_t es = kf_dtype_size(dt);
+  const size_t align = dt == KF_F32X2 ? 4 : es;
+  if ((uintptr_t)src % align || (uintptr_t)dst % align)
+    return kf_set_error(KF_EINVAL, "kf_scan: src/dst not aligned to the element type");
+  // Overlap other than exact in-place aliasing would make tiles read data
+  // that other tiles already overwrote.
+  if (src != dst || src_stride != dst_stride) {
+    const uintptr_t s0 = (uintptr_t)src, s1 = s0 + (uintptr_t)((n - 1) * src_stride + 1) * es;
+    const uintptr_t d0 = (uintptr_t)dst, d1 = d0 + (uintptr_t)((n - 1) * dst_stride + 1) * es;
+    if (s0 < d1 && d0 < s1)
+      return kf_set_error(KF_EINVAL, "kf_scan: src and dst overlap without being identical");
+  }
+  const size_t need = kf_scan_scratch_bytes(dt, op, n);
+  if (!scratch || scratch_bytes < need)
+    return kf_set_error(KF_ENOSCRATCH, "kf_scan: scratch of %zu bytes needed, %zu given", need,
+                        scratch ? scratch_bytes : (size_t)0);
+  if ((uintptr_t)scratch % 256)
+    return kf_set_error(KF_EINVAL, "kf_scan: scratch must be 256-byte aligned");
+  if (scan_tiles<f32x2>(n) * kScanBlock > (int64_t)0xffffffffLL)
+    return kf_set_error(KF_EINVAL, "kf_scan: n = %lld exceeds the grid limit", (long long)n);
+  hipStream_t s = (hipStream_t)stream;
+  switch (dt) {
+    case KF_F32: return scan_op<float>(op, f, src, src_stride, dst, dst_stride, n, exclusive, scratch, s);
+    case KF_F64: return scan_op<double>(op, f, src, src_stride, dst, dst_stride, n, exclusive, scratch, s);
+    case KF_I32: return scan_op<int32_t>(op, f, src, src_stride, dst, dst_stride, n, exclusive, scratch, s);
+    case KF_I64: return scan_op<int64_t>(op, f, src, src_stride, dst, dst_stride, n, exclusive, scratch, s);
+    case KF_U8: return scan_op<uint8_t>(op, f, src, src_stride, dst, dst_stride, n, exclusive, scratch, s);
+    case KF_F32X2: return scan_op<f32x2>(op, f, src, src_stride, dst, dst_stride, n, exclusive, scratch, s);
+  }
+  return kf_set_error(KF_EINVAL, "kf_scan: bad dtype");
+}

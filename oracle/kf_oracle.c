@@ -1,0 +1,284 @@
+/*
+ * kf_oracle.c — CPU restatement of KernelForge.jl's scan / mapreduce
+ * semantics. TEST INFRASTRUCTURE ONLY: used by tests/, by
+ * __graft_entry__.smoke() and by bench.py's cpu_baseline leg, as the checker
+ * and as the timed CPU baseline. Nothing in the product links it.
+ *
+ * Two families of functions:
+ *
+ *  (1) Checkers (kfo_*): the reference's results as its own tests define
+ *      them — Julia Base `accumulate(op, x)` for scan!
+ *      (reference test/tests/scan/scan_test.jl:10,54,81,99,119) and Base
+ *      `mapreduce` / `sum` for mapreduce
+ *      (test/tests/mapreduce/mapreduce1d_test.jl:20-29,
+ *      test/tests/mapreduce/mapreduce2d_test.jl:8-35). Float inputs are
+ *      accumulated in double (the Float64 host accumulation the tolerance
+ *      is stated against); integer inputs are computed exactly in their own
+ *      width with wrap-around, which is Julia's Int32/Int64/UInt8 `+`.
+ *      The in-thread left fold follows src/helpers.jl:170-174
+ *      (a_i = op(a_{i-1}, v_i)); prefixes compose as op(older, newer)
+ *      (src/scan/scan_kernel.jl:1-7, :396-412).
+ *
+ *  (2) CPU baseline (kfb_*): the same operations in the element's own
+ *      arithmetic (what Base.accumulate! / Base.mapreduce compute on the
+ *      host), single-threaded and OpenMP-chunked, for the bench's
+ *      cpu_baseline figure.
+ *
+ * Codes: dtype 0 f32, 1 f64, 2 i32, 3 i64, 4 u8, 5 (a,b) f32 pairs;
+ *        op 0 +, 1 max, 2 min, 3 affine; map 0 identity, 1 abs2.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+enum { D_F32 = 0, D_F64 = 1, D_I32 = 2, D_I64 = 3, D_U8 = 4, D_F32X2 = 5 };
+enum { OP_ADD = 0, OP_MAX = 1, OP_MIN = 2, OP_AFFINE = 3 };
+
+/* Julia `max`/`min` on IEEE floats: NaN-propagating, -0.0 < +0.0. */
+static double jl_max(double x, double y) {
+  if (isnan(x) || isnan(y)) return NAN;
+  if (x == y) return signbit(x) ? y : x;
+  return x > y ? x : y;
+}
+static double jl_min(double x, double y) {
+  if (isnan(x) || isnan(y)) return NAN;
+  if (x == y) return signbit(x) ? x : y;
+  return x < y ? x : y;
+}
+
+static double fop(int op, double x, double y) {
+  switch (op) {
+    case OP_ADD: return x + y;
+    case OP_MAX: return jl_max(x, y);
+    default: return jl_min(x, y);
+  }
+}
+
+static double fload(const void* p, int dt, int64_t i, int map) {
+  double v = dt == D_F32 ? (double)((const float*)p)[i] : ((const double*)p)[i];
+  return map ? v * v : v;
+}
+
+/* Integers are carried as uint64 and truncated to the element width after
+ * every operation (wrap-around); max/min compare in the signed (or, for u8,
+ * unsigned) domain of the element type. */
+static uint64_t wrap(int dt, uint64_t v) {
+  switch (dt) {
+    case D_I32: return (uint64_t)(int64_t)(int32_t)(uint32_t)v;
+    case D_U8: return v & 0xffu;
+    default: return v;
+  }
+}
+static uint64_t iload(const void* p, int dt, int64_t i, int map) {
+  uint64_t v;
+  switch (dt) {
+    case D_I32: v = (uint64_t)(int64_t)((const int32_t*)p)[i]; break;
+    case D_I64: v = (uint64_t)((const int64_t*)p)[i]; break;
+    default: v = ((const uint8_t*)p)[i]; break;
+  }
+  if (map) v = wrap(dt, v * v);
+  return v;
+}
+static uint64_t iop(int dt, int op, uint64_t x, uint64_t y) {
+  if (op == OP_ADD) return wrap(dt, x + y);
+  if (dt == D_U8) {
+    if (op == OP_MAX) return x > y ? x : y;
+    return x < y ? x : y;
+  }
+  if (op == OP_MAX) return (int64_t)x > (int64_t)y ? x : y;
+  return (int64_t)x < (int64_t)y ? x : y;
+}
+static uint64_t iidentity(int dt, int op) {
+  if (op == OP_ADD) return 0;
+  if (dt == D_U8) return op == OP_MAX ? 0 : 255;
+  if (dt == D_I32) return op == OP_MAX ? (uint64_t)(int64_t)INT32_MIN : (uint64_t)(int64_t)INT32_MAX;
+  return op == OP_MAX ? (uint64_t)INT64_MIN : (uint64_t)INT64_MAX;
+}
+static void istore(void* p, int dt, int64_t i, uint64_t v) {
+  switch (dt) {
+    case D_I32: ((int32_t*)p)[i] = (int32_t)(uint32_t)v; break;
+    case D_I64: ((int64_t*)p)[i] = (int64_t)v; break;
+    default: ((uint8_t*)p)[i] = (uint8_t)v; break;
+  }
+}
+
+/* ---------------------------------------------------------------- scan ---- */
+
+/* Float scan, double accumulation. Exclusive: out[0] = identity (+0.0 for
+ * +, -Inf for max, +Inf for min), out[i] = inclusive[i-1]. */
+void kfo_scan_f(const void* src, int dt, int64_t n, int64_t stride, int op, int map, int excl, double* out) {
+  double acc = 0.0;
+  const double id = op == OP_ADD ? 0.0 : (op == OP_MAX ? -INFINITY : INFINITY);
+  for (int64_t i = 0; i < n; ++i) {
+    const double v = fload(src, dt, i * stride, map);
+    const double prev = i == 0 ? id : acc;
+    acc = i == 0 ? v : fop(op, acc, v);
+    out[i] = excl ? prev : acc;
+  }
+}
+
+/* Integer scan, exact, result in the element type. */
+void kfo_scan_i(const void* src, int dt, int64_t n, int64_t stride, int op, int map, int excl, void* out) {
+  uint64_t acc = 0;
+  const uint64_t id = iidentity(dt, op);
+  for (int64_t i = 0; i < n; ++i) {
+    const uint64_t v = iload(src, dt, i * stride, map);
+    const uint64_t prev = i == 0 ? id : acc;
+    acc = i == 0 ? v : iop(dt, op, acc, v);
+    istore(out, dt, i, excl ? prev : acc);
+  }
+}
+
+/* Affine-composition scan of (a, b) float pairs in double:
+ * (a1,b1) o (a2,b2) = (a2*a1, a2*b1 + b2). The b-component of the inclusive
+ * result is the recurrence x_t = a_t x_{t-1} + b_t with x_0 = 0, the
+ * a-component the running product. Exclusive: out[0] = (1, 0). */
+void kfo_scan_affine(const float* ab, int64_t n, int excl, double* out) {
+  double A = 1.0, B = 0.0;
+  for (int64_t i = 0; i < n; ++i) {
+    const double a = ab[2 * i], b = ab[2 * i + 1];
+    if (excl) {
+      out[2 * i] = A;
+      out[2 * i + 1] = B;
+    }
+    const double nA = a * A, nB = a * B + b;
+    A = nA;
+    B = nB;
+    if (!excl) {
+      out[2 * i] = A;
+      out[2 * i + 1] = B;
+    }
+  }
+}
+
+/* -------------------------------------------------------------- reduce ---- */
+
+double kfo_reduce_f(const void* src, int dt, int64_t n, int64_t stride, int op, int map) {
+  double acc = fload(src, dt, 0, map);
+  for (int64_t i = 1; i < n; ++i) acc = fop(op, acc, fload(src, dt, i * stride, map));
+  return acc;
+}
+
+/* Also writes the element-typed result to *out (an int32/int64/uint8). */
+void kfo_reduce_i(const void* src, int dt, int64_t n, int64_t stride, int op, int map, void* out) {
+  uint64_t acc = iload(src, dt, 0, map);
+  for (int64_t i = 1; i < n; ++i) acc = iop(dt, op, acc, iload(src, dt, i * stride, map));
+  istore(out, dt, 0, acc);
+}
+
+/* Column-major A[i, j] = A[i + j*col_stride]. dim 1 -> cols outputs, dim 2
+ * -> rows outputs (reference src/mapreduce/2D/mapreduce2d.jl:49-64). */
+void kfo_reduce_dim_f(const void* A, int dt, int64_t rows, int64_t cols, int64_t col_stride, int dim, int op,
+                      int map, double* out) {
+  if (dim == 1) {
+    for (int64_t j = 0; j < cols; ++j) {
+      double acc = fload(A, dt, j * col_stride, map);
+      for (int64_t i = 1; i < rows; ++i) acc = fop(op, acc, fload(A, dt, i + j * col_stride, map));
+      out[j] = acc;
+    }
+  } else {
+    for (int64_t i = 0; i < rows; ++i) out[i] = fload(A, dt, i, map);
+    for (int64_t j = 1; j < cols; ++j)
+      for (int64_t i = 0; i < rows; ++i) out[i] = fop(op, out[i], fload(A, dt, i + j * col_stride, map));
+  }
+}
+
+void kfo_reduce_dim_i(const void* A, int dt, int64_t rows, int64_t cols, int64_t col_stride, int dim, int op,
+                      int map, void* out) {
+  if (dim == 1) {
+    for (int64_t j = 0; j < cols; ++j) {
+      uint64_t acc = iload(A, dt, j * col_stride, map);
+      for (int64_t i = 1; i < rows; ++i) acc = iop(dt, op, acc, iload(A, dt, i + j * col_stride, map));
+      istore(out, dt, j, acc);
+    }
+  } else {
+    for (int64_t i = 0; i < rows; ++i) {
+      uint64_t acc = iload(A, dt, i, map);
+      for (int64_t j = 1; j < cols; ++j) acc = iop(dt, op, acc, iload(A, dt, i + j * col_stride, map));
+      istore(out, dt, i, acc);
+    }
+  }
+}
+
+/* ------------------------------------------------------- CPU baseline ---- */
+
+/* Base.accumulate!(+, dst, src) on Float32: sequential, Float32 arithmetic. */
+void kfb_scan_add_f32_seq(const float* x, float* y, int64_t n) {
+  float acc = 0.0f;
+  for (int64_t i = 0; i < n; ++i) {
+    acc = i == 0 ? x[0] : acc + x[i];
+    y[i] = acc;
+  }
+}
+
+/* Two-pass chunked scan on `threads` threads (per-chunk totals, exclusive
+ * scan of the totals, then a re-scan with the chunk offset). */
+void kfb_scan_add_f32_par(const float* x, float* y, int64_t n, int threads) {
+#ifdef _OPENMP
+  if (threads < 1) threads = 1;
+  float totals[1024];
+  if (threads > 1024) threads = 1024;
+  const int64_t chunk = (n + threads - 1) / threads;
+#pragma omp parallel num_threads(threads)
+  {
+    const int t = omp_get_thread_num();
+    const int64_t lo = t * chunk, hi = lo + chunk < n ? lo + chunk : n;
+    float s = 0.0f;
+    for (int64_t i = lo; i < hi; ++i) s += x[i];
+    totals[t] = s;
+#pragma omp barrier
+    float off = 0.0f;
+    for (int k = 0; k < t; ++k) off += totals[k];
+    float acc = off;
+    for (int64_t i = lo; i < hi; ++i) {
+      acc += x[i];
+      y[i] = acc;
+    }
+  }
+#else
+  (void)threads;
+  kfb_scan_add_f32_seq(x, y, n);
+#endif
+}
+
+/* Base.mapreduce(identity, +, x) on Float32 (single thread, Float32
+ * arithmetic, 8 independent partial sums like Base's pairwise blocks). */
+float kfb_sum_f32_seq(const float* x, int64_t n) {
+  float s[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  int64_t i = 0;
+  for (; i + 8 <= n; i += 8)
+    for (int k = 0; k < 8; ++k) s[k] += x[i + k];
+  for (; i < n; ++i) s[0] += x[i];
+  float r = 0.0f;
+  for (int k = 0; k < 8; ++k) r += s[k];
+  return r;
+}
+
+float kfb_sum_f32_par(const float* x, int64_t n, int threads) {
+  double total = 0.0;
+#ifdef _OPENMP
+  if (threads < 1) threads = 1;
+  const int64_t chunk = (n + threads - 1) / threads;
+#pragma omp parallel num_threads(threads) reduction(+ : total)
+  {
+    const int t = omp_get_thread_num();
+    const int64_t lo = t * chunk, hi = lo + chunk < n ? lo + chunk : n;
+    if (hi > lo) total += kfb_sum_f32_seq(x + lo, hi - lo);
+  }
+#else
+  (void)threads;
+  total = kfb_sum_f32_seq(x, n);
+#endif
+  return (float)total;
+}
+
+int kfo_omp_max_threads(void) {
+#ifdef _OPENMP
+  return omp_get_max_threads();
+#else
+  return 1;
+#endif
+}

@@ -1,0 +1,132 @@
+"""ctypes wrapper of liboracle.so — the CPU checker and CPU baseline.
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg. The product (kernelforge.jl_amd) never imports
+it. Semantics and reference citations are in kf_oracle.c.
+
+Every function takes numpy arrays. Float results come back as float64
+(the Float64 host accumulation tolerances are stated against); integer
+results come back exactly, in the input's dtype.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB = os.path.join(HERE, "liboracle.so")
+
+DT = {np.dtype(np.float32): 0, np.dtype(np.float64): 1, np.dtype(np.int32): 2,
+      np.dtype(np.int64): 3, np.dtype(np.uint8): 4}
+OPS = {"+": 0, "max": 1, "min": 2, "affine": 3}
+MAPS = {"identity": 0, "abs2": 1}
+
+_lib = None
+
+
+def build():
+    r = subprocess.run(["make", "-s", "-B", "-C", HERE, "liboracle.so"], capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError("oracle build failed:\n" + r.stderr)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB):
+            build()
+        L = ctypes.CDLL(LIB)
+        P, I64, I, D = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_double
+        L.kfo_scan_f.argtypes = [P, I, I64, I64, I, I, I, P]
+        L.kfo_scan_i.argtypes = [P, I, I64, I64, I, I, I, P]
+        L.kfo_scan_affine.argtypes = [P, I64, I, P]
+        L.kfo_reduce_f.argtypes = [P, I, I64, I64, I, I]
+        L.kfo_reduce_f.restype = D
+        L.kfo_reduce_i.argtypes = [P, I, I64, I64, I, I, P]
+        L.kfo_reduce_dim_f.argtypes = [P, I, I64, I64, I64, I, I, I, P]
+        L.kfo_reduce_dim_i.argtypes = [P, I, I64, I64, I64, I, I, I, P]
+        L.kfb_scan_add_f32_seq.argtypes = [P, P, I64]
+        L.kfb_scan_add_f32_par.argtypes = [P, P, I64, I]
+        L.kfb_sum_f32_seq.argtypes = [P, I64]
+        L.kfb_sum_f32_seq.restype = ctypes.c_float
+        L.kfb_sum_f32_par.argtypes = [P, I64, I]
+        L.kfb_sum_f32_par.restype = ctypes.c_float
+        L.kfo_omp_max_threads.restype = I
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _is_float(a):
+    return a.dtype in (np.float32, np.float64)
+
+
+def scan(x, op="+", f="identity", exclusive=False):
+    """Base.accumulate(op, f.(x)) (exclusive: shifted right, identity first).
+    x: 1-D numpy array (any stride); (n, 2) float32 pairs for op='affine'."""
+    L = lib()
+    if op == "affine":
+        ab = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, 2)
+        out = np.empty((ab.shape[0], 2), np.float64)
+        L.kfo_scan_affine(_p(ab), ab.shape[0], int(exclusive), _p(out))
+        return out
+    x = np.ascontiguousarray(x)
+    n = x.shape[0]
+    if _is_float(x):
+        out = np.empty(n, np.float64)
+        L.kfo_scan_f(_p(x), DT[x.dtype], n, 1, OPS[op], MAPS[f], int(exclusive), _p(out))
+    else:
+        out = np.empty(n, x.dtype)
+        L.kfo_scan_i(_p(x), DT[x.dtype], n, 1, OPS[op], MAPS[f], int(exclusive), _p(out))
+    return out
+
+
+def reduce(x, op="+", f="identity"):
+    """Base.mapreduce(f, op, x) over a non-empty 1-D array."""
+    L = lib()
+    x = np.ascontiguousarray(x)
+    if _is_float(x):
+        return L.kfo_reduce_f(_p(x), DT[x.dtype], x.shape[0], 1, OPS[op], MAPS[f])
+    out = np.empty(1, x.dtype)
+    L.kfo_reduce_i(_p(x), DT[x.dtype], x.shape[0], 1, OPS[op], MAPS[f], _p(out))
+    return out[0]
+
+
+def reduce_dim(buf, rows, cols, col_stride, dim, op="+", f="identity"):
+    """Base.mapreduce(f, op, A; dims=dim) of the column-major matrix
+    A[i, j] = buf[i + j*col_stride] (buf 1-D). Returns the 1-D result."""
+    L = lib()
+    buf = np.ascontiguousarray(buf)
+    assert buf.ndim == 1 and (cols - 1) * col_stride + rows <= buf.shape[0]
+    m = cols if dim == 1 else rows
+    if _is_float(buf):
+        out = np.empty(m, np.float64)
+        L.kfo_reduce_dim_f(_p(buf), DT[buf.dtype], rows, cols, col_stride, dim, OPS[op], MAPS[f], _p(out))
+    else:
+        out = np.empty(m, buf.dtype)
+        L.kfo_reduce_dim_i(_p(buf), DT[buf.dtype], rows, cols, col_stride, dim, OPS[op], MAPS[f], _p(out))
+    return out
+
+
+# --- CPU baseline (element-type arithmetic, as Base computes on the host) ---
+def baseline_scan_add_f32(x, y, threads=1):
+    L = lib()
+    if threads <= 1:
+        L.kfb_scan_add_f32_seq(_p(x), _p(y), x.shape[0])
+    else:
+        L.kfb_scan_add_f32_par(_p(x), _p(y), x.shape[0], threads)
+
+
+def baseline_sum_f32(x, threads=1):
+    L = lib()
+    if threads <= 1:
+        return L.kfb_sum_f32_seq(_p(x), x.shape[0])
+    return L.kfb_sum_f32_par(_p(x), x.shape[0], threads)
+
+
+def omp_max_threads():
+    return lib().kfo_omp_max_threads()

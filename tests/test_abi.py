@@ -1,0 +1,76 @@
+"""The C-ABI library loads, exports every symbol include/kf.h declares, and
+rejects bad arguments before touching a GPU (no compute calls here)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_symbols():
+    text = open(os.path.join(REPO, "include", "kf.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(kf_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_expected_surface():
+    assert declared_symbols() == sorted([
+        "kf_version", "kf_last_error", "kf_scratch_reset", "kf_scan_scratch_bytes", "kf_scan",
+        "kf_reduce_scratch_bytes", "kf_reduce", "kf_reduce_dim_scratch_bytes", "kf_reduce_dim", "kf_copy"])
+
+
+def test_library_exports_every_declared_symbol(kf):
+    L = kf._lib.lib()
+    for name in declared_symbols():
+        assert hasattr(L, name), name
+        assert name in kf._lib.SIGNATURES, name
+
+
+def test_version(kf):
+    assert kf._lib.lib().kf_version() == 100
+
+
+def test_scratch_queries(kf):
+    L = kf._lib.lib()
+    # one 8-byte descriptor word per 16 KiB tile + a 256-byte header
+    assert L.kf_scan_scratch_bytes(kf._lib.F32, kf._lib.OP_ADD, 2**28) == 256 + (2**28 // 4096) * 8
+    assert L.kf_scan_scratch_bytes(kf._lib.F32X2, kf._lib.OP_AFFINE, 2**26) == 256 + (2**26 // 2048) * 16
+    assert L.kf_scan_scratch_bytes(kf._lib.U8, kf._lib.OP_ADD, 1) == 256 + 8
+    assert L.kf_reduce_scratch_bytes(kf._lib.F64, 10) >= 256 + 4096 * 8
+    assert L.kf_reduce_dim_scratch_bytes(kf._lib.F32, 4096, 65536, 1) >= 256
+    # few columns -> split rows: partials for every (split, column)
+    assert L.kf_reduce_dim_scratch_bytes(kf._lib.F32, 2**24, 2, 1) > 256
+
+
+def _err(kf):
+    return kf._lib.lib().kf_last_error().decode()
+
+
+def test_invalid_arguments_rejected_without_gpu(kf):
+    L, K = kf._lib.lib(), kf._lib
+    p = ctypes.c_void_p(4096)
+    assert L.kf_scan(99, 0, K.F32, 0, p, 1, p, 1, 10, p, 1 << 20, None) == K.KF_EINVAL
+    assert "op" in _err(kf)
+    # affine needs the pair type and vice versa
+    assert L.kf_scan(K.OP_AFFINE, 0, K.F32, 0, p, 1, p, 1, 10, p, 1 << 20, None) == K.KF_EINVAL
+    assert L.kf_scan(K.OP_ADD, 0, K.F32X2, 0, p, 1, p, 1, 10, p, 1 << 20, None) == K.KF_EINVAL
+    # affine is scan-only
+    assert L.kf_reduce(K.OP_AFFINE, 0, K.F32X2, p, 10, 1, p, p, 1 << 20, None) == K.KF_EINVAL
+    # n == 0 is a successful no-op, n < 0 an error
+    assert L.kf_scan(K.OP_ADD, 0, K.F32, 0, p, 1, p, 1, 0, None, 0, None) == K.KF_OK
+    assert L.kf_scan(K.OP_ADD, 0, K.F32, 0, p, 1, p, 1, -1, None, 0, None) == K.KF_EINVAL
+    # scratch too small
+    q = ctypes.c_void_p(1 << 20)
+    assert L.kf_scan(K.OP_ADD, 0, K.F32, 0, p, 1, q, 1, 10, p, 8, None) == K.KF_ENOSCRATCH
+    # partial overlap of src and dst
+    assert L.kf_scan(K.OP_ADD, 0, K.F32, 0, ctypes.c_void_p(4096), 1, ctypes.c_void_p(4100), 1, 10, q, 1 << 20,
+                     None) == K.KF_EINVAL
+    assert "overlap" in _err(kf)
+    # misaligned element pointer
+    assert L.kf_scan(K.OP_ADD, 0, K.F32, 0, ctypes.c_void_p(4097), 1, q, 1, 10, q, 1 << 20, None) == K.KF_EINVAL
+    # reduce_dim: bad dim, col_stride < rows
+    assert L.kf_reduce_dim(K.OP_ADD, 0, K.F32, p, 4, 4, 4, 3, q, 1, q, 1 << 20, None) == K.KF_EINVAL
+    assert L.kf_reduce_dim(K.OP_ADD, 0, K.F32, p, 4, 4, 2, 1, q, 1, q, 1 << 20, None) == K.KF_EINVAL
+    assert L.kf_copy(p, p, 0, None) == K.KF_OK

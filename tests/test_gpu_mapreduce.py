@@ -1,0 +1,230 @@
+"""mapreduce parity on the GPU (full reduction and dims), through the C ABI,
+against the pinned CPU oracle. Integers and max/min are exact; float sums
+are checked against a Float64 host sum with |err| <= rtol * sum(|f(x)|)
+(the error bound of any summation order), rtol stated per test."""
+import numpy as np
+import pytest
+import torch
+
+from helpers import NP, assert_close, dec
+
+pytestmark = pytest.mark.gpu
+
+SIZES = list(range(1, 11)) + [33, 100, 1023, 1025, 10001, 100_000, 1 << 20, (1 << 22) + 7]
+F = {"identity": None, "abs2": None}
+
+
+def fmap(kf, f):
+    return {"identity": kf.identity, "abs2": kf.abs2}[f]
+
+
+def gen(rng, dt, n):
+    if dt == np.int32:
+        return rng.integers(-2**31, 2**31 - 1, n, dtype=np.int64).astype(np.int32)
+    if dt == np.int64:
+        return rng.integers(-1000, 1000, n).astype(np.int64)
+    if dt == np.uint8:
+        return rng.integers(0, 256, n).astype(np.uint8)
+    return rng.standard_normal(n).astype(dt)
+
+
+def sum_abs(x, f):
+    x = x.astype(np.float64)
+    return float(np.sum(x * x if f == "abs2" else np.abs(x)))
+
+
+@pytest.mark.parametrize("dt", [np.float32, np.float64, np.int32, np.int64, np.uint8])
+@pytest.mark.parametrize("op", ["+", "max", "min"])
+@pytest.mark.parametrize("f", ["identity", "abs2"])
+def test_full_reduce(kf, oracle, dev, dt, op, f):
+    rng = np.random.default_rng(31)
+    rtol = 1e-6 if dt == np.float32 else 1e-14
+    for n in SIZES:
+        x = gen(rng, dt, n)
+        got = kf.mapreduce(fmap(kf, f), op, torch.from_numpy(x).to(dev))
+        ref = oracle.reduce(x, op, f)
+        if dt in (np.float32, np.float64) and op == "+":
+            assert abs(got - ref) <= rtol * sum_abs(x, f) + 1e-300, (n, got, ref)
+        elif dt in (np.float32, np.float64):
+            assert got == ref, (n, got, ref)
+        else:
+            assert got == int(ref), (n, got, ref)
+
+
+@pytest.mark.parametrize("dt", [np.float32, np.float64, np.int32])
+def test_reference_arange_sums(kf, dev, golden, dt):
+    # reference test/tests/mapreduce/mapreduce1d_test.jl:10-55 (sums of 1:n, reused tmp)
+    cases = [c for c in golden["reduce"] if c["dtype"] == np.dtype(dt).name and c["x"] == "arange1"]
+    assert cases
+    src0 = torch.arange(1, 100_001, device=dev).to(getattr(torch, np.dtype(dt).name))
+    tmp = kf.get_allocation(kf.MapReduce1D, kf.identity, "+", src0)
+    for c in cases:
+        x = torch.arange(1, c["n"] + 1, device=dev).to(src0.dtype)
+        f = fmap(kf, c["f"])
+        for t in (None, tmp):
+            got = kf.mapreduce(f, c["op"], x, tmp=t)
+            if dt == np.int32:
+                assert got == c["expected"]
+            else:
+                assert abs(got - c["expected"]) <= 1e-6 * c["expected"]
+        dst = torch.zeros(1, dtype=x.dtype, device=dev)
+        kf.mapreduce_(f, c["op"], dst, x, tmp=tmp)
+        if dt == np.int32:
+            assert dst.item() == c["expected"]
+
+
+def test_views_and_strides(kf, oracle, dev):
+    # reference test/tests/views/views_test.jl:44-65
+    rng = np.random.default_rng(37)
+    x = rng.standard_normal(100_003)
+    src = torch.from_numpy(x).to(dev)
+    for sl in (slice(2, None), slice(1, None), slice(3, -5), slice(None, None, 3), slice(5, None, 7)):
+        v = x[sl]
+        got = kf.mapreduce(kf.identity, "+", src[sl])
+        assert abs(got - oracle.reduce(np.ascontiguousarray(v))) <= 1e-13 * np.abs(v).sum()
+        assert kf.mapreduce(kf.identity, min, src[sl]) == v.min()
+        assert kf.mapreduce(kf.abs2, "+", src[sl], g=np.sqrt) == pytest.approx(np.sqrt((v * v).sum()), rel=1e-13)
+
+
+def test_full_reduce_of_2d_and_3d(kf, dev):
+    # reference test/tests/mapreduce/mapreduce_test.jl:9-28
+    rng = np.random.default_rng(41)
+    a = rng.random((6, 5, 4)).astype(np.float32)       # torch (6,5,4) C-order == Julia 4x5x6
+    x = torch.from_numpy(a).to(dev).permute(2, 1, 0)   # Julia-shaped 4x5x6, column-major
+    s = float(a.astype(np.float64).sum())
+    assert kf.mapreduce(kf.identity, "+", x) == pytest.approx(s, rel=1e-6)
+    assert kf.mapreduce(kf.identity, "+", x, dims=":") == pytest.approx(s, rel=1e-6)
+    r = kf.mapreduce(kf.identity, "+", x, dims=(1, 2, 3))
+    assert tuple(r.shape) == (1, 1, 1) and r.item() == pytest.approx(s, rel=1e-6)
+    # a strided 2-D view that is not one strided vector: two passes
+    A = torch.from_numpy(rng.random((64, 33))).to(dev).T   # 33 x 64 column-major
+    V = A[:, ::2]
+    assert kf.mapreduce(kf.identity, "+", V) == pytest.approx(float(V.sum()), rel=1e-13)
+
+
+def colmajor(rng, rows, cols, dt, view=False, low=-1.0, high=1.0):
+    pc = 2 * cols if view else cols
+    if np.dtype(dt).kind == "f":
+        parent = rng.uniform(low, high, (pc, rows)).astype(dt)
+    else:
+        parent = rng.integers(-1000, 1000, (pc, rows)).astype(dt)
+    buf = parent.reshape(-1)
+    return buf, (2 * rows if view else rows)
+
+
+@pytest.mark.parametrize("dt", [np.float32, np.float64, np.int32, np.uint8])
+@pytest.mark.parametrize("shape", [(128, 64), (1, 64), (128, 1), (1024, 256), (3, 7), (5, 7), (33, 17),
+                                   (1, 1), (4096, 3), (7, 5000), (70000, 2), (100_000, 9)])
+@pytest.mark.parametrize("view", [False, True])
+def test_dims_2d(kf, oracle, dev, dt, shape, view):
+    # reference test/tests/mapreduce/mapreduce2d_test.jl:1-47 and
+    # test/tests/views/views_test.jl:66-160 (column views)
+    rows, cols = shape
+    rng = np.random.default_rng(rows * 131 + cols)
+    buf, cs = colmajor(rng, rows, cols, dt, view)
+    t = torch.from_numpy(buf).to(dev)
+    A = t.as_strided((rows, cols), (1, cs))
+    for dim in (1, 2):
+        for op, f in (("+", "identity"), ("max", "identity"), ("min", "abs2"), ("+", "abs2")):
+            if dt == np.uint8 and f == "abs2":
+                continue
+            got = kf.mapreduce(fmap(kf, f), op, A, dims=dim)
+            assert tuple(got.shape) == ((1, cols) if dim == 1 else (rows, 1))
+            g = got.reshape(-1).cpu().numpy()
+            ref = oracle.reduce_dim(buf, rows, cols, cs, dim, op, f)
+            if np.dtype(dt).kind == "f" and op == "+":
+                M = buf.astype(np.float64)[np.arange(cols)[None, :] * cs + np.arange(rows)[:, None]]
+                M = M * M if f == "abs2" else np.abs(M)
+                bound = M.sum(axis=dim - 1) * (1e-6 if dt == np.float32 else 1e-14)
+                assert np.all(np.abs(g - ref) <= bound + 1e-300), (dim, op, f)
+            elif np.dtype(dt).kind == "f":
+                assert np.array_equal(g.astype(np.float64), ref), (dim, op, f)
+            else:
+                assert np.array_equal(g, ref), (dim, op, f)
+
+
+def test_dims_golden(kf, dev, golden):
+    for c in golden["reduce_dim"]:
+        buf = dec(c["buf"], np.float64)
+        t = torch.from_numpy(buf).to(dev)
+        A = t.as_strided((c["rows"], c["cols"]), (1, c["col_stride"]))
+        assert_close(kf.mapreduce(kf.identity, "+", A, dims=1).reshape(-1).cpu().numpy(),
+                     dec(c["dim1"], np.float64), 1e-12, 1e-12, what="golden dim1")
+        assert_close(kf.mapreduce(kf.identity, "+", A, dims=2).reshape(-1).cpu().numpy(),
+                     dec(c["dim2"], np.float64), 1e-12, 1e-12, what="golden dim2")
+        assert np.array_equal(kf.mapreduce(kf.identity, max, A, dims=1).reshape(-1).cpu().numpy(),
+                              dec(c["dim1_max"], np.float64))
+        assert np.array_equal(kf.mapreduce(kf.identity, min, A, dims=2).reshape(-1).cpu().numpy(),
+                              dec(c["dim2_min"], np.float64))
+
+
+@pytest.mark.parametrize("dims", [1, (1, 2), 3, (2, 3), (1, 3), (1, 2, 3)])
+def test_dims_nd_routing(kf, dev, dims):
+    # reference test/tests/mapreduce/mapreduce_test.jl:30-131
+    rng = np.random.default_rng(43)
+    a = rng.random((6, 5, 8))                            # C-order (6,5,8) == Julia 8x5x6
+    x = torch.from_numpy(a).to(dev).permute(2, 1, 0)     # Julia 8x5x6
+    got = kf.mapreduce(kf.identity, "+", x, dims=dims)
+    d = (dims,) if isinstance(dims, int) else dims
+    ref = x.cpu().numpy().sum(axis=tuple(k - 1 for k in d), keepdims=True)
+    assert tuple(got.shape) == ref.shape
+    np.testing.assert_allclose(got.cpu().numpy(), ref, rtol=1e-13)
+
+
+def test_dims_errors(kf, dev):
+    x = torch.zeros(4, 5, device=dev).T
+    with pytest.raises(kf.ArgumentError):
+        kf.mapreduce(kf.identity, "+", x, dims=3)
+    with pytest.raises(kf.ArgumentError):
+        kf.mapreduce(kf.identity, "+", x, dims=(1, 1))
+    with pytest.raises(kf.ArgumentError):
+        kf.mapreduce(kf.identity, kf.affine, x)
+    with pytest.raises(NotImplementedError):
+        kf.mapreduce(kf.identity, "+", torch.zeros(2, 3, 4, device=dev).permute(2, 1, 0), dims=2)
+
+
+# ---- BASELINE.json configurations at full size -------------------------------
+def test_config3a_abs2_sum_f32_2pow30(kf, oracle, dev):
+    g = torch.Generator(device=dev).manual_seed(20261201 + 3)
+    x = torch.randn(2**30, device=dev, generator=g, dtype=torch.float32)
+    got = kf.mapreduce(kf.abs2, "+", x)
+    ref = oracle.reduce(x.cpu().numpy(), "+", "abs2")
+    assert abs(got - ref) <= 1e-5 * ref, (got, ref)  # rel tol 1e-5 vs the Float64 host sum
+
+
+def test_config3b_abs2_sum_f64_2pow28(kf, oracle, dev):
+    g = torch.Generator(device=dev).manual_seed(20261201 + 31)
+    x = torch.randn(2**28, device=dev, generator=g, dtype=torch.float64)
+    got = kf.mapreduce(kf.abs2, "+", x)
+    ref = oracle.reduce(x.cpu().numpy(), "+", "abs2")
+    assert abs(got - ref) <= 1e-12 * ref, (got, ref)
+
+
+def test_config3c_int32_max_2pow28(kf, oracle, dev):
+    rng = np.random.default_rng(20261201 + 32)
+    x = rng.integers(-2**31, 2**31 - 1, 2**28, dtype=np.int64).astype(np.int32)
+    t = torch.from_numpy(x).to(dev)
+    assert kf.mapreduce(kf.identity, max, t) == oracle.reduce(x, "max")
+    assert kf.mapreduce(kf.identity, min, t) == oracle.reduce(x, "min")
+
+
+@pytest.mark.parametrize("which", ["dims1", "dims2", "dims1_view", "dims2_view"])
+def test_config5_dims(kf, oracle, dev, which):
+    g = torch.Generator(device=dev).manual_seed(20261201 + 5)
+    if which.startswith("dims1"):
+        rows, cols, dim = 4096, 65536, 1
+    else:
+        rows, cols, dim = 65536, 4096, 2
+    t = torch.rand(rows * cols, device=dev, generator=g) * 2 - 1
+    A = t.as_strided((rows, cols), (1, rows))
+    if which.endswith("view"):
+        A = A[:, ::2]
+    kcols = A.shape[1]
+    got = kf.mapreduce(kf.identity, "+", A, dims=dim).reshape(-1).cpu().numpy()
+    buf = t.cpu().numpy()
+    cs = A.stride(1)
+    ref = oracle.reduce_dim(buf, rows, kcols, cs, dim)
+    absA = np.abs(buf.astype(np.float64))
+    absA = absA.reshape(cols, rows)[:: (2 if which.endswith("view") else 1)]  # (kcols, rows)
+    bound = absA.sum(axis=1 if dim == 1 else 0) * 1e-6
+    assert np.all(np.abs(got - ref) <= bound), which

@@ -1,0 +1,242 @@
+"""scan! parity on the GPU: the HIP kernels (through the C ABI) against the
+pinned CPU oracle. Integer scans are bit-exact; float max/min are exact (they
+select an input); float + is checked against a Float64 host accumulation
+with the tolerance stated per test."""
+import zlib
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import NP, assert_close, assert_mixed, dec
+
+pytestmark = pytest.mark.gpu
+
+EDGE = list(range(1, 11))
+TILE_EDGES = [63, 64, 65, 255, 256, 257, 1023, 1024, 1025, 2047, 2048, 2049, 4095, 4096, 4097, 8191, 8192,
+              8193, 16383, 16384, 16385, 65536 * 4 + 3]
+SIZES = EDGE + TILE_EDGES + [100_003, 1_000_000]
+
+
+def gen(rng, dt, n):
+    if dt == np.int32:
+        return rng.integers(1, 11, n).astype(np.int32)          # rand(1:10), reference scan_test.jl:51
+    if dt == np.int64:
+        return rng.integers(-4, 5, n).astype(np.int64)
+    if dt == np.uint8:
+        return rng.integers(0, 256, n).astype(np.uint8)
+    return rng.random(n).astype(dt)
+
+
+def run(kf, dev, x, op, f="identity", exclusive=False):
+    fn = {"identity": kf.identity, "abs2": kf.abs2}[f]
+    t = torch.from_numpy(x).to(dev)
+    y = kf.scan(fn, op, t, exclusive=exclusive)
+    torch.cuda.synchronize()
+    return y.cpu().numpy()
+
+
+@pytest.mark.parametrize("dt", [np.int32, np.int64, np.uint8])
+@pytest.mark.parametrize("op", ["+", "max", "min"])
+@pytest.mark.parametrize("exclusive", [False, True])
+def test_int_scan_exact(kf, oracle, dev, dt, op, exclusive):
+    rng = np.random.default_rng(zlib.crc32(f"{dt.__name__}{op}{exclusive}".encode()))
+    for n in SIZES:
+        x = gen(rng, dt, n)
+        got = run(kf, dev, x, op, exclusive=exclusive)
+        ref = oracle.scan(x, op, exclusive=exclusive)
+        assert np.array_equal(got, ref), f"{dt.__name__} {op} excl={exclusive} n={n}: first diff at " \
+            f"{np.nonzero(got != ref)[0][:1]}"
+
+
+@pytest.mark.parametrize("dt", [np.int32, np.uint8])
+def test_abs2_map_exact(kf, oracle, dev, dt):
+    rng = np.random.default_rng(7)
+    for n in (1, 5, 4097, 100_003):
+        x = gen(rng, dt, n)
+        for exclusive in (False, True):
+            assert np.array_equal(run(kf, dev, x, "+", "abs2", exclusive), oracle.scan(x, "+", "abs2", exclusive))
+
+
+@pytest.mark.parametrize("dt", [np.float32, np.float64])
+@pytest.mark.parametrize("op", ["max", "min"])
+def test_float_minmax_exact(kf, oracle, dev, dt, op):
+    rng = np.random.default_rng(11)
+    for n in EDGE + [4097, 100_003]:
+        x = (rng.random(n) - 0.5).astype(dt)
+        for exclusive in (False, True):
+            got = run(kf, dev, x, op, exclusive=exclusive)
+            assert np.array_equal(got.astype(np.float64), oracle.scan(x, op, exclusive=exclusive))
+
+
+def test_float_max_signed_zero_and_nan(kf, oracle, dev):
+    x = np.array([0.0, -0.0, 1.0, np.nan, 2.0] * 1000, np.float32)
+    for op in ("max", "min"):
+        got = run(kf, dev, x, op)
+        ref = oracle.scan(x, op)
+        assert np.array_equal(np.isnan(got), np.isnan(ref))
+        m = ~np.isnan(ref)
+        assert np.array_equal(got[m], ref[m]) and np.array_equal(np.signbit(got[m]), np.signbit(ref[m]))
+
+
+@pytest.mark.parametrize("dt,rtol", [(np.float32, 1e-5), (np.float64, 1e-12)])
+def test_float_add_scan(kf, oracle, dev, dt, rtol):
+    # U[0,1) inputs: every prefix is positive, so a relative tolerance applies
+    rng = np.random.default_rng(13)
+    for n in SIZES:
+        x = rng.random(n).astype(dt)
+        for exclusive in (False, True):
+            got = run(kf, dev, x, "+", exclusive=exclusive)
+            ref = oracle.scan(x, "+", exclusive=exclusive)
+            assert_close(got, ref, rtol, atol=1e-30, what=f"{dt.__name__} + n={n} excl={exclusive}")
+            if exclusive:
+                assert got[0] == 0 and not np.signbit(got[0])
+
+
+def test_golden_vectors(kf, dev, golden):
+    for c in golden["scan"]:
+        dt = NP[c["dtype"]]
+        x = dec(c["x"], dt)
+        for mode in ("inclusive", "exclusive"):
+            got = run(kf, dev, x, c["op"], exclusive=mode == "exclusive")
+            exp = dec(c[mode], np.float64 if dt == np.float64 else dt)
+            if dt == np.float64 and c["op"] == "+":
+                assert_close(got, exp, 1e-12, 1e-300, what=f"golden {c['op']} n={c['n']}")
+            elif dt == np.float64:
+                nan = np.isnan(exp)
+                assert np.array_equal(np.isnan(got), nan)
+                assert np.array_equal(got[~nan], exp[~nan])
+            else:
+                assert np.array_equal(got, exp), (c["dtype"], c["op"], c["n"], mode)
+
+
+def test_affine_golden(kf, dev, golden):
+    for c in golden["affine"]:
+        ab = np.stack([dec(c["a"], np.float32), dec(c["b"], np.float32)], axis=1)
+        for mode in ("inclusive", "exclusive"):
+            got = kf.scan(kf.affine, torch.from_numpy(ab).to(dev), exclusive=mode == "exclusive").cpu().numpy()
+            assert_mixed(got, np.array(c[mode]), 1e-5, what=f"affine golden n={c['n']} {mode}")
+
+
+@pytest.mark.parametrize("n", EDGE + [2047, 2048, 2049, 100_003, 1 << 20])
+def test_affine_scan(kf, oracle, dev, n):
+    # BASELINE config 4 distribution: a ~ U[0.9, 1), b ~ N(0, 1); tolerance
+    # |gpu - ref| <= 1e-5 * max(|ref|, 1) against the Float64 recurrence.
+    rng = np.random.default_rng(n)
+    ab = np.stack([rng.uniform(0.9, 1.0, n), rng.standard_normal(n)], 1).astype(np.float32)
+    for exclusive in (False, True):
+        got = kf.scan(kf.affine, torch.from_numpy(ab).to(dev), exclusive=exclusive).cpu().numpy()
+        assert_mixed(got, oracle.scan(ab, "affine", exclusive), 1e-5, what=f"affine n={n} excl={exclusive}")
+
+
+def test_affine_is_order_sensitive(kf, oracle, dev):
+    # a = 2 on even, 1/2 on odd positions with b = index: any reordering of
+    # combines changes the result, exact in binary floating point
+    n = 20000
+    a = np.where(np.arange(n) % 2 == 0, 2.0, 0.5).astype(np.float32)
+    b = (np.arange(n) % 7).astype(np.float32)
+    ab = np.stack([a, b], 1)
+    got = kf.scan(kf.affine, torch.from_numpy(ab).to(dev)).cpu().numpy()
+    ref = oracle.scan(ab, "affine")
+    assert np.array_equal(got[:, 0].astype(np.float64), ref[:, 0])
+    assert_mixed(got, ref, 1e-6, what="alternating affine")
+
+
+def test_reused_tmp_changing_data(kf, oracle, dev):
+    # reference test/tests/scan/scan_test.jl:103-125: a stale descriptor from
+    # the previous call would show up as an exact integer mismatch
+    rng = np.random.default_rng(17)
+    x0 = torch.zeros(1_000_000, dtype=torch.int32, device=dev)
+    tmp = kf.get_allocation(kf.Scan1D, kf.identity, "+", x0)
+    for call in range(12):
+        n = [1_000_000, 1000, 100_000, 4097, 1_000_000, 65][call % 6]
+        x = rng.integers(-4, 5, n).astype(np.int32)
+        src = torch.from_numpy(x).to(dev)
+        dst = torch.empty_like(src)
+        kf.scan_("+", dst, src, tmp=tmp, exclusive=bool(call % 2))
+        torch.cuda.synchronize()
+        assert np.array_equal(dst.cpu().numpy(), oracle.scan(x, "+", exclusive=bool(call % 2))), call
+    # the same buffer serves other element types and operators
+    for dt in (np.int64, np.uint8):
+        x = gen(rng, dt, 100_000)
+        src = torch.from_numpy(x).to(dev)
+        dst = torch.empty_like(src)
+        kf.scan_("max", dst, src, tmp=tmp)
+        assert np.array_equal(dst.cpu().numpy(), oracle.scan(x, "max"))
+    # header word 1 is the lookback's give-up flag: never raised
+    assert int(tmp.arr[8:16].cpu().numpy().view(np.uint64)[0]) == 0
+
+
+def test_views_offsets_strides_inplace(kf, oracle, dev):
+    # reference test/tests/views/views_test.jl:1-42 (views of src/dst)
+    rng = np.random.default_rng(19)
+    n = 100_003
+    x = rng.integers(0, 16, n).astype(np.int32)
+    src = torch.from_numpy(x).to(dev)
+    v = src[1:]                                       # view(src, 2:n): not 16-byte aligned
+    out = kf.scan("+", v)
+    assert np.array_equal(out.cpu().numpy(), oracle.scan(x[1:]))
+    full = torch.zeros(n, dtype=torch.int32, device=dev)
+    kf.scan_("+", full[2:], src[2:])                  # scan!(+, view(dst, 3:n), view(src, 3:n))
+    got = full.cpu().numpy()
+    assert np.array_equal(got[2:], oracle.scan(x[2:])) and np.all(got[:2] == 0)
+    s = src[::3]                                      # strided source
+    d = torch.zeros(2 * s.shape[0], dtype=torch.int32, device=dev)[::2]
+    kf.scan_("+", d, s)
+    assert np.array_equal(d.cpu().numpy(), oracle.scan(x[::3]))
+    y = src.clone()                                   # in place
+    kf.scan_("+", y, y)
+    assert np.array_equal(y.cpu().numpy(), oracle.scan(x))
+
+
+def test_errors(kf, dev):
+    a = torch.zeros(10, device=dev)
+    with pytest.raises(kf.ArgumentError):
+        kf.scan_("+", torch.zeros(9, device=dev), a)
+    with pytest.raises(kf.ArgumentError):
+        kf.scan_("+", torch.zeros(10, dtype=torch.float64, device=dev), a)
+    with pytest.raises(kf.ArgumentError):
+        kf.scan_("+", a[1:], a[:-1])  # partial overlap
+    with pytest.raises(kf.ArgumentError):
+        kf.scan(kf.affine, a)
+    assert kf.scan("+", torch.zeros(0, device=dev)).numel() == 0
+
+
+# ---- BASELINE.json configurations at full size -------------------------------
+def test_config1_f32_inclusive_1e6(kf, oracle, dev):
+    rng = np.random.default_rng(20261201 + 1)
+    x = rng.random(10**6, dtype=np.float32)
+    got = run(kf, dev, x, "+")
+    assert_close(got, oracle.scan(x), 1e-5, what="config 1")  # rel tol 1e-5 vs Float64
+
+
+@pytest.mark.parametrize("exclusive", [False, True])
+def test_config2_int32_2pow28_exact(kf, oracle, dev, exclusive):
+    rng = np.random.default_rng(20261201 + 2)
+    n = 2**28
+    x = rng.integers(0, 16, n, dtype=np.int32)
+    print(f"config 2: Int32 n=2^28 exclusive={exclusive}", flush=True)
+    got = run(kf, dev, x, "+", exclusive=exclusive)
+    ref = oracle.scan(x, "+", exclusive=exclusive)
+    assert np.array_equal(got, ref)
+    # size-independent property: the last inclusive value is the total
+    assert int(ref[-1]) + (int(x[-1]) if exclusive else 0) == int(x.sum(dtype=np.int64))
+
+
+def test_config4_affine_2pow26(kf, oracle, dev):
+    rng = np.random.default_rng(20261201 + 4)
+    n = 2**26
+    ab = np.empty((n, 2), np.float32)
+    ab[:, 0] = rng.uniform(0.9, 1.0, n)
+    ab[:, 1] = rng.standard_normal(n, dtype=np.float32)
+    got = kf.scan(kf.affine, torch.from_numpy(ab).to(dev)).cpu().numpy()
+    assert_mixed(got, oracle.scan(ab, "affine"), 1e-5, what="config 4")
+
+
+def test_headline_f32_2pow28(kf, oracle, dev):
+    # the bench workload; tolerance 1e-4 relative (the lookback chain over
+    # 65536 tiles adds one Float32 rounding per tile to the running prefix)
+    rng = np.random.default_rng(20261201 + 5)
+    x = rng.random(2**28, dtype=np.float32)
+    got = run(kf, dev, x, "+")
+    assert_close(got, oracle.scan(x), 1e-4, what="F32 n=2^28")

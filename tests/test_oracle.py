@@ -1,0 +1,171 @@
+"""Pins the CPU oracle (oracle/kf_oracle.c) before any GPU result is checked
+against it: golden vectors computed independently with numpy / plain Python,
+closed forms, and the special cases Julia's operators define."""
+import numpy as np
+import pytest
+
+from helpers import NP, dec, same_float
+
+
+def test_scan_golden(oracle, golden):
+    for c in golden["scan"]:
+        dt = NP[c["dtype"]]
+        x = dec(c["x"], dt)
+        for mode in ("inclusive", "exclusive"):
+            got = oracle.scan(x, c["op"], exclusive=mode == "exclusive")
+            exp = dec(c[mode], np.float64 if dt == np.float64 else dt)
+            if dt == np.float64:
+                if c.get("signed_zero"):
+                    assert same_float(got, exp), (c["op"], mode, got, exp)
+                else:
+                    # numpy's cumsum adds in the same left-to-right order: equal bits
+                    assert same_float(got, exp), (c["dtype"], c["op"], c["n"], mode)
+            else:
+                assert np.array_equal(got, exp), (c["dtype"], c["op"], c["n"], mode)
+
+
+def test_affine_golden(oracle, golden):
+    for c in golden["affine"]:
+        ab = np.stack([dec(c["a"], np.float32), dec(c["b"], np.float32)], axis=1)
+        for mode in ("inclusive", "exclusive"):
+            got = oracle.scan(ab, "affine", exclusive=mode == "exclusive")
+            assert np.array_equal(got, np.array(c[mode], np.float64)), (c["n"], mode)
+
+
+def test_reduce_golden(oracle, golden):
+    for c in golden["reduce"]:
+        dt = NP[c["dtype"]]
+        x = np.arange(1, c["n"] + 1).astype(dt) if c["x"] == "arange1" else dec(c["x"], dt)
+        got = oracle.reduce(x, c["op"], c["f"])
+        assert got == c["expected"], (c, got)
+
+
+def test_reduce_dim_golden(oracle, golden):
+    for c in golden["reduce_dim"]:
+        buf = dec(c["buf"], np.float64)
+        r, k, cs = c["rows"], c["cols"], c["col_stride"]
+        np.testing.assert_allclose(oracle.reduce_dim(buf, r, k, cs, 1), dec(c["dim1"], np.float64), rtol=1e-14)
+        np.testing.assert_allclose(oracle.reduce_dim(buf, r, k, cs, 2), dec(c["dim2"], np.float64), rtol=1e-14)
+        assert np.array_equal(oracle.reduce_dim(buf, r, k, cs, 1, "max"), dec(c["dim1_max"], np.float64))
+        assert np.array_equal(oracle.reduce_dim(buf, r, k, cs, 2, "min"), dec(c["dim2_min"], np.float64))
+
+
+# ---- closed forms and invariants -------------------------------------------
+@pytest.mark.parametrize("n", [1, 2, 17, 4096, 100_003])
+def test_scan_closed_forms(oracle, n):
+    ones = np.ones(n, np.int32)
+    assert np.array_equal(oracle.scan(ones), np.arange(1, n + 1, dtype=np.int32))
+    assert np.array_equal(oracle.scan(ones, exclusive=True), np.arange(0, n, dtype=np.int32))
+    r = np.arange(1, n + 1, dtype=np.int64)
+    tri = r * (r + 1) // 2
+    assert np.array_equal(oracle.scan(r), tri)
+    # abs2 map: running sum of squares
+    assert np.array_equal(oracle.scan(r, "+", "abs2"), r * (r + 1) * (2 * r + 1) // 6)
+    # max of an increasing sequence is itself; min of it is the first element
+    assert np.array_equal(oracle.scan(r, "max"), r)
+    assert np.array_equal(oracle.scan(r, "min"), np.ones(n, np.int64))
+
+
+def test_scan_int_wraps(oracle):
+    x = np.array([2**31 - 1, 1, 1], np.int32)
+    assert oracle.scan(x).tolist() == [2**31 - 1, -2**31, -2**31 + 1]
+    u = np.array([250, 10, 255], np.uint8)
+    assert oracle.scan(u).tolist() == [250, 4, 3]
+    assert oracle.scan(u, "+", "abs2").tolist() == [(250 * 250) % 256, (250 * 250 + 100) % 256,
+                                                    (250 * 250 + 100 + 255 * 255) % 256]
+
+
+def test_exclusive_is_shifted_inclusive(oracle):
+    rng = np.random.default_rng(1)
+    for dt, op, ident in ((np.int32, "max", np.iinfo(np.int32).min), (np.int32, "min", np.iinfo(np.int32).max),
+                          (np.int64, "+", 0), (np.uint8, "min", 255)):
+        x = rng.integers(0, 100, 999).astype(dt)
+        inc, exc = oracle.scan(x, op), oracle.scan(x, op, exclusive=True)
+        assert exc[0] == ident and np.array_equal(exc[1:], inc[:-1])
+
+
+def test_julia_max_min_special_values(oracle):
+    # Julia: max(-0.0, 0.0) == 0.0, min(0.0, -0.0) == -0.0, NaN propagates
+    x = np.array([-0.0, 0.0], np.float64)
+    assert not np.signbit(oracle.scan(x, "max")[1])
+    y = np.array([0.0, -0.0], np.float64)
+    assert np.signbit(oracle.scan(y, "min")[1])
+    z = np.array([1.0, np.nan, 5.0], np.float64)
+    assert np.isnan(oracle.scan(z, "max")[2]) and np.isnan(oracle.reduce(z, "min"))
+
+
+def test_affine_closed_forms(oracle):
+    n = 1000
+    rng = np.random.default_rng(2)
+    b = rng.standard_normal(n).astype(np.float32)
+    # a = 1: x_t is the prefix sum of b
+    ab = np.stack([np.ones(n, np.float32), b], 1)
+    out = oracle.scan(ab, "affine")
+    np.testing.assert_allclose(out[:, 1], np.cumsum(b.astype(np.float64)), rtol=1e-12, atol=1e-12)
+    assert np.all(out[:, 0] == 1.0)
+    # b = 0: the a-component is the running product
+    a = rng.uniform(0.9, 1.0, n).astype(np.float32)
+    out = oracle.scan(np.stack([a, np.zeros(n, np.float32)], 1), "affine")
+    np.testing.assert_allclose(out[:, 0], np.cumprod(a.astype(np.float64)), rtol=1e-12)
+    assert np.all(out[:, 1] == 0.0)
+    # constant a, b = 1: geometric series x_t = (1 - a^t) / (1 - a)
+    a0 = np.float32(0.5)
+    out = oracle.scan(np.stack([np.full(60, a0), np.ones(60, np.float32)], 1), "affine")
+    t = np.arange(1, 61)
+    np.testing.assert_allclose(out[:, 1], (1 - 0.5**t) / 0.5, rtol=1e-14)
+    # non-commutativity: swapping two elements changes the result
+    p = np.array([[2, 1], [3, 5]], np.float32)
+    assert oracle.scan(p, "affine")[1].tolist() == [6.0, 3 * 1 + 5]
+    assert oracle.scan(p[::-1], "affine")[1].tolist() == [6.0, 2 * 5 + 1]
+
+
+@pytest.mark.parametrize("n", [1, 33, 100, 10001, 100000])
+def test_reduce_closed_forms(oracle, n):
+    for dt in (np.float32, np.float64, np.int32, np.int64):
+        x = np.arange(1, n + 1).astype(dt)
+        tri = n * (n + 1) // 2
+        if dt == np.int32:
+            tri = int(np.uint32(tri % 2**32).astype(np.int32))
+        assert oracle.reduce(x) == tri
+        assert oracle.reduce(x, "max") == n and oracle.reduce(x, "min") == 1
+    u = np.full(n, 3, np.uint8)
+    assert oracle.reduce(u) == (3 * n) % 256
+
+
+def test_reduce_matches_numpy(oracle):
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal(100_000).astype(np.float32)
+    np.testing.assert_allclose(oracle.reduce(x, "+", "abs2"), np.sum(x.astype(np.float64) ** 2), rtol=1e-12)
+    i = rng.integers(-2**31, 2**31 - 1, 100_000).astype(np.int32)
+    assert oracle.reduce(i, "max") == i.max() and oracle.reduce(i, "min") == i.min()
+
+
+def test_reduce_dim_matches_numpy_fortran(oracle):
+    rng = np.random.default_rng(4)
+    rows, cols = 37, 23
+    A = np.asfortranarray(rng.standard_normal((rows, 2 * cols)))
+    buf = A.reshape(-1, order="F")
+    V = A[:, ::2]  # view(A, :, 1:2:end): col_stride = 2*rows
+    np.testing.assert_allclose(oracle.reduce_dim(buf, rows, cols, 2 * rows, 1), V.sum(0), rtol=1e-13)
+    np.testing.assert_allclose(oracle.reduce_dim(buf, rows, cols, 2 * rows, 2), V.sum(1), rtol=1e-13)
+    np.testing.assert_allclose(oracle.reduce_dim(buf, rows, cols, 2 * rows, 2, "+", "abs2"), (V**2).sum(1),
+                               rtol=1e-13)
+    I = rng.integers(-1000, 1000, (rows, cols)).astype(np.int32)
+    ib = I.reshape(-1, order="F")
+    assert np.array_equal(oracle.reduce_dim(ib, rows, cols, rows, 1), I.sum(0).astype(np.int32))
+    assert np.array_equal(oracle.reduce_dim(ib, rows, cols, rows, 2, "max"), I.max(1))
+
+
+def test_cpu_baseline_agrees(oracle):
+    rng = np.random.default_rng(5)
+    x = rng.random(200_000, dtype=np.float32)
+    ref = oracle.scan(x)
+    y1 = np.empty_like(x)
+    y4 = np.empty_like(x)
+    oracle.baseline_scan_add_f32(x, y1, 1)
+    oracle.baseline_scan_add_f32(x, y4, 4)
+    np.testing.assert_allclose(y1, ref, rtol=1e-4)
+    np.testing.assert_allclose(y4, ref, rtol=1e-4)
+    s = oracle.reduce(x)
+    assert abs(oracle.baseline_sum_f32(x, 1) - s) <= 1e-4 * s
+    assert abs(oracle.baseline_sum_f32(x, 4) - s) <= 1e-4 * s
