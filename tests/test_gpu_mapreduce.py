@@ -38,7 +38,7 @@ def sum_abs(x, f):
 @pytest.mark.parametrize("f", ["identity", "abs2"])
 def test_full_reduce(kf, oracle, dev, dt, op, f):
     rng = np.random.default_rng(31)
-    rtol = 1e-6 if dt == np.float32 else 1e-14
+    rtol = 1e-6 if dt == np.float32 else 1e-12
     for n in SIZES:
         x = gen(rng, dt, n)
         got = kf.mapreduce(fmap(kf, f), op, torch.from_numpy(x).to(dev))
@@ -46,7 +46,10 @@ def test_full_reduce(kf, oracle, dev, dt, op, f):
         if dt in (np.float32, np.float64) and op == "+":
             assert abs(got - ref) <= rtol * sum_abs(x, f) + 1e-300, (n, got, ref)
         elif dt in (np.float32, np.float64):
-            assert got == ref, (n, got, ref)
+            # max/min select an element: exact once the oracle's Float64
+            # f(x) is rounded to the element type (exact for abs2 too, as
+            # the double product of two floats rounds to the float product)
+            assert dt(got) == dt(ref), (n, got, ref)
         else:
             assert got == int(ref), (n, got, ref)
 
@@ -81,9 +84,9 @@ def test_views_and_strides(kf, oracle, dev):
     for sl in (slice(2, None), slice(1, None), slice(3, -5), slice(None, None, 3), slice(5, None, 7)):
         v = x[sl]
         got = kf.mapreduce(kf.identity, "+", src[sl])
-        assert abs(got - oracle.reduce(np.ascontiguousarray(v))) <= 1e-13 * np.abs(v).sum()
+        assert abs(got - oracle.reduce(np.ascontiguousarray(v))) <= 1e-12 * np.abs(v).sum()
         assert kf.mapreduce(kf.identity, min, src[sl]) == v.min()
-        assert kf.mapreduce(kf.abs2, "+", src[sl], g=np.sqrt) == pytest.approx(np.sqrt((v * v).sum()), rel=1e-13)
+        assert kf.mapreduce(kf.abs2, "+", src[sl], g=np.sqrt) == pytest.approx(np.sqrt((v * v).sum()), rel=1e-12)
 
 
 def test_full_reduce_of_2d_and_3d(kf, dev):
@@ -99,7 +102,7 @@ def test_full_reduce_of_2d_and_3d(kf, dev):
     # a strided 2-D view that is not one strided vector: two passes
     A = torch.from_numpy(rng.random((64, 33))).to(dev).T   # 33 x 64 column-major
     V = A[:, ::2]
-    assert kf.mapreduce(kf.identity, "+", V) == pytest.approx(float(V.sum()), rel=1e-13)
+    assert kf.mapreduce(kf.identity, "+", V) == pytest.approx(float(V.sum()), rel=1e-12)
 
 
 def colmajor(rng, rows, cols, dt, view=False, low=-1.0, high=1.0):
@@ -135,10 +138,10 @@ def test_dims_2d(kf, oracle, dev, dt, shape, view):
             if np.dtype(dt).kind == "f" and op == "+":
                 M = buf.astype(np.float64)[np.arange(cols)[None, :] * cs + np.arange(rows)[:, None]]
                 M = M * M if f == "abs2" else np.abs(M)
-                bound = M.sum(axis=dim - 1) * (1e-6 if dt == np.float32 else 1e-14)
+                bound = M.sum(axis=dim - 1) * (1e-6 if dt == np.float32 else 1e-12)
                 assert np.all(np.abs(g - ref) <= bound + 1e-300), (dim, op, f)
             elif np.dtype(dt).kind == "f":
-                assert np.array_equal(g.astype(np.float64), ref), (dim, op, f)
+                assert np.array_equal(g, ref.astype(dt)), (dim, op, f)
             else:
                 assert np.array_equal(g, ref), (dim, op, f)
 
@@ -168,7 +171,7 @@ def test_dims_nd_routing(kf, dev, dims):
     d = (dims,) if isinstance(dims, int) else dims
     ref = x.cpu().numpy().sum(axis=tuple(k - 1 for k in d), keepdims=True)
     assert tuple(got.shape) == ref.shape
-    np.testing.assert_allclose(got.cpu().numpy(), ref, rtol=1e-13)
+    np.testing.assert_allclose(got.cpu().numpy(), ref, rtol=1e-12)
 
 
 def test_dims_errors(kf, dev):
@@ -197,7 +200,7 @@ def test_config3b_abs2_sum_f64_2pow28(kf, oracle, dev):
     x = torch.randn(2**28, device=dev, generator=g, dtype=torch.float64)
     got = kf.mapreduce(kf.abs2, "+", x)
     ref = oracle.reduce(x.cpu().numpy(), "+", "abs2")
-    assert abs(got - ref) <= 1e-12 * ref, (got, ref)
+    assert abs(got - ref) <= 1e-10 * ref, (got, ref)  # the host Float64 sum itself errs ~sqrt(n)*eps
 
 
 def test_config3c_int32_max_2pow28(kf, oracle, dev):

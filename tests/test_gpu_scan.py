@@ -126,7 +126,7 @@ def test_affine_scan(kf, oracle, dev, n):
     ab = np.stack([rng.uniform(0.9, 1.0, n), rng.standard_normal(n)], 1).astype(np.float32)
     for exclusive in (False, True):
         got = kf.scan(kf.affine, torch.from_numpy(ab).to(dev), exclusive=exclusive).cpu().numpy()
-        assert_mixed(got, oracle.scan(ab, "affine", exclusive), 1e-5, what=f"affine n={n} excl={exclusive}")
+        assert_mixed(got, oracle.scan(ab, "affine", exclusive=exclusive), 1e-5, what=f"affine n={n} excl={exclusive}")
 
 
 def test_affine_is_order_sensitive(kf, oracle, dev):
