@@ -7,21 +7,28 @@
 // publish the tile's own PREFIX, apply the prefix and store. The MI355X
 // design differs from the reference in these ways:
 //
-//  * Tile = 256 threads x 64 bytes per lane = 16 KiB. Each wave loads its
-//    4 KiB chunk with 16-byte streaming loads in striped order (fully
-//    coalesced), transposes it through a bank-padded LDS region into a
-//    per-lane blocked run, and transposes back for 16-byte stores.
-//  * Wave scans use DPP row shifts and row broadcasts (no LDS, no
-//    ds_bpermute). The lookback window is one wave: lane j reads the
-//    descriptor of tile (t - 64 + j) so lane order is tile order and a DPP
-//    scan combines the window in the order a non-commutative op needs.
-//  * Descriptors are W 64-bit words per tile (W = sizeof(T)/4, at least 1).
-//    Every word carries a 32-bit tag {epoch:30, state:2} next to 32 bits of
-//    the value, and is written/read with relaxed device-scope atomics, so a
-//    reader either sees all W words with one tag (a consistent value) or
-//    retries; no fences are needed for any element size (the reference uses
-//    one packed word for <= 4-byte types and a split flag/partial layout
-//    with fences otherwise, scan_kernel.jl:24-58, :94-299).
+//  * Tile = 1024 threads x 8 (2 for uint8) 16-byte vectors per lane =
+//    128 KiB (32 KiB for uint8), so 2^28 Float32 is 8192 tiles and the
+//    per-tile lookback is amortised over a large streaming body. The tile
+//    stays in registers in "striped" order: lane l of wave w holds vector
+//    j*64 + l of the wave's contiguous chunk, so every load and store is a
+//    fully coalesced 16-byte access and no LDS transpose is needed. Each
+//    row j (64 lanes x 16 bytes) is scanned in-lane, then across the wave
+//    with DPP row shifts/broadcasts, and rows are chained with a carry.
+//  * The lookback window is one wave: lane j reads the descriptor of tile
+//    (t - 64 + j), so lane order is tile order and a DPP scan combines the
+//    window in the order a non-commutative op needs.
+//  * Each tile descriptor owns a 128-byte line (kDescWords words): tiles are
+//    published from different XCDs, and packing several descriptors per line
+//    made those writers and the pollers contend for one line (measured: 5.0
+//    vs 5.8 TB/s for Float32 at 2^28).
+//  * A descriptor is W 64-bit words (W = sizeof(T)/4, at least 1). Every
+//    word carries a 32-bit tag {epoch:30, state:2} next to 32 bits of the
+//    value, written and read with relaxed device-scope atomics: a reader
+//    either sees all W words with one tag (a consistent value) or retries,
+//    so no fences are needed for any element size (the reference uses one
+//    packed word for <= 4-byte types and a split flag/partial layout with
+//    fences otherwise, scan_kernel.jl:24-58, :94-299).
 //  * Tiles are numbered by an atomic ticket, not by workgroup id, so a tile
 //    only ever waits on tiles that already started. The ticket counter and
 //    the epoch share one 64-bit word; the block holding the last ticket
@@ -33,37 +40,27 @@
 
 namespace kf {
 
-constexpr int kScanBlock = 256;
+constexpr int kScanBlock = 1024;
 constexpr int kScanWaves = kScanBlock / kWave;
-constexpr int kLaneBytes = 64;                         // bytes of the tile each lane owns
-constexpr int kWaveSlots = 256 + 32;                   // 16-byte LDS slots per wave, incl. padding
 constexpr uint32_t kStatePartial = 1, kStatePrefix = 2;
 constexpr size_t kScanHeaderBytes = 256;
+constexpr int kDescWords = 16;             // 128 bytes per tile descriptor
 constexpr uint32_t kSpinLimit = 1u << 24;  // lookback polls before giving up (seconds)
 
 template <class T> struct ScanShape {
-  static constexpr int ITEMS = kLaneBytes / (int)sizeof(T);
-  static constexpr int TILE = kScanBlock * ITEMS;
+  static constexpr int EPV = 16 / (int)sizeof(T);   // elements per 16-byte vector
+  static constexpr int V = sizeof(T) >= 4 ? 8 : 2;  // vectors per lane
+  static constexpr int WAVE_ELEMS = kWave * V * EPV;
+  static constexpr int TILE = kScanBlock * V * EPV;
   static constexpr int W = Words<T>::W;
 };
-
-// One 16-byte pad slot after every 8 slots: both the striped pattern
-// (consecutive lanes -> consecutive slots) and the blocked pattern
-// (lane l -> slots 4l..4l+3) hit distinct 16-byte bank groups.
-__device__ inline int pad_slot(int s) { return s + (s >> 3); }
-
-template <class T> __device__ inline int pad_elem(int e) {
-  constexpr int per_slot = 16 / (int)sizeof(T);
-  const int s = e / per_slot;
-  return pad_slot(s) * per_slot + (e - s * per_slot);
-}
 
 template <class T>
 __device__ inline void publish(uint64_t* desc, int64_t tile, uint32_t tag, T v) {
   const Words<T> w = to_words(v);
 #pragma unroll
   for (int i = 0; i < ScanShape<T>::W; ++i)
-    st_agent(desc + tile * ScanShape<T>::W + i, ((uint64_t)tag << 32) | w.w[i]);
+    st_agent(desc + tile * kDescWords + i, ((uint64_t)tag << 32) | w.w[i]);
 }
 
 // Decoupled lookback, executed by one full wave. Returns the combination of
@@ -90,7 +87,7 @@ __device__ inline T lookback(const uint64_t* desc, int64_t tile, uint32_t epoch3
     if (t >= 0) {
       uint64_t d[W];
 #pragma unroll
-      for (int i = 0; i < W; ++i) d[i] = ld_agent(desc + t * W + i);
+      for (int i = 0; i < W; ++i) d[i] = ld_agent(desc + t * kDescWords + i);
       const uint32_t tag = (uint32_t)(d[0] >> 32);
       bool ok = (tag >> 2) == epoch30;
 #pragma unroll
@@ -126,13 +123,12 @@ template <class T, class Op> __device__ inline T exclusive_first() {
     return Op::template identity<T>();
 }
 
-template <class T, class Op, class Map>
+template <class T, class Op, class Map, bool EXCL>
 __global__ __launch_bounds__(kScanBlock) void scan_kernel(
     const T* src, int64_t src_stride, T* dst, int64_t dst_stride, int64_t n,
-    int64_t ntiles, uint64_t* scratch, int exclusive, int vec) {
-  constexpr int ITEMS = ScanShape<T>::ITEMS;
-  constexpr int TILE = ScanShape<T>::TILE;
-  __shared__ uint4 lds[kScanWaves * kWaveSlots];
+    int64_t ntiles, uint64_t* scratch, int vec) {
+  using S = ScanShape<T>;
+  constexpr int V = S::V, EPV = S::EPV;
   __shared__ T wave_agg[kScanWaves];
   __shared__ T block_excl;
   __shared__ uint64_t s_ticket;
@@ -154,50 +150,50 @@ __global__ __launch_bounds__(kScanBlock) void scan_kernel(
   const uint32_t epoch30 = (uint32_t)(tk >> 32) & 0x3fffffffu;
   uint64_t* desc = scratch + kScanHeaderBytes / sizeof(uint64_t);
 
-  const int64_t wbase = tile * TILE + (int64_t)wave * kWave * ITEMS;  // first element of this wave's chunk
-  const bool full = vec && (tile + 1) * TILE <= n;
-  uint4* wl = lds + wave * kWaveSlots;
-  T* wlt = reinterpret_cast<T*>(wl);
+  const int64_t wbase = tile * S::TILE + (int64_t)wave * S::WAVE_ELEMS;  // this wave's chunk
+  const bool full = vec && (tile + 1) * S::TILE <= n;
 
-  // ---- load: striped global -> LDS -> blocked registers -------------------
-  T items[ITEMS];
+  // ---- load, striped: lane holds vector j*64 + lane of the wave chunk ------
+  T x[V][EPV];
   if (full) {
     const uint4* g = reinterpret_cast<const uint4*>(src + wbase);
-    uint4 r[4];
+    uint4 r[V];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) r[j] = ld_stream(g + j * kWave + lane);
+    for (int j = 0; j < V; ++j) r[j] = ld_stream(g + j * kWave + lane);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) wl[pad_slot(j * kWave + lane)] = r[j];
+    for (int j = 0; j < V; ++j) {
+      __builtin_memcpy(x[j], &r[j], 16);
+#pragma unroll
+      for (int k = 0; k < EPV; ++k) x[j][k] = Map::apply(x[j][k]);
+    }
   } else {
 #pragma unroll
-    for (int i = 0; i < ITEMS; ++i) {
-      const int e = i * kWave + lane;
-      const int64_t idx = wbase + e;
-      wlt[pad_elem<T>(e)] = idx < n ? Map::apply(src[idx * src_stride]) : id;
-    }
-  }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  {
-    uint4 q[4];
+    for (int j = 0; j < V; ++j)
 #pragma unroll
-    for (int k = 0; k < 4; ++k) q[k] = wl[pad_slot(lane * 4 + k)];
-    __builtin_memcpy(items, q, sizeof(items));
-  }
-  if (full) {
-#pragma unroll
-    for (int i = 0; i < ITEMS; ++i) items[i] = Map::apply(items[i]);
+      for (int k = 0; k < EPV; ++k) {
+        const int64_t idx = wbase + (int64_t)(j * kWave + lane) * EPV + k;
+        x[j][k] = idx < n ? Map::apply(src[idx * src_stride]) : id;
+      }
   }
 
-  // ---- thread, wave and block scans ---------------------------------------
+  // ---- in-lane, wave and row-chain scans; row prefixes folded in ----------
+  T carry = id;
+  T rowpre[EXCL ? V : 1];
 #pragma unroll
-  for (int i = 1; i < ITEMS; ++i) items[i] = Op::combine(items[i - 1], items[i]);
-  const T lane_incl = wave_inclusive_scan<Op>(items[ITEMS - 1]);
-  const T lane_excl = wave_shift_right<Op>(lane_incl);
-  if (lane == kWave - 1) wave_agg[wave] = lane_incl;
+  for (int j = 0; j < V; ++j) {
+#pragma unroll
+    for (int k = 1; k < EPV; ++k) x[j][k] = Op::combine(x[j][k - 1], x[j][k]);
+    const T incl = wave_inclusive_scan<Op>(x[j][EPV - 1]);
+    const T p = Op::combine(carry, wave_shift_right<Op>(incl));
+    carry = Op::combine(carry, read_lane(incl, kWave - 1));
+    if constexpr (EXCL) rowpre[j] = p;
+#pragma unroll
+    for (int k = 0; k < EPV; ++k) x[j][k] = Op::combine(p, x[j][k]);
+  }
+  if (lane == 0) wave_agg[wave] = carry;
   __syncthreads();
 
+  // ---- publish, look back, publish the inclusive prefix (wave 0) ----------
   if (wave == 0) {
     T agg = wave_agg[0];
 #pragma unroll
@@ -216,37 +212,30 @@ __global__ __launch_bounds__(kScanBlock) void scan_kernel(
 
   T prefix = block_excl;
   for (int w = 0; w < wave; ++w) prefix = Op::combine(prefix, wave_agg[w]);
-  prefix = Op::combine(prefix, lane_excl);
 
-  if (exclusive) {
+  // ---- apply and store ----------------------------------------------------
 #pragma unroll
-    for (int i = ITEMS - 1; i > 0; --i) items[i] = Op::combine(prefix, items[i - 1]);
-    items[0] = (tile == 0 && tid == 0) ? exclusive_first<T, Op>() : prefix;
-  } else {
+  for (int j = 0; j < V; ++j) {
+    T o[EPV];
+    if constexpr (EXCL) {
+      o[0] = Op::combine(prefix, rowpre[j]);
 #pragma unroll
-    for (int i = 0; i < ITEMS; ++i) items[i] = Op::combine(prefix, items[i]);
-  }
-
-  // ---- store: blocked registers -> LDS -> striped global ------------------
-  {
-    uint4 q[4];
-    __builtin_memcpy(q, items, sizeof(items));
+      for (int k = 1; k < EPV; ++k) o[k] = Op::combine(prefix, x[j][k - 1]);
+      if (j == 0 && tile == 0 && tid == 0) o[0] = exclusive_first<T, Op>();
+    } else {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) wl[pad_slot(lane * 4 + k)] = q[k];
-  }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  if (full) {
-    uint4* g = reinterpret_cast<uint4*>(dst + wbase);
+      for (int k = 0; k < EPV; ++k) o[k] = Op::combine(prefix, x[j][k]);
+    }
+    if (full) {
+      uint4 r;
+      __builtin_memcpy(&r, o, 16);
+      st_stream(reinterpret_cast<uint4*>(dst + wbase) + j * kWave + lane, r);
+    } else {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) st_stream(g + j * kWave + lane, wl[pad_slot(j * kWave + lane)]);
-  } else {
-#pragma unroll
-    for (int i = 0; i < ITEMS; ++i) {
-      const int e = i * kWave + lane;
-      const int64_t idx = wbase + e;
-      if (idx < n) dst[idx * dst_stride] = wlt[pad_elem<T>(e)];
+      for (int k = 0; k < EPV; ++k) {
+        const int64_t idx = wbase + (int64_t)(j * kWave + lane) * EPV + k;
+        if (idx < n) dst[idx * dst_stride] = o[k];
+      }
     }
   }
 }
@@ -256,16 +245,20 @@ template <class T> int64_t scan_tiles(int64_t n) {
 }
 
 template <class T> size_t scan_scratch(int64_t n) {
-  return kScanHeaderBytes + (size_t)scan_tiles<T>(n) * ScanShape<T>::W * sizeof(uint64_t);
+  return kScanHeaderBytes + (size_t)scan_tiles<T>(n) * kDescWords * sizeof(uint64_t);
 }
 
 template <class T, class Op, class Map>
 int launch_scan(const void* src, int64_t ss, void* dst, int64_t ds, int64_t n, int excl,
                 void* scratch, hipStream_t stream) {
   const int64_t ntiles = scan_tiles<T>(n);
-  const bool vec = ss == 1 && ds == 1 && ((uintptr_t)src % 16 == 0) && ((uintptr_t)dst % 16 == 0);
-  hipLaunchKernelGGL((scan_kernel<T, Op, Map>), dim3((unsigned)ntiles), dim3(kScanBlock), 0, stream,
-                     (const T*)src, ss, (T*)dst, ds, n, ntiles, (uint64_t*)scratch, excl, (int)vec);
+  const int vec = ss == 1 && ds == 1 && ((uintptr_t)src % 16 == 0) && ((uintptr_t)dst % 16 == 0);
+  if (excl)
+    hipLaunchKernelGGL((scan_kernel<T, Op, Map, true>), dim3((unsigned)ntiles), dim3(kScanBlock), 0, stream,
+                       (const T*)src, ss, (T*)dst, ds, n, ntiles, (uint64_t*)scratch, vec);
+  else
+    hipLaunchKernelGGL((scan_kernel<T, Op, Map, false>), dim3((unsigned)ntiles), dim3(kScanBlock), 0, stream,
+                       (const T*)src, ss, (T*)dst, ds, n, ntiles, (uint64_t*)scratch, vec);
   return kf_check_launch("scan_kernel");
 }
 
