@@ -1,22 +1,21 @@
-// Full reduction (mapreduce with dims = nothing) for gfx950.
+// Reductions (mapreduce) for gfx950: full, along dim 1 and along dim 2.
 //
-// Same two stages as the reference's mapreduce1d_kernel!
-// (reference src/mapreduce/1D/mapreduce1d_kernel.jl:5-93): a grid-stride
-// pass producing one partial per workgroup, then a single workgroup
-// combining the partials. MI355X design:
-//  * 16-byte streaming loads, 4 in flight per lane, each vector element
-//    folded into its own accumulator (16 independent float sums per lane),
-//    which keeps Float32 sums accurate and the loop free of dependencies.
-//  * The grid is sized to 8 workgroups per CU (2048 on 256 CUs, capped at
-//    kRedMaxBlocks). An unaligned head and the ragged tail are folded in by
-//    workgroup 0, so any 4-byte-aligned view takes the vector path.
-//  * Stage 2 is "last workgroup done": every workgroup publishes its partial
-//    and takes a ticket with an acq_rel device-scope atomic; the workgroup
-//    that draws the last ticket combines all partials in index order and
-//    clears the counter for the next call. Nothing spins (the reference's
-//    block 1 spins on per-block flags, mapreduce1d_kernel.jl:66-92), and
-//    the combine order depends only on n and alignment, so results are
-//    bit-for-bit reproducible.
+// Same two stages as the reference's kernels (reference
+// src/mapreduce/1D/mapreduce1d_kernel.jl:5-93 for the full reduction,
+// src/mapreduce/2D/vecmat_kernel.jl:1-169 for dims=1 and
+// src/mapreduce/2D/matvec_kernel.jl:1-239 for dims=2): partial results per
+// workgroup, then a combine. MI355X design:
+//  * Stage 1 streams with 16-byte nontemporal loads, several in flight per
+//    lane, every vector element folded into its own accumulator (16
+//    independent Float32 sums per lane: accurate and dependency-free).
+//  * Stage 2 is a second, tiny kernel on the same stream. The reference's
+//    single launch lets workgroup 1 spin on per-workgroup flags
+//    (mapreduce1d_kernel.jl:66-92); a "last workgroup done" ticket was
+//    measured here to serialise thousands of same-address device atomics
+//    at the end of the grid (the full reduction ran at 1.8 TB/s with 8192
+//    workgroups), so stage 2 uses no atomics, fences or flags at all.
+//  * Combine orders depend only on the shape and pointer alignment, so every
+//    result is bit-for-bit reproducible run to run.
 #include "kf_common.h"
 
 namespace kf {
@@ -24,8 +23,7 @@ namespace kf {
 constexpr int kRedBlock = 256;
 constexpr int kRedWaves = kRedBlock / kWave;
 constexpr int kRedUnroll = 4;
-constexpr int kRedMaxBlocks = 4096;
-constexpr size_t kRedHeaderBytes = 256;
+constexpr int kRedMaxBlocks = 8192;
 
 // Block-wide combine in wave order; result valid in thread 0.
 template <class T, class Op> __device__ inline T block_reduce(T x, T* s_wave) {
@@ -39,27 +37,16 @@ template <class T, class Op> __device__ inline T block_reduce(T x, T* s_wave) {
   return r;
 }
 
-// Stage 2 shared by the full and the per-column/row reductions: publish a
-// partial, draw a ticket, and let the last of `count` workgroups return true.
-__device__ inline bool last_block_done(uint32_t* counter, uint32_t count, bool* s_flag) {
-  if (threadIdx.x == 0) {
-    const uint32_t old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    const bool last = old == count - 1;
-    if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    *s_flag = last;
-  }
-  __syncthreads();
-  const bool last = *s_flag;
-  if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-  return last;
-}
-
+// ---------------------------------------------------------------------------
+// Full reduction, stage 1: grid-stride over 16-byte vectors. An unaligned
+// head and the ragged tail are folded in by workgroup 0, so any
+// element-aligned contiguous view takes the vector path.
+// ---------------------------------------------------------------------------
 template <class T, class Op, class Map>
 __global__ __launch_bounds__(kRedBlock) void reduce_kernel(const T* src, int64_t n, int64_t stride,
-                                                           T* dst, uint8_t* scratch, int vec) {
+                                                           T* out, int vec) {
   constexpr int EPV = 16 / (int)sizeof(T);
   __shared__ T s_wave[kRedWaves];
-  __shared__ bool s_last;
   const T id = Op::template identity<T>();
   const int tid = threadIdx.x;
   const int64_t gtid = (int64_t)blockIdx.x * kRedBlock + tid;
@@ -120,27 +107,35 @@ __global__ __launch_bounds__(kRedBlock) void reduce_kernel(const T* src, int64_t
 #pragma unroll
     for (int u = 0; u < kRedUnroll; ++u) acc = Op::combine(acc, a[u]);
   }
-
   const T part = block_reduce<T, Op>(acc, s_wave);
-  if (gridDim.x == 1) {
-    if (tid == 0) dst[0] = part;
-    return;
-  }
-  uint32_t* counter = reinterpret_cast<uint32_t*>(scratch);
-  T* partials = reinterpret_cast<T*>(scratch + kRedHeaderBytes);
-  if (tid == 0) partials[blockIdx.x] = part;
-  if (!last_block_done(counter, gridDim.x, &s_last)) return;
-  __syncthreads();  // s_wave is reused below
-  T x = id;
-  for (uint32_t j = tid; j < gridDim.x; j += kRedBlock) x = Op::combine(x, partials[j]);
+  if (tid == 0) out[blockIdx.x] = part;  // a partial, or the result when gridDim.x == 1
+}
+
+// Full reduction, stage 2: one workgroup combines `count` partials.
+template <class T, class Op>
+__global__ __launch_bounds__(kRedBlock) void combine_all_kernel(const T* partials, int count, T* dst) {
+  __shared__ T s_wave[kRedWaves];
+  T x = Op::template identity<T>();
+  for (int j = threadIdx.x; j < count; j += kRedBlock) x = Op::combine(x, partials[j]);
   const T total = block_reduce<T, Op>(x, s_wave);
-  if (tid == 0) dst[0] = total;
+  if (threadIdx.x == 0) dst[0] = total;
+}
+
+// Stage 2 of the split dims reductions: out[i*ds] = op_s partials[s*m + i].
+template <class T, class Op>
+__global__ __launch_bounds__(kRedBlock) void combine_split_kernel(const T* partials, int S, int64_t m, T* dst,
+                                                                  int64_t ds) {
+  const int64_t i = (int64_t)blockIdx.x * kRedBlock + threadIdx.x;
+  if (i >= m) return;
+  T x = partials[i];
+  for (int s = 1; s < S; ++s) x = Op::combine(x, partials[(int64_t)s * m + i]);
+  dst[i * ds] = x;
 }
 
 template <class T> int reduce_grid(int64_t n) {
-  constexpr int64_t per_block = (int64_t)kRedBlock * kRedUnroll * (16 / sizeof(T)) * 4;
+  constexpr int64_t per_block = (int64_t)kRedBlock * kRedUnroll * (16 / sizeof(T)) * 2;
   int64_t g = (n + per_block - 1) / per_block;
-  const int64_t cap = kmin<int64_t>(kRedMaxBlocks, (int64_t)kf_device_cu_count() * 8);
+  const int64_t cap = kmin<int64_t>(kRedMaxBlocks, (int64_t)kf_device_cu_count() * 32);
   if (g > cap) g = cap;
   return (int)kmax<int64_t>(g, 1);
 }
@@ -150,263 +145,228 @@ int launch_reduce(const void* src, int64_t n, int64_t stride, void* dst, void* s
                   hipStream_t stream) {
   const int grid = reduce_grid<T>(n);
   const int vec = stride == 1;
+  T* out = grid == 1 ? (T*)dst : (T*)scratch;
   hipLaunchKernelGGL((reduce_kernel<T, Op, Map>), dim3(grid), dim3(kRedBlock), 0, stream,
-                     (const T*)src, n, stride, (T*)dst, (uint8_t*)scratch, vec);
+                     (const T*)src, n, stride, out, vec);
+  if (grid > 1)
+    hipLaunchKernelGGL((combine_all_kernel<T, Op>), dim3(1), dim3(kRedBlock), 0, stream, (const T*)scratch, grid,
+                       (T*)dst);
   return kf_check_launch("reduce_kernel");
 }
 
 // ---------------------------------------------------------------------------
 // dim = 1: one wave per column (a column of a column-major matrix is
 // contiguous), optionally split into S row segments when there are too few
-// columns to fill the GPU. Follows vecmat_kernel! (reference
-// src/mapreduce/2D/vecmat_kernel.jl:1-169) in what it computes; the wave-per-
-// column layout with 16-byte loads replaces its tuned Nthreads/Nitem table.
+// columns to fill the GPU.
 // ---------------------------------------------------------------------------
 constexpr int kDimBlock = 256;
 constexpr int kDimWaves = kDimBlock / kWave;
 constexpr int kDimUnroll = 4;
 constexpr int kDimMaxSplit = 64;
-
-struct DimPlan {
-  int64_t groups;  // column groups (dim 1) or row strips (dim 2)
-  int split;       // S workgroups cooperating on one group
-  size_t counter_bytes, partial_bytes;
-};
+constexpr int kRowVecs = 4;      // dim 2: 16-byte vectors per thread per column
+constexpr int kColUnroll = 2;    // dim 2: columns in flight per thread
 
 template <class T, class Op, class Map>
 __global__ __launch_bounds__(kDimBlock) void reduce_cols_kernel(
-    const T* A, int64_t rows, int64_t cols, int64_t col_stride, T* dst, int64_t dst_stride,
-    uint8_t* scratch, size_t counter_bytes, int64_t seg_rows, int vec) {
+    const T* A, int64_t rows, int64_t cols, int64_t col_stride, T* out, int64_t out_stride,
+    int64_t seg_rows, int vec) {
   constexpr int EPV = 16 / (int)sizeof(T);
-  __shared__ bool s_last;
   const T id = Op::template identity<T>();
   const int lane = lane_id();
   const int wave = threadIdx.x / kWave;
   const int64_t col = (int64_t)blockIdx.x * kDimWaves + wave;
-  const int S = gridDim.y;
   const int s = blockIdx.y;
+  if (col >= cols) return;  // whole wave leaves together
   T acc = id;
-  if (col < cols) {
-    const T* c = A + col * col_stride;
-    const int64_t r0 = (int64_t)s * seg_rows;
-    const int64_t r1 = kmin<int64_t>(rows, r0 + seg_rows);
-    if (vec) {
-      // seg_rows is a multiple of EPV and columns are 16-byte aligned.
-      const int64_t nv = (r1 - r0) / EPV;
-      const uint4* v = reinterpret_cast<const uint4*>(c + r0);
-      T a[kDimUnroll][EPV];
+  const T* c = A + col * col_stride;
+  const int64_t r0 = (int64_t)s * seg_rows;
+  const int64_t r1 = kmin<int64_t>(rows, r0 + seg_rows);
+  if (vec) {
+    // seg_rows is a multiple of EPV and columns are 16-byte aligned.
+    const int64_t nv = r1 > r0 ? (r1 - r0) / EPV : 0;
+    const uint4* v = reinterpret_cast<const uint4*>(c + r0);
+    T a[kDimUnroll][EPV];
 #pragma unroll
-      for (int u = 0; u < kDimUnroll; ++u)
+    for (int u = 0; u < kDimUnroll; ++u)
 #pragma unroll
-        for (int e = 0; e < EPV; ++e) a[u][e] = id;
-      int64_t i = lane;
-      for (; i + (kDimUnroll - 1) * kWave < nv; i += kDimUnroll * kWave) {
-        uint4 r[kDimUnroll];
-#pragma unroll
-        for (int u = 0; u < kDimUnroll; ++u) r[u] = ld_stream(v + i + u * kWave);
-#pragma unroll
-        for (int u = 0; u < kDimUnroll; ++u) {
-          T x[EPV];
-          __builtin_memcpy(x, &r[u], 16);
-#pragma unroll
-          for (int e = 0; e < EPV; ++e) a[u][e] = Op::combine(a[u][e], Map::apply(x[e]));
-        }
-      }
-      for (; i < nv; i += kWave) {
-        const uint4 r = ld_stream(v + i);
-        T x[EPV];
-        __builtin_memcpy(x, &r, 16);
-#pragma unroll
-        for (int e = 0; e < EPV; ++e) a[0][e] = Op::combine(a[0][e], Map::apply(x[e]));
-      }
-#pragma unroll
-      for (int u = 0; u < kDimUnroll; ++u)
-#pragma unroll
-        for (int e = 0; e < EPV; ++e) acc = Op::combine(acc, a[u][e]);
-      const int64_t t = r0 + nv * EPV + lane;
-      if (t < r1) acc = Op::combine(acc, Map::apply(c[t]));
-    } else {
-      for (int64_t r = r0 + lane; r < r1; r += kWave) acc = Op::combine(acc, Map::apply(c[r]));
-    }
-  }
-  acc = wave_reduce<Op>(acc);
-  if (S == 1) {
-    if (col < cols && lane == 0) dst[col * dst_stride] = acc;
-    return;
-  }
-  uint32_t* counters = reinterpret_cast<uint32_t*>(scratch);
-  T* partials = reinterpret_cast<T*>(scratch + counter_bytes);
-  if (col < cols && lane == 0) {
-    partials[(int64_t)s * cols + col] = acc;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-  }
-  __syncthreads();
-  if (!last_block_done(counters + blockIdx.x, (uint32_t)S, &s_last)) return;
-  if (col < cols) {
-    T x = lane < S ? partials[(int64_t)lane * cols + col] : id;
-    x = wave_reduce<Op>(x);
-    if (lane == 0) dst[col * dst_stride] = x;
-  }
-}
-
-// ---------------------------------------------------------------------------
-// dim = 2: a workgroup owns a strip of 64*EPV rows (each lane EPV adjacent
-// rows, one 16-byte load per column) and a range of columns; its 4 waves
-// take interleaved columns and are combined through LDS in wave order.
-// Strips with too few workgroups are split over S column ranges whose
-// partials the last-done workgroup combines. Computes what matvec_kernel!
-// computes (reference src/mapreduce/2D/matvec_kernel.jl:1-239).
-// ---------------------------------------------------------------------------
-template <class T, class Op, class Map, bool VEC>
-__global__ __launch_bounds__(kDimBlock) void reduce_rows_kernel(
-    const T* A, int64_t rows, int64_t cols, int64_t col_stride, T* dst, int64_t dst_stride,
-    uint8_t* scratch, size_t counter_bytes, int64_t seg_cols) {
-  constexpr int EPV = VEC ? 16 / (int)sizeof(T) : 1;
-  constexpr int RS = kWave * EPV;
-  __shared__ T s_part[kDimWaves][RS];
-  __shared__ bool s_last;
-  const T id = Op::template identity<T>();
-  const int lane = lane_id();
-  const int wave = threadIdx.x / kWave;
-  const int S = gridDim.y;
-  const int s = blockIdx.y;
-  const int64_t row0 = (int64_t)blockIdx.x * RS + (int64_t)lane * EPV;
-  const int64_t c0 = (int64_t)s * seg_cols;
-  const int64_t c1 = kmin<int64_t>(cols, c0 + seg_cols);
-
-  T a[EPV];
-#pragma unroll
-  for (int e = 0; e < EPV; ++e) a[e] = id;
-  if (VEC && row0 + EPV <= rows) {
-    const T* p = A + row0;
-    int64_t c = c0 + wave;
-    for (; c + (kDimUnroll - 1) * kDimWaves < c1; c += kDimUnroll * kDimWaves) {
+      for (int e = 0; e < EPV; ++e) a[u][e] = id;
+    int64_t i = lane;
+    for (; i + (kDimUnroll - 1) * kWave < nv; i += kDimUnroll * kWave) {
       uint4 r[kDimUnroll];
 #pragma unroll
-      for (int u = 0; u < kDimUnroll; ++u)
-        r[u] = ld_stream(reinterpret_cast<const uint4*>(p + (c + u * kDimWaves) * col_stride));
+      for (int u = 0; u < kDimUnroll; ++u) r[u] = ld_stream(v + i + u * kWave);
 #pragma unroll
       for (int u = 0; u < kDimUnroll; ++u) {
         T x[EPV];
-        __builtin_memcpy(x, &r[u], sizeof(x));
+        __builtin_memcpy(x, &r[u], 16);
 #pragma unroll
-        for (int e = 0; e < EPV; ++e) a[e] = Op::combine(a[e], Map::apply(x[e]));
+        for (int e = 0; e < EPV; ++e) a[u][e] = Op::combine(a[u][e], Map::apply(x[e]));
       }
     }
-    for (; c < c1; c += kDimWaves) {
-      const uint4 r = ld_stream(reinterpret_cast<const uint4*>(p + c * col_stride));
+    for (; i < nv; i += kWave) {
+      const uint4 r = ld_stream(v + i);
       T x[EPV];
-      __builtin_memcpy(x, &r, sizeof(x));
+      __builtin_memcpy(x, &r, 16);
 #pragma unroll
-      for (int e = 0; e < EPV; ++e) a[e] = Op::combine(a[e], Map::apply(x[e]));
+      for (int e = 0; e < EPV; ++e) a[0][e] = Op::combine(a[0][e], Map::apply(x[e]));
+    }
+#pragma unroll
+    for (int u = 0; u < kDimUnroll; ++u)
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) acc = Op::combine(acc, a[u][e]);
+    const int64_t t = r0 + nv * EPV + lane;
+    if (t < r1) acc = Op::combine(acc, Map::apply(c[t]));
+  } else {
+    for (int64_t r = r0 + lane; r < r1; r += kWave) acc = Op::combine(acc, Map::apply(c[r]));
+  }
+  acc = wave_reduce<Op>(acc);
+  // S == 1: out is dst; otherwise out is partials[s*cols + col]
+  if (lane == 0) out[gridDim.y == 1 ? col * out_stride : (int64_t)s * cols + col] = acc;
+}
+
+// ---------------------------------------------------------------------------
+// dim = 2: a workgroup owns a strip of 256*kRowVecs*EPV rows (16 KiB of each
+// column; thread t holds vectors t, t+256, ... of the strip) and a range of
+// columns, which it walks kColUnroll at a time, so every load is part of a
+// 16 KiB contiguous run. Strips are split over S column ranges whose
+// partials stage 2 combines.
+// ---------------------------------------------------------------------------
+template <class T, class Op, class Map, bool VEC>
+__global__ __launch_bounds__(kDimBlock) void reduce_rows_kernel(
+    const T* A, int64_t rows, int64_t cols, int64_t col_stride, T* out, int64_t out_stride, int64_t seg_cols) {
+  constexpr int EPV = VEC ? 16 / (int)sizeof(T) : 1;
+  constexpr int RS = kDimBlock * kRowVecs * EPV;
+  const T id = Op::template identity<T>();
+  const int tid = threadIdx.x;
+  const int s = blockIdx.y;
+  const int64_t strip = (int64_t)blockIdx.x * RS;
+  const int64_t c0 = (int64_t)s * seg_cols;
+  const int64_t c1 = kmin<int64_t>(cols, c0 + seg_cols);
+
+  T a[kRowVecs][EPV];
+#pragma unroll
+  for (int u = 0; u < kRowVecs; ++u)
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) a[u][e] = id;
+  const bool full = strip + RS <= rows;
+  if (VEC && full) {
+    const T* p = A + strip;
+    int64_t c = c0;
+    for (; c + kColUnroll <= c1; c += kColUnroll) {
+      uint4 r[kColUnroll][kRowVecs];
+#pragma unroll
+      for (int q = 0; q < kColUnroll; ++q)
+#pragma unroll
+        for (int u = 0; u < kRowVecs; ++u)
+          r[q][u] = ld_stream(reinterpret_cast<const uint4*>(p + (c + q) * col_stride) + u * kDimBlock + tid);
+#pragma unroll
+      for (int q = 0; q < kColUnroll; ++q)
+#pragma unroll
+        for (int u = 0; u < kRowVecs; ++u) {
+          T x[EPV];
+          __builtin_memcpy(x, &r[q][u], sizeof(x));
+#pragma unroll
+          for (int e = 0; e < EPV; ++e) a[u][e] = Op::combine(a[u][e], Map::apply(x[e]));
+        }
+    }
+    for (; c < c1; ++c) {
+#pragma unroll
+      for (int u = 0; u < kRowVecs; ++u) {
+        const uint4 r = ld_stream(reinterpret_cast<const uint4*>(p + c * col_stride) + u * kDimBlock + tid);
+        T x[EPV];
+        __builtin_memcpy(x, &r, sizeof(x));
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) a[u][e] = Op::combine(a[u][e], Map::apply(x[e]));
+      }
     }
   } else {
+    for (int64_t c = c0; c < c1; ++c)
+#pragma unroll
+      for (int u = 0; u < kRowVecs; ++u)
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) {
+          const int64_t r = strip + (int64_t)(u * kDimBlock + tid) * EPV + e;
+          if (r < rows) a[u][e] = Op::combine(a[u][e], Map::apply(A[r + c * col_stride]));
+        }
+  }
+#pragma unroll
+  for (int u = 0; u < kRowVecs; ++u)
 #pragma unroll
     for (int e = 0; e < EPV; ++e) {
-      const int64_t r = row0 + e;
-      if (r < rows) {
-        T x = id;
-        for (int64_t c = c0 + wave; c < c1; c += kDimWaves) x = Op::combine(x, Map::apply(A[r + c * col_stride]));
-        a[e] = x;
-      }
+      const int64_t r = strip + (int64_t)(u * kDimBlock + tid) * EPV + e;
+      if (r < rows) out[gridDim.y == 1 ? r * out_stride : (int64_t)s * rows + r] = a[u][e];
     }
-  }
-#pragma unroll
-  for (int e = 0; e < EPV; ++e) s_part[wave][lane * EPV + e] = a[e];
-  __syncthreads();
-  // Each thread now owns one row of the strip (RS <= kDimBlock for EPV <= 4;
-  // wider types loop).
-  uint32_t* counters = reinterpret_cast<uint32_t*>(scratch);
-  T* partials = reinterpret_cast<T*>(scratch + counter_bytes);
-  for (int lr = threadIdx.x; lr < RS; lr += kDimBlock) {
-    T x = s_part[0][lr];
-#pragma unroll
-    for (int w = 1; w < kDimWaves; ++w) x = Op::combine(x, s_part[w][lr]);
-    const int64_t r = (int64_t)blockIdx.x * RS + lr;
-    if (r < rows) {
-      if (S == 1) dst[r * dst_stride] = x;
-      else partials[(int64_t)s * rows + r] = x;
-    }
-  }
-  if (S == 1) return;
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-  __syncthreads();
-  if (!last_block_done(counters + blockIdx.x, (uint32_t)S, &s_last)) return;
-  for (int lr = threadIdx.x; lr < RS; lr += kDimBlock) {
-    const int64_t r = (int64_t)blockIdx.x * RS + lr;
-    if (r < rows) {
-      T x = partials[r];
-      for (int j = 1; j < S; ++j) x = Op::combine(x, partials[(int64_t)j * rows + r]);
-      dst[r * dst_stride] = x;
-    }
-  }
 }
 
 inline size_t round256(size_t b) { return (b + 255) & ~(size_t)255; }
 
-// Launch plan. Targets ~16K waves for dim 1 and ~2K workgroups for dim 2;
-// must be a pure function of (dtype size, rows, cols, dim) so the scratch
-// size query and the launch agree.
-inline DimPlan plan_dim(size_t es, int64_t rows, int64_t cols, int dim) {
+struct DimPlan {
+  int64_t groups;  // column groups (dim 1) or row strips (dim 2)
+  int split;       // S workgroups cooperating on one group
+  size_t partial_bytes;
+};
+
+// Launch plan; a pure function of (element size, shape, dim, alignment) so
+// the scratch query and the launch agree.
+inline DimPlan plan_dim(size_t es, int64_t rows, int64_t cols, int dim, bool vec) {
   DimPlan p{};
-  const int epv = (int)(16 / es);
+  const int epv = vec ? (int)(16 / es) : 1;
   if (dim == 1) {
     p.groups = (cols + kDimWaves - 1) / kDimWaves;
     int64_t S = 1;
     if (cols < 16384) {
       S = (16384 + cols - 1) / cols;
-      const int64_t by_rows = rows / ((int64_t)kWave * epv * kDimUnroll * 4);  // >= 4 unrolled passes each
+      const int64_t by_rows = rows / ((int64_t)kWave * 4 * kDimUnroll * 4);  // >= 4 unrolled passes each
       S = kmin<int64_t>(S, kmax<int64_t>(by_rows, 1));
       S = kmin<int64_t>(S, kDimMaxSplit);
     }
     p.split = (int)S;
   } else {
-    const int64_t rs = (int64_t)kWave * epv;
+    const int64_t rs = (int64_t)kDimBlock * kRowVecs * epv;
     p.groups = (rows + rs - 1) / rs;
     int64_t S = 1;
-    if (p.groups < 2048) {
-      S = (2048 + p.groups - 1) / p.groups;
-      const int64_t by_cols = cols / ((int64_t)kDimWaves * 16);  // >= 16 columns per wave
-      S = kmin<int64_t>(S, kmax<int64_t>(by_cols, 1));
-      S = kmin<int64_t>(S, kDimMaxSplit);
+    if (p.groups < 1024) {
+      S = (1024 + p.groups - 1) / p.groups;
+      S = kmin<int64_t>(S, kmax<int64_t>(cols / 8, 1));  // >= 8 columns per workgroup
+      S = kmin<int64_t>(S, 256);
     }
     p.split = (int)S;
   }
-  if (p.split > 1) {
-    // dim 2 counts counters per 64-row strip: enough for the vector variant
-    // (64*EPV rows) and for the unaligned scalar variant (64 rows).
-    const int64_t ncounters = dim == 1 ? p.groups : (rows + kWave - 1) / kWave;
-    p.counter_bytes = round256((size_t)ncounters * sizeof(uint32_t));
-    p.partial_bytes = round256((size_t)p.split * (size_t)(dim == 1 ? cols : rows) * es);
-  }
+  if (p.split > 1) p.partial_bytes = round256((size_t)p.split * (size_t)(dim == 1 ? cols : rows) * es);
   return p;
+}
+
+inline bool dim_vec_ok(const void* A, int64_t cs, size_t es) {
+  return ((uintptr_t)A % 16 == 0) && ((cs * (int64_t)es) % 16 == 0);
 }
 
 template <class T, class Op, class Map>
 int launch_reduce_dim(const void* A, int64_t rows, int64_t cols, int64_t cs, int dim, void* dst,
                       int64_t ds, void* scratch, hipStream_t stream) {
-  const DimPlan p = plan_dim(sizeof(T), rows, cols, dim);
-  const bool aligned = ((uintptr_t)A % 16 == 0) && ((cs * (int64_t)sizeof(T)) % 16 == 0);
+  const bool vec = dim_vec_ok(A, cs, sizeof(T));
+  const DimPlan p = plan_dim(sizeof(T), rows, cols, dim, vec);
+  T* out = p.split > 1 ? (T*)scratch : (T*)dst;
   if (dim == 1) {
     constexpr int EPV = 16 / (int)sizeof(T);
     int64_t seg = (rows + p.split - 1) / p.split;
     seg = (seg + EPV - 1) / EPV * EPV;
     hipLaunchKernelGGL((reduce_cols_kernel<T, Op, Map>), dim3((unsigned)p.groups, p.split), dim3(kDimBlock), 0,
-                       stream, (const T*)A, rows, cols, cs, (T*)dst, ds, (uint8_t*)scratch, p.counter_bytes,
-                       seg, (int)aligned);
-    return kf_check_launch("reduce_cols_kernel");
-  }
-  const int64_t seg = (cols + p.split - 1) / p.split;
-  if (aligned) {
-    hipLaunchKernelGGL((reduce_rows_kernel<T, Op, Map, true>), dim3((unsigned)p.groups, p.split), dim3(kDimBlock),
-                       0, stream, (const T*)A, rows, cols, cs, (T*)dst, ds, (uint8_t*)scratch, p.counter_bytes, seg);
+                       stream, (const T*)A, rows, cols, cs, out, ds, seg, (int)vec);
   } else {
-    // The scalar variant has 64-row strips: re-plan its grid for that width.
-    const int64_t groups = (rows + kWave - 1) / kWave;
-    hipLaunchKernelGGL((reduce_rows_kernel<T, Op, Map, false>), dim3((unsigned)groups, p.split), dim3(kDimBlock),
-                       0, stream, (const T*)A, rows, cols, cs, (T*)dst, ds, (uint8_t*)scratch, p.counter_bytes, seg);
+    const int64_t seg = (cols + p.split - 1) / p.split;
+    if (vec)
+      hipLaunchKernelGGL((reduce_rows_kernel<T, Op, Map, true>), dim3((unsigned)p.groups, p.split), dim3(kDimBlock),
+                         0, stream, (const T*)A, rows, cols, cs, out, ds, seg);
+    else
+      hipLaunchKernelGGL((reduce_rows_kernel<T, Op, Map, false>), dim3((unsigned)p.groups, p.split),
+                         dim3(kDimBlock), 0, stream, (const T*)A, rows, cols, cs, out, ds, seg);
   }
-  return kf_check_launch("reduce_rows_kernel");
+  if (p.split > 1) {
+    const int64_t m = dim == 1 ? cols : rows;
+    hipLaunchKernelGGL((combine_split_kernel<T, Op>), dim3((unsigned)((m + kRedBlock - 1) / kRedBlock)),
+                       dim3(kRedBlock), 0, stream, (const T*)scratch, p.split, m, (T*)dst, ds);
+  }
+  return kf_check_launch(dim == 1 ? "reduce_cols_kernel" : "reduce_rows_kernel");
 }
 
 // ---------------------------------------------------------------------------
@@ -455,17 +415,18 @@ template <class T, class Op, class Map> struct ReduceDimL {
 // ---------------------------------------------------------------------------
 // Copy ceiling and scratch fill.
 // ---------------------------------------------------------------------------
+// One-shot copy: every thread moves 4 vectors spaced a workgroup apart and
+// the grid covers the whole buffer (no grid-stride loop); measured faster
+// than grid-stride copies and hipMemcpyDtoD on MI355X.
 __global__ __launch_bounds__(256) void copy_kernel(uint4* dst, const uint4* src, int64_t nvec) {
-  const int64_t gsize = (int64_t)gridDim.x * blockDim.x;
-  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  for (; i + 3 * gsize < nvec; i += 4 * gsize) {
-    uint4 r[4];
+  const int64_t base = (int64_t)blockIdx.x * 1024 + threadIdx.x;
+  uint4 r[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) r[u] = ld_stream(src + i + u * gsize);
+  for (int u = 0; u < 4; ++u)
+    if (base + u * 256 < nvec) r[u] = ld_stream(src + base + u * 256);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) st_stream(dst + i + u * gsize, r[u]);
-  }
-  for (; i < nvec; i += gsize) st_stream(dst + i, ld_stream(src + i));
+  for (int u = 0; u < 4; ++u)
+    if (base + u * 256 < nvec) st_stream(dst + base + u * 256, r[u]);
 }
 
 __global__ void copy_bytes_kernel(uint8_t* dst, const uint8_t* src, int64_t n) {
@@ -486,7 +447,7 @@ extern "C" size_t kf_reduce_scratch_bytes(kf_dtype dt, int64_t n) {
   (void)n;
   size_t es = kf_dtype_size(dt);
   if (es == 0) es = 8;
-  return kRedHeaderBytes + (size_t)kRedMaxBlocks * es;
+  return round256((size_t)kRedMaxBlocks * es);
 }
 
 extern "C" int kf_reduce(kf_op op, kf_map f, kf_dtype dt, const void* src, int64_t n, int64_t stride,
@@ -511,8 +472,9 @@ extern "C" int kf_reduce(kf_op op, kf_map f, kf_dtype dt, const void* src, int64
 extern "C" size_t kf_reduce_dim_scratch_bytes(kf_dtype dt, int64_t rows, int64_t cols, int dim) {
   const size_t es = kf_dtype_size(dt);
   if (es == 0 || rows <= 0 || cols <= 0 || (dim != 1 && dim != 2)) return 256;
-  const DimPlan p = plan_dim(es, rows, cols, dim);
-  return kmax<size_t>(256, p.counter_bytes + p.partial_bytes);
+  // the plan depends on alignment: reserve for the larger of the two
+  const DimPlan pv = plan_dim(es, rows, cols, dim, true), ps = plan_dim(es, rows, cols, dim, false);
+  return kmax<size_t>(256, kmax<size_t>(pv.partial_bytes, ps.partial_bytes));
 }
 
 extern "C" int kf_reduce_dim(kf_op op, kf_map f, kf_dtype dt, const void* A, int64_t rows, int64_t cols,
@@ -534,7 +496,7 @@ extern "C" int kf_reduce_dim(kf_op op, kf_map f, kf_dtype dt, const void* A, int
   if ((uintptr_t)A % es || (uintptr_t)dst % es)
     return kf_set_error(KF_EINVAL, "kf_reduce_dim: A/dst not aligned to the element type");
   const size_t need = kf_reduce_dim_scratch_bytes(dt, rows, cols, dim);
-  const DimPlan p = plan_dim(es, rows, cols, dim);
+  const DimPlan p = plan_dim(es, rows, cols, dim, dim_vec_ok(A, col_stride, es));
   if (p.split > 1) {
     if (!scratch || scratch_bytes < need)
       return kf_set_error(KF_ENOSCRATCH, "kf_reduce_dim: scratch of %zu bytes needed, %zu given", need,
@@ -554,8 +516,9 @@ extern "C" int kf_copy(void* dst, const void* src, size_t bytes, void* stream) {
   if ((uintptr_t)dst % 16 == 0 && (uintptr_t)src % 16 == 0) {
     const int64_t nvec = (int64_t)(bytes / 16);
     if (nvec > 0) {
-      const int grid = (int)kmin<int64_t>(cap, kmax<int64_t>(1, (nvec + 1023) / 1024));
-      hipLaunchKernelGGL(copy_kernel, dim3(grid), dim3(256), 0, s, (uint4*)dst, (const uint4*)src, nvec);
+      const int64_t grid = (nvec + 1023) / 1024;
+      if (grid > 0x7fffffffLL) return kf_set_error(KF_EINVAL, "kf_copy: buffer exceeds the grid limit");
+      hipLaunchKernelGGL(copy_kernel, dim3((unsigned)grid), dim3(256), 0, s, (uint4*)dst, (const uint4*)src, nvec);
     }
     const int64_t rem = (int64_t)(bytes % 16);
     if (rem)
