@@ -111,14 +111,33 @@ __global__ __launch_bounds__(kRedBlock) void reduce_kernel(const T* src, int64_t
   if (tid == 0) out[blockIdx.x] = part;  // a partial, or the result when gridDim.x == 1
 }
 
-// Full reduction, stage 2: one workgroup combines `count` partials.
+// Full reduction, stage 2: one 1024-thread workgroup combines `count`
+// partials; each thread issues all of its (at most kRedMaxBlocks/1024) loads
+// before combining, so the stage costs about one memory latency.
+constexpr int kCombineBlock = 1024;
 template <class T, class Op>
-__global__ __launch_bounds__(kRedBlock) void combine_all_kernel(const T* partials, int count, T* dst) {
-  __shared__ T s_wave[kRedWaves];
-  T x = Op::template identity<T>();
-  for (int j = threadIdx.x; j < count; j += kRedBlock) x = Op::combine(x, partials[j]);
-  const T total = block_reduce<T, Op>(x, s_wave);
-  if (threadIdx.x == 0) dst[0] = total;
+__global__ __launch_bounds__(kCombineBlock) void combine_all_kernel(const T* partials, int count, T* dst) {
+  constexpr int PER = kRedMaxBlocks / kCombineBlock;
+  constexpr int WAVES = kCombineBlock / kWave;
+  __shared__ T s_wave[WAVES];
+  const T id = Op::template identity<T>();
+  T v[PER];
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const int j = k * kCombineBlock + threadIdx.x;
+    v[k] = j < count ? partials[j] : id;
+  }
+  T x = v[0];
+#pragma unroll
+  for (int k = 1; k < PER; ++k) x = Op::combine(x, v[k]);
+  x = wave_reduce<Op>(x);
+  if (lane_id() == 0) s_wave[threadIdx.x / kWave] = x;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    T r = s_wave[0];
+    for (int w = 1; w < WAVES; ++w) r = Op::combine(r, s_wave[w]);
+    dst[0] = r;
+  }
 }
 
 // Stage 2 of the split dims reductions: out[i*ds] = op_s partials[s*m + i].
@@ -149,7 +168,7 @@ int launch_reduce(const void* src, int64_t n, int64_t stride, void* dst, void* s
   hipLaunchKernelGGL((reduce_kernel<T, Op, Map>), dim3(grid), dim3(kRedBlock), 0, stream,
                      (const T*)src, n, stride, out, vec);
   if (grid > 1)
-    hipLaunchKernelGGL((combine_all_kernel<T, Op>), dim3(1), dim3(kRedBlock), 0, stream, (const T*)scratch, grid,
+    hipLaunchKernelGGL((combine_all_kernel<T, Op>), dim3(1), dim3(kCombineBlock), 0, stream, (const T*)scratch, grid,
                        (T*)dst);
   return kf_check_launch("reduce_kernel");
 }

@@ -40,18 +40,18 @@
 
 namespace kf {
 
-constexpr int kScanBlock = 1024;
-constexpr int kScanWaves = kScanBlock / kWave;
+constexpr int kScanBlock = 1024;       // large tiles (default)
+constexpr int kScanBlockSmall = 256;   // small tiles: arrays too short to fill the GPU with large ones
 constexpr uint32_t kStatePartial = 1, kStatePrefix = 2;
 constexpr size_t kScanHeaderBytes = 256;
 constexpr int kDescWords = 16;             // 128 bytes per tile descriptor
 constexpr uint32_t kSpinLimit = 1u << 24;  // lookback polls before giving up (seconds)
 
-template <class T> struct ScanShape {
+template <class T, int BLOCK = kScanBlock> struct ScanShape {
   static constexpr int EPV = 16 / (int)sizeof(T);   // elements per 16-byte vector
   static constexpr int V = sizeof(T) >= 4 ? 8 : 2;  // vectors per lane
   static constexpr int WAVE_ELEMS = kWave * V * EPV;
-  static constexpr int TILE = kScanBlock * V * EPV;
+  static constexpr int TILE = BLOCK * V * EPV;
   static constexpr int W = Words<T>::W;
 };
 
@@ -123,12 +123,13 @@ template <class T, class Op> __device__ inline T exclusive_first() {
     return Op::template identity<T>();
 }
 
-template <class T, class Op, class Map, bool EXCL>
-__global__ __launch_bounds__(kScanBlock) void scan_kernel(
+template <class T, class Op, class Map, bool EXCL, int BLOCK>
+__global__ __launch_bounds__(BLOCK) void scan_kernel(
     const T* src, int64_t src_stride, T* dst, int64_t dst_stride, int64_t n,
     int64_t ntiles, uint64_t* scratch, int vec) {
-  using S = ScanShape<T>;
+  using S = ScanShape<T, BLOCK>;
   constexpr int V = S::V, EPV = S::EPV;
+  constexpr int kScanWaves = BLOCK / kWave;
   __shared__ T wave_agg[kScanWaves];
   __shared__ T block_excl;
   __shared__ uint64_t s_ticket;
@@ -240,12 +241,31 @@ __global__ __launch_bounds__(kScanBlock) void scan_kernel(
   }
 }
 
+// Large tiles unless that leaves fewer than two tiles per CU; a pure function
+// of (T, n) so the scratch query and the launch agree.
+template <class T> bool scan_small_tiles(int64_t n) {
+  const int64_t large = (n + ScanShape<T>::TILE - 1) / ScanShape<T>::TILE;
+  return large < 512;
+}
+
 template <class T> int64_t scan_tiles(int64_t n) {
-  return (n + ScanShape<T>::TILE - 1) / ScanShape<T>::TILE;
+  const int64_t tile = scan_small_tiles<T>(n) ? ScanShape<T, kScanBlockSmall>::TILE : ScanShape<T>::TILE;
+  return (n + tile - 1) / tile;
 }
 
 template <class T> size_t scan_scratch(int64_t n) {
   return kScanHeaderBytes + (size_t)scan_tiles<T>(n) * kDescWords * sizeof(uint64_t);
+}
+
+template <class T, class Op, class Map, int BLOCK>
+void launch_scan_block(const void* src, int64_t ss, void* dst, int64_t ds, int64_t n, int excl, int64_t ntiles,
+                       int vec, void* scratch, hipStream_t stream) {
+  if (excl)
+    hipLaunchKernelGGL((scan_kernel<T, Op, Map, true, BLOCK>), dim3((unsigned)ntiles), dim3(BLOCK), 0, stream,
+                       (const T*)src, ss, (T*)dst, ds, n, ntiles, (uint64_t*)scratch, vec);
+  else
+    hipLaunchKernelGGL((scan_kernel<T, Op, Map, false, BLOCK>), dim3((unsigned)ntiles), dim3(BLOCK), 0, stream,
+                       (const T*)src, ss, (T*)dst, ds, n, ntiles, (uint64_t*)scratch, vec);
 }
 
 template <class T, class Op, class Map>
@@ -253,12 +273,10 @@ int launch_scan(const void* src, int64_t ss, void* dst, int64_t ds, int64_t n, i
                 void* scratch, hipStream_t stream) {
   const int64_t ntiles = scan_tiles<T>(n);
   const int vec = ss == 1 && ds == 1 && ((uintptr_t)src % 16 == 0) && ((uintptr_t)dst % 16 == 0);
-  if (excl)
-    hipLaunchKernelGGL((scan_kernel<T, Op, Map, true>), dim3((unsigned)ntiles), dim3(kScanBlock), 0, stream,
-                       (const T*)src, ss, (T*)dst, ds, n, ntiles, (uint64_t*)scratch, vec);
+  if (scan_small_tiles<T>(n))
+    launch_scan_block<T, Op, Map, kScanBlockSmall>(src, ss, dst, ds, n, excl, ntiles, vec, scratch, stream);
   else
-    hipLaunchKernelGGL((scan_kernel<T, Op, Map, false>), dim3((unsigned)ntiles), dim3(kScanBlock), 0, stream,
-                       (const T*)src, ss, (T*)dst, ds, n, ntiles, (uint64_t*)scratch, vec);
+    launch_scan_block<T, Op, Map, kScanBlock>(src, ss, dst, ds, n, excl, ntiles, vec, scratch, stream);
   return kf_check_launch("scan_kernel");
 }
 

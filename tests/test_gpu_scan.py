@@ -14,7 +14,7 @@ pytestmark = pytest.mark.gpu
 
 EDGE = list(range(1, 11))
 TILE_EDGES = [63, 64, 65, 255, 256, 257, 1023, 1024, 1025, 2047, 2048, 2049, 4095, 4096, 4097, 8191, 8192,
-              8193, 16383, 16384, 16385, 65536 * 4 + 3]
+              8193, 16383, 16384, 16385, 32767, 32768, 32769, 65536 * 4 + 3]
 SIZES = EDGE + TILE_EDGES + [100_003, 1_000_000]
 
 
@@ -187,6 +187,18 @@ def test_views_offsets_strides_inplace(kf, oracle, dev):
     y = src.clone()                                   # in place
     kf.scan_("+", y, y)
     assert np.array_equal(y.cpu().numpy(), oracle.scan(x))
+
+
+@pytest.mark.parametrize("dt", [np.int32, np.int64, np.uint8])
+def test_tile_size_switchover(kf, oracle, dev, dt):
+    # arrays with fewer than 512 large tiles use 256-thread tiles; check both
+    # sides of the switch (large tile = 128 KiB, 32 KiB for uint8)
+    large = 131072 // np.dtype(dt).itemsize if dt != np.uint8 else 32768
+    rng = np.random.default_rng(23)
+    for n in (512 * large - 1, 512 * large, 512 * large + 1):
+        x = gen(rng, dt, n)
+        for exclusive in (False, True):
+            assert np.array_equal(run(kf, dev, x, "+", exclusive=exclusive), oracle.scan(x, "+", exclusive=exclusive))
 
 
 def test_errors(kf, dev):
