@@ -231,3 +231,18 @@ def test_config5_dims(kf, oracle, dev, which):
     absA = absA.reshape(cols, rows)[:: (2 if which.endswith("view") else 1)]  # (kcols, rows)
     bound = absA.sum(axis=1 if dim == 1 else 0) * 1e-6
     assert np.all(np.abs(got - ref) <= bound), which
+
+
+@pytest.mark.parametrize("dt", [np.int32, np.int64, np.uint8])
+def test_multilevel_full_reduce_exact(kf, oracle, dev, dt):
+    # sizes whose partials need one, two and three combine levels, with
+    # aligned and unaligned starts (exact integer results)
+    rng = np.random.default_rng(47)
+    epv = 16 // np.dtype(dt).itemsize
+    for n in (8192 * 512 * epv - 1, 8192 * 512 * epv + 5, 2**26 + 3):
+        x = gen(rng, dt, n + 3)
+        t = torch.from_numpy(x).to(dev)
+        for off in (0, 1, 3):
+            v = x[off:off + n]
+            for op in ("+", "max"):
+                assert kf.mapreduce(kf.identity, op, t[off:off + n]) == int(oracle.reduce(v, op)), (n, off, op)
