@@ -284,8 +284,9 @@ constexpr int kDimBlock = 256;
 constexpr int kDimWaves = kDimBlock / kWave;
 constexpr int kDimUnroll = 4;
 constexpr int kDimMaxSplit = 64;
-constexpr int kRowVecs = 4;      // dim 2: 16-byte vectors per thread per column
-constexpr int kColUnroll = 2;    // dim 2: columns in flight per thread
+constexpr int kRowVecsDefault = 2;    // dim 2: 16-byte vectors per thread per column
+constexpr int kColUnrollDefault = 8;  // dim 2: columns in flight per thread
+constexpr int kDim2Blocks = 256;      // dim 2: target workgroups (one per CU)
 
 template <class T, class Op, class Map>
 __global__ __launch_bounds__(kDimBlock) void reduce_cols_kernel(
@@ -346,13 +347,13 @@ __global__ __launch_bounds__(kDimBlock) void reduce_cols_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// dim = 2: a workgroup owns a strip of 256*kRowVecs*EPV rows (16 KiB of each
+// dim = 2: a workgroup owns a strip of 256*kRowVecs*EPV rows (8 KiB of each
 // column; thread t holds vectors t, t+256, ... of the strip) and a range of
 // columns, which it walks kColUnroll at a time, so every load is part of a
-// 16 KiB contiguous run. Strips are split over S column ranges whose
+// 8 KiB contiguous run. Strips are split over S column ranges whose
 // partials stage 2 combines.
 // ---------------------------------------------------------------------------
-template <class T, class Op, class Map, bool VEC>
+template <class T, class Op, class Map, bool VEC, int kRowVecs = kRowVecsDefault, int kColUnroll = kColUnrollDefault>
 __global__ __launch_bounds__(kDimBlock) void reduce_rows_kernel(
     const T* A, int64_t rows, int64_t cols, int64_t col_stride, T* out, int64_t out_stride, int64_t seg_cols) {
   constexpr int EPV = VEC ? 16 / (int)sizeof(T) : 1;
@@ -442,12 +443,15 @@ inline DimPlan plan_dim(size_t es, int64_t rows, int64_t cols, int dim, bool vec
     }
     p.split = (int)S;
   } else {
-    const int64_t rs = (int64_t)kDimBlock * kRowVecs * epv;
+    const int64_t rs = (int64_t)kDimBlock * kRowVecsDefault * epv;
     p.groups = (rows + rs - 1) / rs;
+    // Few workgroups with 16 loads in flight per thread beat many
+    // workgroups with more split partials (65536 x 4096 Float32: 6.6 TB/s at
+    // 256 workgroups, 5.4 TB/s at 1024 with 4 loads per thread).
     int64_t S = 1;
-    if (p.groups < 1024) {
-      S = (1024 + p.groups - 1) / p.groups;
-      S = kmin<int64_t>(S, kmax<int64_t>(cols / 8, 1));  // >= 8 columns per workgroup
+    if (p.groups < kDim2Blocks) {
+      S = (kDim2Blocks + p.groups - 1) / p.groups;
+      S = kmin<int64_t>(S, kmax<int64_t>(cols / (2 * kColUnrollDefault), 1));
       S = kmin<int64_t>(S, 256);
     }
     p.split = (int)S;
