@@ -57,6 +57,12 @@ typedef enum {
   KF_MAP_ABS2 = 1
 } kf_map;
 
+/* Two-argument element map of kf_reduce2: f(x, y). */
+typedef enum {
+  KF_MAP2_MUL = 0,    /* x * y       (dot product)       */
+  KF_MAP2_SQDIFF = 1  /* (x - y)^2   (squared distance)  */
+} kf_map2;
+
 /* Element types. KF_F32X2 is an interleaved (a, b) pair of float32. */
 typedef enum {
   KF_F32 = 0,
@@ -112,6 +118,19 @@ int kf_reduce(kf_op op, kf_map f, kf_dtype dt,
               const void* src, int64_t n, int64_t stride,
               void* dst, void* scratch, size_t scratch_bytes, void* stream);
 
+/* ------------------------------------------------------------- reduce2 ----
+ * dst[0] = f(x[0], y[0]) op ... op f(x[n-1], y[n-1]) (element strides xs, ys).
+ * The two-array form of the reference's
+ *   mapreduce(f, op, (x, y))  src/mapreduce/mapreduce.jl:228-239 ->
+ *   mapreduce1d(f, op, srcs::NTuple)  src/mapreduce/1D/mapreduce1d.jl:186-204
+ * for the maps x*y and (x-y)^2 (its tests' dot products and distances,
+ * test/tests/mapreduce/mapreduce1d_test.jl:231-319). */
+size_t kf_reduce2_scratch_bytes(kf_dtype dt, int64_t n);
+
+int kf_reduce2(kf_op op, kf_map2 f, kf_dtype dt,
+               const void* x, int64_t x_stride, const void* y, int64_t y_stride, int64_t n,
+               void* dst, void* scratch, size_t scratch_bytes, void* stream);
+
 /* ---------------------------------------------------------- reduce_dim ----
  * A is a column-major rows x cols matrix: A[i, j] at A + i + j*col_stride
  * (col_stride >= rows; col_stride = 2*rows is the view A[:, 1:2:end]).
@@ -130,6 +149,22 @@ int kf_reduce_dim(kf_op op, kf_map f, kf_dtype dt,
                   const void* A, int64_t rows, int64_t cols, int64_t col_stride,
                   int dim, void* dst, int64_t dst_stride,
                   void* scratch, size_t scratch_bytes, void* stream);
+
+/* Batched dim-2 reduction: `batch` column-major rows x cols matrices, the
+ * z-th starting at A + z*batch_stride:
+ *   dst[(i + z*rows) * dst_stride] = op_j f(A[i + j*col_stride + z*batch_stride])
+ * This reduces the middle block of dims of an array viewed as
+ * (pre = rows, mid = cols, post = batch); with it the host reduces any set
+ * of dims one contiguous block at a time. Replaces the reference's general
+ * fallback mapreducedims!(f, op, dst, src, dims)
+ *   src/mapreduce/ND/mapreducedims.jl:90-140 (kernel mapreducedims_kernel.jl:1-23). */
+size_t kf_reduce_dim_batched_scratch_bytes(kf_dtype dt, int64_t rows, int64_t cols, int64_t batch);
+
+int kf_reduce_dim_batched(kf_op op, kf_map f, kf_dtype dt,
+                          const void* A, int64_t rows, int64_t cols, int64_t col_stride,
+                          int64_t batch, int64_t batch_stride,
+                          void* dst, int64_t dst_stride,
+                          void* scratch, size_t scratch_bytes, void* stream);
 
 /* ---------------------------------------------------------------- copy ----
  * dst[0:bytes] = src[0:bytes] with 16-byte streaming loads/stores: the

@@ -36,7 +36,7 @@ import torch
 from . import _lib as _L
 
 __all__ = [
-    "ArgumentError", "KernelBuffer", "AffineOp", "affine", "identity", "abs2",
+    "ArgumentError", "KernelBuffer", "AffineOp", "affine", "identity", "abs2", "sqdiff",
     "scan", "scan_", "mapreduce", "mapreduce_", "get_allocation", "vcopy_",
     "Scan1D", "MapReduce1D", "MapReduce2D",
 ]
@@ -66,6 +66,24 @@ class AffineOp:
 
 
 affine = AffineOp()
+
+
+def sqdiff(a, b):
+    """(a - b)^2: the two-array map of a squared Euclidean distance."""
+    return (a - b) * (a - b)
+
+
+_MAP2 = {"mul": _L.MAP2_MUL, "*": _L.MAP2_MUL, "sqdiff": _L.MAP2_SQDIFF}
+
+
+def _map2_code(f):
+    if f is operator.mul:
+        return _L.MAP2_MUL
+    if f is sqdiff:
+        return _L.MAP2_SQDIFF
+    if isinstance(f, str) and f in _MAP2:
+        return _MAP2[f]
+    raise ArgumentError(f"unsupported two-array map {f!r}: expected operator.mul or sqdiff")
 
 # Allocation kinds (reference src/algorithms.jl:16-31 tags).
 Scan1D, MapReduce1D, MapReduce2D = "Scan1D", "MapReduce1D", "MapReduce2D"
@@ -369,6 +387,8 @@ def mapreduce(f, op, src, dims=None, g=None, tmp=None, **tuning):
     dims=None or ":" -> host scalar; otherwise a tensor with size 1 along the
     reduced dims, laid out column-major. `g` (post-map) is supported for the
     full reduction, where it is applied to the returned scalar."""
+    if isinstance(src, (tuple, list)):
+        return _mapreduce_multi(f, op, src, dims, g, tmp)
     fc, opc = _map_code(f), _op_code(op)
     _require_device(src)
     _check_reducible(src, opc, fc)
@@ -386,6 +406,38 @@ def mapreduce(f, op, src, dims=None, g=None, tmp=None, **tuning):
     dst = _colmajor_empty(out_shape, src.dtype, src.device)
     mapreduce_(f, op, dst, src, dims=dims_t, tmp=tmp)
     return dst
+
+
+def _mapreduce_multi(f, op, srcs, dims, g, tmp):
+    """mapreduce(f, op, (x, y)) (reference src/mapreduce/mapreduce.jl:228-239):
+    full reduction only, f(x, y) = x*y or (x-y)^2, equal-length vectors."""
+    if dims is not None and dims != ":" and dims is not Ellipsis:
+        raise ArgumentError("Multi-array mapreduce only supports full reduction (dims=nothing)")
+    if len(srcs) != 2:
+        raise ArgumentError(f"multi-array mapreduce takes two arrays here, got {len(srcs)}")
+    x, y = srcs
+    fc, opc = _map2_code(f), _op_code(op)
+    _require_device(x, y)
+    if x.dtype != y.dtype or x.dtype not in _DTYPES:
+        raise ArgumentError(f"element types {x.dtype} and {y.dtype}: expected one supported type")
+    if x.dim() != 1 or y.dim() != 1 or x.shape[0] != y.shape[0]:
+        raise ArgumentError("multi-array mapreduce takes vectors of equal length")
+    if opc == _L.OP_AFFINE:
+        raise ArgumentError("mapreduce needs a commutative operator; the affine operator is scan-only")
+    n = x.shape[0]
+    if n == 0:
+        raise ArgumentError("reducing over an empty collection is not allowed")
+    L = _L.lib()
+    dt = _DTYPES[x.dtype]
+    out = torch.empty(1, dtype=x.dtype, device=x.device)
+    buf = _scratch(MapReduce1D, L.kf_reduce2_scratch_bytes(dt, n), x.device, tmp)
+    with torch.cuda.device(x.device):
+        rc = L.kf_reduce2(opc, fc, dt, ctypes_void(x.data_ptr()), x.stride(0) if n > 1 else 1,
+                          ctypes_void(y.data_ptr()), y.stride(0) if n > 1 else 1, n, ctypes_void(out.data_ptr()),
+                          ctypes_void(buf.ptr), buf.nbytes, _stream_ptr(x))
+    _L.check(rc, "mapreduce")
+    val = _to_scalar(out)
+    return g(val) if g is not None else val
 
 
 def mapreduce_(f, op, dst, src, dims=None, g=None, tmp=None, **tuning):
@@ -444,9 +496,67 @@ def mapreduce_(f, op, dst, src, dims=None, g=None, tmp=None, **tuning):
             lead *= s
         _reduce_dim_into(_L.MAP_IDENTITY, opc, dst, dst_stride, mid, lead, rows // lead, lead, 1, tmp)
         return dst
-    raise NotImplementedError(
-        f"dims={dims_t} on a {nd}-d array needs the general-dims kernel (reference mapreducedims), "
-        "which this build does not provide yet")
+    _reduce_dims_general(fc, opc, dst, dst_stride, src, dims_t, tmp)
+    return dst
+
+
+def _blocks_of(dims0):
+    """Contiguous runs [(d0, d1), ...] (0-based, half-open) of sorted dims."""
+    out = []
+    for d in dims0:
+        if out and out[-1][1] == d:
+            out[-1] = (out[-1][0], d + 1)
+        else:
+            out.append((d, d + 1))
+    return out
+
+
+def _reduce_dims_general(fc, opc, dst, dst_stride, src, dims_t, tmp):
+    """Any set of dims: reduce one contiguous block of dims at a time, each
+    block as the middle of a (pre, mid, post) view, with the batched dim-2
+    kernel (or the dim-1 kernel when pre == 1). The reference does this
+    with one thread per output in mapreducedims_kernel!
+    (reference src/mapreduce/ND/mapreducedims_kernel.jl:1-23); the
+    block-by-block form keeps every pass a coalesced streaming reduction.
+    Valid for the commutative operators accepted here."""
+    L = _L.lib()
+    dt = _DTYPES[src.dtype]
+    blocks = _blocks_of([d - 1 for d in dims_t])
+    cur, cur_fc = src, fc
+    for bi, (d0, d1) in enumerate(blocks):
+        shape, strides = list(cur.shape), list(cur.stride())
+        pre_m = _merge(shape[:d0], strides[:d0])
+        mid_m = _merge(shape[d0:d1], strides[d0:d1])
+        post_m = _merge(shape[d1:], strides[d1:])
+        if pre_m is None or mid_m is None or post_m is None or (pre_m[0] > 1 and pre_m[1] != 1):
+            raise NotImplementedError(
+                f"layout with shape {tuple(shape)} and strides {tuple(strides)} cannot be reduced over "
+                f"dims {d0 + 1}..{d1} without a copy")
+        pre, mid, post = pre_m[0], mid_m[0], post_m[0]
+        mid_stride = mid_m[1] if mid > 1 else max(pre, 1)
+        post_stride = post_m[1] if post > 1 else 0
+        last = bi == len(blocks) - 1
+        out_shape = [1 if d0 <= i < d1 else v for i, v in enumerate(shape)]
+        if last:
+            out, out_stride = dst, dst_stride
+        else:
+            out, out_stride = _colmajor_empty(out_shape, src.dtype, src.device), 1
+        with torch.cuda.device(src.device):
+            if pre == 1 and mid_stride == 1:
+                # leading block of a (mid, post) matrix: dim-1 kernel
+                need = L.kf_reduce_dim_scratch_bytes(dt, mid, post, 1)
+                buf = _scratch(MapReduce2D, need, src.device, tmp)
+                rc = L.kf_reduce_dim(opc, cur_fc, dt, ctypes_void(cur.data_ptr()), mid, post,
+                                     post_stride if post > 1 else mid, 1, ctypes_void(out.data_ptr()), out_stride,
+                                     ctypes_void(buf.ptr), buf.nbytes, _stream_ptr(src))
+            else:
+                need = L.kf_reduce_dim_batched_scratch_bytes(dt, pre, mid, post)
+                buf = _scratch(MapReduce2D, need, src.device, tmp)
+                rc = L.kf_reduce_dim_batched(opc, cur_fc, dt, ctypes_void(cur.data_ptr()), pre, mid, mid_stride,
+                                             post, post_stride, ctypes_void(out.data_ptr()), out_stride,
+                                             ctypes_void(buf.ptr), buf.nbytes, _stream_ptr(src))
+        _L.check(rc, f"mapreduce(dims={dims_t})")
+        cur, cur_fc = out if not last else None, _L.MAP_IDENTITY
 
 
 def get_allocation(kind, f, op, src, *args, **kwargs):

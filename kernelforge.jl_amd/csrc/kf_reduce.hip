@@ -188,12 +188,15 @@ __global__ __launch_bounds__(kCombineBlock) void combine_all_kernel(const T* par
   }
 }
 
-// Stage 2 of the split dims reductions: out[i*ds] = op_s partials[s*m + i].
+// Stage 2 of the split dims reductions: out[i*ds] = op_s partials[s*m + i],
+// for batch z = blockIdx.y: partials at z*S*m, outputs at z*dst_bstride.
 template <class T, class Op>
 __global__ __launch_bounds__(kRedBlock) void combine_split_kernel(const T* partials, int S, int64_t m, T* dst,
-                                                                  int64_t ds) {
+                                                                  int64_t ds, int64_t dst_bstride) {
   const int64_t i = (int64_t)blockIdx.x * kRedBlock + threadIdx.x;
   if (i >= m) return;
+  partials += (int64_t)blockIdx.y * S * m;
+  dst += (int64_t)blockIdx.y * dst_bstride;
   T x = partials[i];
   for (int s = 1; s < S; ++s) x = Op::combine(x, partials[(int64_t)s * m + i]);
   dst[i * ds] = x;
@@ -276,6 +279,113 @@ int launch_reduce(const void* src, int64_t n, int64_t stride, void* dst, void* s
 }
 
 // ---------------------------------------------------------------------------
+// Two-array full reduction: dst = op_i f2(x[i], y[i]) with f2 = x*y (dot
+// product) or (x-y)^2 (squared distance). Level 0 reads both arrays
+// (one-shot when both are 16-byte aligned and contiguous, grid-stride
+// otherwise); later levels reuse the partial reduction above.
+// ---------------------------------------------------------------------------
+struct Map2Mul {
+  template <class T> __device__ static T apply(T a, T b) { return a * b; }
+  __device__ static int32_t apply(int32_t a, int32_t b) { return (int32_t)((uint32_t)a * (uint32_t)b); }
+  __device__ static int64_t apply(int64_t a, int64_t b) { return (int64_t)((uint64_t)a * (uint64_t)b); }
+  __device__ static uint8_t apply(uint8_t a, uint8_t b) { return (uint8_t)(a * b); }
+};
+struct Map2SqDiff {
+  template <class T> __device__ static T apply(T a, T b) { const T d = a - b; return d * d; }
+  __device__ static int32_t apply(int32_t a, int32_t b) {
+    const uint32_t d = (uint32_t)a - (uint32_t)b;
+    return (int32_t)(d * d);
+  }
+  __device__ static int64_t apply(int64_t a, int64_t b) {
+    const uint64_t d = (uint64_t)a - (uint64_t)b;
+    return (int64_t)(d * d);
+  }
+  __device__ static uint8_t apply(uint8_t a, uint8_t b) { const uint8_t d = (uint8_t)(a - b); return (uint8_t)(d * d); }
+};
+
+template <class T, class Op, class M2>
+__global__ __launch_bounds__(kRedBlock) void reduce2_once_kernel(const T* x, const T* y, int64_t n, T* out) {
+  constexpr int EPV = 16 / (int)sizeof(T);
+  __shared__ T s_wave[kRedWaves];
+  const T id = Op::template identity<T>();
+  const int tid = threadIdx.x;
+  const int64_t nvec = n / EPV;
+  const uint4* vx = reinterpret_cast<const uint4*>(x);
+  const uint4* vy = reinterpret_cast<const uint4*>(y);
+  const int64_t base = (int64_t)blockIdx.x * kOnceVecs + tid;
+  uint4 rx[kOnceUnroll], ry[kOnceUnroll];
+#pragma unroll
+  for (int u = 0; u < kOnceUnroll; ++u)
+    if (base + u * kRedBlock < nvec) {
+      rx[u] = ld_stream(vx + base + u * kRedBlock);
+      ry[u] = ld_stream(vy + base + u * kRedBlock);
+    }
+  T a[EPV];
+#pragma unroll
+  for (int e = 0; e < EPV; ++e) a[e] = id;
+#pragma unroll
+  for (int u = 0; u < kOnceUnroll; ++u)
+    if (base + u * kRedBlock < nvec) {
+      T p[EPV], q[EPV];
+      __builtin_memcpy(p, &rx[u], 16);
+      __builtin_memcpy(q, &ry[u], 16);
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) a[e] = Op::combine(a[e], M2::apply(p[e], q[e]));
+    }
+  T acc = a[0];
+#pragma unroll
+  for (int e = 1; e < EPV; ++e) acc = Op::combine(acc, a[e]);
+  if (blockIdx.x == 0 && nvec * EPV + tid < n) acc = Op::combine(acc, M2::apply(x[nvec * EPV + tid], y[nvec * EPV + tid]));
+  const T part = block_reduce<T, Op>(acc, s_wave);
+  if (tid == 0) out[blockIdx.x] = part;
+}
+
+template <class T, class Op, class M2>
+__global__ __launch_bounds__(kRedBlock) void reduce2_kernel(const T* x, int64_t xs, const T* y, int64_t ys, int64_t n,
+                                                            T* out) {
+  __shared__ T s_wave[kRedWaves];
+  T acc = Op::template identity<T>();
+  const int64_t gsize = (int64_t)gridDim.x * kRedBlock;
+  for (int64_t i = (int64_t)blockIdx.x * kRedBlock + threadIdx.x; i < n; i += gsize)
+    acc = Op::combine(acc, M2::apply(x[i * xs], y[i * ys]));
+  const T part = block_reduce<T, Op>(acc, s_wave);
+  if (threadIdx.x == 0) out[blockIdx.x] = part;
+}
+
+template <class T, class Op, class M2>
+int launch_reduce2(const void* x, int64_t xs, const void* y, int64_t ys, int64_t n, void* dst, void* scratch,
+                   hipStream_t stream) {
+  constexpr int EPV = 16 / (int)sizeof(T);
+  const bool vec = xs == 1 && ys == 1 && (uintptr_t)x % 16 == 0 && (uintptr_t)y % 16 == 0;
+  if (!vec) {
+    const int grid = reduce_grid<T>(n);
+    T* out = grid == 1 ? (T*)dst : (T*)scratch;
+    hipLaunchKernelGGL((reduce2_kernel<T, Op, M2>), dim3(grid), dim3(kRedBlock), 0, stream, (const T*)x, xs,
+                       (const T*)y, ys, n, out);
+    if (grid > 1)
+      hipLaunchKernelGGL((combine_all_kernel<T, Op>), dim3(1), dim3(kCombineBlock), 0, stream,
+                         (const T*)scratch, grid, (T*)dst);
+    return kf_check_launch("reduce2_kernel");
+  }
+  const OnceLevels L = once_levels(n / EPV, EPV);
+  size_t abytes = 0;
+  for (int i = 0; i < L.nlev; i += 2) abytes = kmax(abytes, round256((size_t)L.count[i] * sizeof(T) + 16));
+  T* buf[2] = {(T*)scratch, (T*)((uint8_t*)scratch + abytes)};
+  T* out0 = (L.nlev == 1 && L.count[0] == 1) ? (T*)dst : buf[0];
+  hipLaunchKernelGGL((reduce2_once_kernel<T, Op, M2>), dim3((unsigned)L.count[0]), dim3(kRedBlock), 0, stream,
+                     (const T*)x, (const T*)y, n, out0);
+  for (int i = 1; i < L.nlev; ++i) {
+    const int64_t m = L.count[i - 1];
+    hipLaunchKernelGGL((reduce_once_kernel<T, Op, MapIdentity>), dim3((unsigned)L.count[i]), dim3(kRedBlock), 0,
+                       stream, (const T*)buf[(i - 1) % 2], m, (int64_t)0, m / EPV, buf[i % 2]);
+  }
+  if (out0 != (T*)dst)
+    hipLaunchKernelGGL((combine_all_kernel<T, Op>), dim3(1), dim3(kCombineBlock), 0, stream,
+                       (const T*)buf[(L.nlev - 1) % 2], (int)L.count[L.nlev - 1], (T*)dst);
+  return kf_check_launch("reduce2_once_kernel");
+}
+
+// ---------------------------------------------------------------------------
 // dim = 1: one wave per column (a column of a column-major matrix is
 // contiguous), optionally split into S row segments when there are too few
 // columns to fill the GPU.
@@ -355,8 +465,12 @@ __global__ __launch_bounds__(kDimBlock) void reduce_cols_kernel(
 // ---------------------------------------------------------------------------
 template <class T, class Op, class Map, bool VEC, int kRowVecs = kRowVecsDefault, int kColUnroll = kColUnrollDefault>
 __global__ __launch_bounds__(kDimBlock) void reduce_rows_kernel(
-    const T* A, int64_t rows, int64_t cols, int64_t col_stride, T* out, int64_t out_stride, int64_t seg_cols) {
+    const T* A, int64_t rows, int64_t cols, int64_t col_stride, T* out, int64_t out_stride, int64_t seg_cols,
+    int64_t a_bstride, int64_t out_bstride) {
   constexpr int EPV = VEC ? 16 / (int)sizeof(T) : 1;
+  // batch z = blockIdx.z: one (rows x cols) matrix per batch entry
+  A += (int64_t)blockIdx.z * a_bstride;
+  out += gridDim.y == 1 ? (int64_t)blockIdx.z * out_bstride : (int64_t)blockIdx.z * gridDim.y * rows;
   constexpr int RS = kDimBlock * kRowVecs * EPV;
   const T id = Op::template identity<T>();
   const int tid = threadIdx.x;
@@ -429,7 +543,10 @@ struct DimPlan {
 
 // Launch plan; a pure function of (element size, shape, dim, alignment) so
 // the scratch query and the launch agree.
-inline DimPlan plan_dim(size_t es, int64_t rows, int64_t cols, int dim, bool vec) {
+constexpr int64_t kMaxBatchPerLaunch = 65535;  // grid.z limit
+
+inline DimPlan plan_dim(size_t es, int64_t rows, int64_t cols, int dim, bool vec, int64_t batch = 1) {
+  const int64_t nb = kmin<int64_t>(kmax<int64_t>(batch, 1), kMaxBatchPerLaunch);
   DimPlan p{};
   const int epv = vec ? (int)(16 / es) : 1;
   if (dim == 1) {
@@ -449,14 +566,14 @@ inline DimPlan plan_dim(size_t es, int64_t rows, int64_t cols, int dim, bool vec
     // workgroups with more split partials (65536 x 4096 Float32: 6.6 TB/s at
     // 256 workgroups, 5.4 TB/s at 1024 with 4 loads per thread).
     int64_t S = 1;
-    if (p.groups < kDim2Blocks) {
-      S = (kDim2Blocks + p.groups - 1) / p.groups;
+    if (p.groups * nb < kDim2Blocks) {
+      S = (kDim2Blocks + p.groups * nb - 1) / (p.groups * nb);
       S = kmin<int64_t>(S, kmax<int64_t>(cols / (2 * kColUnrollDefault), 1));
       S = kmin<int64_t>(S, 256);
     }
     p.split = (int)S;
   }
-  if (p.split > 1) p.partial_bytes = round256((size_t)p.split * (size_t)(dim == 1 ? cols : rows) * es);
+  if (p.split > 1) p.partial_bytes = round256((size_t)p.split * (size_t)(dim == 1 ? cols : rows) * es * (size_t)nb);
   return p;
 }
 
@@ -466,31 +583,41 @@ inline bool dim_vec_ok(const void* A, int64_t cs, size_t es) {
 
 template <class T, class Op, class Map>
 int launch_reduce_dim(const void* A, int64_t rows, int64_t cols, int64_t cs, int dim, void* dst,
-                      int64_t ds, void* scratch, hipStream_t stream) {
-  const bool vec = dim_vec_ok(A, cs, sizeof(T));
-  const DimPlan p = plan_dim(sizeof(T), rows, cols, dim, vec);
-  T* out = p.split > 1 ? (T*)scratch : (T*)dst;
+                      int64_t ds, void* scratch, hipStream_t stream, int64_t batch = 1, int64_t a_bstride = 0) {
+  const bool vec = dim_vec_ok(A, cs, sizeof(T)) && (batch == 1 || (a_bstride * (int64_t)sizeof(T)) % 16 == 0);
+  const DimPlan p = plan_dim(sizeof(T), rows, cols, dim, vec, batch);
   if (dim == 1) {
+    T* out = p.split > 1 ? (T*)scratch : (T*)dst;
     constexpr int EPV = 16 / (int)sizeof(T);
     int64_t seg = (rows + p.split - 1) / p.split;
     seg = (seg + EPV - 1) / EPV * EPV;
     hipLaunchKernelGGL((reduce_cols_kernel<T, Op, Map>), dim3((unsigned)p.groups, p.split), dim3(kDimBlock), 0,
                        stream, (const T*)A, rows, cols, cs, out, ds, seg, (int)vec);
-  } else {
-    const int64_t seg = (cols + p.split - 1) / p.split;
+    if (p.split > 1)
+      hipLaunchKernelGGL((combine_split_kernel<T, Op>), dim3((unsigned)((cols + kRedBlock - 1) / kRedBlock), 1),
+                         dim3(kRedBlock), 0, stream, (const T*)scratch, p.split, cols, (T*)dst, ds, (int64_t)0);
+    return kf_check_launch("reduce_cols_kernel");
+  }
+  // dim 2, batched: dst[(i + z*rows)*ds] = op_j f(A[i + j*cs + z*a_bstride])
+  const int64_t seg = (cols + p.split - 1) / p.split;
+  const int64_t dst_bstride = rows * ds;
+  for (int64_t z0 = 0; z0 < batch; z0 += kMaxBatchPerLaunch) {
+    const unsigned nz = (unsigned)kmin<int64_t>(kMaxBatchPerLaunch, batch - z0);
+    const T* Az = (const T*)A + z0 * a_bstride;
+    T* dz = (T*)dst + z0 * dst_bstride;
+    T* out = p.split > 1 ? (T*)scratch : dz;
+    const dim3 grid((unsigned)p.groups, p.split, nz);
     if (vec)
-      hipLaunchKernelGGL((reduce_rows_kernel<T, Op, Map, true>), dim3((unsigned)p.groups, p.split), dim3(kDimBlock),
-                         0, stream, (const T*)A, rows, cols, cs, out, ds, seg);
+      hipLaunchKernelGGL((reduce_rows_kernel<T, Op, Map, true>), grid, dim3(kDimBlock), 0, stream, Az, rows, cols, cs,
+                         out, ds, seg, a_bstride, dst_bstride);
     else
-      hipLaunchKernelGGL((reduce_rows_kernel<T, Op, Map, false>), dim3((unsigned)p.groups, p.split),
-                         dim3(kDimBlock), 0, stream, (const T*)A, rows, cols, cs, out, ds, seg);
+      hipLaunchKernelGGL((reduce_rows_kernel<T, Op, Map, false>), grid, dim3(kDimBlock), 0, stream, Az, rows, cols,
+                         cs, out, ds, seg, a_bstride, dst_bstride);
+    if (p.split > 1)
+      hipLaunchKernelGGL((combine_split_kernel<T, Op>), dim3((unsigned)((rows + kRedBlock - 1) / kRedBlock), nz),
+                         dim3(kRedBlock), 0, stream, (const T*)scratch, p.split, rows, dz, ds, dst_bstride);
   }
-  if (p.split > 1) {
-    const int64_t m = dim == 1 ? cols : rows;
-    hipLaunchKernelGGL((combine_split_kernel<T, Op>), dim3((unsigned)((m + kRedBlock - 1) / kRedBlock)),
-                       dim3(kRedBlock), 0, stream, (const T*)scratch, p.split, m, (T*)dst, ds);
-  }
-  return kf_check_launch(dim == 1 ? "reduce_cols_kernel" : "reduce_rows_kernel");
+  return kf_check_launch("reduce_rows_kernel");
 }
 
 // ---------------------------------------------------------------------------
@@ -529,10 +656,16 @@ template <class T, class Op, class Map> struct ReduceL {
     return launch_reduce<T, Op, Map>(src, n, stride, dst, scratch, s);
   }
 };
+template <class T, class Op, class Map2> struct Reduce2L {
+  static int run(const void* x, int64_t xs, const void* y, int64_t ys, int64_t n, void* dst, void* scratch,
+                 hipStream_t s) {
+    return launch_reduce2<T, Op, Map2>(x, xs, y, ys, n, dst, scratch, s);
+  }
+};
 template <class T, class Op, class Map> struct ReduceDimL {
   static int run(const void* A, int64_t rows, int64_t cols, int64_t cs, int dim, void* dst, int64_t ds,
-                 void* scratch, hipStream_t s) {
-    return launch_reduce_dim<T, Op, Map>(A, rows, cols, cs, dim, dst, ds, scratch, s);
+                 void* scratch, hipStream_t s, int64_t batch, int64_t a_bstride) {
+    return launch_reduce_dim<T, Op, Map>(A, rows, cols, cs, dim, dst, ds, scratch, s, batch, a_bstride);
   }
 };
 
@@ -587,6 +720,51 @@ extern "C" int kf_reduce(kf_op op, kf_map f, kf_dtype dt, const void* src, int64
   return dispatch_all<ReduceL>(dt, op, f, src, n, stride, dst, scratch, (hipStream_t)stream);
 }
 
+extern "C" size_t kf_reduce2_scratch_bytes(kf_dtype dt, int64_t n) { return kf_reduce_scratch_bytes(dt, n); }
+
+template <class T, class... A> int dispatch_reduce2(kf_op op, kf_map2 f, A... args) {
+  if (f == KF_MAP2_SQDIFF) {
+    switch (op) {
+      case KF_OP_ADD: return Reduce2L<T, OpAdd, Map2SqDiff>::run(args...);
+      case KF_OP_MAX: return Reduce2L<T, OpMax, Map2SqDiff>::run(args...);
+      default: return Reduce2L<T, OpMin, Map2SqDiff>::run(args...);
+    }
+  }
+  switch (op) {
+    case KF_OP_ADD: return Reduce2L<T, OpAdd, Map2Mul>::run(args...);
+    case KF_OP_MAX: return Reduce2L<T, OpMax, Map2Mul>::run(args...);
+    default: return Reduce2L<T, OpMin, Map2Mul>::run(args...);
+  }
+}
+
+extern "C" int kf_reduce2(kf_op op, kf_map2 f, kf_dtype dt, const void* x, int64_t x_stride, const void* y,
+                          int64_t y_stride, int64_t n, void* dst, void* scratch, size_t scratch_bytes, void* stream) {
+  int rc = kf_validate_op(op, KF_MAP_IDENTITY, dt, /*allow_affine=*/0);
+  if (rc) return rc;
+  if (f != KF_MAP2_MUL && f != KF_MAP2_SQDIFF) return kf_set_error(KF_EINVAL, "kf_reduce2: unknown map %d", (int)f);
+  if (n < 0) return kf_set_error(KF_EINVAL, "kf_reduce2: n = %lld < 0", (long long)n);
+  if (n == 0) return KF_OK;
+  if (!x || !y || !dst) return kf_set_error(KF_EINVAL, "kf_reduce2: null pointer");
+  if (x_stride < 1 || y_stride < 1) return kf_set_error(KF_EINVAL, "kf_reduce2: strides must be >= 1");
+  const size_t es = kf_dtype_size(dt);
+  if ((uintptr_t)x % es || (uintptr_t)y % es || (uintptr_t)dst % es)
+    return kf_set_error(KF_EINVAL, "kf_reduce2: pointers not aligned to the element type");
+  const size_t need = kf_reduce2_scratch_bytes(dt, n);
+  if (!scratch || scratch_bytes < need)
+    return kf_set_error(KF_ENOSCRATCH, "kf_reduce2: scratch of %zu bytes needed, %zu given", need,
+                        scratch ? scratch_bytes : (size_t)0);
+  if ((uintptr_t)scratch % 256) return kf_set_error(KF_EINVAL, "kf_reduce2: scratch must be 256-byte aligned");
+  hipStream_t s = (hipStream_t)stream;
+  switch (dt) {
+    case KF_F32: return dispatch_reduce2<float>(op, f, x, x_stride, y, y_stride, n, dst, scratch, s);
+    case KF_F64: return dispatch_reduce2<double>(op, f, x, x_stride, y, y_stride, n, dst, scratch, s);
+    case KF_I32: return dispatch_reduce2<int32_t>(op, f, x, x_stride, y, y_stride, n, dst, scratch, s);
+    case KF_I64: return dispatch_reduce2<int64_t>(op, f, x, x_stride, y, y_stride, n, dst, scratch, s);
+    case KF_U8: return dispatch_reduce2<uint8_t>(op, f, x, x_stride, y, y_stride, n, dst, scratch, s);
+    default: return kf_set_error(KF_EINVAL, "kf_reduce2: bad dtype %d", (int)dt);
+  }
+}
+
 extern "C" size_t kf_reduce_dim_scratch_bytes(kf_dtype dt, int64_t rows, int64_t cols, int dim) {
   const size_t es = kf_dtype_size(dt);
   if (es == 0 || rows <= 0 || cols <= 0 || (dim != 1 && dim != 2)) return 256;
@@ -623,7 +801,45 @@ extern "C" int kf_reduce_dim(kf_op op, kf_map f, kf_dtype dt, const void* A, int
   }
   if (p.groups > 0x7fffffffLL) return kf_set_error(KF_EINVAL, "kf_reduce_dim: shape exceeds the grid limit");
   return dispatch_all<ReduceDimL>(dt, op, f, A, rows, cols, col_stride, dim, dst, dst_stride, scratch,
-                                  (hipStream_t)stream);
+                                  (hipStream_t)stream, (int64_t)1, (int64_t)0);
+}
+
+extern "C" size_t kf_reduce_dim_batched_scratch_bytes(kf_dtype dt, int64_t rows, int64_t cols, int64_t batch) {
+  const size_t es = kf_dtype_size(dt);
+  if (es == 0 || rows <= 0 || cols <= 0 || batch <= 0) return 256;
+  const DimPlan pv = plan_dim(es, rows, cols, 2, true, batch), ps = plan_dim(es, rows, cols, 2, false, batch);
+  return kmax<size_t>(256, kmax<size_t>(pv.partial_bytes, ps.partial_bytes));
+}
+
+extern "C" int kf_reduce_dim_batched(kf_op op, kf_map f, kf_dtype dt, const void* A, int64_t rows, int64_t cols,
+                                     int64_t col_stride, int64_t batch, int64_t batch_stride, void* dst,
+                                     int64_t dst_stride, void* scratch, size_t scratch_bytes, void* stream) {
+  int rc = kf_validate_op(op, f, dt, /*allow_affine=*/0);
+  if (rc) return rc;
+  if (rows < 0 || cols < 0 || batch < 0) return kf_set_error(KF_EINVAL, "kf_reduce_dim_batched: negative shape");
+  if (rows == 0 || batch == 0) return KF_OK;
+  if (cols == 0)
+    return kf_set_error(KF_EINVAL, "kf_reduce_dim_batched: reducing an empty dimension has no identity-free result");
+  if (!A || !dst) return kf_set_error(KF_EINVAL, "kf_reduce_dim_batched: null A or dst");
+  if (col_stride < rows) return kf_set_error(KF_EINVAL, "kf_reduce_dim_batched: col_stride < rows");
+  if (batch > 1 && batch_stride < 1) return kf_set_error(KF_EINVAL, "kf_reduce_dim_batched: batch_stride < 1");
+  if (dst_stride < 1) return kf_set_error(KF_EINVAL, "kf_reduce_dim_batched: dst_stride must be >= 1");
+  const size_t es = kf_dtype_size(dt);
+  if ((uintptr_t)A % es || (uintptr_t)dst % es)
+    return kf_set_error(KF_EINVAL, "kf_reduce_dim_batched: A/dst not aligned to the element type");
+  const bool vec = dim_vec_ok(A, col_stride, es) && (batch == 1 || (batch_stride * (int64_t)es) % 16 == 0);
+  const DimPlan p = plan_dim(es, rows, cols, 2, vec, batch);
+  if (p.split > 1) {
+    const size_t need = kf_reduce_dim_batched_scratch_bytes(dt, rows, cols, batch);
+    if (!scratch || scratch_bytes < need)
+      return kf_set_error(KF_ENOSCRATCH, "kf_reduce_dim_batched: scratch of %zu bytes needed, %zu given", need,
+                          scratch ? scratch_bytes : (size_t)0);
+    if ((uintptr_t)scratch % 256)
+      return kf_set_error(KF_EINVAL, "kf_reduce_dim_batched: scratch must be 256-byte aligned");
+  }
+  if (p.groups > 0x7fffffffLL) return kf_set_error(KF_EINVAL, "kf_reduce_dim_batched: shape exceeds the grid limit");
+  return dispatch_all<ReduceDimL>(dt, op, f, A, rows, cols, col_stride, 2, dst, dst_stride, scratch,
+                                  (hipStream_t)stream, batch, batch_stride);
 }
 
 extern "C" int kf_copy(void* dst, const void* src, size_t bytes, void* stream) {

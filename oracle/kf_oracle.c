@@ -169,6 +169,34 @@ void kfo_reduce_i(const void* src, int dt, int64_t n, int64_t stride, int op, in
   istore(out, dt, 0, acc);
 }
 
+/* Two-array reduction: f2 = 0 -> x*y, 1 -> (x-y)^2 (the reference's
+ * mapreduce(f, op, (x, y)), src/mapreduce/1D/mapreduce1d.jl:186-204). */
+double kfo_reduce2_f(const void* x, const void* y, int dt, int64_t n, int op, int f2) {
+  double acc = 0.0;
+  for (int64_t i = 0; i < n; ++i) {
+    const double a = fload(x, dt, i, 0), b = fload(y, dt, i, 0);
+    const double v = f2 ? (a - b) * (a - b) : a * b;
+    acc = i == 0 ? v : fop(op, acc, v);
+  }
+  return acc;
+}
+
+void kfo_reduce2_i(const void* x, const void* y, int dt, int64_t n, int op, int f2, void* out) {
+  uint64_t acc = 0;
+  for (int64_t i = 0; i < n; ++i) {
+    const uint64_t a = iload(x, dt, i, 0), b = iload(y, dt, i, 0);
+    uint64_t v;
+    if (f2) {
+      const uint64_t d = wrap(dt, a - b);
+      v = wrap(dt, d * d);
+    } else {
+      v = wrap(dt, a * b);
+    }
+    acc = i == 0 ? v : iop(dt, op, acc, v);
+  }
+  istore(out, dt, 0, acc);
+}
+
 /* Column-major A[i, j] = A[i + j*col_stride]. dim 1 -> cols outputs, dim 2
  * -> rows outputs (reference src/mapreduce/2D/mapreduce2d.jl:49-64). */
 void kfo_reduce_dim_f(const void* A, int dt, int64_t rows, int64_t cols, int64_t col_stride, int dim, int op,

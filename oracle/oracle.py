@@ -44,6 +44,9 @@ def lib():
         L.kfo_reduce_f.argtypes = [P, I, I64, I64, I, I]
         L.kfo_reduce_f.restype = D
         L.kfo_reduce_i.argtypes = [P, I, I64, I64, I, I, P]
+        L.kfo_reduce2_f.argtypes = [P, P, I, I64, I, I]
+        L.kfo_reduce2_f.restype = D
+        L.kfo_reduce2_i.argtypes = [P, P, I, I64, I, I, P]
         L.kfo_reduce_dim_f.argtypes = [P, I, I64, I64, I64, I, I, I, P]
         L.kfo_reduce_dim_i.argtypes = [P, I, I64, I64, I64, I, I, I, P]
         L.kfb_scan_add_f32_seq.argtypes = [P, P, I64]
@@ -93,6 +96,19 @@ def reduce(x, op="+", f="identity"):
         return L.kfo_reduce_f(_p(x), DT[x.dtype], x.shape[0], 1, OPS[op], MAPS[f])
     out = np.empty(1, x.dtype)
     L.kfo_reduce_i(_p(x), DT[x.dtype], x.shape[0], 1, OPS[op], MAPS[f], _p(out))
+    return out[0]
+
+
+def reduce2(x, y, op="+", f2="mul"):
+    """Base.mapreduce(f2, op, x, y) for f2 in {"mul": x*y, "sqdiff": (x-y)^2}."""
+    L = lib()
+    x, y = np.ascontiguousarray(x), np.ascontiguousarray(y)
+    assert x.dtype == y.dtype and x.shape == y.shape and x.ndim == 1
+    code = {"mul": 0, "sqdiff": 1}[f2]
+    if _is_float(x):
+        return L.kfo_reduce2_f(_p(x), _p(y), DT[x.dtype], x.shape[0], OPS[op], code)
+    out = np.empty(1, x.dtype)
+    L.kfo_reduce2_i(_p(x), _p(y), DT[x.dtype], x.shape[0], OPS[op], code, _p(out))
     return out[0]
 
 

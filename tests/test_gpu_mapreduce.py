@@ -182,8 +182,8 @@ def test_dims_errors(kf, dev):
         kf.mapreduce(kf.identity, "+", x, dims=(1, 1))
     with pytest.raises(kf.ArgumentError):
         kf.mapreduce(kf.identity, kf.affine, x)
-    with pytest.raises(NotImplementedError):
-        kf.mapreduce(kf.identity, "+", torch.zeros(2, 3, 4, device=dev).permute(2, 1, 0), dims=2)
+    with pytest.raises(kf.ArgumentError):
+        kf.mapreduce(kf.identity, "+", (x, x), dims=1)   # multi-array: full reduction only
 
 
 # ---- BASELINE.json configurations at full size -------------------------------
@@ -246,3 +246,70 @@ def test_multilevel_full_reduce_exact(kf, oracle, dev, dt):
             v = x[off:off + n]
             for op in ("+", "max"):
                 assert kf.mapreduce(kf.identity, op, t[off:off + n]) == int(oracle.reduce(v, op)), (n, off, op)
+
+
+@pytest.mark.parametrize("shape,dims", [
+    ((8, 5, 6), 2),                  # middle dim (the reference's mapreducedims fallback)
+    ((4, 5, 6, 7), (2, 3)),          # middle block
+    ((4, 5, 6, 7, 3), (2, 4)),       # two separate blocks, neither at an end
+    ((3, 4, 5, 6, 7), (1, 3, 5)),    # three blocks
+    ((64, 33, 40), 2),               # larger middle reduction (vector path, splits)
+    ((1000, 7, 3), 2),
+    ((5, 1, 4), 2),                  # size-1 reduced dim
+])
+@pytest.mark.parametrize("dt", [np.float64, np.int32])
+def test_general_dims(kf, dev, shape, dims, dt):
+    # reference test/tests/mapreduce/mapreducedims_test.jl: any dims set
+    rng = np.random.default_rng(53)
+    a = (rng.integers(-50, 50, shape[::-1]) if dt == np.int32 else rng.standard_normal(shape[::-1])).astype(dt)
+    x = torch.from_numpy(a).to(dev).permute(*reversed(range(len(shape))))   # Julia-shaped, column-major
+    d = (dims,) if isinstance(dims, int) else dims
+    axes = tuple(k - 1 for k in d)
+    xn = x.cpu().numpy()
+    for f, op, ref in (("identity", "+", xn.sum(axis=axes, keepdims=True)),
+                       ("abs2", "+", (xn * xn).sum(axis=axes, keepdims=True)),
+                       ("identity", "max", xn.max(axis=axes, keepdims=True))):
+        got = kf.mapreduce(fmap(kf, f), op, x, dims=dims)
+        assert tuple(got.shape) == ref.shape
+        if dt == np.int32:
+            assert np.array_equal(got.cpu().numpy(), ref.astype(np.int32)), (f, op)
+        else:
+            np.testing.assert_allclose(got.cpu().numpy(), ref, rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("dt", [np.float32, np.float64, np.int32, np.int64, np.uint8])
+def test_two_array_mapreduce(kf, oracle, dev, dt):
+    # reference test/tests/mapreduce/mapreduce1d_test.jl:231-319 (dot products,
+    # distances, g = sqrt); exact for integers, rtol * sum|f| for floats
+    import operator
+    rng = np.random.default_rng(59)
+    for n in (1, 7, 33, 4097, 100_003, (1 << 22) + 5):
+        x, y = gen(rng, dt, n), gen(rng, dt, n)
+        tx, ty = torch.from_numpy(x).to(dev), torch.from_numpy(y).to(dev)
+        for f, name in ((operator.mul, "mul"), (kf.sqdiff, "sqdiff")):
+            for op in ("+", "max"):
+                got = kf.mapreduce(f, op, (tx, ty))
+                ref = oracle.reduce2(x, y, op, name)
+                if np.dtype(dt).kind == "f" and op == "+":
+                    xf, yf = x.astype(np.float64), y.astype(np.float64)
+                    bound = np.sum(np.abs(xf * yf) if name == "mul" else (xf - yf) ** 2)
+                    tol = 1e-6 if dt == np.float32 else 1e-12
+                    assert abs(got - ref) <= tol * bound + 1e-300, (n, name, got, ref)
+                elif np.dtype(dt).kind == "f" and name == "mul":
+                    assert dt(got) == dt(ref), (n, name, op)   # one rounding: exact
+                elif np.dtype(dt).kind == "f":
+                    # (x-y)^2 rounds twice in the element type, once in the oracle
+                    assert got == pytest.approx(ref, rel=1e-6 if dt == np.float32 else 1e-15), (n, name, op)
+                else:
+                    assert got == int(ref), (n, name, op)
+        # strided / unaligned operands take the scalar path
+        if n > 8:
+            got = kf.mapreduce(operator.mul, "+", (tx[1::2], ty[:-1:2]))
+            ref = oracle.reduce2(x[1::2], y[:-1:2], "+", "mul")
+            if np.dtype(dt).kind != "f":
+                assert got == int(ref)
+    # g = sqrt: Euclidean distance
+    x = rng.random(15_000)
+    y = rng.random(15_000)
+    d = kf.mapreduce(kf.sqdiff, "+", (torch.from_numpy(x).to(dev), torch.from_numpy(y).to(dev)), g=np.sqrt)
+    assert d == pytest.approx(np.sqrt(np.sum((x - y) ** 2)), rel=1e-12)

@@ -169,3 +169,18 @@ def test_cpu_baseline_agrees(oracle):
     s = oracle.reduce(x)
     assert abs(oracle.baseline_sum_f32(x, 1) - s) <= 1e-4 * s
     assert abs(oracle.baseline_sum_f32(x, 4) - s) <= 1e-4 * s
+
+
+def test_reduce2_matches_numpy_and_closed_forms(oracle):
+    rng = np.random.default_rng(6)
+    x = rng.standard_normal(10_000)
+    y = rng.standard_normal(10_000)
+    np.testing.assert_allclose(oracle.reduce2(x, y), np.dot(x, y), rtol=1e-12)
+    np.testing.assert_allclose(oracle.reduce2(x, y, "+", "sqdiff"), np.sum((x - y) ** 2), rtol=1e-12)
+    assert oracle.reduce2(x, y, "max") == np.max(x * y)
+    n = 1000
+    r = np.arange(1, n + 1, dtype=np.int64)
+    assert oracle.reduce2(r, r) == n * (n + 1) * (2 * n + 1) // 6          # sum of squares
+    assert oracle.reduce2(r, r - 1, "+", "sqdiff") == n                     # unit differences
+    i = np.array([2**16, 3], np.int32)
+    assert oracle.reduce2(i, i) == np.int32(9)                              # 2^32 wraps to 0
