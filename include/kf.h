@@ -57,6 +57,13 @@ typedef enum {
   KF_MAP_ABS2 = 1
 } kf_map;
 
+/* Post-map `g` applied to results (the reference's `g` keyword). */
+typedef enum {
+  KF_POST_IDENTITY = 0,
+  KF_POST_SQRT = 1,   /* floating-point types only */
+  KF_POST_ABS2 = 2
+} kf_post;
+
 /* Two-argument element map of kf_reduce2: f(x, y). */
 typedef enum {
   KF_MAP2_MUL = 0,    /* x * y       (dot product)       */
@@ -165,6 +172,12 @@ int kf_reduce_dim_batched(kf_op op, kf_map f, kf_dtype dt,
                           int64_t batch, int64_t batch_stride,
                           void* dst, int64_t dst_stride,
                           void* scratch, size_t scratch_bytes, void* stream);
+
+/* x[i*stride] = g(x[i*stride]) for i < n, in place. Applies the reference's
+ * post-map `g` (mapreduce(f, op, x; dims, g), src/mapreduce/mapreduce.jl:51-58;
+ * scan!(f, op, dst, src; g), src/scan/scan.jl:261-271) to reduction outputs
+ * and, as one extra pass, to scan outputs. */
+int kf_post_map(kf_post g, kf_dtype dt, void* x, int64_t n, int64_t stride, void* stream);
 
 /* ---------------------------------------------------------------- copy ----
  * dst[0:bytes] = src[0:bytes] with 16-byte streaming loads/stores: the

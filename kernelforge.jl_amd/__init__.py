@@ -118,6 +118,33 @@ def _map_code(f):
     raise ArgumentError(f"unsupported map {f!r}: expected identity or abs2")
 
 
+def _post_code(g):
+    """Post-map g on device results: identity, sqrt or abs2 (else None)."""
+    import math
+    if g is None or g is identity:
+        return _L.POST_IDENTITY
+    if g is abs2 or g == "abs2":
+        return _L.POST_ABS2
+    if g in (math.sqrt, torch.sqrt) or g == "sqrt" or getattr(g, "__name__", "") == "sqrt":
+        return _L.POST_SQRT
+    return None
+
+
+def _apply_post(g, t, n, stride):
+    """t[i*stride] = g(t[i*stride]) on the device for the supported post-maps."""
+    code = _post_code(g)
+    if code is None:
+        raise ArgumentError(f"unsupported post-map g={g!r} on device results: expected identity, sqrt or abs2")
+    if code == _L.POST_IDENTITY or n == 0:
+        return
+    dt = _DTYPES.get(t.dtype)
+    if dt is None:
+        raise ArgumentError(f"post-map on unsupported element type {t.dtype}")
+    with torch.cuda.device(t.device):
+        rc = _L.lib().kf_post_map(code, dt, ctypes_void(t.data_ptr()), n, stride, _stream_ptr(t))
+    _L.check(rc, "post-map g")
+
+
 def _stream_ptr(t):
     return ctypes_void(torch.cuda.current_stream(t.device).cuda_stream)
 
@@ -215,9 +242,9 @@ def scan_(*args, exclusive=False, tmp=None, g=None, **tuning):
     mode), or the exclusive variant dst[1] = identity(op),
     dst[i] = inclusive[i-1]. In place (dst is src) is allowed."""
     f, op, (dst, src) = _split_f_op(args, 2, "scan!")
-    if g is not None and g is not identity:
-        raise ArgumentError("scan!: only g = identity is supported")
     opc, fc = _op_code(op), _map_code(f)
+    if _post_code(g) is None or (g not in (None, identity) and opc == _L.OP_AFFINE):
+        raise ArgumentError(f"scan!: unsupported post-map g={g!r}: expected identity, sqrt or abs2")
     _require_device(dst, src)
     dt, n, ss = _scan_operand(src, opc)
     ddt, dn, ds = _scan_operand(dst, opc)
@@ -234,6 +261,7 @@ def scan_(*args, exclusive=False, tmp=None, g=None, **tuning):
         rc = L.kf_scan(opc, fc, dt, int(bool(exclusive)), ctypes_void(src.data_ptr()), ss,
                        ctypes_void(dst.data_ptr()), ds, n, ctypes_void(buf.ptr), buf.nbytes, _stream_ptr(src))
     _L.check(rc, "scan!")
+    _apply_post(g, dst, n, ds)  # g as one extra in-place pass over dst
     return dst
 
 
@@ -397,14 +425,12 @@ def mapreduce(f, op, src, dims=None, g=None, tmp=None, **tuning):
         _reduce_full_into(fc, opc, out, src, tmp)
         val = _to_scalar(out)
         return g(val) if g is not None else val
-    if g is not None and g is not identity:
-        raise ArgumentError("mapreduce with dims: only g = identity is supported")
     nd = src.dim()
     dims_t = _normalize_dims(dims, nd)
     shape = list(src.shape)
     out_shape = [1 if (i + 1) in dims_t else s for i, s in enumerate(shape)]
     dst = _colmajor_empty(out_shape, src.dtype, src.device)
-    mapreduce_(f, op, dst, src, dims=dims_t, tmp=tmp)
+    mapreduce_(f, op, dst, src, dims=dims_t, g=g, tmp=tmp)
     return dst
 
 
@@ -445,14 +471,16 @@ def mapreduce_(f, op, dst, src, dims=None, g=None, tmp=None, **tuning):
     fc, opc = _map_code(f), _op_code(op)
     _require_device(dst, src)
     _check_reducible(src, opc, fc)
-    if g is not None and g is not identity:
-        raise ArgumentError("mapreduce!: only g = identity is supported")
+    if _post_code(g) is None:
+        raise ArgumentError(f"mapreduce!: unsupported post-map g={g!r} on device results: "
+                            "expected identity, sqrt or abs2")
     if dst.dtype != src.dtype:
         raise ArgumentError(f"dst eltype {dst.dtype} differs from src eltype {src.dtype}")
     if dims is None or dims == ":" or dims is Ellipsis:
         if dst.numel() < 1:
             raise ArgumentError("dst must hold at least one element")
         _reduce_full_into(fc, opc, dst.as_strided((1,), (1,)), src, tmp)
+        _apply_post(g, dst, 1, 1)
         return dst
     nd = src.dim()
     dims_t = _normalize_dims(dims, nd)
@@ -471,6 +499,15 @@ def mapreduce_(f, op, dst, src, dims=None, g=None, tmp=None, **tuning):
         if nkeep:
             raise ArgumentError("reducing over an empty dimension is not allowed")
         return dst
+    _mapreduce_dims_into(fc, opc, dst, dst_stride, src, dims_t, tmp)
+    _apply_post(g, dst, nkeep, dst_stride)
+    return dst
+
+
+def _mapreduce_dims_into(fc, opc, dst, dst_stride, src, dims_t, tmp):
+    """Route a dims reduction (reference src/mapreduce/mapreduce.jl:151-212)."""
+    nd = src.dim()
+    shape = list(src.shape)
     if len(dims_t) == nd:  # every dim: a full reduction into a (1,...,1) array
         _reduce_full_into(fc, opc, dst, src, tmp)
         return dst

@@ -15,6 +15,7 @@ KF_OK, KF_EINVAL, KF_ENOSCRATCH, KF_EHIP = 0, 1, 2, 3
 OP_ADD, OP_MAX, OP_MIN, OP_AFFINE = 0, 1, 2, 3
 MAP_IDENTITY, MAP_ABS2 = 0, 1
 MAP2_MUL, MAP2_SQDIFF = 0, 1
+POST_IDENTITY, POST_SQRT, POST_ABS2 = 0, 1, 2
 F32, F64, I32, I64, U8, F32X2 = 0, 1, 2, 3, 4, 5
 
 # Every symbol include/kf.h declares, with its ctypes signature.
@@ -33,6 +34,7 @@ SIGNATURES = {
     "kf_reduce2": ([_I, _I, _I, _P, _I64, _P, _I64, _I64, _P, _P, _SZ, _P], _I),
     "kf_reduce_dim_batched_scratch_bytes": ([_I, _I64, _I64, _I64], _SZ),
     "kf_reduce_dim_batched": ([_I, _I, _I, _P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P, _SZ, _P], _I),
+    "kf_post_map": ([_I, _I, _P, _I64, _I64, _P], _I),
     "kf_copy": ([_P, _P, _SZ, _P], _I),
 }
 

@@ -685,6 +685,17 @@ __global__ void copy_bytes_kernel(uint8_t* dst, const uint8_t* src, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gsize) dst[i] = src[i];
 }
 
+struct PostSqrt {
+  __device__ static float apply(float x) { return __builtin_sqrtf(x); }
+  __device__ static double apply(double x) { return __builtin_sqrt(x); }
+};
+template <class T, class G>
+__global__ __launch_bounds__(256) void post_map_kernel(T* x, int64_t n, int64_t stride) {
+  const int64_t gsize = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gsize)
+    x[i * stride] = G::apply(x[i * stride]);
+}
+
 __global__ void fill_zero_kernel(uint8_t* p, int64_t n) {
   const int64_t gsize = (int64_t)gridDim.x * blockDim.x;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gsize) p[i] = 0;
@@ -864,6 +875,37 @@ extern "C" int kf_copy(void* dst, const void* src, size_t bytes, void* stream) {
                        (int64_t)bytes);
   }
   return kf_check_launch("copy_kernel");
+}
+
+template <class T, class G> int launch_post(void* x, int64_t n, int64_t stride, hipStream_t s) {
+  const int grid = (int)kmin<int64_t>(8192, kmax<int64_t>(1, (n + 255) / 256));
+  hipLaunchKernelGGL((post_map_kernel<T, G>), dim3(grid), dim3(256), 0, s, (T*)x, n, stride);
+  return kf_check_launch("post_map_kernel");
+}
+
+extern "C" int kf_post_map(kf_post g, kf_dtype dt, void* x, int64_t n, int64_t stride, void* stream) {
+  if (g == KF_POST_IDENTITY || n == 0) return KF_OK;
+  if (n < 0 || stride < 1) return kf_set_error(KF_EINVAL, "kf_post_map: bad n or stride");
+  if (!x) return kf_set_error(KF_EINVAL, "kf_post_map: null pointer");
+  const size_t es = kf_dtype_size(dt);
+  if (es == 0 || dt == KF_F32X2) return kf_set_error(KF_EINVAL, "kf_post_map: unsupported dtype %d", (int)dt);
+  if ((uintptr_t)x % es) return kf_set_error(KF_EINVAL, "kf_post_map: pointer not aligned to the element type");
+  hipStream_t s = (hipStream_t)stream;
+  if (g == KF_POST_SQRT) {
+    if (dt == KF_F32) return launch_post<float, PostSqrt>(x, n, stride, s);
+    if (dt == KF_F64) return launch_post<double, PostSqrt>(x, n, stride, s);
+    return kf_set_error(KF_EINVAL, "kf_post_map: sqrt needs a floating-point type");
+  }
+  if (g == KF_POST_ABS2) {
+    switch (dt) {
+      case KF_F32: return launch_post<float, MapAbs2>(x, n, stride, s);
+      case KF_F64: return launch_post<double, MapAbs2>(x, n, stride, s);
+      case KF_I32: return launch_post<int32_t, MapAbs2>(x, n, stride, s);
+      case KF_I64: return launch_post<int64_t, MapAbs2>(x, n, stride, s);
+      default: return launch_post<uint8_t, MapAbs2>(x, n, stride, s);
+    }
+  }
+  return kf_set_error(KF_EINVAL, "kf_post_map: unknown post-map %d", (int)g);
 }
 
 extern "C" int kf_scratch_reset(void* scratch, size_t bytes, void* stream) {

@@ -313,3 +313,26 @@ def test_two_array_mapreduce(kf, oracle, dev, dt):
     y = rng.random(15_000)
     d = kf.mapreduce(kf.sqdiff, "+", (torch.from_numpy(x).to(dev), torch.from_numpy(y).to(dev)), g=np.sqrt)
     assert d == pytest.approx(np.sqrt(np.sum((x - y) ** 2)), rel=1e-12)
+
+
+def test_post_map_g(kf, dev):
+    # reference test/tests/mapreduce/mapreduce2d_test.jl:30-35: abs2 + g = sqrt row norms
+    import math
+    rng = np.random.default_rng(61)
+    a = rng.standard_normal((64, 128))                     # C-order (64,128) == Julia 128x64
+    A = torch.from_numpy(a).to(dev).T
+    An = A.cpu().numpy()
+    got = kf.mapreduce(kf.abs2, "+", A, dims=2, g=math.sqrt).reshape(-1).cpu().numpy()
+    np.testing.assert_allclose(got, np.sqrt((An ** 2).sum(axis=1)), rtol=1e-13)
+    got = kf.mapreduce(kf.identity, "+", A, dims=1, g=kf.abs2).reshape(-1).cpu().numpy()
+    np.testing.assert_allclose(got, An.sum(axis=0) ** 2, rtol=1e-12)
+    dst = torch.zeros(1, dtype=torch.float64, device=dev)
+    kf.mapreduce_(kf.abs2, "+", dst, A, g="sqrt")
+    assert dst.item() == pytest.approx(np.sqrt((An ** 2).sum()), rel=1e-13)
+    # scan!(f, op, dst, src; g): g applied to every prefix
+    x = torch.from_numpy(rng.random(10_001)).to(dev)
+    y = kf.scan("+", x, g=torch.sqrt).cpu().numpy()
+    np.testing.assert_allclose(y, np.sqrt(np.cumsum(x.cpu().numpy())), rtol=1e-12)
+    with pytest.raises(kf.ArgumentError):
+        kf.mapreduce(kf.identity, "+", A, dims=1, g=lambda v: v / 2)   # arbitrary g only on host scalars
+    assert kf.mapreduce(kf.identity, "+", x, g=lambda v: v / 2) == pytest.approx(x.sum().item() / 2, rel=1e-12)
