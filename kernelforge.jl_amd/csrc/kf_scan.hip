@@ -15,9 +15,10 @@
 //    fully coalesced 16-byte access and no LDS transpose is needed. Each
 //    row j (64 lanes x 16 bytes) is scanned in-lane, then across the wave
 //    with DPP row shifts/broadcasts, and rows are chained with a carry.
-//  * The lookback window is one wave: lane j reads the descriptor of tile
-//    (t - 64 + j), so lane order is tile order and a DPP scan combines the
-//    window in the order a non-commutative op needs.
+//  * The lookback window lives in the top lanes of one wave: lane j reads
+//    the descriptor of tile (t - 64 + j) for the last kLookWindow lanes, so
+//    lane order is tile order and a DPP scan combines the window in the
+//    order a non-commutative op needs.
 //  * Each tile descriptor owns a 128-byte line (kDescWords words): tiles are
 //    published from different XCDs, and packing several descriptors per line
 //    made those writers and the pollers contend for one line (measured: 5.0
@@ -46,6 +47,11 @@ constexpr uint32_t kStatePartial = 1, kStatePrefix = 2;
 constexpr size_t kScanHeaderBytes = 256;
 constexpr int kDescWords = 16;             // 128 bytes per tile descriptor
 constexpr uint32_t kSpinLimit = 1u << 24;  // lookback polls before giving up (seconds)
+// Predecessors polled per lookback round (lanes 64-WIN..63). Each descriptor
+// is its own 128-byte line, and a poll completes only when its slowest line
+// returns: for large tiles 8 lines per poll measured 6.09 vs 5.82 TB/s for
+// 64. Small tiles (short arrays, all tiles in flight at once) keep 64.
+template <int BLOCK> constexpr int look_window() { return BLOCK == kScanBlock ? 8 : kWave; }
 
 template <class T, int BLOCK = kScanBlock> struct ScanShape {
   static constexpr int EPV = 16 / (int)sizeof(T);   // elements per 16-byte vector
@@ -65,7 +71,7 @@ __device__ inline void publish(uint64_t* desc, int64_t tile, uint32_t tag, T v) 
 
 // Decoupled lookback, executed by one full wave. Returns the combination of
 // every tile before `tile` (tile > 0), in tile order.
-template <class T, class Op>
+template <class T, class Op, int kLookWindow>
 __device__ inline T lookback(const uint64_t* desc, int64_t tile, uint32_t epoch30) {
   constexpr int W = ScanShape<T>::W;
   const int lane = lane_id();
@@ -82,9 +88,11 @@ __device__ inline T lookback(const uint64_t* desc, int64_t tile, uint32_t epoch3
       return run;
     }
     const int64_t t = newest - (kWave - 1) + lane;
+    const bool in_win = lane >= kWave - kLookWindow;
     T v = id;
-    uint32_t state = kStatePrefix;  // tiles before 0: an identity prefix
-    if (t >= 0) {
+    // tiles before 0: an identity prefix; lanes outside the window: identity partials
+    uint32_t state = in_win ? kStatePrefix : kStatePartial;
+    if (t >= 0 && in_win) {
       uint64_t d[W];
 #pragma unroll
       for (int i = 0; i < W; ++i) d[i] = ld_agent(desc + t * kDescWords + i);
@@ -109,7 +117,7 @@ __device__ inline T lookback(const uint64_t* desc, int64_t tile, uint32_t epoch3
     } else if (invalid == 0) {
       const T tot = wave_reduce<Op>(v);
       run = Op::combine(tot, run);
-      newest -= kWave;
+      newest -= kLookWindow;
       continue;
     }
     __builtin_amdgcn_s_sleep(1);
@@ -204,7 +212,7 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
       if (lane == 0) publish(desc, tile, (epoch30 << 2) | kStatePrefix, agg);
     } else {
       if (lane == 0) publish(desc, tile, (epoch30 << 2) | kStatePartial, agg);
-      excl = lookback<T, Op>(desc, tile, epoch30);
+      excl = lookback<T, Op, look_window<BLOCK>()>(desc, tile, epoch30);
       if (lane == 0) publish(desc, tile, (epoch30 << 2) | kStatePrefix, Op::combine(excl, agg));
     }
     if (lane == 0) block_excl = excl;
