@@ -44,3 +44,23 @@ def test_graph_replays_match_eager(kf, oracle, dev):
         y2 = torch.empty_like(y)
         kf.scan_("+", y2, x, tmp=t_scan, exclusive=True)
         assert torch.equal(y2, y), rep
+
+
+def test_two_streams_concurrently(kf, oracle, dev):
+    # calls on different streams use different default scratch buffers and
+    # may overlap; each stream's results must match its own data
+    rng = np.random.default_rng(31)
+    xs = [rng.integers(-8, 9, 3_000_017).astype(np.int32) for _ in range(2)]
+    streams = [torch.cuda.Stream(device=dev) for _ in range(2)]
+    outs = [None, None]
+    srcs = [torch.from_numpy(x).to(dev) for x in xs]
+    torch.cuda.synchronize()
+    for rep in range(3):
+        for i, s in enumerate(streams):
+            with torch.cuda.stream(s):
+                outs[i] = kf.scan("+", srcs[i])
+                kf.scan_("max", outs[i], outs[i])   # in place on the same stream
+        torch.cuda.synchronize()
+        for i in range(2):
+            ref = np.maximum.accumulate(oracle.scan(xs[i], "+"))
+            assert np.array_equal(outs[i].cpu().numpy(), ref), (rep, i)
