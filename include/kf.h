@@ -157,6 +157,18 @@ int kf_reduce_dim(kf_op op, kf_map f, kf_dtype dt,
                   int dim, void* dst, int64_t dst_stride,
                   void* scratch, size_t scratch_bytes, void* stream);
 
+/* Reduction along a dim with a vector operand x (scratch:
+ * kf_reduce_dim_scratch_bytes with the same shape and dim):
+ *   dim = 2 (matvec): dst[i * dst_stride] = op_j f(A[i, j], x[j * x_stride])
+ *   dim = 1 (vecmat): dst[j * dst_stride] = op_i f(x[i * x_stride], A[i, j])
+ * with f = x*y (A*x, x'*A) or (x-y)^2. Replaces the reference's
+ *   matvec(f, op, A, x) src/mapreduce/2D/matvec.jl:393-474 and
+ *   vecmat(f, op, x, A) src/mapreduce/2D/vecmat.jl:328-405. */
+int kf_reduce_dim_x(kf_op op, kf_map2 f, kf_dtype dt,
+                    const void* A, int64_t rows, int64_t cols, int64_t col_stride, int dim,
+                    const void* x, int64_t x_stride, void* dst, int64_t dst_stride,
+                    void* scratch, size_t scratch_bytes, void* stream);
+
 /* Batched dim-2 reduction: `batch` column-major rows x cols matrices, the
  * z-th starting at A + z*batch_stride:
  *   dst[(i + z*rows) * dst_stride] = op_j f(A[i + j*col_stride + z*batch_stride])

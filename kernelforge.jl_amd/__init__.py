@@ -38,7 +38,7 @@ from . import _lib as _L
 __all__ = [
     "ArgumentError", "KernelBuffer", "AffineOp", "affine", "identity", "abs2", "sqdiff",
     "scan", "scan_", "mapreduce", "mapreduce_", "get_allocation", "vcopy_",
-    "Scan1D", "MapReduce1D", "MapReduce2D",
+    "Scan1D", "MapReduce1D", "MapReduce2D", "matvec", "matvec_", "vecmat", "vecmat_",
 ]
 
 
@@ -594,6 +594,84 @@ def _reduce_dims_general(fc, opc, dst, dst_stride, src, dims_t, tmp):
                                              ctypes_void(buf.ptr), buf.nbytes, _stream_ptr(src))
         _L.check(rc, f"mapreduce(dims={dims_t})")
         cur, cur_fc = out if not last else None, _L.MAP_IDENTITY
+
+
+# ---------------------------------------------------------------------------
+# matvec / vecmat (reference src/mapreduce/2D/matvec.jl:393-474,
+# src/mapreduce/2D/vecmat.jl:328-405)
+# ---------------------------------------------------------------------------
+def _split_fop_kw(args, n_arrays, f, op, name):
+    if len(args) == n_arrays + 2:
+        return args[0], args[1], args[2:]
+    if len(args) == n_arrays:
+        return f, op, args
+    raise ArgumentError(f"{name} takes ([f, op,] {n_arrays} arrays)")
+
+
+def _dim_x_into(f, op, dst, A, x, dim, g, tmp, name):
+    opc = _op_code(op)
+    _require_device(dst, A, *(() if x is None else (x,)))
+    if A.dim() != 2:
+        raise ArgumentError(f"{name}: expected a matrix, got a {A.dim()}-d tensor")
+    if A.dtype not in _DTYPES or dst.dtype != A.dtype or (x is not None and x.dtype != A.dtype):
+        raise ArgumentError(f"{name}: operands must share one supported element type")
+    if opc == _L.OP_AFFINE:
+        raise ArgumentError(f"{name} needs a commutative operator")
+    if _post_code(g) is None:
+        raise ArgumentError(f"{name}: unsupported post-map g={g!r}: expected identity, sqrt or abs2")
+    rows, cols, cs = _as_matrix(A, 1)
+    m = rows if dim == 2 else cols
+    k = cols if dim == 2 else rows
+    dflat = _merge(list(dst.shape), list(dst.stride()))
+    if dflat is None or dst.numel() != m:
+        raise ArgumentError(f"{name}: dst must be a vector of length {m}")
+    if x is None:  # the reference's x = nothing: a plain reduction with f applied to A
+        fc = _L.MAP_ABS2 if (f is abs2 or f == "abs2") else _L.MAP_IDENTITY
+        _reduce_dim_into(fc, opc, dst, dflat[1], A, rows, cols, cs, dim, tmp)
+    else:
+        if x.dim() != 1 or x.shape[0] != k:
+            raise ArgumentError(f"{name}: x must be a vector of length {k}")
+        fc = _map2_code(f)
+        L = _L.lib()
+        dt = _DTYPES[A.dtype]
+        buf = _scratch(MapReduce2D, L.kf_reduce_dim_scratch_bytes(dt, rows, cols, dim), A.device, tmp)
+        with torch.cuda.device(A.device):
+            rc = L.kf_reduce_dim_x(opc, fc, dt, ctypes_void(A.data_ptr()), rows, cols, cs, dim,
+                                   ctypes_void(x.data_ptr()), x.stride(0) if k > 1 else 1,
+                                   ctypes_void(dst.data_ptr()), dflat[1], ctypes_void(buf.ptr), buf.nbytes,
+                                   _stream_ptr(A))
+        _L.check(rc, name)
+    _apply_post(g, dst, m, dflat[1])
+    return dst
+
+
+def matvec(*args, f=operator.mul, op="+", g=None, tmp=None, **tuning):
+    """matvec(A, x; f=*, op=+) or matvec(f, op, A, x): dst[i] = op_j f(A[i,j], x[j]).
+    f: operator.mul or sqdiff; x=None reduces the rows of A (f unary)."""
+    f, op, (A, x) = _split_fop_kw(args, 2, f, op, "matvec")
+    _require_device(A)
+    dst = torch.empty(A.shape[0], dtype=A.dtype, device=A.device)
+    return _dim_x_into(f, op, dst, A, x, 2, g, tmp, "matvec")
+
+
+def matvec_(*args, f=operator.mul, op="+", g=None, tmp=None, **tuning):
+    """matvec!(dst, A, x; f=*, op=+) or matvec!(f, op, dst, A, x)."""
+    f, op, (dst, A, x) = _split_fop_kw(args, 3, f, op, "matvec!")
+    return _dim_x_into(f, op, dst, A, x, 2, g, tmp, "matvec!")
+
+
+def vecmat(*args, f=operator.mul, op="+", g=None, tmp=None, **tuning):
+    """vecmat(x, A; f=*, op=+) or vecmat(f, op, x, A): dst[j] = op_i f(x[i], A[i,j])."""
+    f, op, (x, A) = _split_fop_kw(args, 2, f, op, "vecmat")
+    _require_device(A)
+    dst = torch.empty(A.shape[1], dtype=A.dtype, device=A.device)
+    return _dim_x_into(f, op, dst, A, x, 1, g, tmp, "vecmat")
+
+
+def vecmat_(*args, f=operator.mul, op="+", g=None, tmp=None, **tuning):
+    """vecmat!(dst, x, A; f=*, op=+) or vecmat!(f, op, dst, x, A)."""
+    f, op, (dst, x, A) = _split_fop_kw(args, 3, f, op, "vecmat!")
+    return _dim_x_into(f, op, dst, A, x, 1, g, tmp, "vecmat!")
 
 
 def get_allocation(kind, f, op, src, *args, **kwargs):

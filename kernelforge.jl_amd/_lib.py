@@ -34,6 +34,7 @@ SIGNATURES = {
     "kf_reduce2": ([_I, _I, _I, _P, _I64, _P, _I64, _I64, _P, _P, _SZ, _P], _I),
     "kf_reduce_dim_batched_scratch_bytes": ([_I, _I64, _I64, _I64], _SZ),
     "kf_reduce_dim_batched": ([_I, _I, _I, _P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P, _SZ, _P], _I),
+    "kf_reduce_dim_x": ([_I, _I, _I, _P, _I64, _I64, _I64, _I, _P, _I64, _P, _I64, _P, _SZ, _P], _I),
     "kf_post_map": ([_I, _I, _P, _I64, _I64, _P], _I),
     "kf_copy": ([_P, _P, _SZ, _P], _I),
 }

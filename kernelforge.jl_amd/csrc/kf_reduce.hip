@@ -285,12 +285,14 @@ int launch_reduce(const void* src, int64_t n, int64_t stride, void* dst, void* s
 // otherwise); later levels reuse the partial reduction above.
 // ---------------------------------------------------------------------------
 struct Map2Mul {
+  static constexpr bool kHasX = true;
   template <class T> __device__ static T apply(T a, T b) { return a * b; }
   __device__ static int32_t apply(int32_t a, int32_t b) { return (int32_t)((uint32_t)a * (uint32_t)b); }
   __device__ static int64_t apply(int64_t a, int64_t b) { return (int64_t)((uint64_t)a * (uint64_t)b); }
   __device__ static uint8_t apply(uint8_t a, uint8_t b) { return (uint8_t)(a * b); }
 };
 struct Map2SqDiff {
+  static constexpr bool kHasX = true;
   template <class T> __device__ static T apply(T a, T b) { const T d = a - b; return d * d; }
   __device__ static int32_t apply(int32_t a, int32_t b) {
     const uint32_t d = (uint32_t)a - (uint32_t)b;
@@ -390,6 +392,14 @@ int launch_reduce2(const void* x, int64_t xs, const void* y, int64_t ys, int64_t
 // contiguous), optionally split into S row segments when there are too few
 // columns to fill the GPU.
 // ---------------------------------------------------------------------------
+// Element function of the dims kernels: f(a) for a plain reduction, or
+// f(a, x) with a vector operand x (matvec: x[j] per column; vecmat: x[i]
+// per row).
+template <class Map> struct Unary {
+  static constexpr bool kHasX = false;
+  template <class T> __device__ static T apply(T a, T) { return Map::apply(a); }
+};
+
 constexpr int kDimBlock = 256;
 constexpr int kDimWaves = kDimBlock / kWave;
 constexpr int kDimUnroll = 4;
@@ -398,10 +408,10 @@ constexpr int kRowVecsDefault = 2;    // dim 2: 16-byte vectors per thread per c
 constexpr int kColUnrollDefault = 8;  // dim 2: columns in flight per thread
 constexpr int kDim2Blocks = 256;      // dim 2: target workgroups (one per CU)
 
-template <class T, class Op, class Map>
+template <class T, class Op, class F>
 __global__ __launch_bounds__(kDimBlock) void reduce_cols_kernel(
     const T* A, int64_t rows, int64_t cols, int64_t col_stride, T* out, int64_t out_stride,
-    int64_t seg_rows, int vec) {
+    int64_t seg_rows, int vec, const T* xv, int64_t xs) {
   constexpr int EPV = 16 / (int)sizeof(T);
   const T id = Op::template identity<T>();
   const int lane = lane_id();
@@ -417,6 +427,7 @@ __global__ __launch_bounds__(kDimBlock) void reduce_cols_kernel(
     // seg_rows is a multiple of EPV and columns are 16-byte aligned.
     const int64_t nv = r1 > r0 ? (r1 - r0) / EPV : 0;
     const uint4* v = reinterpret_cast<const uint4*>(c + r0);
+    const uint4* vx = reinterpret_cast<const uint4*>(xv + r0);  // used only with an operand (16-B aligned, xs = 1)
     T a[kDimUnroll][EPV];
 #pragma unroll
     for (int u = 0; u < kDimUnroll; ++u)
@@ -424,32 +435,41 @@ __global__ __launch_bounds__(kDimBlock) void reduce_cols_kernel(
       for (int e = 0; e < EPV; ++e) a[u][e] = id;
     int64_t i = lane;
     for (; i + (kDimUnroll - 1) * kWave < nv; i += kDimUnroll * kWave) {
-      uint4 r[kDimUnroll];
-#pragma unroll
-      for (int u = 0; u < kDimUnroll; ++u) r[u] = ld_stream(v + i + u * kWave);
+      uint4 r[kDimUnroll], rx[kDimUnroll];
 #pragma unroll
       for (int u = 0; u < kDimUnroll; ++u) {
-        T x[EPV];
-        __builtin_memcpy(x, &r[u], 16);
+        r[u] = ld_stream(v + i + u * kWave);
+        if constexpr (F::kHasX) rx[u] = vx[i + u * kWave];
+      }
 #pragma unroll
-        for (int e = 0; e < EPV; ++e) a[u][e] = Op::combine(a[u][e], Map::apply(x[e]));
+      for (int u = 0; u < kDimUnroll; ++u) {
+        T x[EPV], w[EPV];
+        __builtin_memcpy(x, &r[u], 16);
+        if constexpr (F::kHasX) __builtin_memcpy(w, &rx[u], 16);
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) a[u][e] = Op::combine(a[u][e], F::apply(x[e], F::kHasX ? w[e] : x[e]));
       }
     }
     for (; i < nv; i += kWave) {
       const uint4 r = ld_stream(v + i);
-      T x[EPV];
+      T x[EPV], w[EPV];
       __builtin_memcpy(x, &r, 16);
+      if constexpr (F::kHasX) {
+        const uint4 q = vx[i];
+        __builtin_memcpy(w, &q, 16);
+      }
 #pragma unroll
-      for (int e = 0; e < EPV; ++e) a[0][e] = Op::combine(a[0][e], Map::apply(x[e]));
+      for (int e = 0; e < EPV; ++e) a[0][e] = Op::combine(a[0][e], F::apply(x[e], F::kHasX ? w[e] : x[e]));
     }
 #pragma unroll
     for (int u = 0; u < kDimUnroll; ++u)
 #pragma unroll
       for (int e = 0; e < EPV; ++e) acc = Op::combine(acc, a[u][e]);
     const int64_t t = r0 + nv * EPV + lane;
-    if (t < r1) acc = Op::combine(acc, Map::apply(c[t]));
+    if (t < r1) acc = Op::combine(acc, F::apply(c[t], F::kHasX ? xv[t] : c[t]));
   } else {
-    for (int64_t r = r0 + lane; r < r1; r += kWave) acc = Op::combine(acc, Map::apply(c[r]));
+    for (int64_t r = r0 + lane; r < r1; r += kWave)
+      acc = Op::combine(acc, F::apply(c[r], F::kHasX ? xv[r * xs] : c[r]));
   }
   acc = wave_reduce<Op>(acc);
   // S == 1: out is dst; otherwise out is partials[s*cols + col]
@@ -463,10 +483,10 @@ __global__ __launch_bounds__(kDimBlock) void reduce_cols_kernel(
 // 8 KiB contiguous run. Strips are split over S column ranges whose
 // partials stage 2 combines.
 // ---------------------------------------------------------------------------
-template <class T, class Op, class Map, bool VEC, int kRowVecs = kRowVecsDefault, int kColUnroll = kColUnrollDefault>
+template <class T, class Op, class F, bool VEC, int kRowVecs = kRowVecsDefault, int kColUnroll = kColUnrollDefault>
 __global__ __launch_bounds__(kDimBlock) void reduce_rows_kernel(
     const T* A, int64_t rows, int64_t cols, int64_t col_stride, T* out, int64_t out_stride, int64_t seg_cols,
-    int64_t a_bstride, int64_t out_bstride) {
+    int64_t a_bstride, int64_t out_bstride, const T* xv, int64_t xs) {
   constexpr int EPV = VEC ? 16 / (int)sizeof(T) : 1;
   // batch z = blockIdx.z: one (rows x cols) matrix per batch entry
   A += (int64_t)blockIdx.z * a_bstride;
@@ -496,23 +516,26 @@ __global__ __launch_bounds__(kDimBlock) void reduce_rows_kernel(
         for (int u = 0; u < kRowVecs; ++u)
           r[q][u] = ld_stream(reinterpret_cast<const uint4*>(p + (c + q) * col_stride) + u * kDimBlock + tid);
 #pragma unroll
-      for (int q = 0; q < kColUnroll; ++q)
+      for (int q = 0; q < kColUnroll; ++q) {
+        const T w = F::kHasX ? xv[(c + q) * xs] : id;
 #pragma unroll
         for (int u = 0; u < kRowVecs; ++u) {
           T x[EPV];
           __builtin_memcpy(x, &r[q][u], sizeof(x));
 #pragma unroll
-          for (int e = 0; e < EPV; ++e) a[u][e] = Op::combine(a[u][e], Map::apply(x[e]));
+          for (int e = 0; e < EPV; ++e) a[u][e] = Op::combine(a[u][e], F::apply(x[e], w));
         }
+      }
     }
     for (; c < c1; ++c) {
+      const T w = F::kHasX ? xv[c * xs] : id;
 #pragma unroll
       for (int u = 0; u < kRowVecs; ++u) {
         const uint4 r = ld_stream(reinterpret_cast<const uint4*>(p + c * col_stride) + u * kDimBlock + tid);
         T x[EPV];
         __builtin_memcpy(x, &r, sizeof(x));
 #pragma unroll
-        for (int e = 0; e < EPV; ++e) a[u][e] = Op::combine(a[u][e], Map::apply(x[e]));
+        for (int e = 0; e < EPV; ++e) a[u][e] = Op::combine(a[u][e], F::apply(x[e], w));
       }
     }
   } else {
@@ -522,7 +545,7 @@ __global__ __launch_bounds__(kDimBlock) void reduce_rows_kernel(
 #pragma unroll
         for (int e = 0; e < EPV; ++e) {
           const int64_t r = strip + (int64_t)(u * kDimBlock + tid) * EPV + e;
-          if (r < rows) a[u][e] = Op::combine(a[u][e], Map::apply(A[r + c * col_stride]));
+          if (r < rows) a[u][e] = Op::combine(a[u][e], F::apply(A[r + c * col_stride], F::kHasX ? xv[c * xs] : id));
         }
   }
 #pragma unroll
@@ -581,18 +604,21 @@ inline bool dim_vec_ok(const void* A, int64_t cs, size_t es) {
   return ((uintptr_t)A % 16 == 0) && ((cs * (int64_t)es) % 16 == 0);
 }
 
-template <class T, class Op, class Map>
+template <class T, class Op, class F>
 int launch_reduce_dim(const void* A, int64_t rows, int64_t cols, int64_t cs, int dim, void* dst,
-                      int64_t ds, void* scratch, hipStream_t stream, int64_t batch = 1, int64_t a_bstride = 0) {
-  const bool vec = dim_vec_ok(A, cs, sizeof(T)) && (batch == 1 || (a_bstride * (int64_t)sizeof(T)) % 16 == 0);
+                      int64_t ds, void* scratch, hipStream_t stream, int64_t batch = 1, int64_t a_bstride = 0,
+                      const void* x = nullptr, int64_t xs = 0) {
+  bool vec = dim_vec_ok(A, cs, sizeof(T)) && (batch == 1 || (a_bstride * (int64_t)sizeof(T)) % 16 == 0);
+  // vecmat (dim 1 with an operand) reads x along the rows: same vector path only if x is too
+  if (F::kHasX && dim == 1) vec = vec && xs == 1 && (uintptr_t)x % 16 == 0;
   const DimPlan p = plan_dim(sizeof(T), rows, cols, dim, vec, batch);
   if (dim == 1) {
     T* out = p.split > 1 ? (T*)scratch : (T*)dst;
     constexpr int EPV = 16 / (int)sizeof(T);
     int64_t seg = (rows + p.split - 1) / p.split;
     seg = (seg + EPV - 1) / EPV * EPV;
-    hipLaunchKernelGGL((reduce_cols_kernel<T, Op, Map>), dim3((unsigned)p.groups, p.split), dim3(kDimBlock), 0,
-                       stream, (const T*)A, rows, cols, cs, out, ds, seg, (int)vec);
+    hipLaunchKernelGGL((reduce_cols_kernel<T, Op, F>), dim3((unsigned)p.groups, p.split), dim3(kDimBlock), 0,
+                       stream, (const T*)A, rows, cols, cs, out, ds, seg, (int)vec, (const T*)x, xs);
     if (p.split > 1)
       hipLaunchKernelGGL((combine_split_kernel<T, Op>), dim3((unsigned)((cols + kRedBlock - 1) / kRedBlock), 1),
                          dim3(kRedBlock), 0, stream, (const T*)scratch, p.split, cols, (T*)dst, ds, (int64_t)0);
@@ -608,11 +634,11 @@ int launch_reduce_dim(const void* A, int64_t rows, int64_t cols, int64_t cs, int
     T* out = p.split > 1 ? (T*)scratch : dz;
     const dim3 grid((unsigned)p.groups, p.split, nz);
     if (vec)
-      hipLaunchKernelGGL((reduce_rows_kernel<T, Op, Map, true>), grid, dim3(kDimBlock), 0, stream, Az, rows, cols, cs,
-                         out, ds, seg, a_bstride, dst_bstride);
+      hipLaunchKernelGGL((reduce_rows_kernel<T, Op, F, true>), grid, dim3(kDimBlock), 0, stream, Az, rows, cols, cs,
+                         out, ds, seg, a_bstride, dst_bstride, (const T*)x, xs);
     else
-      hipLaunchKernelGGL((reduce_rows_kernel<T, Op, Map, false>), grid, dim3(kDimBlock), 0, stream, Az, rows, cols,
-                         cs, out, ds, seg, a_bstride, dst_bstride);
+      hipLaunchKernelGGL((reduce_rows_kernel<T, Op, F, false>), grid, dim3(kDimBlock), 0, stream, Az, rows, cols,
+                         cs, out, ds, seg, a_bstride, dst_bstride, (const T*)x, xs);
     if (p.split > 1)
       hipLaunchKernelGGL((combine_split_kernel<T, Op>), dim3((unsigned)((rows + kRedBlock - 1) / kRedBlock), nz),
                          dim3(kRedBlock), 0, stream, (const T*)scratch, p.split, rows, dz, ds, dst_bstride);
@@ -665,7 +691,7 @@ template <class T, class Op, class Map2> struct Reduce2L {
 template <class T, class Op, class Map> struct ReduceDimL {
   static int run(const void* A, int64_t rows, int64_t cols, int64_t cs, int dim, void* dst, int64_t ds,
                  void* scratch, hipStream_t s, int64_t batch, int64_t a_bstride) {
-    return launch_reduce_dim<T, Op, Map>(A, rows, cols, cs, dim, dst, ds, scratch, s, batch, a_bstride);
+    return launch_reduce_dim<T, Op, Unary<Map>>(A, rows, cols, cs, dim, dst, ds, scratch, s, batch, a_bstride);
   }
 };
 
@@ -851,6 +877,59 @@ extern "C" int kf_reduce_dim_batched(kf_op op, kf_map f, kf_dtype dt, const void
   if (p.groups > 0x7fffffffLL) return kf_set_error(KF_EINVAL, "kf_reduce_dim_batched: shape exceeds the grid limit");
   return dispatch_all<ReduceDimL>(dt, op, f, A, rows, cols, col_stride, 2, dst, dst_stride, scratch,
                                   (hipStream_t)stream, batch, batch_stride);
+}
+
+template <class T, class... A> int dispatch_dim_x(kf_op op, kf_map2 f, A... args) {
+  if (f == KF_MAP2_SQDIFF) {
+    switch (op) {
+      case KF_OP_ADD: return launch_reduce_dim<T, OpAdd, Map2SqDiff>(args...);
+      case KF_OP_MAX: return launch_reduce_dim<T, OpMax, Map2SqDiff>(args...);
+      default: return launch_reduce_dim<T, OpMin, Map2SqDiff>(args...);
+    }
+  }
+  switch (op) {
+    case KF_OP_ADD: return launch_reduce_dim<T, OpAdd, Map2Mul>(args...);
+    case KF_OP_MAX: return launch_reduce_dim<T, OpMax, Map2Mul>(args...);
+    default: return launch_reduce_dim<T, OpMin, Map2Mul>(args...);
+  }
+}
+
+extern "C" int kf_reduce_dim_x(kf_op op, kf_map2 f, kf_dtype dt, const void* A, int64_t rows, int64_t cols,
+                               int64_t col_stride, int dim, const void* x, int64_t x_stride, void* dst,
+                               int64_t dst_stride, void* scratch, size_t scratch_bytes, void* stream) {
+  int rc = kf_validate_op(op, KF_MAP_IDENTITY, dt, /*allow_affine=*/0);
+  if (rc) return rc;
+  if (f != KF_MAP2_MUL && f != KF_MAP2_SQDIFF) return kf_set_error(KF_EINVAL, "kf_reduce_dim_x: unknown map %d", (int)f);
+  if (dim != 1 && dim != 2) return kf_set_error(KF_EINVAL, "kf_reduce_dim_x: dim must be 1 or 2 (got %d)", dim);
+  if (rows < 0 || cols < 0) return kf_set_error(KF_EINVAL, "kf_reduce_dim_x: negative shape");
+  if ((dim == 1 ? cols : rows) == 0) return KF_OK;
+  if ((dim == 1 ? rows : cols) == 0)
+    return kf_set_error(KF_EINVAL, "kf_reduce_dim_x: reducing an empty dimension has no identity-free result");
+  if (!A || !dst || !x) return kf_set_error(KF_EINVAL, "kf_reduce_dim_x: null pointer");
+  if (col_stride < rows) return kf_set_error(KF_EINVAL, "kf_reduce_dim_x: col_stride < rows");
+  if (dst_stride < 1 || x_stride < 1) return kf_set_error(KF_EINVAL, "kf_reduce_dim_x: strides must be >= 1");
+  const size_t es = kf_dtype_size(dt);
+  if ((uintptr_t)A % es || (uintptr_t)dst % es || (uintptr_t)x % es)
+    return kf_set_error(KF_EINVAL, "kf_reduce_dim_x: pointers not aligned to the element type");
+  const DimPlan p = plan_dim(es, rows, cols, dim, dim_vec_ok(A, col_stride, es));
+  if (p.split > 1) {
+    const size_t need = kf_reduce_dim_scratch_bytes(dt, rows, cols, dim);
+    if (!scratch || scratch_bytes < need)
+      return kf_set_error(KF_ENOSCRATCH, "kf_reduce_dim_x: scratch of %zu bytes needed, %zu given", need,
+                          scratch ? scratch_bytes : (size_t)0);
+    if ((uintptr_t)scratch % 256) return kf_set_error(KF_EINVAL, "kf_reduce_dim_x: scratch must be 256-byte aligned");
+  }
+  if (p.groups > 0x7fffffffLL) return kf_set_error(KF_EINVAL, "kf_reduce_dim_x: shape exceeds the grid limit");
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t one = 1, zero = 0;
+  switch (dt) {
+    case KF_F32: return dispatch_dim_x<float>(op, f, A, rows, cols, col_stride, dim, dst, dst_stride, scratch, s, one, zero, x, x_stride);
+    case KF_F64: return dispatch_dim_x<double>(op, f, A, rows, cols, col_stride, dim, dst, dst_stride, scratch, s, one, zero, x, x_stride);
+    case KF_I32: return dispatch_dim_x<int32_t>(op, f, A, rows, cols, col_stride, dim, dst, dst_stride, scratch, s, one, zero, x, x_stride);
+    case KF_I64: return dispatch_dim_x<int64_t>(op, f, A, rows, cols, col_stride, dim, dst, dst_stride, scratch, s, one, zero, x, x_stride);
+    case KF_U8: return dispatch_dim_x<uint8_t>(op, f, A, rows, cols, col_stride, dim, dst, dst_stride, scratch, s, one, zero, x, x_stride);
+    default: return kf_set_error(KF_EINVAL, "kf_reduce_dim_x: bad dtype %d", (int)dt);
+  }
 }
 
 extern "C" int kf_copy(void* dst, const void* src, size_t bytes, void* stream) {

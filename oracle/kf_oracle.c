@@ -197,6 +197,45 @@ void kfo_reduce2_i(const void* x, const void* y, int dt, int64_t n, int op, int 
   istore(out, dt, 0, acc);
 }
 
+/* matvec (dim 2): out[i] = op_j f(A[i,j], x[j]); vecmat (dim 1):
+ * out[j] = op_i f(x[i], A[i,j]); f2 = 0 -> product, 1 -> squared difference
+ * (reference src/mapreduce/2D/matvec.jl:393-474, vecmat.jl:328-405). */
+void kfo_reduce_dim_x_f(const void* A, const void* x, int dt, int64_t rows, int64_t cols, int64_t cs, int dim,
+                        int op, int f2, double* out) {
+  const int64_t m = dim == 2 ? rows : cols, k = dim == 2 ? cols : rows;
+  for (int64_t o = 0; o < m; ++o) {
+    double acc = 0.0;
+    for (int64_t q = 0; q < k; ++q) {
+      const int64_t i = dim == 2 ? o : q, j = dim == 2 ? q : o;
+      const double a = fload(A, dt, i + j * cs, 0), b = fload(x, dt, q, 0);
+      const double v = f2 ? (a - b) * (a - b) : a * b;
+      acc = q == 0 ? v : fop(op, acc, v);
+    }
+    out[o] = acc;
+  }
+}
+
+void kfo_reduce_dim_x_i(const void* A, const void* x, int dt, int64_t rows, int64_t cols, int64_t cs, int dim,
+                        int op, int f2, void* out) {
+  const int64_t m = dim == 2 ? rows : cols, k = dim == 2 ? cols : rows;
+  for (int64_t o = 0; o < m; ++o) {
+    uint64_t acc = 0;
+    for (int64_t q = 0; q < k; ++q) {
+      const int64_t i = dim == 2 ? o : q, j = dim == 2 ? q : o;
+      const uint64_t a = iload(A, dt, i + j * cs, 0), b = iload(x, dt, q, 0);
+      uint64_t v;
+      if (f2) {
+        const uint64_t d = wrap(dt, a - b);
+        v = wrap(dt, d * d);
+      } else {
+        v = wrap(dt, a * b);
+      }
+      acc = q == 0 ? v : iop(dt, op, acc, v);
+    }
+    istore(out, dt, o, acc);
+  }
+}
+
 /* Column-major A[i, j] = A[i + j*col_stride]. dim 1 -> cols outputs, dim 2
  * -> rows outputs (reference src/mapreduce/2D/mapreduce2d.jl:49-64). */
 void kfo_reduce_dim_f(const void* A, int dt, int64_t rows, int64_t cols, int64_t col_stride, int dim, int op,

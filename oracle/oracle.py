@@ -47,6 +47,8 @@ def lib():
         L.kfo_reduce2_f.argtypes = [P, P, I, I64, I, I]
         L.kfo_reduce2_f.restype = D
         L.kfo_reduce2_i.argtypes = [P, P, I, I64, I, I, P]
+        L.kfo_reduce_dim_x_f.argtypes = [P, P, I, I64, I64, I64, I, I, I, P]
+        L.kfo_reduce_dim_x_i.argtypes = [P, P, I, I64, I64, I64, I, I, I, P]
         L.kfo_reduce_dim_f.argtypes = [P, I, I64, I64, I64, I, I, I, P]
         L.kfo_reduce_dim_i.argtypes = [P, I, I64, I64, I64, I, I, I, P]
         L.kfb_scan_add_f32_seq.argtypes = [P, P, I64]
@@ -125,6 +127,22 @@ def reduce_dim(buf, rows, cols, col_stride, dim, op="+", f="identity"):
     else:
         out = np.empty(m, buf.dtype)
         L.kfo_reduce_dim_i(_p(buf), DT[buf.dtype], rows, cols, col_stride, dim, OPS[op], MAPS[f], _p(out))
+    return out
+
+
+def reduce_dim_x(buf, rows, cols, col_stride, x, dim, op="+", f2="mul"):
+    """matvec (dim 2) / vecmat (dim 1) of the column-major matrix in buf with x."""
+    L = lib()
+    buf, x = np.ascontiguousarray(buf), np.ascontiguousarray(x)
+    assert buf.dtype == x.dtype and x.shape[0] == (cols if dim == 2 else rows)
+    m = rows if dim == 2 else cols
+    code = {"mul": 0, "sqdiff": 1}[f2]
+    if _is_float(buf):
+        out = np.empty(m, np.float64)
+        L.kfo_reduce_dim_x_f(_p(buf), _p(x), DT[buf.dtype], rows, cols, col_stride, dim, OPS[op], code, _p(out))
+    else:
+        out = np.empty(m, buf.dtype)
+        L.kfo_reduce_dim_x_i(_p(buf), _p(x), DT[buf.dtype], rows, cols, col_stride, dim, OPS[op], code, _p(out))
     return out
 
 

@@ -19,7 +19,7 @@ def test_header_declares_the_expected_surface():
     assert declared_symbols() == sorted([
         "kf_version", "kf_last_error", "kf_scratch_reset", "kf_scan_scratch_bytes", "kf_scan",
         "kf_reduce_scratch_bytes", "kf_reduce", "kf_reduce_dim_scratch_bytes", "kf_reduce_dim", "kf_copy",
-        "kf_reduce2_scratch_bytes", "kf_reduce2", "kf_reduce_dim_batched_scratch_bytes", "kf_reduce_dim_batched", "kf_post_map"])
+        "kf_reduce2_scratch_bytes", "kf_reduce2", "kf_reduce_dim_batched_scratch_bytes", "kf_reduce_dim_batched", "kf_post_map", "kf_reduce_dim_x"])
 
 
 def test_library_exports_every_declared_symbol(kf):

@@ -1,0 +1,74 @@
+"""matvec / vecmat with a vector operand on the GPU against the oracle
+(reference test/tests/mapreduce/matvec_test.jl, vecmat_test.jl shape sweeps:
+square, tall, wide, small and large n; views). Integers exact; floats within
+rtol * sum|f| (the bound of any summation order)."""
+import operator
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(1, 1), (3, 3), (101, 101), (512, 512), (1000, 1000), (1024, 10), (4096, 32), (65536, 16),
+          (3, 10_000), (32, 50_000), (4, 1000), (63, 1000), (2048, 1000), (32768, 50)]
+
+
+def mk(rng, dt, shape):
+    if np.dtype(dt).kind == "f":
+        return rng.random(shape).astype(dt)
+    return rng.integers(-20, 20, shape).astype(dt)
+
+
+@pytest.mark.parametrize("dt", [np.float32, np.float64, np.int32])
+@pytest.mark.parametrize("view", [False, True])
+def test_matvec_vecmat(kf, oracle, dev, dt, view):
+    rng = np.random.default_rng(71)
+    for rows, cols in SHAPES:
+        pc = 2 * cols if view else cols
+        parent = mk(rng, dt, (pc, rows))           # row k of parent = column k of the matrix
+        buf = parent.reshape(-1)
+        cs = 2 * rows if view else rows
+        A = torch.from_numpy(buf).to(dev).as_strided((rows, cols), (1, cs))
+        x2, x1 = mk(rng, dt, cols), mk(rng, dt, rows)
+        tx2, tx1 = torch.from_numpy(x2).to(dev), torch.from_numpy(x1).to(dev)
+        M = buf.astype(np.float64)[np.arange(cols)[None, :] * cs + np.arange(rows)[:, None]]
+        for name, f in (("mul", operator.mul), ("sqdiff", kf.sqdiff)):
+            for dim, fn, x, tx in ((2, kf.matvec, x2, tx2), (1, kf.vecmat, x1, tx1)):
+                args = (tx, A) if dim == 1 else (A, tx)
+                got = fn(f, "+", *args).cpu().numpy()
+                ref = oracle.reduce_dim_x(buf, rows, cols, cs, x, dim, "+", name)
+                if np.dtype(dt).kind == "f":
+                    xv = x.astype(np.float64)
+                    T = M * (xv[None, :] if dim == 2 else xv[:, None]) if name == "mul" else \
+                        (M - (xv[None, :] if dim == 2 else xv[:, None])) ** 2
+                    bound = np.abs(T).sum(axis=1 if dim == 2 else 0) * (1e-6 if dt == np.float32 else 1e-12)
+                    assert np.all(np.abs(got - ref) <= bound + 1e-300), (rows, cols, name, dim)
+                else:
+                    assert np.array_equal(got, ref), (rows, cols, name, dim)
+
+
+def test_api_forms_and_errors(kf, dev):
+    rng = np.random.default_rng(73)
+    a = rng.random((40, 30))                                   # Julia 30 x 40
+    A = torch.from_numpy(a).to(dev).T
+    x = torch.from_numpy(rng.random(40)).to(dev)
+    y = torch.from_numpy(rng.random(30)).to(dev)
+    An = A.cpu().numpy()
+    np.testing.assert_allclose(kf.matvec(A, x).cpu().numpy(), An @ x.cpu().numpy(), rtol=1e-12)
+    np.testing.assert_allclose(kf.vecmat(y, A).cpu().numpy(), y.cpu().numpy() @ An, rtol=1e-12)
+    dst = torch.zeros(30, dtype=torch.float64, device=dev)
+    kf.matvec_(operator.mul, "+", dst, A, x)
+    np.testing.assert_allclose(dst.cpu().numpy(), An @ x.cpu().numpy(), rtol=1e-12)
+    dst2 = torch.zeros(40, dtype=torch.float64, device=dev)
+    kf.vecmat_(dst2, y, A)
+    np.testing.assert_allclose(dst2.cpu().numpy(), y.cpu().numpy() @ An, rtol=1e-12)
+    # x = nothing: plain row / column reductions; g = sqrt: row norms
+    np.testing.assert_allclose(kf.matvec(A, None).cpu().numpy(), An.sum(1), rtol=1e-12)
+    np.testing.assert_allclose(kf.matvec(kf.abs2, "+", A, None, g="sqrt").cpu().numpy(),
+                               np.sqrt((An ** 2).sum(1)), rtol=1e-12)
+    np.testing.assert_allclose(kf.vecmat(None, A).cpu().numpy(), An.sum(0), rtol=1e-12)
+    with pytest.raises(kf.ArgumentError):
+        kf.matvec(A, y)                                        # wrong length
+    with pytest.raises(kf.ArgumentError):
+        kf.matvec(A, x.float())                                # mixed types

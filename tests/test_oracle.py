@@ -184,3 +184,21 @@ def test_reduce2_matches_numpy_and_closed_forms(oracle):
     assert oracle.reduce2(r, r - 1, "+", "sqdiff") == n                     # unit differences
     i = np.array([2**16, 3], np.int32)
     assert oracle.reduce2(i, i) == np.int32(9)                              # 2^32 wraps to 0
+
+
+def test_matvec_vecmat_oracle_matches_numpy(oracle):
+    rng = np.random.default_rng(8)
+    rows, cols = 29, 17
+    A = np.asfortranarray(rng.standard_normal((rows, 2 * cols)))
+    buf = A.reshape(-1, order="F")
+    V = A[:, ::2]
+    x2, x1 = rng.standard_normal(cols), rng.standard_normal(rows)
+    np.testing.assert_allclose(oracle.reduce_dim_x(buf, rows, cols, 2 * rows, x2, 2), V @ x2, rtol=1e-12)
+    np.testing.assert_allclose(oracle.reduce_dim_x(buf, rows, cols, 2 * rows, x1, 1), x1 @ V, rtol=1e-12)
+    np.testing.assert_allclose(oracle.reduce_dim_x(buf, rows, cols, 2 * rows, x2, 2, "+", "sqdiff"),
+                               ((V - x2[None, :]) ** 2).sum(1), rtol=1e-12)
+    I = rng.integers(-9, 9, (rows, cols)).astype(np.int32)
+    xi = rng.integers(-9, 9, cols).astype(np.int32)
+    assert np.array_equal(oracle.reduce_dim_x(I.reshape(-1, order="F"), rows, cols, rows, xi, 2), I @ xi)
+    assert np.array_equal(oracle.reduce_dim_x(I.reshape(-1, order="F"), rows, cols, rows, xi, 2, "max"),
+                          (I * xi[None, :]).max(1))
