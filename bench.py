@@ -268,6 +268,22 @@ def bench_all(kf, dev, ceiling):
     V2 = A2[:, ::2]
     rec("C5d dims=2 view 65536x(4096/2)", 4 * 2**27 + 4 * 65536,
         lambda: kf.mapreduce_(kf.identity, "+", d2, V2, dims=2, tmp=t5))
+    # beyond the BASELINE configs: vector operands and layouts off the vector path
+    import operator
+    xv = torch.rand(4096, device=dev, generator=g)
+    rec("X1 matvec 65536x4096 F32", 4 * 2**28 + 8 * 65536 + 4 * 4096,
+        lambda: kf.matvec_(operator.mul, "+", d2, A2, xv, tmp=t5))
+    xr = torch.rand(4096, device=dev, generator=g)
+    rec("X2 vecmat 4096x65536 F32", 4 * 2**28 + 8 * 65536,
+        lambda: kf.vecmat_(operator.mul, "+", d1, xr, A1, tmp=t5))
+    xs = torch.rand(2**28, device=dev, generator=g)
+    ys = torch.empty_like(xs)
+    ts = tmp_for(kf.Scan1D, xs)
+    of1 = torch.empty(1, device=dev)
+    t3s = tmp_for(kf.MapReduce1D, xs)
+    rec("X3 scan F32 unaligned view x[1:] n=2^28-1", 8 * (2**28 - 1), lambda: kf.scan_("+", ys[1:], xs[1:], tmp=ts))
+    rec("X4 mapreduce F32 unaligned view x[1:]", 4 * (2**28 - 1),
+        lambda: kf.mapreduce_(kf.identity, "+", of1, xs[1:], tmp=t3s))
     os.makedirs(os.path.join(REPO, "gpurun_out"), exist_ok=True)
     with open(os.path.join(REPO, "gpurun_out", "bench_all.json"), "w") as fh:
         json.dump({"copy_ceiling_gbps": ceiling, "rows": rows}, fh, indent=1)

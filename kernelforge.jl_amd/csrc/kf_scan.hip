@@ -134,7 +134,12 @@ template <class T, class Op> __device__ inline T exclusive_first() {
 template <class T, class Op, class Map, bool EXCL, int BLOCK>
 __global__ __launch_bounds__(BLOCK) void scan_kernel(
     const T* src, int64_t src_stride, T* dst, int64_t dst_stride, int64_t n,
-    int64_t ntiles, uint64_t* scratch, int vec) {
+    int64_t ntiles, uint64_t* scratch, int vec, int off) {
+  // Tiles cover the virtual range [0, n + off): element i sits at virtual
+  // position i + off, so that when src and dst share a misalignment of `off`
+  // elements every interior tile starts on a 16-byte boundary. Virtual
+  // positions before `off` and after the end hold the identity and are
+  // never stored.
   using S = ScanShape<T, BLOCK>;
   constexpr int V = S::V, EPV = S::EPV;
   constexpr int kScanWaves = BLOCK / kWave;
@@ -159,13 +164,16 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
   const uint32_t epoch30 = (uint32_t)(tk >> 32) & 0x3fffffffu;
   uint64_t* desc = scratch + kScanHeaderBytes / sizeof(uint64_t);
 
-  const int64_t wbase = tile * S::TILE + (int64_t)wave * S::WAVE_ELEMS;  // this wave's chunk
-  const bool full = vec && (tile + 1) * S::TILE <= n;
+  const int64_t wbase = tile * S::TILE + (int64_t)wave * S::WAVE_ELEMS;  // this wave's virtual chunk
+  const int64_t nv = n + off;
+  const bool full = vec && (tile > 0 || off == 0) && (tile + 1) * S::TILE <= nv;
+  const T* srcv = src - off;  // 16-byte aligned when vec
+  T* dstv = dst - off;
 
   // ---- load, striped: lane holds vector j*64 + lane of the wave chunk ------
   T x[V][EPV];
   if (full) {
-    const uint4* g = reinterpret_cast<const uint4*>(src + wbase);
+    const uint4* g = reinterpret_cast<const uint4*>(srcv + wbase);
     uint4 r[V];
 #pragma unroll
     for (int j = 0; j < V; ++j) r[j] = ld_stream(g + j * kWave + lane);
@@ -180,8 +188,8 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
     for (int j = 0; j < V; ++j)
 #pragma unroll
       for (int k = 0; k < EPV; ++k) {
-        const int64_t idx = wbase + (int64_t)(j * kWave + lane) * EPV + k;
-        x[j][k] = idx < n ? Map::apply(src[idx * src_stride]) : id;
+        const int64_t idx = wbase + (int64_t)(j * kWave + lane) * EPV + k - off;  // real index
+        x[j][k] = (idx >= 0 && idx < n) ? Map::apply(src[idx * src_stride]) : id;
       }
   }
 
@@ -230,7 +238,7 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
       o[0] = Op::combine(prefix, rowpre[j]);
 #pragma unroll
       for (int k = 1; k < EPV; ++k) o[k] = Op::combine(prefix, x[j][k - 1]);
-      if (j == 0 && tile == 0 && tid == 0) o[0] = exclusive_first<T, Op>();
+      if (j == 0 && tile == 0 && tid == 0) o[off] = exclusive_first<T, Op>();  // element 0
     } else {
 #pragma unroll
       for (int k = 0; k < EPV; ++k) o[k] = Op::combine(prefix, x[j][k]);
@@ -238,12 +246,12 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
     if (full) {
       uint4 r;
       __builtin_memcpy(&r, o, 16);
-      st_stream(reinterpret_cast<uint4*>(dst + wbase) + j * kWave + lane, r);
+      st_stream(reinterpret_cast<uint4*>(dstv + wbase) + j * kWave + lane, r);
     } else {
 #pragma unroll
       for (int k = 0; k < EPV; ++k) {
-        const int64_t idx = wbase + (int64_t)(j * kWave + lane) * EPV + k;
-        if (idx < n) dst[idx * dst_stride] = o[k];
+        const int64_t idx = wbase + (int64_t)(j * kWave + lane) * EPV + k - off;
+        if (idx >= 0 && idx < n) dst[idx * dst_stride] = o[k];
       }
     }
   }
@@ -256,35 +264,41 @@ template <class T> bool scan_small_tiles(int64_t n) {
   return large < 512;
 }
 
-template <class T> int64_t scan_tiles(int64_t n) {
+// Tiles for n elements starting `off` elements after a 16-byte boundary.
+template <class T> int64_t scan_tiles(int64_t n, int off = 0) {
   const int64_t tile = scan_small_tiles<T>(n) ? ScanShape<T, kScanBlockSmall>::TILE : ScanShape<T>::TILE;
-  return (n + tile - 1) / tile;
+  return (n + off + tile - 1) / tile;
 }
 
 template <class T> size_t scan_scratch(int64_t n) {
-  return kScanHeaderBytes + (size_t)scan_tiles<T>(n) * kDescWords * sizeof(uint64_t);
+  constexpr int kMaxOff = 16 / (int)sizeof(T) - 1 > 0 ? 16 / (int)sizeof(T) - 1 : 0;
+  return kScanHeaderBytes + (size_t)scan_tiles<T>(n, kMaxOff) * kDescWords * sizeof(uint64_t);
 }
 
 template <class T, class Op, class Map, int BLOCK>
 void launch_scan_block(const void* src, int64_t ss, void* dst, int64_t ds, int64_t n, int excl, int64_t ntiles,
-                       int vec, void* scratch, hipStream_t stream) {
+                       int vec, int off, void* scratch, hipStream_t stream) {
   if (excl)
     hipLaunchKernelGGL((scan_kernel<T, Op, Map, true, BLOCK>), dim3((unsigned)ntiles), dim3(BLOCK), 0, stream,
-                       (const T*)src, ss, (T*)dst, ds, n, ntiles, (uint64_t*)scratch, vec);
+                       (const T*)src, ss, (T*)dst, ds, n, ntiles, (uint64_t*)scratch, vec, off);
   else
     hipLaunchKernelGGL((scan_kernel<T, Op, Map, false, BLOCK>), dim3((unsigned)ntiles), dim3(BLOCK), 0, stream,
-                       (const T*)src, ss, (T*)dst, ds, n, ntiles, (uint64_t*)scratch, vec);
+                       (const T*)src, ss, (T*)dst, ds, n, ntiles, (uint64_t*)scratch, vec, off);
 }
 
 template <class T, class Op, class Map>
 int launch_scan(const void* src, int64_t ss, void* dst, int64_t ds, int64_t n, int excl,
                 void* scratch, hipStream_t stream) {
-  const int64_t ntiles = scan_tiles<T>(n);
-  const int vec = ss == 1 && ds == 1 && ((uintptr_t)src % 16 == 0) && ((uintptr_t)dst % 16 == 0);
+  // Vector path when both operands are contiguous and equally misaligned
+  // (e.g. views src[k:], dst[k:] of aligned buffers); `off` shifts the tiles.
+  const int vec = ss == 1 && ds == 1 && ((uintptr_t)src % 16 == (uintptr_t)dst % 16) &&
+                  ((uintptr_t)src % sizeof(T) == 0);
+  const int off = vec ? (int)(((uintptr_t)src % 16) / sizeof(T)) : 0;
+  const int64_t ntiles = scan_tiles<T>(n, off);
   if (scan_small_tiles<T>(n))
-    launch_scan_block<T, Op, Map, kScanBlockSmall>(src, ss, dst, ds, n, excl, ntiles, vec, scratch, stream);
+    launch_scan_block<T, Op, Map, kScanBlockSmall>(src, ss, dst, ds, n, excl, ntiles, vec, off, scratch, stream);
   else
-    launch_scan_block<T, Op, Map, kScanBlock>(src, ss, dst, ds, n, excl, ntiles, vec, scratch, stream);
+    launch_scan_block<T, Op, Map, kScanBlock>(src, ss, dst, ds, n, excl, ntiles, vec, off, scratch, stream);
   return kf_check_launch("scan_kernel");
 }
 

@@ -201,6 +201,42 @@ def test_tile_size_switchover(kf, oracle, dev, dt):
             assert np.array_equal(run(kf, dev, x, "+", exclusive=exclusive), oracle.scan(x, "+", exclusive=exclusive))
 
 
+@pytest.mark.parametrize("dt", [np.int32, np.int64, np.uint8])
+def test_equally_misaligned_views_vector_path(kf, oracle, dev, dt):
+    # src[k:] scanned into dst[k:]: both start k elements past a 16-byte
+    # boundary, so the tile grid is shifted by k and interior tiles stay on
+    # the vector path; results must be exact at every offset and size
+    rng = np.random.default_rng(83)
+    epv = 16 // np.dtype(dt).itemsize
+    for n in (5, 4097, 8192 * 3 + 7, 512 * 32768 + 9, 1_000_003):
+        x = gen(rng, dt, n + epv)
+        src = torch.from_numpy(x).to(dev)
+        for k in sorted({1, epv // 2, epv - 1}):
+            for exclusive in (False, True):
+                out = torch.zeros(n + epv, dtype=src.dtype, device=dev)
+                kf.scan_("+", out[k:k + n], src[k:k + n], exclusive=exclusive)
+                got = out.cpu().numpy()
+                assert np.array_equal(got[k:k + n], oracle.scan(x[k:k + n], "+", exclusive=exclusive)), (n, k)
+                assert not got[:k].any() and not got[k + n:].any()   # nothing written outside the view
+
+
+def test_misaligned_affine_and_float(kf, oracle, dev):
+    rng = np.random.default_rng(89)
+    n = 300_001
+    ab = np.stack([rng.uniform(0.9, 1.0, n + 1), rng.standard_normal(n + 1)], 1).astype(np.float32)
+    t = torch.from_numpy(ab).to(dev)
+    out = torch.zeros_like(t)
+    kf.scan_(kf.affine, out[1:], t[1:])   # pairs offset by 8 bytes
+    assert_mixed(out[1:].cpu().numpy(), oracle.scan(ab[1:], "affine"), 1e-5, what="misaligned affine")
+    x = rng.random(n + 3)
+    tx = torch.from_numpy(x).to(dev)
+    y = torch.zeros_like(tx)
+    kf.scan_("+", y[1:], tx[1:], exclusive=True)
+    got = y[1:].cpu().numpy()
+    assert got[0] == 0 and not np.signbit(got[0])
+    assert_close(got, oracle.scan(x[1:], "+", exclusive=True), 1e-12, 1e-300, what="misaligned f64 excl")
+
+
 def test_errors(kf, dev):
     a = torch.zeros(10, device=dev)
     with pytest.raises(kf.ArgumentError):
