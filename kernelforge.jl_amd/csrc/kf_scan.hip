@@ -16,7 +16,7 @@
 //    row j (64 lanes x 16 bytes) is scanned in-lane, then across the wave
 //    with DPP row shifts/broadcasts, and rows are chained with a carry.
 //  * The lookback window lives in the top lanes of one wave: lane j reads
-//    the descriptor of tile (t - 64 + j) for the last kLookWindow lanes, so
+//    the descriptor of tile (t - 64 + j) for the last `win` lanes, so
 //    lane order is tile order and a DPP scan combines the window in the
 //    order a non-commutative op needs.
 //  * Each tile descriptor owns a 128-byte line (kDescWords words): tiles are
@@ -47,11 +47,12 @@ constexpr uint32_t kStatePartial = 1, kStatePrefix = 2;
 constexpr size_t kScanHeaderBytes = 256;
 constexpr int kDescWords = 16;             // 128 bytes per tile descriptor
 constexpr uint32_t kSpinLimit = 1u << 24;  // lookback polls before giving up (seconds)
-// Predecessors polled per lookback round (lanes 64-WIN..63). Each descriptor
-// is its own 128-byte line, and a poll completes only when its slowest line
-// returns: for large tiles 8 lines per poll measured 6.09 vs 5.82 TB/s for
-// 64. Small tiles (short arrays, all tiles in flight at once) keep 64.
-template <int BLOCK> constexpr int look_window() { return BLOCK == kScanBlock ? 8 : kWave; }
+// Predecessors polled per lookback round (lanes 64-win..63). Each
+// descriptor is its own 128-byte line, and a poll completes only when its
+// slowest line returns: with >= 512 tiles, 8 lines per poll measured 6.09 vs
+// 5.82 TB/s for 64; with fewer tiles (all in flight at once, long walks) the
+// full 64-tile window is faster (2^23 Float32: 14.8 vs 15.1 us).
+inline int look_window(int64_t ntiles) { return ntiles >= 512 ? 8 : kWave; }
 
 template <class T, int BLOCK = kScanBlock> struct ScanShape {
   static constexpr int EPV = 16 / (int)sizeof(T);   // elements per 16-byte vector
@@ -71,8 +72,8 @@ __device__ inline void publish(uint64_t* desc, int64_t tile, uint32_t tag, T v) 
 
 // Decoupled lookback, executed by one full wave. Returns the combination of
 // every tile before `tile` (tile > 0), in tile order.
-template <class T, class Op, int kLookWindow>
-__device__ inline T lookback(const uint64_t* desc, int64_t tile, uint32_t epoch30) {
+template <class T, class Op>
+__device__ inline T lookback(const uint64_t* desc, int64_t tile, uint32_t epoch30, int win) {
   constexpr int W = ScanShape<T>::W;
   const int lane = lane_id();
   const T id = Op::template identity<T>();
@@ -88,7 +89,7 @@ __device__ inline T lookback(const uint64_t* desc, int64_t tile, uint32_t epoch3
       return run;
     }
     const int64_t t = newest - (kWave - 1) + lane;
-    const bool in_win = lane >= kWave - kLookWindow;
+    const bool in_win = lane >= kWave - win;
     T v = id;
     // tiles before 0: an identity prefix; lanes outside the window: identity partials
     uint32_t state = in_win ? kStatePrefix : kStatePartial;
@@ -117,7 +118,7 @@ __device__ inline T lookback(const uint64_t* desc, int64_t tile, uint32_t epoch3
     } else if (invalid == 0) {
       const T tot = wave_reduce<Op>(v);
       run = Op::combine(tot, run);
-      newest -= kLookWindow;
+      newest -= win;
       continue;
     }
     __builtin_amdgcn_s_sleep(1);
@@ -134,7 +135,7 @@ template <class T, class Op> __device__ inline T exclusive_first() {
 template <class T, class Op, class Map, bool EXCL, int BLOCK>
 __global__ __launch_bounds__(BLOCK) void scan_kernel(
     const T* src, int64_t src_stride, T* dst, int64_t dst_stride, int64_t n,
-    int64_t ntiles, uint64_t* scratch, int vec, int off) {
+    int64_t ntiles, uint64_t* scratch, int vec, int off, int win) {
   // Tiles cover the virtual range [0, n + off): element i sits at virtual
   // position i + off, so that when src and dst share a misalignment of `off`
   // elements every interior tile starts on a 16-byte boundary. Virtual
@@ -220,7 +221,7 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
       if (lane == 0) publish(desc, tile, (epoch30 << 2) | kStatePrefix, agg);
     } else {
       if (lane == 0) publish(desc, tile, (epoch30 << 2) | kStatePartial, agg);
-      excl = lookback<T, Op, look_window<BLOCK>()>(desc, tile, epoch30);
+      excl = lookback<T, Op>(desc, tile, epoch30, win);
       if (lane == 0) publish(desc, tile, (epoch30 << 2) | kStatePrefix, Op::combine(excl, agg));
     }
     if (lane == 0) block_excl = excl;
@@ -257,11 +258,12 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
   }
 }
 
-// Large tiles unless that leaves fewer than two tiles per CU; a pure function
-// of (T, n) so the scratch query and the launch agree.
+// Large tiles unless the array holds fewer than 64 of them (measured: large
+// tiles win from 2^21 Float32 elements up, 256-thread tiles below); a pure
+// function of (T, n) so the scratch query and the launch agree.
 template <class T> bool scan_small_tiles(int64_t n) {
   const int64_t large = (n + ScanShape<T>::TILE - 1) / ScanShape<T>::TILE;
-  return large < 512;
+  return large < 64;
 }
 
 // Tiles for n elements starting `off` elements after a 16-byte boundary.
@@ -280,10 +282,12 @@ void launch_scan_block(const void* src, int64_t ss, void* dst, int64_t ds, int64
                        int vec, int off, void* scratch, hipStream_t stream) {
   if (excl)
     hipLaunchKernelGGL((scan_kernel<T, Op, Map, true, BLOCK>), dim3((unsigned)ntiles), dim3(BLOCK), 0, stream,
-                       (const T*)src, ss, (T*)dst, ds, n, ntiles, (uint64_t*)scratch, vec, off);
+                       (const T*)src, ss, (T*)dst, ds, n, ntiles, (uint64_t*)scratch, vec, off,
+                       look_window(ntiles));
   else
     hipLaunchKernelGGL((scan_kernel<T, Op, Map, false, BLOCK>), dim3((unsigned)ntiles), dim3(BLOCK), 0, stream,
-                       (const T*)src, ss, (T*)dst, ds, n, ntiles, (uint64_t*)scratch, vec, off);
+                       (const T*)src, ss, (T*)dst, ds, n, ntiles, (uint64_t*)scratch, vec, off,
+                       look_window(ntiles));
 }
 
 template <class T, class Op, class Map>

@@ -191,11 +191,12 @@ def test_views_offsets_strides_inplace(kf, oracle, dev):
 
 @pytest.mark.parametrize("dt", [np.int32, np.int64, np.uint8])
 def test_tile_size_switchover(kf, oracle, dev, dt):
-    # arrays with fewer than 512 large tiles use 256-thread tiles; check both
-    # sides of the switch (large tile = 128 KiB, 32 KiB for uint8)
+    # arrays with fewer than 64 large tiles use 256-thread tiles, and from 512
+    # tiles on the lookback polls 8 tiles per round; check both sides of both
+    # switches (large tile = 128 KiB, 32 KiB for uint8)
     large = 131072 // np.dtype(dt).itemsize if dt != np.uint8 else 32768
     rng = np.random.default_rng(23)
-    for n in (512 * large - 1, 512 * large, 512 * large + 1):
+    for n in (64 * large - 1, 64 * large, 64 * large + 1, 512 * large - 1, 512 * large + 1):
         x = gen(rng, dt, n)
         for exclusive in (False, True):
             assert np.array_equal(run(kf, dev, x, "+", exclusive=exclusive), oracle.scan(x, "+", exclusive=exclusive))
