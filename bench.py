@@ -284,6 +284,16 @@ def bench_all(kf, dev, ceiling):
     rec("X3 scan F32 unaligned view x[1:] n=2^28-1", 8 * (2**28 - 1), lambda: kf.scan_("+", ys[1:], xs[1:], tmp=ts))
     rec("X4 mapreduce F32 unaligned view x[1:]", 4 * (2**28 - 1),
         lambda: kf.mapreduce_(kf.identity, "+", of1, xs[1:], tmp=t3s))
+    del xs, ys
+    xd = torch.rand(2**27, device=dev, generator=g, dtype=torch.float64)
+    yd = torch.empty_like(xd)
+    td = tmp_for(kf.Scan1D, xd)
+    rec("X5 scan F64 incl n=2^27", 16 * 2**27, lambda: kf.scan_("+", yd, xd, tmp=td))
+    del xd, yd
+    xb = torch.randint(0, 255, (2**30,), device=dev, generator=g, dtype=torch.uint8)
+    yb = torch.empty_like(xb)
+    tb = tmp_for(kf.Scan1D, xb)
+    rec("X6 scan UInt8 incl n=2^30", 2 * 2**30, lambda: kf.scan_("+", yb, xb, tmp=tb))
     os.makedirs(os.path.join(REPO, "gpurun_out"), exist_ok=True)
     with open(os.path.join(REPO, "gpurun_out", "bench_all.json"), "w") as fh:
         json.dump({"copy_ceiling_gbps": ceiling, "rows": rows}, fh, indent=1)
