@@ -7,8 +7,8 @@
 // publish the tile's own PREFIX, apply the prefix and store. The MI355X
 // design differs from the reference in these ways:
 //
-//  * Tile = 1024 threads x 8 (2 for uint8) 16-byte vectors per lane =
-//    128 KiB (32 KiB for uint8), so 2^28 Float32 is 8192 tiles and the
+//  * Tile = 1024 threads x 8 16-byte vectors per lane = 128 KiB for
+//    every element type, so 2^28 Float32 is 8192 tiles and the
 //    per-tile lookback is amortised over a large streaming body. The tile
 //    stays in registers in "striped" order: lane l of wave w holds vector
 //    j*64 + l of the wave's contiguous chunk, so every load and store is a
@@ -56,7 +56,7 @@ inline int look_window(int64_t ntiles) { return ntiles >= 512 ? 8 : kWave; }
 
 template <class T, int BLOCK = kScanBlock> struct ScanShape {
   static constexpr int EPV = 16 / (int)sizeof(T);   // elements per 16-byte vector
-  static constexpr int V = sizeof(T) >= 4 ? 8 : 2;  // vectors per lane
+  static constexpr int V = 8;                       // vectors per lane
   static constexpr int WAVE_ELEMS = kWave * V * EPV;
   static constexpr int TILE = BLOCK * V * EPV;
   static constexpr int W = Words<T>::W;
@@ -132,6 +132,13 @@ template <class T, class Op> __device__ inline T exclusive_first() {
     return Op::template identity<T>();
 }
 
+// For sub-dword T, make the packed dwords of a vector the only live copy at
+// this point; the compiler would otherwise keep all V*EPV unpacked values
+// in registers between the phases of the scan (and spill).
+template <class T> __device__ inline void pin_packed(uint4& v) {
+  if constexpr (sizeof(T) < 4) asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w));
+}
+
 template <class T, class Op, class Map, bool EXCL, int BLOCK>
 __global__ __launch_bounds__(BLOCK) void scan_kernel(
     const T* src, int64_t src_stride, T* dst, int64_t dst_stride, int64_t n,
@@ -172,41 +179,54 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
   T* dstv = dst - off;
 
   // ---- load, striped: lane holds vector j*64 + lane of the wave chunk ------
-  T x[V][EPV];
+  // The tile stays packed in registers (4 dwords per vector whatever T is,
+  // so 16 uint8 elements cost what 4 floats do); each vector is unpacked
+  // only while it is being combined.
+  uint4 r[V];
   if (full) {
     const uint4* g = reinterpret_cast<const uint4*>(srcv + wbase);
-    uint4 r[V];
 #pragma unroll
     for (int j = 0; j < V; ++j) r[j] = ld_stream(g + j * kWave + lane);
+    if constexpr (!__is_same(Map, MapIdentity)) {
 #pragma unroll
-    for (int j = 0; j < V; ++j) {
-      __builtin_memcpy(x[j], &r[j], 16);
+      for (int j = 0; j < V; ++j) {
+        T x[EPV];
+        __builtin_memcpy(x, &r[j], 16);
 #pragma unroll
-      for (int k = 0; k < EPV; ++k) x[j][k] = Map::apply(x[j][k]);
+        for (int k = 0; k < EPV; ++k) x[k] = Map::apply(x[k]);
+        __builtin_memcpy(&r[j], x, 16);
+        pin_packed<T>(r[j]);
+      }
     }
   } else {
 #pragma unroll
-    for (int j = 0; j < V; ++j)
+    for (int j = 0; j < V; ++j) {
+      T x[EPV];
 #pragma unroll
       for (int k = 0; k < EPV; ++k) {
         const int64_t idx = wbase + (int64_t)(j * kWave + lane) * EPV + k - off;  // real index
-        x[j][k] = (idx >= 0 && idx < n) ? Map::apply(src[idx * src_stride]) : id;
+        x[k] = (idx >= 0 && idx < n) ? Map::apply(src[idx * src_stride]) : id;
       }
+      __builtin_memcpy(&r[j], x, 16);
+      pin_packed<T>(r[j]);
+    }
   }
 
-  // ---- in-lane, wave and row-chain scans; row prefixes folded in ----------
+  // ---- in-lane and wave scans; rowpre[j] = everything in the wave before
+  // vector j's lane (earlier rows and earlier lanes of row j) --------------
   T carry = id;
-  T rowpre[EXCL ? V : 1];
+  T rowpre[V];
 #pragma unroll
   for (int j = 0; j < V; ++j) {
+    T x[EPV];
+    __builtin_memcpy(x, &r[j], 16);
 #pragma unroll
-    for (int k = 1; k < EPV; ++k) x[j][k] = Op::combine(x[j][k - 1], x[j][k]);
-    const T incl = wave_inclusive_scan<Op>(x[j][EPV - 1]);
-    const T p = Op::combine(carry, wave_shift_right<Op>(incl));
+    for (int k = 1; k < EPV; ++k) x[k] = Op::combine(x[k - 1], x[k]);
+    __builtin_memcpy(&r[j], x, 16);
+    pin_packed<T>(r[j]);
+    const T incl = wave_inclusive_scan<Op>(x[EPV - 1]);
+    rowpre[j] = Op::combine(carry, wave_shift_right<Op>(incl));
     carry = Op::combine(carry, read_lane(incl, kWave - 1));
-    if constexpr (EXCL) rowpre[j] = p;
-#pragma unroll
-    for (int k = 0; k < EPV; ++k) x[j][k] = Op::combine(p, x[j][k]);
   }
   if (lane == 0) wave_agg[wave] = carry;
   __syncthreads();
@@ -234,20 +254,22 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
   // ---- apply and store ----------------------------------------------------
 #pragma unroll
   for (int j = 0; j < V; ++j) {
-    T o[EPV];
+    T x[EPV], o[EPV];
+    __builtin_memcpy(x, &r[j], 16);
+    const T p = Op::combine(prefix, rowpre[j]);
     if constexpr (EXCL) {
-      o[0] = Op::combine(prefix, rowpre[j]);
+      o[0] = p;
 #pragma unroll
-      for (int k = 1; k < EPV; ++k) o[k] = Op::combine(prefix, x[j][k - 1]);
+      for (int k = 1; k < EPV; ++k) o[k] = Op::combine(p, x[k - 1]);
       if (j == 0 && tile == 0 && tid == 0) o[off] = exclusive_first<T, Op>();  // element 0
     } else {
 #pragma unroll
-      for (int k = 0; k < EPV; ++k) o[k] = Op::combine(prefix, x[j][k]);
+      for (int k = 0; k < EPV; ++k) o[k] = Op::combine(p, x[k]);
     }
     if (full) {
-      uint4 r;
-      __builtin_memcpy(&r, o, 16);
-      st_stream(reinterpret_cast<uint4*>(dstv + wbase) + j * kWave + lane, r);
+      uint4 w;
+      __builtin_memcpy(&w, o, 16);
+      st_stream(reinterpret_cast<uint4*>(dstv + wbase) + j * kWave + lane, w);
     } else {
 #pragma unroll
       for (int k = 0; k < EPV; ++k) {

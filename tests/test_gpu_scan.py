@@ -14,7 +14,7 @@ pytestmark = pytest.mark.gpu
 
 EDGE = list(range(1, 11))
 TILE_EDGES = [63, 64, 65, 255, 256, 257, 1023, 1024, 1025, 2047, 2048, 2049, 4095, 4096, 4097, 8191, 8192,
-              8193, 16383, 16384, 16385, 32767, 32768, 32769, 65536 * 4 + 3]
+              8193, 16383, 16384, 16385, 32767, 32768, 32769, 131071, 131072, 131073, 65536 * 4 + 3]
 SIZES = EDGE + TILE_EDGES + [100_003, 1_000_000]
 
 
@@ -193,8 +193,8 @@ def test_views_offsets_strides_inplace(kf, oracle, dev):
 def test_tile_size_switchover(kf, oracle, dev, dt):
     # arrays with fewer than 64 large tiles use 256-thread tiles, and from 512
     # tiles on the lookback polls 8 tiles per round; check both sides of both
-    # switches (large tile = 128 KiB, 32 KiB for uint8)
-    large = 131072 // np.dtype(dt).itemsize if dt != np.uint8 else 32768
+    # switches (large tile = 128 KiB for every element type)
+    large = 131072 // np.dtype(dt).itemsize
     rng = np.random.default_rng(23)
     for n in (64 * large - 1, 64 * large, 64 * large + 1, 512 * large - 1, 512 * large + 1):
         x = gen(rng, dt, n)
