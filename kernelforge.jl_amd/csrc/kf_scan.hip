@@ -152,7 +152,7 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
   constexpr int V = S::V, EPV = S::EPV;
   constexpr int kScanWaves = BLOCK / kWave;
   __shared__ T wave_agg[kScanWaves];
-  __shared__ T block_excl;
+  __shared__ T wave_pre[kScanWaves];
   __shared__ uint64_t s_ticket;
 
   const int tid = threadIdx.x;
@@ -232,10 +232,13 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
   __syncthreads();
 
   // ---- publish, look back, publish the inclusive prefix (wave 0) ----------
+  // Lane w of wave 0 holds wave w's aggregate; a DPP scan over those lanes
+  // gives the tile aggregate and every wave's exclusive prefix in the tile.
   if (wave == 0) {
-    T agg = wave_agg[0];
-#pragma unroll
-    for (int w = 1; w < kScanWaves; ++w) agg = Op::combine(agg, wave_agg[w]);
+    const T wagg = lane < kScanWaves ? wave_agg[lane] : id;
+    const T wincl = wave_inclusive_scan<Op>(wagg);
+    const T wexcl = wave_shift_right<Op>(wincl);
+    const T agg = read_lane(wincl, kScanWaves - 1);
     T excl = id;
     if (tile == 0) {
       if (lane == 0) publish(desc, tile, (epoch30 << 2) | kStatePrefix, agg);
@@ -244,12 +247,10 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
       excl = lookback<T, Op>(desc, tile, epoch30, win);
       if (lane == 0) publish(desc, tile, (epoch30 << 2) | kStatePrefix, Op::combine(excl, agg));
     }
-    if (lane == 0) block_excl = excl;
+    if (lane < kScanWaves) wave_pre[lane] = lane == 0 ? excl : Op::combine(excl, wexcl);
   }
   __syncthreads();
-
-  T prefix = block_excl;
-  for (int w = 0; w < wave; ++w) prefix = Op::combine(prefix, wave_agg[w]);
+  const T prefix = wave_pre[wave];
 
   // ---- apply and store ----------------------------------------------------
 #pragma unroll
