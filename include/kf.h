@@ -10,9 +10,12 @@
  * before its first use (kf_scratch_reset does that on a stream). After that
  * the kernels keep it valid themselves (epoch-tagged tile descriptors and
  * self-resetting counters), so one scratch buffer may be reused across calls,
- * dtypes, operators and sizes without clearing. Calls that share a scratch
- * buffer must be ordered on one stream; concurrent calls need distinct
- * buffers.
+ * dtypes, operators and sizes without clearing. A buffer serves one family:
+ * scan calls (kf_scan), or reduction calls (kf_reduce, kf_reduce2,
+ * kf_reduce_dim*). Reduction partials written over scan descriptors could
+ * read as current ones, so never share one buffer between the two.
+ * Calls that share a scratch buffer must be ordered on one stream;
+ * concurrent calls need distinct buffers.
  *
  * Return codes: KF_OK, KF_EINVAL (bad enum, shape, stride or alignment),
  * KF_ENOSCRATCH (scratch missing or too small), KF_EHIP (a HIP error; the

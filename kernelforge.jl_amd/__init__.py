@@ -198,6 +198,11 @@ def _scratch(kind, need, device, tmp):
     if tmp is not None:
         if not isinstance(tmp, KernelBuffer):
             raise ArgumentError(f"tmp must be a KernelBuffer, got {type(tmp).__name__}")
+        if (tmp.kind == Scan1D) != (kind == Scan1D):
+            # scan descriptors and reduction partials must not share memory:
+            # a stale partial could read as a current-epoch descriptor
+            raise ArgumentError(f"tmp was allocated for {tmp.kind}; this call needs a "
+                                f"{'Scan1D' if kind == Scan1D else 'MapReduce'} buffer")
         if tmp.nbytes < need:
             raise ArgumentError(f"tmp holds {tmp.nbytes} bytes, this call needs {need}")
         return tmp

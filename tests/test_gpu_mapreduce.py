@@ -336,3 +336,43 @@ def test_post_map_g(kf, dev):
     with pytest.raises(kf.ArgumentError):
         kf.mapreduce(kf.identity, "+", A, dims=1, g=lambda v: v / 2)   # arbitrary g only on host scalars
     assert kf.mapreduce(kf.identity, "+", x, g=lambda v: v / 2) == pytest.approx(x.sum().item() / 2, rel=1e-12)
+
+
+def test_one_reduction_buffer_across_kinds_and_levels(kf, oracle, dev):
+    # One MapReduce buffer serves full reductions of one, two and three
+    # levels, two-array reductions, strided reductions and split dims
+    # reductions, in interleaved order, three times: any state a call left
+    # in the buffer that a later call relied on would corrupt a result.
+    import operator
+    rng = np.random.default_rng(101)
+    buf = kf.KernelBuffer(kf.MapReduce1D, 64 << 20, dev)
+    sizes = (1000, 300_000, 524_288, 524_289, (1 << 22) + 3, (1 << 24) + 5)
+    xs = {n: gen(rng, np.int32, n) for n in sizes}
+    ts = {n: torch.from_numpy(x).to(dev) for n, x in xs.items()}
+    rows, cols = 65536, 64
+    a = gen(rng, np.int32, rows * cols)
+    A = torch.from_numpy(a).to(dev).view(cols, rows).T          # column-major rows x cols
+    for rep in range(3):
+        for n in sizes:
+            for op in ("+", "max"):
+                got = kf.mapreduce(kf.identity, op, ts[n], tmp=buf)
+                assert got == int(oracle.reduce(xs[n], op)), (rep, n, op)
+            y = ts[n].flip(0).contiguous()
+            got = kf.mapreduce(operator.mul, "+", (ts[n], y), tmp=buf)
+            assert got == int(oracle.reduce2(xs[n], xs[n][::-1].copy(), "+", "mul")), (rep, n)
+            got = kf.mapreduce(kf.identity, "+", ts[n][::3], tmp=buf)
+            assert got == int(oracle.reduce(xs[n][::3], "+")), (rep, n, "strided")
+            for dim in (1, 2):
+                got = kf.mapreduce(kf.identity, "+", A, dims=dim, tmp=buf).cpu().numpy().ravel()
+                ref = oracle.reduce_dim(a, rows, cols, rows, dim, "+")
+                assert np.array_equal(got, ref), (rep, n, dim)
+
+
+def test_scan_buffer_is_refused_for_reductions(kf, dev):
+    x = torch.arange(100, dtype=torch.int32, device=dev)
+    sbuf = kf.get_allocation(kf.Scan1D, kf.identity, "+", x)
+    with pytest.raises(kf.ArgumentError):
+        kf.mapreduce(kf.identity, "+", x, tmp=sbuf)
+    rbuf = kf.KernelBuffer(kf.MapReduce1D, 1 << 20, dev)
+    with pytest.raises(kf.ArgumentError):
+        kf.scan_("+", torch.empty_like(x), x, tmp=rbuf)

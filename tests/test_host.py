@@ -70,3 +70,20 @@ def test_cpu_tensors_are_rejected(kf):
         kf.scan("+", x)
     with pytest.raises(kf.ArgumentError, match="GPU"):
         kf.mapreduce(kf.identity, "+", x)
+
+
+def test_scratch_family_check(kf):
+    # a scan buffer must not serve reductions and vice versa (reduction
+    # partials written over scan descriptors could read as current ones)
+    cpu = torch.device("cpu")
+    sbuf = kf.KernelBuffer(kf.Scan1D, 1024, cpu)
+    rbuf = kf.KernelBuffer(kf.MapReduce1D, 1024, cpu)
+    with pytest.raises(kf.ArgumentError):
+        kf._scratch(kf.MapReduce1D, 256, cpu, sbuf)
+    with pytest.raises(kf.ArgumentError):
+        kf._scratch(kf.MapReduce2D, 256, cpu, sbuf)
+    with pytest.raises(kf.ArgumentError):
+        kf._scratch(kf.Scan1D, 256, cpu, rbuf)
+    assert kf._scratch(kf.MapReduce2D, 256, cpu, rbuf) is rbuf      # one family: shared
+    with pytest.raises(kf.ArgumentError):
+        kf._scratch(kf.MapReduce1D, 4096, cpu, rbuf)                  # too small
