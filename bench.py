@@ -294,6 +294,12 @@ def bench_all(kf, dev, ceiling):
     yb = torch.empty_like(xb)
     tb = tmp_for(kf.Scan1D, xb)
     rec("X6 scan UInt8 incl n=2^30", 2 * 2**30, lambda: kf.scan_("+", yb, xb, tmp=tb))
+    del xb, yb
+    for n, label in ((10**5, "10^5"), (2**21, "2^21"), (2**23, "2^23")):
+        xs = torch.rand(n, device=dev, generator=g)
+        ys = torch.empty_like(xs)
+        ts = tmp_for(kf.Scan1D, xs)
+        rec(f"X7 scan F32 incl n={label}", 8 * n, lambda: kf.scan_("+", ys, xs, tmp=ts))
     os.makedirs(os.path.join(REPO, "gpurun_out"), exist_ok=True)
     with open(os.path.join(REPO, "gpurun_out", "bench_all.json"), "w") as fh:
         json.dump({"copy_ceiling_gbps": ceiling, "rows": rows}, fh, indent=1)

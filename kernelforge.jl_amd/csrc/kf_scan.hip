@@ -8,7 +8,8 @@
 // design differs from the reference in these ways:
 //
 //  * Tile = 1024 threads x 8 16-byte vectors per lane = 128 KiB for
-//    every element type, so 2^28 Float32 is 8192 tiles and the
+//    every element type (1, 2 or 4 vectors for arrays too small to make
+//    120 such tiles), so 2^28 Float32 is 8192 tiles and the
 //    per-tile lookback is amortised over a large streaming body. The tile
 //    stays in registers in "striped" order: lane l of wave w holds vector
 //    j*64 + l of the wave's contiguous chunk, so every load and store is a
@@ -42,7 +43,16 @@
 namespace kf {
 
 constexpr int kScanBlock = 1024;       // large tiles (default)
-constexpr int kScanBlockSmall = 256;   // small tiles: arrays too short to fill the GPU with large ones
+// Tile shapes: 1024 threads x kTierV[t] 16-byte vectors per lane (16 KiB
+// to 128 KiB). An array takes the largest shape that still cuts it into at
+// least kMinTiles tiles (scan_tier). Measured on MI355X over shapes of
+// 256-1024 threads x 1-8 vectors: 1024-thread tiles win at every size, and
+// fewer, larger tiles win once there are ~120 of them (Float32: 10^5 3.8 us
+// at 1 vector; 10^6 6.4-6.5 us at 2-4; 2^21 7.7 us at 4, 17.8 us with 64
+// tiles of 8; from 4*10^6 on 8 vectors).
+constexpr int kTiers = 4;
+constexpr int kTierV[kTiers] = {1, 2, 4, 8};
+constexpr int64_t kMinTiles = 120;
 constexpr uint32_t kStatePartial = 1, kStatePrefix = 2;
 constexpr size_t kScanHeaderBytes = 256;
 constexpr int kDescWords = 16;             // 128 bytes per tile descriptor
@@ -54,9 +64,9 @@ constexpr uint32_t kSpinLimit = 1u << 24;  // lookback polls before giving up (s
 // full 64-tile window is faster (2^23 Float32: 14.8 vs 15.1 us).
 inline int look_window(int64_t ntiles) { return ntiles >= 512 ? 8 : kWave; }
 
-template <class T, int BLOCK = kScanBlock> struct ScanShape {
+template <class T, int BLOCK = kScanBlock, int VPL = 8> struct ScanShape {
   static constexpr int EPV = 16 / (int)sizeof(T);   // elements per 16-byte vector
-  static constexpr int V = 8;                       // vectors per lane
+  static constexpr int V = VPL;                     // vectors per lane
   static constexpr int WAVE_ELEMS = kWave * V * EPV;
   static constexpr int TILE = BLOCK * V * EPV;
   static constexpr int W = Words<T>::W;
@@ -139,7 +149,7 @@ template <class T> __device__ inline void pin_packed(uint4& v) {
   if constexpr (sizeof(T) < 4) asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w));
 }
 
-template <class T, class Op, class Map, bool EXCL, int BLOCK>
+template <class T, class Op, class Map, bool EXCL, int BLOCK, int VPL>
 __global__ __launch_bounds__(BLOCK) void scan_kernel(
     const T* src, int64_t src_stride, T* dst, int64_t dst_stride, int64_t n,
     int64_t ntiles, uint64_t* scratch, int vec, int off, int win) {
@@ -148,7 +158,7 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
   // elements every interior tile starts on a 16-byte boundary. Virtual
   // positions before `off` and after the end hold the identity and are
   // never stored.
-  using S = ScanShape<T, BLOCK>;
+  using S = ScanShape<T, BLOCK, VPL>;
   constexpr int V = S::V, EPV = S::EPV;
   constexpr int kScanWaves = BLOCK / kWave;
   __shared__ T wave_agg[kScanWaves];
@@ -281,17 +291,22 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
   }
 }
 
-// Large tiles unless the array holds fewer than 64 of them (measured: large
-// tiles win from 2^21 Float32 elements up, 256-thread tiles below); a pure
-// function of (T, n) so the scratch query and the launch agree.
-template <class T> bool scan_small_tiles(int64_t n) {
-  const int64_t large = (n + ScanShape<T>::TILE - 1) / ScanShape<T>::TILE;
-  return large < 64;
+// Tile shape for n elements of T: a pure function of (T, n) so that the
+// scratch query and the launch agree.
+template <class T> int scan_tier(int64_t n) {
+  const int64_t bytes = n * (int64_t)sizeof(T);
+  int t = kTiers - 1;
+  while (t > 0 && bytes < kMinTiles * (int64_t)kScanBlock * kTierV[t] * 16) --t;
+  return t;
+}
+
+template <class T> int64_t tier_tile(int tier) {
+  return (int64_t)kScanBlock * kTierV[tier] * (16 / (int64_t)sizeof(T));
 }
 
 // Tiles for n elements starting `off` elements after a 16-byte boundary.
 template <class T> int64_t scan_tiles(int64_t n, int off = 0) {
-  const int64_t tile = scan_small_tiles<T>(n) ? ScanShape<T, kScanBlockSmall>::TILE : ScanShape<T>::TILE;
+  const int64_t tile = tier_tile<T>(scan_tier<T>(n));
   return (n + off + tile - 1) / tile;
 }
 
@@ -300,15 +315,16 @@ template <class T> size_t scan_scratch(int64_t n) {
   return kScanHeaderBytes + (size_t)scan_tiles<T>(n, kMaxOff) * kDescWords * sizeof(uint64_t);
 }
 
-template <class T, class Op, class Map, int BLOCK>
-void launch_scan_block(const void* src, int64_t ss, void* dst, int64_t ds, int64_t n, int excl, int64_t ntiles,
-                       int vec, int off, void* scratch, hipStream_t stream) {
+template <class T, class Op, class Map, int TIER>
+void launch_scan_tier(const void* src, int64_t ss, void* dst, int64_t ds, int64_t n, int excl, int64_t ntiles,
+                      int vec, int off, void* scratch, hipStream_t stream) {
+  constexpr int B = kScanBlock, V = kTierV[TIER];
   if (excl)
-    hipLaunchKernelGGL((scan_kernel<T, Op, Map, true, BLOCK>), dim3((unsigned)ntiles), dim3(BLOCK), 0, stream,
+    hipLaunchKernelGGL((scan_kernel<T, Op, Map, true, B, V>), dim3((unsigned)ntiles), dim3(B), 0, stream,
                        (const T*)src, ss, (T*)dst, ds, n, ntiles, (uint64_t*)scratch, vec, off,
                        look_window(ntiles));
   else
-    hipLaunchKernelGGL((scan_kernel<T, Op, Map, false, BLOCK>), dim3((unsigned)ntiles), dim3(BLOCK), 0, stream,
+    hipLaunchKernelGGL((scan_kernel<T, Op, Map, false, B, V>), dim3((unsigned)ntiles), dim3(B), 0, stream,
                        (const T*)src, ss, (T*)dst, ds, n, ntiles, (uint64_t*)scratch, vec, off,
                        look_window(ntiles));
 }
@@ -322,10 +338,12 @@ int launch_scan(const void* src, int64_t ss, void* dst, int64_t ds, int64_t n, i
                   ((uintptr_t)src % sizeof(T) == 0);
   const int off = vec ? (int)(((uintptr_t)src % 16) / sizeof(T)) : 0;
   const int64_t ntiles = scan_tiles<T>(n, off);
-  if (scan_small_tiles<T>(n))
-    launch_scan_block<T, Op, Map, kScanBlockSmall>(src, ss, dst, ds, n, excl, ntiles, vec, off, scratch, stream);
-  else
-    launch_scan_block<T, Op, Map, kScanBlock>(src, ss, dst, ds, n, excl, ntiles, vec, off, scratch, stream);
+  switch (scan_tier<T>(n)) {
+    case 0: launch_scan_tier<T, Op, Map, 0>(src, ss, dst, ds, n, excl, ntiles, vec, off, scratch, stream); break;
+    case 1: launch_scan_tier<T, Op, Map, 1>(src, ss, dst, ds, n, excl, ntiles, vec, off, scratch, stream); break;
+    case 2: launch_scan_tier<T, Op, Map, 2>(src, ss, dst, ds, n, excl, ntiles, vec, off, scratch, stream); break;
+    default: launch_scan_tier<T, Op, Map, 3>(src, ss, dst, ds, n, excl, ntiles, vec, off, scratch, stream);
+  }
   return kf_check_launch("scan_kernel");
 }
 

@@ -191,15 +191,18 @@ def test_views_offsets_strides_inplace(kf, oracle, dev):
 
 @pytest.mark.parametrize("dt", [np.int32, np.int64, np.uint8])
 def test_tile_size_switchover(kf, oracle, dev, dt):
-    # arrays with fewer than 64 large tiles use 256-thread tiles, and from 512
-    # tiles on the lookback polls 8 tiles per round; check both sides of both
-    # switches (large tile = 128 KiB for every element type)
-    large = 131072 // np.dtype(dt).itemsize
+    # tiles are 1024 threads x V 16-byte vectors, V in (1, 2, 4, 8): the
+    # largest V that still makes >= 120 tiles; from 512 tiles on the
+    # lookback polls 8 tiles per round. Check both sides of every switch.
+    epv = 16 // np.dtype(dt).itemsize
     rng = np.random.default_rng(23)
-    for n in (64 * large - 1, 64 * large, 64 * large + 1, 512 * large - 1, 512 * large + 1):
-        x = gen(rng, dt, n)
-        for exclusive in (False, True):
-            assert np.array_equal(run(kf, dev, x, "+", exclusive=exclusive), oracle.scan(x, "+", exclusive=exclusive))
+    edges = [120 * 1024 * v * epv for v in (2, 4, 8)] + [512 * 1024 * 8 * epv]
+    for e in edges:
+        for n in (e - 1, e, e + 1):
+            x = gen(rng, dt, n)
+            for exclusive in (False, True):
+                assert np.array_equal(run(kf, dev, x, "+", exclusive=exclusive),
+                                      oracle.scan(x, "+", exclusive=exclusive)), (n, exclusive)
 
 
 @pytest.mark.parametrize("dt", [np.int32, np.int64, np.uint8])
