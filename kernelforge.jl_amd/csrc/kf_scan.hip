@@ -44,15 +44,20 @@ namespace kf {
 
 constexpr int kScanBlock = 1024;       // large tiles (default)
 // Tile shapes: 1024 threads x kTierV[t] 16-byte vectors per lane (16 KiB
-// to 128 KiB). An array takes the largest shape that still cuts it into at
+// to 128 KiB; 512 threads for UInt8). An array takes the largest shape that still cuts it into at
 // least kMinTiles tiles (scan_tier). Measured on MI355X over shapes of
 // 256-1024 threads x 1-8 vectors: 1024-thread tiles win at every size, and
 // fewer, larger tiles win once there are ~120 of them (Float32: 10^5 3.8 us
 // at 1 vector; 10^6 6.4-6.5 us at 2-4; 2^21 7.7 us at 4, 17.8 us with 64
 // tiles of 8; from 4*10^6 on 8 vectors).
+// UInt8 tiles use 512 threads: its 16 elements per vector make the in-tile
+// work long enough that two co-resident workgroups per CU, one computing
+// while the other streams, win (2^30 UInt8: 5.74 vs 5.43 TB/s; 512-thread
+// tiles lose 1-5 % for the wider types).
 constexpr int kTiers = 4;
 constexpr int kTierV[kTiers] = {1, 2, 4, 8};
 constexpr int64_t kMinTiles = 120;
+template <class T> constexpr int scan_block() { return sizeof(T) == 1 ? 512 : kScanBlock; }
 constexpr uint32_t kStatePartial = 1, kStatePrefix = 2;
 constexpr size_t kScanHeaderBytes = 256;
 constexpr int kDescWords = 16;             // 128 bytes per tile descriptor
@@ -296,12 +301,12 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
 template <class T> int scan_tier(int64_t n) {
   const int64_t bytes = n * (int64_t)sizeof(T);
   int t = kTiers - 1;
-  while (t > 0 && bytes < kMinTiles * (int64_t)kScanBlock * kTierV[t] * 16) --t;
+  while (t > 0 && bytes < kMinTiles * (int64_t)scan_block<T>() * kTierV[t] * 16) --t;
   return t;
 }
 
 template <class T> int64_t tier_tile(int tier) {
-  return (int64_t)kScanBlock * kTierV[tier] * (16 / (int64_t)sizeof(T));
+  return (int64_t)scan_block<T>() * kTierV[tier] * (16 / (int64_t)sizeof(T));
 }
 
 // Tiles for n elements starting `off` elements after a 16-byte boundary.
@@ -318,7 +323,7 @@ template <class T> size_t scan_scratch(int64_t n) {
 template <class T, class Op, class Map, int TIER>
 void launch_scan_tier(const void* src, int64_t ss, void* dst, int64_t ds, int64_t n, int excl, int64_t ntiles,
                       int vec, int off, void* scratch, hipStream_t stream) {
-  constexpr int B = kScanBlock, V = kTierV[TIER];
+  constexpr int B = scan_block<T>(), V = kTierV[TIER];
   if (excl)
     hipLaunchKernelGGL((scan_kernel<T, Op, Map, true, B, V>), dim3((unsigned)ntiles), dim3(B), 0, stream,
                        (const T*)src, ss, (T*)dst, ds, n, ntiles, (uint64_t*)scratch, vec, off,

@@ -191,12 +191,14 @@ def test_views_offsets_strides_inplace(kf, oracle, dev):
 
 @pytest.mark.parametrize("dt", [np.int32, np.int64, np.uint8])
 def test_tile_size_switchover(kf, oracle, dev, dt):
-    # tiles are 1024 threads x V 16-byte vectors, V in (1, 2, 4, 8): the
-    # largest V that still makes >= 120 tiles; from 512 tiles on the
-    # lookback polls 8 tiles per round. Check both sides of every switch.
+    # tiles are 1024 threads (512 for uint8) x V 16-byte vectors, V in
+    # (1, 2, 4, 8): the largest V that still makes >= 120 tiles; from 512
+    # tiles on the lookback polls 8 tiles per round. Check both sides of
+    # every switch.
     epv = 16 // np.dtype(dt).itemsize
+    block = 512 if dt == np.uint8 else 1024
     rng = np.random.default_rng(23)
-    edges = [120 * 1024 * v * epv for v in (2, 4, 8)] + [512 * 1024 * 8 * epv]
+    edges = [120 * block * v * epv for v in (2, 4, 8)] + [512 * block * 8 * epv]
     for e in edges:
         for n in (e - 1, e, e + 1):
             x = gen(rng, dt, n)
