@@ -7,9 +7,10 @@
 // publish the tile's own PREFIX, apply the prefix and store. The MI355X
 // design differs from the reference in these ways:
 //
-//  * Tile = 1024 threads x 8 16-byte vectors per lane = 128 KiB for
-//    every element type (1, 2 or 4 vectors for arrays too small to make
-//    120 such tiles), so 2^28 Float32 is 8192 tiles and the
+//  * Tile = 1024 threads (768 for Float32 from 2^27 elements on, 512 for UInt8) x 8 16-byte
+//    vectors per lane = 128 KiB (96 KiB, 64 KiB; 1, 2 or 4 vectors for
+//    arrays too small to make 120 such tiles), so 2^28 Float32 is 10923
+//    tiles and the
 //    per-tile lookback is amortised over a large streaming body. The tile
 //    stays in registers in "striped" order: lane l of wave w holds vector
 //    j*64 + l of the wave's contiguous chunk, so every load and store is a
@@ -50,14 +51,26 @@ constexpr int kScanBlock = 1024;       // large tiles (default)
 // fewer, larger tiles win once there are ~120 of them (Float32: 10^5 3.8 us
 // at 1 vector; 10^6 6.4-6.5 us at 2-4; 2^21 7.7 us at 4, 17.8 us with 64
 // tiles of 8; from 4*10^6 on 8 vectors).
-// UInt8 tiles use 512 threads: its 16 elements per vector make the in-tile
-// work long enough that two co-resident workgroups per CU, one computing
-// while the other streams, win (2^30 UInt8: 5.74 vs 5.43 TB/s; 512-thread
-// tiles lose 1-5 % for the wider types).
+// Threads per tile by element type, measured at 2^28 Float32 / Int32,
+// 2^27 Float64, 2^26 affine pairs and 2^30 UInt8 over 512, 768 and 1024:
+// UInt8 (16 elements per vector, long in-tile work) gains most from two
+// co-resident workgroups per CU, one computing while the other streams
+// (512: 5.74 vs 5.43 TB/s at 1024); Float32 tiles of 768 threads (68
+// VGPRs, two workgroups per CU) run 6.18 vs 6.11 TB/s at 2^28 and 6.01
+// vs 5.94 at 2^27, but lose below (2^26 -2.5 %, 2^24 -20 %, smaller shapes
+// -15 %); Int32, Float64 and the affine pairs are fastest at 1024 (768:
+// -0.2 %, -2 %, -4 %).
 constexpr int kTiers = 4;
 constexpr int kTierV[kTiers] = {1, 2, 4, 8};
 constexpr int64_t kMinTiles = 120;
-template <class T> constexpr int scan_block() { return sizeof(T) == 1 ? 512 : kScanBlock; }
+// Float32 arrays of at least kF32WideBytes (2^27 elements) take the
+// 768-thread shape.
+constexpr int64_t kF32WideBytes = 1LL << 29;
+constexpr int kTierF32Wide = kTiers;  // tier index of that shape (8 vectors per lane)
+template <class T> constexpr int scan_block(int tier) {
+  return sizeof(T) == 1 ? 512 : tier == kTierF32Wide ? 768 : kScanBlock;
+}
+constexpr int tier_v(int tier) { return tier == kTierF32Wide ? 8 : kTierV[tier]; }
 constexpr uint32_t kStatePartial = 1, kStatePrefix = 2;
 constexpr size_t kScanHeaderBytes = 256;
 constexpr int kDescWords = 16;             // 128 bytes per tile descriptor
@@ -300,13 +313,14 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
 // scratch query and the launch agree.
 template <class T> int scan_tier(int64_t n) {
   const int64_t bytes = n * (int64_t)sizeof(T);
+  if (__is_same(T, float) && bytes >= kF32WideBytes) return kTierF32Wide;
   int t = kTiers - 1;
-  while (t > 0 && bytes < kMinTiles * (int64_t)scan_block<T>() * kTierV[t] * 16) --t;
+  while (t > 0 && bytes < kMinTiles * (int64_t)scan_block<T>(t) * kTierV[t] * 16) --t;
   return t;
 }
 
 template <class T> int64_t tier_tile(int tier) {
-  return (int64_t)scan_block<T>() * kTierV[tier] * (16 / (int64_t)sizeof(T));
+  return (int64_t)scan_block<T>(tier) * tier_v(tier) * (16 / (int64_t)sizeof(T));
 }
 
 // Tiles for n elements starting `off` elements after a 16-byte boundary.
@@ -323,7 +337,7 @@ template <class T> size_t scan_scratch(int64_t n) {
 template <class T, class Op, class Map, int TIER>
 void launch_scan_tier(const void* src, int64_t ss, void* dst, int64_t ds, int64_t n, int excl, int64_t ntiles,
                       int vec, int off, void* scratch, hipStream_t stream) {
-  constexpr int B = scan_block<T>(), V = kTierV[TIER];
+  constexpr int B = scan_block<T>(TIER), V = tier_v(TIER);
   if (excl)
     hipLaunchKernelGGL((scan_kernel<T, Op, Map, true, B, V>), dim3((unsigned)ntiles), dim3(B), 0, stream,
                        (const T*)src, ss, (T*)dst, ds, n, ntiles, (uint64_t*)scratch, vec, off,
@@ -347,7 +361,10 @@ int launch_scan(const void* src, int64_t ss, void* dst, int64_t ds, int64_t n, i
     case 0: launch_scan_tier<T, Op, Map, 0>(src, ss, dst, ds, n, excl, ntiles, vec, off, scratch, stream); break;
     case 1: launch_scan_tier<T, Op, Map, 1>(src, ss, dst, ds, n, excl, ntiles, vec, off, scratch, stream); break;
     case 2: launch_scan_tier<T, Op, Map, 2>(src, ss, dst, ds, n, excl, ntiles, vec, off, scratch, stream); break;
-    default: launch_scan_tier<T, Op, Map, 3>(src, ss, dst, ds, n, excl, ntiles, vec, off, scratch, stream);
+    case 3: launch_scan_tier<T, Op, Map, 3>(src, ss, dst, ds, n, excl, ntiles, vec, off, scratch, stream); break;
+    default:
+      if constexpr (__is_same(T, float))
+        launch_scan_tier<T, Op, Map, kTierF32Wide>(src, ss, dst, ds, n, excl, ntiles, vec, off, scratch, stream);
   }
   return kf_check_launch("scan_kernel");
 }
