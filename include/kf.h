@@ -195,11 +195,19 @@ int kf_reduce_dim_batched(kf_op op, kf_map f, kf_dtype dt,
 int kf_post_map(kf_post g, kf_dtype dt, void* x, int64_t n, int64_t stride, void* stream);
 
 /* ---------------------------------------------------------------- copy ----
- * dst[0:bytes] = src[0:bytes] with 16-byte streaming loads/stores: the
- * bandwidth ceiling the scan/reduce kernels are measured against.
- * Replaces the reference's vcopy! src/copy/copy.jl:24-28 /
- * copy_kernel! src/copy/copy_kernel.jl:3-18. */
+ * dst[0:bytes] = src[0:bytes] with 16-byte streaming loads/stores (when dst
+ * and src are equally misaligned, after a byte head): the bandwidth
+ * ceiling the scan/reduce kernels are measured against. Any element type:
+ * the copy is of bytes. Replaces the reference's vcopy!
+ * src/copy/copy.jl:24-28 / copy_kernel! src/copy/copy_kernel.jl:3-18. */
 int kf_copy(void* dst, const void* src, size_t bytes, void* stream);
+
+/* dst[i] = value for i < count, elements of value_bytes (1..64) bytes each;
+ * `value` is a host pointer, read before the call returns. 16-byte
+ * streaming stores when value_bytes divides 16 and dst is aligned to it,
+ * element-wise stores otherwise. Replaces the reference's setvalue!
+ * src/copy/copy.jl:52-56 / setvalue_kernel! src/copy/copy_kernel.jl:20-35. */
+int kf_fill(void* dst, int64_t count, const void* value, size_t value_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -29,6 +29,7 @@ gfx950. Calls are asynchronous on torch's current stream except the full
 `mapreduce`, which returns a host scalar (like the reference's
 `Array(dst)[1]`, src/mapreduce/1D/mapreduce1d.jl:203).
 """
+import ctypes
 import operator
 
 import torch
@@ -37,7 +38,7 @@ from . import _lib as _L
 
 __all__ = [
     "ArgumentError", "KernelBuffer", "AffineOp", "affine", "identity", "abs2", "sqdiff",
-    "scan", "scan_", "mapreduce", "mapreduce_", "get_allocation", "vcopy_",
+    "scan", "scan_", "mapreduce", "mapreduce_", "get_allocation", "vcopy_", "setvalue_",
     "Scan1D", "MapReduce1D", "MapReduce2D", "matvec", "matvec_", "vecmat", "vecmat_",
 ]
 
@@ -150,7 +151,6 @@ def _stream_ptr(t):
 
 
 def ctypes_void(x):
-    import ctypes
     return ctypes.c_void_p(x)
 
 
@@ -713,4 +713,28 @@ def vcopy_(dst, src):
     with torch.cuda.device(src.device):
         rc = _L.lib().kf_copy(ctypes_void(dst.data_ptr()), ctypes_void(src.data_ptr()), nb, _stream_ptr(src))
     _L.check(rc, "vcopy!")
+    return dst
+
+
+def setvalue_(dst, val):
+    """setvalue!(dst, val) (reference src/copy/copy.jl:52-56): every element
+    of the contiguous tensor dst becomes val. A tuple val fills the rows of a
+    2-D dst (one element = one row, e.g. affine (a, b) pairs)."""
+    _require_device(dst)
+    if not dst.is_contiguous():
+        raise ArgumentError("setvalue! needs a contiguous tensor")
+    if isinstance(val, (tuple, list)):
+        if dst.dim() != 2 or dst.shape[1] != len(val):
+            raise ArgumentError(f"a {len(val)}-tuple fills the rows of an (n, {len(val)}) tensor")
+        elem = torch.tensor(list(val), dtype=dst.dtype)
+        count = dst.shape[0]
+    else:
+        elem = torch.tensor([val], dtype=dst.dtype)
+        count = dst.numel()
+    raw = bytes(elem.view(torch.uint8).tolist())
+    buf = ctypes.create_string_buffer(raw, len(raw))
+    with torch.cuda.device(dst.device):
+        rc = _L.lib().kf_fill(ctypes_void(dst.data_ptr()), count, ctypes.cast(buf, ctypes.c_void_p), len(raw),
+                              _stream_ptr(dst))
+    _L.check(rc, "setvalue!")
     return dst

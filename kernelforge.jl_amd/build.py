@@ -13,7 +13,7 @@ REPO = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libkfhip.so")
-SOURCES = ["kf_api.hip", "kf_scan.hip", "kf_reduce.hip"]
+SOURCES = ["kf_api.hip", "kf_scan.hip", "kf_reduce.hip", "kf_copy.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [

@@ -696,21 +696,8 @@ template <class T, class Op, class Map> struct ReduceDimL {
 };
 
 // ---------------------------------------------------------------------------
-// Copy ceiling and scratch fill.
+// Post-map and scratch fill.
 // ---------------------------------------------------------------------------
-// One-shot copy: one 16-byte vector per thread, the grid covers the whole
-// buffer. Measured on MI355X: 6.7 TB/s, against 6.0 TB/s with 4 vectors per
-// thread, 5.2 TB/s for grid-stride copies and 5.0-5.5 TB/s for hipMemcpyDtoD.
-__global__ __launch_bounds__(256) void copy_kernel(uint4* dst, const uint4* src, int64_t nvec) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i < nvec) st_stream(dst + i, ld_stream(src + i));
-}
-
-__global__ void copy_bytes_kernel(uint8_t* dst, const uint8_t* src, int64_t n) {
-  const int64_t gsize = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gsize) dst[i] = src[i];
-}
-
 struct PostSqrt {
   __device__ static float apply(float x) { return __builtin_sqrtf(x); }
   __device__ static double apply(double x) { return __builtin_sqrt(x); }
@@ -930,30 +917,6 @@ extern "C" int kf_reduce_dim_x(kf_op op, kf_map2 f, kf_dtype dt, const void* A, 
     case KF_U8: return dispatch_dim_x<uint8_t>(op, f, A, rows, cols, col_stride, dim, dst, dst_stride, scratch, s, one, zero, x, x_stride);
     default: return kf_set_error(KF_EINVAL, "kf_reduce_dim_x: bad dtype %d", (int)dt);
   }
-}
-
-extern "C" int kf_copy(void* dst, const void* src, size_t bytes, void* stream) {
-  if (bytes == 0) return KF_OK;
-  if (!dst || !src) return kf_set_error(KF_EINVAL, "kf_copy: null pointer");
-  hipStream_t s = (hipStream_t)stream;
-  const int cap = kf_device_cu_count() * 8;
-  if ((uintptr_t)dst % 16 == 0 && (uintptr_t)src % 16 == 0) {
-    const int64_t nvec = (int64_t)(bytes / 16);
-    if (nvec > 0) {
-      const int64_t grid = (nvec + 255) / 256;
-      if (grid > 0x7fffffffLL) return kf_set_error(KF_EINVAL, "kf_copy: buffer exceeds the grid limit");
-      hipLaunchKernelGGL(copy_kernel, dim3((unsigned)grid), dim3(256), 0, s, (uint4*)dst, (const uint4*)src, nvec);
-    }
-    const int64_t rem = (int64_t)(bytes % 16);
-    if (rem)
-      hipLaunchKernelGGL(copy_bytes_kernel, dim3(1), dim3(64), 0, s, (uint8_t*)dst + nvec * 16,
-                         (const uint8_t*)src + nvec * 16, rem);
-  } else {
-    const int grid = (int)kmin<int64_t>(cap, kmax<int64_t>(1, ((int64_t)bytes + 255) / 256));
-    hipLaunchKernelGGL(copy_bytes_kernel, dim3(grid), dim3(256), 0, s, (uint8_t*)dst, (const uint8_t*)src,
-                       (int64_t)bytes);
-  }
-  return kf_check_launch("copy_kernel");
 }
 
 template <class T, class G> int launch_post(void* x, int64_t n, int64_t stride, hipStream_t s) {
