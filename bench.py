@@ -35,9 +35,10 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def time_calls(fn, reps, batches=5):
+def time_calls(fn, reps, batches=5, with_min=False):
     """Average seconds per call: `batches` event-timed batches of `reps`
-    back-to-back calls on the current stream; returns the median batch."""
+    back-to-back calls on the current stream; returns the median batch
+    (and the fastest batch when with_min)."""
     s = torch.cuda.current_stream()
     out = []
     for _ in range(batches):
@@ -48,7 +49,8 @@ def time_calls(fn, reps, batches=5):
         e1.record(s)
         e1.synchronize()
         out.append(e0.elapsed_time(e1) / 1e3 / reps)
-    return float(np.median(out))
+    med = float(np.median(out))
+    return (med, float(np.min(out))) if with_min else med
 
 
 def load_traffic():
@@ -61,11 +63,9 @@ def load_traffic():
     return None
 
 
-def cpu_baseline(oracle, budget_s=12.0):
-    threads = max(1, min(16, os.cpu_count() or 1))
-    n = N
-    x = np.random.default_rng(20261201).random(n, dtype=np.float32)
-    y = np.empty_like(x)
+def _cpu_rate(oracle, x, y, threads, budget_s):
+    """GB/s of steps (scan + sum over x) on `threads` host threads."""
+    n = x.shape[0]
     oracle.baseline_scan_add_f32(x[: 1 << 20], y[: 1 << 20], threads)
     reps, t0 = 0, time.perf_counter()
     while True:
@@ -75,10 +75,25 @@ def cpu_baseline(oracle, budget_s=12.0):
         el = time.perf_counter() - t0
         if el >= budget_s or reps >= 400:
             break
-    gbps = reps * 12 * n / el / 1e9
+    return reps * 12 * n / el / 1e9, reps, el
+
+
+def cpu_baseline(oracle, budget_s=12.0, single_budget_s=4.0):
+    """The reference's CPU path (Base.accumulate! + Base.mapreduce) restated in
+    C: multithreaded (two-pass chunked scan + chunked sum, OpenMP) on the whole
+    workload, and single-threaded (the sequential left folds) on 2^24 elements."""
+    threads = max(1, min(16, os.cpu_count() or 1))
+    x = np.random.default_rng(20261201).random(N, dtype=np.float32)
+    y = np.empty_like(x)
+    gbps, reps, el = _cpu_rate(oracle, x, y, threads, budget_s)
+    xs, ys = x[: 1 << 24], y[: 1 << 24]
+    g1, reps1, el1 = _cpu_rate(oracle, xs, ys, 1, single_budget_s)
     return {"value": round(gbps, 3), "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"{reps} steps of the same workload (2^28 F32 two-pass chunked scan + chunked sum, "
-                      f"Float32 arithmetic, OpenMP) on {threads} host threads, {el:.1f} s"}
+                      f"Float32 arithmetic, OpenMP) on {threads} host threads, {el:.1f} s",
+            "single_thread": {"value": round(g1, 3), "unit": "GB/s", "cores": 1,
+                              "sample": f"{reps1} steps of sequential accumulate + sum over the first 2^24 "
+                                        f"elements, {el1:.1f} s"}}
 
 
 def main():
@@ -135,8 +150,8 @@ def main():
     value = 12 * N / step_s / 1e9
 
     # per-kernel averages over the timed pattern (events on the launch stream)
-    scan_s = time_calls(do_scan, 20)
-    red_s = time_calls(do_reduce, 20)
+    scan_s, scan_min = time_calls(do_scan, 20, batches=10, with_min=True)
+    red_s, red_min = time_calls(do_reduce, 20, batches=10, with_min=True)
     cbuf = torch.empty_like(src)
 
     def do_copy():
@@ -185,6 +200,8 @@ def main():
             "scan_gbps": round(scan_gbps, 1), "scan_frac_of_copy": round(scan_gbps / ceiling, 4),
             "mapreduce_gbps": round(red_gbps, 1), "mapreduce_frac_of_copy": round(red_gbps / ceiling, 4),
             "mapreduce_frac_of_peak": round(red_gbps / PEAK_HBM_GBPS, 4), "mapreduce_avg_launch_us": round(red_s * 1e6, 2),
+            "scan_gbps_best_batch": round(8 * N / scan_min / 1e9, 1),
+            "mapreduce_gbps_best_batch": round(4 * N / red_min / 1e9, 1),
             "copy_kernel_gbps": round(copy_gbps, 1), "hipMemcpyDtoD_gbps": round(dtod_gbps, 1),
             "copy_ceiling_gbps": round(ceiling, 1),
         },
