@@ -29,6 +29,7 @@ gfx950. Calls are asynchronous on torch's current stream except the full
 `mapreduce`, which returns a host scalar (like the reference's
 `Array(dst)[1]`, src/mapreduce/1D/mapreduce1d.jl:203).
 """
+import contextlib
 import ctypes
 import operator
 
@@ -141,17 +142,37 @@ def _apply_post(g, t, n, stride):
     dt = _DTYPES.get(t.dtype)
     if dt is None:
         raise ArgumentError(f"post-map on unsupported element type {t.dtype}")
-    with torch.cuda.device(t.device):
+    with _on(t.device):
         rc = _L.lib().kf_post_map(code, dt, ctypes_void(t.data_ptr()), n, stride, _stream_ptr(t))
     _L.check(rc, "post-map g")
 
 
+_raw_stream_of = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def _raw_stream(device):
+    """hipStream_t (as an int) of the current stream on `device`."""
+    if _raw_stream_of is not None:
+        return _raw_stream_of(device.index)
+    return torch.cuda.current_stream(device).cuda_stream
+
+
 def _stream_ptr(t):
-    return ctypes_void(torch.cuda.current_stream(t.device).cuda_stream)
+    return _raw_stream(t.device)
 
 
 def ctypes_void(x):
-    return ctypes.c_void_p(x)
+    """A device address for a c_void_p argument (ctypes converts ints)."""
+    return x
+
+
+_NO_SWITCH = contextlib.nullcontext()
+
+
+def _on(device):
+    """Make `device` current for the launches in the block (no switch, and
+    no cost, when it already is)."""
+    return _NO_SWITCH if device.index == torch.cuda.current_device() else torch.cuda.device(device)
 
 
 def _require_device(*ts):
@@ -194,7 +215,7 @@ class KernelBuffer:
 _default_tmp = {}
 
 
-def _scratch(kind, need, device, tmp):
+def _scratch(kind, need, device, tmp, stream=None):
     if tmp is not None:
         if not isinstance(tmp, KernelBuffer):
             raise ArgumentError(f"tmp must be a KernelBuffer, got {type(tmp).__name__}")
@@ -206,7 +227,7 @@ def _scratch(kind, need, device, tmp):
         if tmp.nbytes < need:
             raise ArgumentError(f"tmp holds {tmp.nbytes} bytes, this call needs {need}")
         return tmp
-    key = (kind, device, torch.cuda.current_stream(device).cuda_stream)
+    key = (kind, device, _raw_stream(device) if stream is None else stream)
     buf = _default_tmp.get(key)
     if buf is None or buf.nbytes < need:
         buf = KernelBuffer(kind, max(need, 2 * (buf.nbytes if buf else 0)), device)
@@ -262,7 +283,7 @@ def scan_(*args, exclusive=False, tmp=None, g=None, **tuning):
     L = _L.lib()
     need = L.kf_scan_scratch_bytes(dt, opc, n)
     buf = _scratch(Scan1D, need, src.device, tmp)
-    with torch.cuda.device(src.device):
+    with _on(src.device):
         rc = L.kf_scan(opc, fc, dt, int(bool(exclusive)), ctypes_void(src.data_ptr()), ss,
                        ctypes_void(dst.data_ptr()), ds, n, ctypes_void(buf.ptr), buf.nbytes, _stream_ptr(src))
     _L.check(rc, "scan!")
@@ -379,7 +400,7 @@ def _reduce_full_into(fc, opc, dst, src, tmp):
         raise ArgumentError("reducing over an empty collection is not allowed")
     merged = _merge(list(src.shape), list(src.stride()))
     stream = _stream_ptr(src)
-    with torch.cuda.device(src.device):
+    with _on(src.device):
         if merged is not None:
             need = L.kf_reduce_scratch_bytes(dt, n)
             buf = _scratch(MapReduce1D, need, src.device, tmp)
@@ -404,7 +425,7 @@ def _reduce_dim_into(fc, opc, dst, dst_stride, src, rows, cols, cs, dim, tmp, ba
     need = L.kf_reduce_dim_scratch_bytes(dt, rows, cols, dim)
     buf = _scratch(MapReduce2D, need, src.device, tmp)
     ptr = src.data_ptr() if base_ptr is None else base_ptr
-    with torch.cuda.device(src.device):
+    with _on(src.device):
         rc = L.kf_reduce_dim(opc, fc, dt, ctypes_void(ptr), rows, cols, cs, dim, ctypes_void(dst.data_ptr()),
                              dst_stride, ctypes_void(buf.ptr), buf.nbytes, _stream_ptr(src))
     _L.check(rc, f"mapreduce(dims={dim})")
@@ -462,7 +483,7 @@ def _mapreduce_multi(f, op, srcs, dims, g, tmp):
     dt = _DTYPES[x.dtype]
     out = torch.empty(1, dtype=x.dtype, device=x.device)
     buf = _scratch(MapReduce1D, L.kf_reduce2_scratch_bytes(dt, n), x.device, tmp)
-    with torch.cuda.device(x.device):
+    with _on(x.device):
         rc = L.kf_reduce2(opc, fc, dt, ctypes_void(x.data_ptr()), x.stride(0) if n > 1 else 1,
                           ctypes_void(y.data_ptr()), y.stride(0) if n > 1 else 1, n, ctypes_void(out.data_ptr()),
                           ctypes_void(buf.ptr), buf.nbytes, _stream_ptr(x))
@@ -583,7 +604,7 @@ def _reduce_dims_general(fc, opc, dst, dst_stride, src, dims_t, tmp):
             out, out_stride = dst, dst_stride
         else:
             out, out_stride = _colmajor_empty(out_shape, src.dtype, src.device), 1
-        with torch.cuda.device(src.device):
+        with _on(src.device):
             if pre == 1 and mid_stride == 1:
                 # leading block of a (mid, post) matrix: dim-1 kernel
                 need = L.kf_reduce_dim_scratch_bytes(dt, mid, post, 1)
@@ -640,7 +661,7 @@ def _dim_x_into(f, op, dst, A, x, dim, g, tmp, name):
         L = _L.lib()
         dt = _DTYPES[A.dtype]
         buf = _scratch(MapReduce2D, L.kf_reduce_dim_scratch_bytes(dt, rows, cols, dim), A.device, tmp)
-        with torch.cuda.device(A.device):
+        with _on(A.device):
             rc = L.kf_reduce_dim_x(opc, fc, dt, ctypes_void(A.data_ptr()), rows, cols, cs, dim,
                                    ctypes_void(x.data_ptr()), x.stride(0) if k > 1 else 1,
                                    ctypes_void(dst.data_ptr()), dflat[1], ctypes_void(buf.ptr), buf.nbytes,
@@ -710,7 +731,7 @@ def vcopy_(dst, src):
     nb = src.numel() * src.element_size()
     if dst.numel() * dst.element_size() != nb:
         raise ArgumentError("vcopy!: size mismatch")
-    with torch.cuda.device(src.device):
+    with _on(src.device):
         rc = _L.lib().kf_copy(ctypes_void(dst.data_ptr()), ctypes_void(src.data_ptr()), nb, _stream_ptr(src))
     _L.check(rc, "vcopy!")
     return dst
@@ -733,7 +754,7 @@ def setvalue_(dst, val):
         count = dst.numel()
     raw = bytes(elem.view(torch.uint8).tolist())
     buf = ctypes.create_string_buffer(raw, len(raw))
-    with torch.cuda.device(dst.device):
+    with _on(dst.device):
         rc = _L.lib().kf_fill(ctypes_void(dst.data_ptr()), count, ctypes.cast(buf, ctypes.c_void_p), len(raw),
                               _stream_ptr(dst))
     _L.check(rc, "setvalue!")
