@@ -113,6 +113,14 @@ int kf_scan(kf_op op, kf_map f, kf_dtype dt, int exclusive,
             void* dst, int64_t dst_stride, int64_t n,
             void* scratch, size_t scratch_bytes, void* stream);
 
+/* Diagnostics (no counterpart in the reference): *gave_up = 1 if a scan on
+ * this scratch since the last query stopped waiting for a predecessor tile
+ * (after 2^24 lookback polls; its results are then invalid). That cannot
+ * happen unless the scratch was corrupted or shared by overlapping calls.
+ * Clears the flag. Synchronises `stream` (the one exception to the
+ * no-synchronisation rule above). */
+int kf_scan_scratch_status(void* scratch, void* stream, int* gave_up);
+
 /* -------------------------------------------------------------- reduce ----
  * dst[0] = f(src[0]) op f(src[stride]) op ... (n terms), written on device.
  * op must be commutative (ADD, MAX, MIN). The result is deterministic: the

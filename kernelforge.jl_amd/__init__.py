@@ -39,7 +39,7 @@ from . import _lib as _L
 
 __all__ = [
     "ArgumentError", "KernelBuffer", "AffineOp", "affine", "identity", "abs2", "sqdiff",
-    "scan", "scan_", "mapreduce", "mapreduce_", "get_allocation", "vcopy_", "setvalue_",
+    "scan", "scan_", "mapreduce", "mapreduce_", "get_allocation", "vcopy_", "setvalue_", "scan_status",
     "Scan1D", "MapReduce1D", "MapReduce2D", "matvec", "matvec_", "vecmat", "vecmat_",
 ]
 
@@ -289,6 +289,20 @@ def scan_(*args, exclusive=False, tmp=None, g=None, **tuning):
     _L.check(rc, "scan!")
     _apply_post(g, dst, n, ds)  # g as one extra in-place pass over dst
     return dst
+
+
+def scan_status(tmp):
+    """True if a scan! on the Scan1D buffer `tmp` gave up waiting for a
+    predecessor tile since the last query (its results are then invalid:
+    only a corrupted or concurrently shared buffer can cause it). Clears the
+    flag; synchronises the current stream. No counterpart in the reference."""
+    if not isinstance(tmp, KernelBuffer) or tmp.kind != Scan1D:
+        raise ArgumentError("scan_status takes the Scan1D KernelBuffer of a scan! call")
+    flag = ctypes.c_int(0)
+    with _on(tmp.arr.device):
+        rc = _L.lib().kf_scan_scratch_status(tmp.ptr, _raw_stream(tmp.arr.device), ctypes.byref(flag))
+    _L.check(rc, "scan_status")
+    return bool(flag.value)
 
 
 def scan(*args, exclusive=False, tmp=None, g=None, **tuning):

@@ -37,6 +37,7 @@ SIGNATURES = {
     "kf_reduce_dim_x": ([_I, _I, _I, _P, _I64, _I64, _I64, _I, _P, _I64, _P, _I64, _P, _SZ, _P], _I),
     "kf_post_map": ([_I, _I, _P, _I64, _I64, _P], _I),
     "kf_copy": ([_P, _P, _SZ, _P], _I),
+    "kf_scan_scratch_status": ([_P, _P, ctypes.POINTER(ctypes.c_int)], _I),
     "kf_fill": ([_P, _I64, _P, _SZ, _P], _I),
 }
 

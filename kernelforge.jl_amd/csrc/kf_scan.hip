@@ -398,6 +398,23 @@ int scan_op(kf_op op, kf_map f, const void* src, int64_t ss, void* dst, int64_t 
 
 using namespace kf;
 
+namespace kf {
+__global__ void clear_word_kernel(uint64_t* w) { *w = 0; }
+}  // namespace kf
+
+extern "C" int kf_scan_scratch_status(void* scratch, void* stream, int* gave_up) {
+  if (!scratch || !gave_up) return kf_set_error(KF_EINVAL, "kf_scan_scratch_status: null pointer");
+  hipStream_t s = (hipStream_t)stream;
+  uint64_t* flag = (uint64_t*)scratch + 1;  // header word 1
+  uint64_t w = 0;
+  if (hipMemcpyAsync(&w, flag, sizeof w, hipMemcpyDeviceToHost, s) != hipSuccess ||
+      hipStreamSynchronize(s) != hipSuccess)
+    return kf_check_launch("kf_scan_scratch_status");
+  *gave_up = (w & 1) != 0;
+  if (w != 0) hipLaunchKernelGGL(clear_word_kernel, dim3(1), dim3(1), 0, s, flag);
+  return kf_check_launch("clear_word_kernel");
+}
+
 extern "C" size_t kf_scan_scratch_bytes(kf_dtype dt, kf_op op, int64_t n) {
   (void)op;
   if (n < 0) n = 0;

@@ -20,7 +20,7 @@ def test_header_declares_the_expected_surface():
         "kf_version", "kf_last_error", "kf_scratch_reset", "kf_scan_scratch_bytes", "kf_scan",
         "kf_reduce_scratch_bytes", "kf_reduce", "kf_reduce_dim_scratch_bytes", "kf_reduce_dim", "kf_copy",
         "kf_reduce2_scratch_bytes", "kf_reduce2", "kf_reduce_dim_batched_scratch_bytes", "kf_reduce_dim_batched", "kf_post_map", "kf_reduce_dim_x",
-        "kf_fill"])
+        "kf_fill", "kf_scan_scratch_status"])
 
 
 def test_library_exports_every_declared_symbol(kf):
@@ -80,6 +80,8 @@ def test_invalid_arguments_rejected_without_gpu(kf):
     assert L.kf_reduce_dim(K.OP_ADD, 0, K.F32, p, 4, 4, 4, 3, q, 1, q, 1 << 20, None) == K.KF_EINVAL
     assert L.kf_reduce_dim(K.OP_ADD, 0, K.F32, p, 4, 4, 2, 1, q, 1, q, 1 << 20, None) == K.KF_EINVAL
     assert L.kf_copy(p, p, 0, None) == K.KF_OK
+    flag = ctypes.c_int(0)
+    assert L.kf_scan_scratch_status(None, None, ctypes.byref(flag)) == K.KF_EINVAL
     # fill: count 0 is a no-op; bad count, missing value, value size 0 or > 64
     v = ctypes.create_string_buffer(b"\x01" * 65, 65)
     assert L.kf_fill(p, 0, v, 4, None) == K.KF_OK

@@ -165,6 +165,13 @@ def test_reused_tmp_changing_data(kf, oracle, dev):
         assert np.array_equal(dst.cpu().numpy(), oracle.scan(x, "max"))
     # header word 1 is the lookback's give-up flag: never raised
     assert int(tmp.arr[8:16].cpu().numpy().view(np.uint64)[0]) == 0
+    assert kf.scan_status(tmp) is False
+    # the status query reads and clears the flag (set here from the host)
+    tmp.arr[8] = 1
+    assert kf.scan_status(tmp) is True
+    assert kf.scan_status(tmp) is False
+    with pytest.raises(kf.ArgumentError):
+        kf.scan_status(kf.get_allocation(kf.MapReduce1D, kf.identity, "+", x0))
 
 
 def test_views_offsets_strides_inplace(kf, oracle, dev):
