@@ -93,8 +93,11 @@ const char* kf_last_error(void);
 int kf_scratch_reset(void* scratch, size_t bytes, void* stream);
 
 /* ---------------------------------------------------------------- scan ----
- * dst[i] = f(src[0]) op ... op f(src[i])              (exclusive = 0)
- * dst[0] = identity(op); dst[i] = incl[i-1]            (exclusive = 1)
+ * dst[i] = g(f(src[0]) op ... op f(src[i]))           (exclusive = 0)
+ * dst[0] = g(identity(op)); dst[i] = g(incl[i-1])      (exclusive = 1)
+ * g (KF_POST_*) is applied to each stored value only, never to the running
+ * prefix, as the reference's kernels do (scan_kernel.jl:284-295); sqrt
+ * needs a floating-point type, the affine scan takes no g.
  * Strides are in elements (1 = contiguous). src and dst may alias only
  * exactly (in-place scan, same pointer and stride).
  *
@@ -108,7 +111,7 @@ int kf_scratch_reset(void* scratch, size_t bytes, void* stream);
  * perfs/rocm_cpp/hipcub_hipcc/rocprim_scan_benchmark.cpp). */
 size_t kf_scan_scratch_bytes(kf_dtype dt, kf_op op, int64_t n);
 
-int kf_scan(kf_op op, kf_map f, kf_dtype dt, int exclusive,
+int kf_scan(kf_op op, kf_map f, kf_post g, kf_dtype dt, int exclusive,
             const void* src, int64_t src_stride,
             void* dst, int64_t dst_stride, int64_t n,
             void* scratch, size_t scratch_bytes, void* stream);
@@ -197,9 +200,8 @@ int kf_reduce_dim_batched(kf_op op, kf_map f, kf_dtype dt,
                           void* scratch, size_t scratch_bytes, void* stream);
 
 /* x[i*stride] = g(x[i*stride]) for i < n, in place. Applies the reference's
- * post-map `g` (mapreduce(f, op, x; dims, g), src/mapreduce/mapreduce.jl:51-58;
- * scan!(f, op, dst, src; g), src/scan/scan.jl:261-271) to reduction outputs
- * and, as one extra pass, to scan outputs. */
+ * post-map `g` (mapreduce(f, op, x; dims, g), src/mapreduce/mapreduce.jl:51-58)
+ * to reduction outputs (kf_scan applies g itself as it stores). */
 int kf_post_map(kf_post g, kf_dtype dt, void* x, int64_t n, int64_t stride, void* stream);
 
 /* ---------------------------------------------------------------- copy ----

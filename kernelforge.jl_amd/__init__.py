@@ -284,10 +284,9 @@ def scan_(*args, exclusive=False, tmp=None, g=None, **tuning):
     need = L.kf_scan_scratch_bytes(dt, opc, n)
     buf = _scratch(Scan1D, need, src.device, tmp)
     with _on(src.device):
-        rc = L.kf_scan(opc, fc, dt, int(bool(exclusive)), ctypes_void(src.data_ptr()), ss,
+        rc = L.kf_scan(opc, fc, _post_code(g), dt, int(bool(exclusive)), ctypes_void(src.data_ptr()), ss,
                        ctypes_void(dst.data_ptr()), ds, n, ctypes_void(buf.ptr), buf.nbytes, _stream_ptr(src))
-    _L.check(rc, "scan!")
-    _apply_post(g, dst, n, ds)  # g as one extra in-place pass over dst
+    _L.check(rc, "scan!")  # g is applied by the kernel as each value is stored
     return dst
 
 

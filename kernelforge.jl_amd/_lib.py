@@ -25,7 +25,7 @@ SIGNATURES = {
     "kf_last_error": ([], ctypes.c_char_p),
     "kf_scratch_reset": ([_P, _SZ, _P], _I),
     "kf_scan_scratch_bytes": ([_I, _I, _I64], _SZ),
-    "kf_scan": ([_I, _I, _I, _I, _P, _I64, _P, _I64, _I64, _P, _SZ, _P], _I),
+    "kf_scan": ([_I, _I, _I, _I, _I, _P, _I64, _P, _I64, _I64, _P, _SZ, _P], _I),
     "kf_reduce_scratch_bytes": ([_I, _I64], _SZ),
     "kf_reduce": ([_I, _I, _I, _P, _I64, _I64, _P, _P, _SZ, _P], _I),
     "kf_reduce_dim_scratch_bytes": ([_I, _I64, _I64, _I], _SZ),

@@ -153,6 +153,20 @@ __device__ inline T lookback(const uint64_t* desc, int64_t tile, uint32_t epoch3
   }
 }
 
+// The post-map g on a stored value: sqrt or abs2 for floats, abs2
+// (wrapping) for integers; kf_scan rejects anything else.
+template <class T> __device__ inline T post_apply(int post, T v) {
+  if constexpr (__is_same(T, f32x2)) {
+    return v;
+  } else if constexpr (__is_same(T, float)) {
+    return post == KF_POST_SQRT ? __builtin_sqrtf(v) : v * v;
+  } else if constexpr (__is_same(T, double)) {
+    return post == KF_POST_SQRT ? __builtin_sqrt(v) : v * v;
+  } else {
+    return MapAbs2::apply(v);
+  }
+}
+
 template <class T, class Op> __device__ inline T exclusive_first() {
   if constexpr (__is_same(Op, OpAdd) && (__is_same(T, float) || __is_same(T, double)))
     return T(0);  // +0.0, as Julia / CUB produce for the first exclusive sum
@@ -170,7 +184,7 @@ template <class T> __device__ inline void pin_packed(uint4& v) {
 template <class T, class Op, class Map, bool EXCL, int BLOCK, int VPL>
 __global__ __launch_bounds__(BLOCK) void scan_kernel(
     const T* src, int64_t src_stride, T* dst, int64_t dst_stride, int64_t n,
-    int64_t ntiles, uint64_t* scratch, int vec, int off, int win) {
+    int64_t ntiles, uint64_t* scratch, int vec, int off, int win, int post) {
   // Tiles cover the virtual range [0, n + off): element i sits at virtual
   // position i + off, so that when src and dst share a misalignment of `off`
   // elements every interior tile starts on a 16-byte boundary. Virtual
@@ -295,6 +309,10 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
 #pragma unroll
       for (int k = 0; k < EPV; ++k) o[k] = Op::combine(p, x[k]);
     }
+    if (post != KF_POST_IDENTITY) {  // the reference's g, applied at the store only
+#pragma unroll
+      for (int k = 0; k < EPV; ++k) o[k] = post_apply(post, o[k]);
+    }
     if (full) {
       uint4 w;
       __builtin_memcpy(&w, o, 16);
@@ -334,18 +352,21 @@ template <class T> size_t scan_scratch(int64_t n) {
   return kScanHeaderBytes + (size_t)scan_tiles<T>(n, kMaxOff) * kDescWords * sizeof(uint64_t);
 }
 
+// `mode` below carries the exclusive flag in bit 0 and the post-map g
+// (kf_post) in the bits above.
 template <class T, class Op, class Map, int TIER>
-void launch_scan_tier(const void* src, int64_t ss, void* dst, int64_t ds, int64_t n, int excl, int64_t ntiles,
+void launch_scan_tier(const void* src, int64_t ss, void* dst, int64_t ds, int64_t n, int mode, int64_t ntiles,
                       int vec, int off, void* scratch, hipStream_t stream) {
   constexpr int B = scan_block<T>(TIER), V = tier_v(TIER);
-  if (excl)
+  const int post = mode >> 1;
+  if (mode & 1)
     hipLaunchKernelGGL((scan_kernel<T, Op, Map, true, B, V>), dim3((unsigned)ntiles), dim3(B), 0, stream,
                        (const T*)src, ss, (T*)dst, ds, n, ntiles, (uint64_t*)scratch, vec, off,
-                       look_window(ntiles));
+                       look_window(ntiles), post);
   else
     hipLaunchKernelGGL((scan_kernel<T, Op, Map, false, B, V>), dim3((unsigned)ntiles), dim3(B), 0, stream,
                        (const T*)src, ss, (T*)dst, ds, n, ntiles, (uint64_t*)scratch, vec, off,
-                       look_window(ntiles));
+                       look_window(ntiles), post);
 }
 
 template <class T, class Op, class Map>
@@ -429,11 +450,17 @@ extern "C" size_t kf_scan_scratch_bytes(kf_dtype dt, kf_op op, int64_t n) {
   return 0;
 }
 
-extern "C" int kf_scan(kf_op op, kf_map f, kf_dtype dt, int exclusive, const void* src,
+extern "C" int kf_scan(kf_op op, kf_map f, kf_post g, kf_dtype dt, int exclusive, const void* src,
                        int64_t src_stride, void* dst, int64_t dst_stride, int64_t n, void* scratch,
                        size_t scratch_bytes, void* stream) {
   int rc = kf_validate_op(op, f, dt, /*allow_affine=*/1);
   if (rc) return rc;
+  if (g != KF_POST_IDENTITY && g != KF_POST_SQRT && g != KF_POST_ABS2)
+    return kf_set_error(KF_EINVAL, "kf_scan: unknown post-map g = %d", (int)g);
+  if (g != KF_POST_IDENTITY && dt == KF_F32X2)
+    return kf_set_error(KF_EINVAL, "kf_scan: the affine scan takes no post-map");
+  if (g == KF_POST_SQRT && dt != KF_F32 && dt != KF_F64)
+    return kf_set_error(KF_EINVAL, "kf_scan: sqrt post-map needs a floating-point type");
   if (n < 0) return kf_set_error(KF_EINVAL, "kf_scan: n = %lld < 0", (long long)n);
   if (n == 0) return KF_OK;
   if (!src || !dst) return kf_set_error(KF_EINVAL, "kf_scan: null src or dst");
@@ -461,13 +488,14 @@ extern "C" int kf_scan(kf_op op, kf_map f, kf_dtype dt, int exclusive, const voi
   if (scan_tiles<f32x2>(n) * kScanBlock > (int64_t)0xffffffffLL)
     return kf_set_error(KF_EINVAL, "kf_scan: n = %lld exceeds the grid limit", (long long)n);
   hipStream_t s = (hipStream_t)stream;
+  const int mode = (exclusive ? 1 : 0) | ((int)g << 1);
   switch (dt) {
-    case KF_F32: return scan_op<float>(op, f, src, src_stride, dst, dst_stride, n, exclusive, scratch, s);
-    case KF_F64: return scan_op<double>(op, f, src, src_stride, dst, dst_stride, n, exclusive, scratch, s);
-    case KF_I32: return scan_op<int32_t>(op, f, src, src_stride, dst, dst_stride, n, exclusive, scratch, s);
-    case KF_I64: return scan_op<int64_t>(op, f, src, src_stride, dst, dst_stride, n, exclusive, scratch, s);
-    case KF_U8: return scan_op<uint8_t>(op, f, src, src_stride, dst, dst_stride, n, exclusive, scratch, s);
-    case KF_F32X2: return scan_op<f32x2>(op, f, src, src_stride, dst, dst_stride, n, exclusive, scratch, s);
+    case KF_F32: return scan_op<float>(op, f, src, src_stride, dst, dst_stride, n, mode, scratch, s);
+    case KF_F64: return scan_op<double>(op, f, src, src_stride, dst, dst_stride, n, mode, scratch, s);
+    case KF_I32: return scan_op<int32_t>(op, f, src, src_stride, dst, dst_stride, n, mode, scratch, s);
+    case KF_I64: return scan_op<int64_t>(op, f, src, src_stride, dst, dst_stride, n, mode, scratch, s);
+    case KF_U8: return scan_op<uint8_t>(op, f, src, src_stride, dst, dst_stride, n, mode, scratch, s);
+    case KF_F32X2: return scan_op<f32x2>(op, f, src, src_stride, dst, dst_stride, n, mode, scratch, s);
   }
   return kf_set_error(KF_EINVAL, "kf_scan: bad dtype");
 }

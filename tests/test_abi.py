@@ -57,25 +57,29 @@ def _err(kf):
 def test_invalid_arguments_rejected_without_gpu(kf):
     L, K = kf._lib.lib(), kf._lib
     p = ctypes.c_void_p(4096)
-    assert L.kf_scan(99, 0, K.F32, 0, p, 1, p, 1, 10, p, 1 << 20, None) == K.KF_EINVAL
+    assert L.kf_scan(99, 0, 0, K.F32, 0, p, 1, p, 1, 10, p, 1 << 20, None) == K.KF_EINVAL
     assert "op" in _err(kf)
     # affine needs the pair type and vice versa
-    assert L.kf_scan(K.OP_AFFINE, 0, K.F32, 0, p, 1, p, 1, 10, p, 1 << 20, None) == K.KF_EINVAL
-    assert L.kf_scan(K.OP_ADD, 0, K.F32X2, 0, p, 1, p, 1, 10, p, 1 << 20, None) == K.KF_EINVAL
+    assert L.kf_scan(K.OP_AFFINE, 0, 0, K.F32, 0, p, 1, p, 1, 10, p, 1 << 20, None) == K.KF_EINVAL
+    assert L.kf_scan(K.OP_ADD, 0, 0, K.F32X2, 0, p, 1, p, 1, 10, p, 1 << 20, None) == K.KF_EINVAL
     # affine is scan-only
     assert L.kf_reduce(K.OP_AFFINE, 0, K.F32X2, p, 10, 1, p, p, 1 << 20, None) == K.KF_EINVAL
+    # post-map g: unknown code, sqrt on integers, any g on the affine scan
+    assert L.kf_scan(K.OP_ADD, 0, 7, K.F32, 0, p, 1, p, 1, 10, p, 1 << 20, None) == K.KF_EINVAL
+    assert L.kf_scan(K.OP_ADD, 0, K.POST_SQRT, K.I32, 0, p, 1, p, 1, 10, p, 1 << 20, None) == K.KF_EINVAL
+    assert L.kf_scan(K.OP_AFFINE, 0, K.POST_ABS2, K.F32X2, 0, p, 1, p, 1, 10, p, 1 << 20, None) == K.KF_EINVAL
     # n == 0 is a successful no-op, n < 0 an error
-    assert L.kf_scan(K.OP_ADD, 0, K.F32, 0, p, 1, p, 1, 0, None, 0, None) == K.KF_OK
-    assert L.kf_scan(K.OP_ADD, 0, K.F32, 0, p, 1, p, 1, -1, None, 0, None) == K.KF_EINVAL
+    assert L.kf_scan(K.OP_ADD, 0, 0, K.F32, 0, p, 1, p, 1, 0, None, 0, None) == K.KF_OK
+    assert L.kf_scan(K.OP_ADD, 0, 0, K.F32, 0, p, 1, p, 1, -1, None, 0, None) == K.KF_EINVAL
     # scratch too small
     q = ctypes.c_void_p(1 << 20)
-    assert L.kf_scan(K.OP_ADD, 0, K.F32, 0, p, 1, q, 1, 10, p, 8, None) == K.KF_ENOSCRATCH
+    assert L.kf_scan(K.OP_ADD, 0, 0, K.F32, 0, p, 1, q, 1, 10, p, 8, None) == K.KF_ENOSCRATCH
     # partial overlap of src and dst
-    assert L.kf_scan(K.OP_ADD, 0, K.F32, 0, ctypes.c_void_p(4096), 1, ctypes.c_void_p(4100), 1, 10, q, 1 << 20,
+    assert L.kf_scan(K.OP_ADD, 0, 0, K.F32, 0, ctypes.c_void_p(4096), 1, ctypes.c_void_p(4100), 1, 10, q, 1 << 20,
                      None) == K.KF_EINVAL
     assert "overlap" in _err(kf)
     # misaligned element pointer
-    assert L.kf_scan(K.OP_ADD, 0, K.F32, 0, ctypes.c_void_p(4097), 1, q, 1, 10, q, 1 << 20, None) == K.KF_EINVAL
+    assert L.kf_scan(K.OP_ADD, 0, 0, K.F32, 0, ctypes.c_void_p(4097), 1, q, 1, 10, q, 1 << 20, None) == K.KF_EINVAL
     # reduce_dim: bad dim, col_stride < rows
     assert L.kf_reduce_dim(K.OP_ADD, 0, K.F32, p, 4, 4, 4, 3, q, 1, q, 1 << 20, None) == K.KF_EINVAL
     assert L.kf_reduce_dim(K.OP_ADD, 0, K.F32, p, 4, 4, 2, 1, q, 1, q, 1 << 20, None) == K.KF_EINVAL

@@ -304,3 +304,31 @@ def test_headline_f32_2pow28(kf, oracle, dev):
     x = rng.random(2**28, dtype=np.float32)
     got = run(kf, dev, x, "+")
     assert_close(got, oracle.scan(x), 1e-4, what="F32 n=2^28")
+
+
+@pytest.mark.parametrize("exclusive", [False, True])
+def test_post_map_g_in_the_store(kf, oracle, dev, exclusive):
+    # reference src/scan/scan_kernel.jl:284-295: dst = g(prefix), g applied to
+    # each stored value only (the running prefix stays un-mapped).
+    # Integers: abs2 wraps, exact; floats: sqrt / abs2 of the Float64 prefix.
+    rng = np.random.default_rng(131)
+    for n in (1, 7, 4097, 100_003, 3 * 2**20 + 5):
+        x = gen(rng, np.int32, n)
+        src = torch.from_numpy(x).to(dev)
+        ref = oracle.scan(x, "+", exclusive=exclusive).astype(np.uint32)
+        got = kf.scan("+", src, exclusive=exclusive, g=kf.abs2).cpu().numpy()
+        assert np.array_equal(got, (ref * ref).view(np.int32)), n
+        # strided view: the element-wise path applies g the same way
+        got = kf.scan("+", src[::2], exclusive=exclusive, g=kf.abs2).cpu().numpy()
+        r2 = oracle.scan(x[::2], "+", exclusive=exclusive).astype(np.uint32)
+        assert np.array_equal(got, (r2 * r2).view(np.int32)), n
+        xf = rng.random(n).astype(np.float32)
+        ref = oracle.scan(xf, "+", exclusive=exclusive)
+        got = kf.scan("+", torch.from_numpy(xf).to(dev), exclusive=exclusive, g="sqrt").cpu().numpy()
+        assert np.allclose(got, np.sqrt(ref), rtol=1e-5, atol=1e-6), n
+        xd = rng.random(n)
+        ref = oracle.scan(xd, "max", exclusive=exclusive)
+        got = kf.scan("max", torch.from_numpy(xd).to(dev), exclusive=exclusive, g=kf.abs2).cpu().numpy()
+        assert np.array_equal(got, ref * ref), n        # max selects an input: exact square
+    with pytest.raises(kf.ArgumentError):
+        kf.scan("+", torch.ones(10, dtype=torch.int32, device=dev), g="sqrt")
