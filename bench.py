@@ -103,6 +103,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--all", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--sweep", action="store_true",
+                    help="the reference's scan/mapreduce size sweep (perfs/julia/benchmarks)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the scan/mapreduce path here is single-GPU "
@@ -210,7 +212,54 @@ def main():
     }
     if args.all:
         line["all_configs"] = bench_all(kf, dev, ceiling)
+    if args.sweep:
+        line["sweep"] = bench_sweep(kf, dev, ceiling)
     print(json.dumps(line), flush=True)
+
+
+def _graph_time(fn, reps=20):
+    """Seconds per call of fn, captured `reps` times in one HIP graph."""
+    fn()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(reps):
+            fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    return time_calls(graph.replay, 1) / reps
+
+
+def bench_sweep(kf, dev, ceiling):
+    """The reference's own size sweep (perfs/julia/benchmarks/
+    scan_perf_comparison.jl:129-131, mapreduce_perf_comparison.jl:121-122):
+    n in 10^6..10^9 for Float32, Float64 and UInt8, scan!(+) inclusive and
+    mapreduce(identity, +). HIP-graph timed; GB/s of algorithmic bytes."""
+    rows = []
+    g = torch.Generator(device=dev).manual_seed(20261201)
+    for n in (10**6, 10**7, 10**8, 10**9):
+        for dt in (torch.float32, torch.float64, torch.uint8):
+            if dt == torch.uint8:
+                x = torch.randint(0, 4, (n,), device=dev, generator=g, dtype=dt)
+            else:
+                x = torch.rand(n, device=dev, generator=g, dtype=dt)
+            es = x.element_size()
+            y = torch.empty_like(x)
+            o = torch.empty(1, device=dev, dtype=dt)
+            ts = kf.get_allocation(kf.Scan1D, kf.identity, "+", x)
+            tr = kf.get_allocation(kf.MapReduce1D, kf.identity, "+", x)
+            for what, bytes_, fn in (
+                    ("scan", 2 * es * n, lambda: kf.scan_("+", y, x, tmp=ts)),
+                    ("mapreduce", es * n, lambda: kf.mapreduce_(kf.identity, "+", o, x, tmp=tr))):
+                sec = _graph_time(fn, reps=20 if n < 10**9 else 5)
+                gb = bytes_ / sec / 1e9
+                rows.append({"op": what, "n": n, "dtype": str(dt).replace("torch.", ""),
+                             "us": round(sec * 1e6, 2), "gbps": round(gb, 1),
+                             "elems_per_s": round(n / sec, 1), "frac_copy": round(gb / ceiling, 4)})
+                log(f"  {what:9s} {str(dt):14s} n={n:>10d} {sec*1e6:10.1f} us {gb:8.0f} GB/s "
+                    f"{gb/ceiling*100:5.1f}% of copy")
+            del x, y, ts, tr
+    return rows
 
 
 def bench_all(kf, dev, ceiling):

@@ -63,6 +63,9 @@ constexpr int kScanBlock = 1024;       // large tiles (default)
 constexpr int kTiers = 4;
 constexpr int kTierV[kTiers] = {1, 2, 4, 8};
 constexpr int64_t kMinTiles = 120;
+// UInt8 tiles carry 4x the elements per byte of work: they need more tiles
+// (480) before a larger shape pays (2^30 unchanged; 10^7: 25.8 -> 18.6 us).
+template <class T> constexpr int64_t min_tiles() { return sizeof(T) == 1 ? 480 : kMinTiles; }
 // Float32 arrays of at least kF32WideBytes (2^27 elements) take the
 // 768-thread shape.
 constexpr int64_t kF32WideBytes = 1LL << 29;
@@ -77,10 +80,13 @@ constexpr int kDescWords = 16;             // 128 bytes per tile descriptor
 constexpr uint32_t kSpinLimit = 1u << 24;  // lookback polls before giving up (seconds)
 // Predecessors polled per lookback round (lanes 64-win..63). Each
 // descriptor is its own 128-byte line, and a poll completes only when its
-// slowest line returns: with >= 512 tiles, 8 lines per poll measured 6.09 vs
-// 5.82 TB/s for 64; with fewer tiles (all in flight at once, long walks) the
-// full 64-tile window is faster (2^23 Float32: 14.8 vs 15.1 us).
-inline int look_window(int64_t ntiles) { return ntiles >= 512 ? 8 : kWave; }
+// slowest line returns, while in the steady state of a long scan the
+// nearest predecessors already hold PREFIX: with >= 512 tiles, 4 lines per
+// poll measured best (2^28 Float32 338 us; 2: 351, 8: 346, 16: 363, 32:
+// 376, 64: ~370; widening the window as the walk moves back only lost).
+// With fewer tiles (all in flight at once, long walks) the full 64-tile
+// window is faster (2^23 Float32: 14.8 vs 15.1 us at 8).
+inline int look_window(int64_t ntiles) { return ntiles >= 512 ? 4 : kWave; }
 
 template <class T, int BLOCK = kScanBlock, int VPL = 8> struct ScanShape {
   static constexpr int EPV = 16 / (int)sizeof(T);   // elements per 16-byte vector
@@ -151,6 +157,16 @@ __device__ inline T lookback(const uint64_t* desc, int64_t tile, uint32_t epoch3
     }
     __builtin_amdgcn_s_sleep(1);
   }
+}
+
+// Byte-wise a + b (mod 256 in every byte) of four packed bytes.
+__device__ inline uint32_t add_bytes(uint32_t a, uint32_t b) {
+  return ((a & 0x7f7f7f7fu) + (b & 0x7f7f7f7fu)) ^ ((a ^ b) & 0x80808080u);
+}
+// The 16 bytes moved up by one position, a zero byte in front.
+__device__ inline uint4 shift_in_byte(uint4 v) {
+  return make_uint4(v.x << 8, __builtin_amdgcn_alignbyte(v.y, v.x, 3), __builtin_amdgcn_alignbyte(v.z, v.y, 3),
+                    __builtin_amdgcn_alignbyte(v.w, v.z, 3));
 }
 
 // The post-map g on a stored value: sqrt or abs2 for floats, abs2
@@ -297,6 +313,19 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
   // ---- apply and store ----------------------------------------------------
 #pragma unroll
   for (int j = 0; j < V; ++j) {
+    if constexpr (__is_same(T, uint8_t) && __is_same(Op, OpAdd)) {
+      // UInt8 +: add the prefix byte to all 16 packed bytes at once (the
+      // exclusive result is the inclusive one shifted by a byte; element 0
+      // and virtual positions before `off` hold the identity 0)
+      if (full && post == KF_POST_IDENTITY) {
+        uint4 w = r[j];
+        if constexpr (EXCL) w = shift_in_byte(w);
+        const uint32_t b = 0x01010101u * (uint32_t)Op::combine(prefix, rowpre[j]);
+        st_stream(reinterpret_cast<uint4*>(dstv + wbase) + j * kWave + lane,
+                  make_uint4(add_bytes(w.x, b), add_bytes(w.y, b), add_bytes(w.z, b), add_bytes(w.w, b)));
+        continue;
+      }
+    }
     T x[EPV], o[EPV];
     __builtin_memcpy(x, &r[j], 16);
     const T p = Op::combine(prefix, rowpre[j]);
@@ -333,7 +362,7 @@ template <class T> int scan_tier(int64_t n) {
   const int64_t bytes = n * (int64_t)sizeof(T);
   if (__is_same(T, float) && bytes >= kF32WideBytes) return kTierF32Wide;
   int t = kTiers - 1;
-  while (t > 0 && bytes < kMinTiles * (int64_t)scan_block<T>(t) * kTierV[t] * 16) --t;
+  while (t > 0 && bytes < min_tiles<T>() * (int64_t)scan_block<T>(t) * kTierV[t] * 16) --t;
   return t;
 }
 

@@ -200,13 +200,14 @@ def test_views_offsets_strides_inplace(kf, oracle, dev):
 def test_tile_size_switchover(kf, oracle, dev, dt):
     # tiles are 1024 threads (512 for uint8; 768 for float32 from 2^27 on)
     # x V 16-byte vectors, V in (1, 2, 4, 8): the largest V that still makes >= 120
-    # tiles; from 512 tiles on the lookback polls 8 tiles per round. Check
+    # tiles (480 for uint8); from 512 tiles on the lookback polls 4 tiles per round. Check
     # both sides of every switch (float32: sparse 0/1 values, so every
     # partial sum is an integer below 2^24 and exact in any order).
     epv = 16 // np.dtype(dt).itemsize
     block = {np.uint8: 512}.get(dt, 1024)
+    min_tiles = 480 if dt == np.uint8 else 120
     rng = np.random.default_rng(23)
-    edges = [120 * block * v * epv for v in (2, 4, 8)] + [512 * block * 8 * epv]
+    edges = [min_tiles * block * v * epv for v in (2, 4, 8)] + [512 * block * 8 * epv]
     if dt == np.float32:
         edges.append(2**27)        # 768-thread tiles from 2^27 elements on
     for e in edges:
