@@ -55,25 +55,27 @@ constexpr int kScanBlock = 1024;       // large tiles (default)
 // 2^27 Float64, 2^26 affine pairs and 2^30 UInt8 over 512, 768 and 1024:
 // UInt8 (16 elements per vector, long in-tile work) gains most from two
 // co-resident workgroups per CU, one computing while the other streams
-// (512: 5.74 vs 5.43 TB/s at 1024); Float32 tiles of 768 threads (68
-// VGPRs, two workgroups per CU) run 6.18 vs 6.11 TB/s at 2^28 and 6.01
-// vs 5.94 at 2^27, but lose below (2^26 -2.5 %, 2^24 -20 %, smaller shapes
-// -15 %); Int32, Float64 and the affine pairs are fastest at 1024 (768:
-// -0.2 %, -2 %, -4 %).
+// (512: 5.74 vs 5.43 TB/s at 1024). Large Float32 and 8-byte arrays take
+// 768-thread tiles, two workgroups per CU (the 8-byte types once wave 0
+// parks its tile in LDS during the lookback, 72-74 VGPRs): Float32 6.18 vs
+// 6.11 TB/s at 2^28, Float64 6.22 vs 5.95 at 2^27, affine 5.91 vs 5.70 at
+// 2^26; below 2^27 Float32 (-2.5 % at 2^26, -20 % at 2^24) and 10^7
+// Float64 (-4 %) they lose. Int32 is equal at 768 and 1024.
 constexpr int kTiers = 4;
 constexpr int kTierV[kTiers] = {1, 2, 4, 8};
 constexpr int64_t kMinTiles = 120;
 // UInt8 tiles carry 4x the elements per byte of work: they need more tiles
 // (480) before a larger shape pays (2^30 unchanged; 10^7: 25.8 -> 18.6 us).
 template <class T> constexpr int64_t min_tiles() { return sizeof(T) == 1 ? 480 : kMinTiles; }
-// Float32 arrays of at least kF32WideBytes (2^27 elements) take the
-// 768-thread shape.
-constexpr int64_t kF32WideBytes = 1LL << 29;
-constexpr int kTierF32Wide = kTiers;  // tier index of that shape (8 vectors per lane)
+// Float32 and 8-byte arrays of at least kWideBytes (2^27 Float32 elements)
+// take the 768-thread shape.
+constexpr int64_t kWideBytes = 1LL << 29;
+constexpr int kTierWide = kTiers;  // tier index of that shape (8 vectors per lane)
+template <class T> constexpr bool has_wide_tier() { return __is_same(T, float) || sizeof(T) == 8; }
 template <class T> constexpr int scan_block(int tier) {
-  return sizeof(T) == 1 ? 512 : tier == kTierF32Wide ? 768 : kScanBlock;
+  return sizeof(T) == 1 ? 512 : tier == kTierWide ? 768 : kScanBlock;
 }
-constexpr int tier_v(int tier) { return tier == kTierF32Wide ? 8 : kTierV[tier]; }
+constexpr int tier_v(int tier) { return tier == kTierWide ? 8 : kTierV[tier]; }
 constexpr uint32_t kStatePartial = 1, kStatePrefix = 2;
 constexpr size_t kScanHeaderBytes = 256;
 constexpr int kDescWords = 16;             // 128 bytes per tile descriptor
@@ -169,6 +171,13 @@ __device__ inline uint4 shift_in_byte(uint4 v) {
                     __builtin_amdgcn_alignbyte(v.w, v.z, 3));
 }
 
+// Tiles whose wave 0 parks its registers in LDS during the lookback: the
+// kernel's VGPR count is the peak over the tile and lookback code, and
+// parking lowers it where that buys a second workgroup per CU (8-byte
+// types 85 -> 72, 1024-thread Float32 66 -> 58; Float32 at 768 already
+// fits two and runs 1 % faster without).
+template <class T, int BLOCK> constexpr bool kStashForLookback = sizeof(T) == 8 || (sizeof(T) == 4 && BLOCK == 1024);
+
 // The post-map g on a stored value: sqrt or abs2 for floats, abs2
 // (wrapping) for integers; kf_scan rejects anything else.
 template <class T> __device__ inline T post_apply(int post, T v) {
@@ -212,6 +221,8 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
   __shared__ T wave_agg[kScanWaves];
   __shared__ T wave_pre[kScanWaves];
   __shared__ uint64_t s_ticket;
+  __shared__ uint4 s_stash[kStashForLookback<T, BLOCK> ? V : 1][kWave];
+  __shared__ T s_rowpre[kStashForLookback<T, BLOCK> ? V : 1][kWave];
 
   const int tid = threadIdx.x;
   const int lane = lane_id();
@@ -293,6 +304,16 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
   // Lane w of wave 0 holds wave w's aggregate; a DPP scan over those lanes
   // gives the tile aggregate and every wave's exclusive prefix in the tile.
   if (wave == 0) {
+    if constexpr (kStashForLookback<T, BLOCK>) {
+      // park wave 0's tile in LDS so the lookback's registers do not add to
+      // the tile's (the kernel's VGPR count is the peak over both)
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        s_stash[j][lane] = r[j];
+        s_rowpre[j][lane] = rowpre[j];
+      }
+      asm volatile("" ::: "memory");
+    }
     const T wagg = lane < kScanWaves ? wave_agg[lane] : id;
     const T wincl = wave_inclusive_scan<Op>(wagg);
     const T wexcl = wave_shift_right<Op>(wincl);
@@ -306,6 +327,14 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
       if (lane == 0) publish(desc, tile, (epoch30 << 2) | kStatePrefix, Op::combine(excl, agg));
     }
     if (lane < kScanWaves) wave_pre[lane] = lane == 0 ? excl : Op::combine(excl, wexcl);
+    if constexpr (kStashForLookback<T, BLOCK>) {
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        r[j] = s_stash[j][lane];
+        rowpre[j] = s_rowpre[j][lane];
+      }
+    }
   }
   __syncthreads();
   const T prefix = wave_pre[wave];
@@ -360,7 +389,7 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
 // scratch query and the launch agree.
 template <class T> int scan_tier(int64_t n) {
   const int64_t bytes = n * (int64_t)sizeof(T);
-  if (__is_same(T, float) && bytes >= kF32WideBytes) return kTierF32Wide;
+  if (has_wide_tier<T>() && bytes >= kWideBytes) return kTierWide;
   int t = kTiers - 1;
   while (t > 0 && bytes < min_tiles<T>() * (int64_t)scan_block<T>(t) * kTierV[t] * 16) --t;
   return t;
@@ -413,8 +442,8 @@ int launch_scan(const void* src, int64_t ss, void* dst, int64_t ds, int64_t n, i
     case 2: launch_scan_tier<T, Op, Map, 2>(src, ss, dst, ds, n, excl, ntiles, vec, off, scratch, stream); break;
     case 3: launch_scan_tier<T, Op, Map, 3>(src, ss, dst, ds, n, excl, ntiles, vec, off, scratch, stream); break;
     default:
-      if constexpr (__is_same(T, float))
-        launch_scan_tier<T, Op, Map, kTierF32Wide>(src, ss, dst, ds, n, excl, ntiles, vec, off, scratch, stream);
+      if constexpr (has_wide_tier<T>())
+        launch_scan_tier<T, Op, Map, kTierWide>(src, ss, dst, ds, n, excl, ntiles, vec, off, scratch, stream);
   }
   return kf_check_launch("scan_kernel");
 }

@@ -196,9 +196,10 @@ def test_views_offsets_strides_inplace(kf, oracle, dev):
     assert np.array_equal(y.cpu().numpy(), oracle.scan(x))
 
 
-@pytest.mark.parametrize("dt", [np.float32, np.int32, np.int64, np.uint8])
+@pytest.mark.parametrize("dt", [np.float32, np.float64, np.int32, np.int64, np.uint8])
 def test_tile_size_switchover(kf, oracle, dev, dt):
-    # tiles are 1024 threads (512 for uint8; 768 for float32 from 2^27 on)
+    # tiles are 1024 threads (512 for uint8; 768 for float32 and 8-byte
+    # types from 512 MiB on)
     # x V 16-byte vectors, V in (1, 2, 4, 8): the largest V that still makes >= 120
     # tiles (480 for uint8); from 512 tiles on the lookback polls 4 tiles per round. Check
     # both sides of every switch (float32: sparse 0/1 values, so every
@@ -208,11 +209,11 @@ def test_tile_size_switchover(kf, oracle, dev, dt):
     min_tiles = 480 if dt == np.uint8 else 120
     rng = np.random.default_rng(23)
     edges = [min_tiles * block * v * epv for v in (2, 4, 8)] + [512 * block * 8 * epv]
-    if dt == np.float32:
-        edges.append(2**27)        # 768-thread tiles from 2^27 elements on
+    if dt in (np.float32, np.float64, np.int64):
+        edges.append(2**29 // np.dtype(dt).itemsize)   # 768-thread tiles from 512 MiB on
     for e in edges:
         for n in (e - 1, e, e + 1):
-            x = (rng.random(n) < 1 / 16).astype(np.float32) if dt == np.float32 else gen(rng, dt, n)
+            x = (rng.random(n) < 1 / 16).astype(dt) if np.dtype(dt).kind == "f" else gen(rng, dt, n)
             for exclusive in (False, True):
                 assert np.array_equal(run(kf, dev, x, "+", exclusive=exclusive),
                                       oracle.scan(x, "+", exclusive=exclusive)), (n, exclusive)
