@@ -7,7 +7,7 @@
 // publish the tile's own PREFIX, apply the prefix and store. The MI355X
 // design differs from the reference in these ways:
 //
-//  * Tile = 1024 threads (768 for Float32 from 2^27 elements on, 512 for UInt8) x 8 16-byte
+//  * Tile = 1024 threads (768 for Float32 and 8-byte types from 512 MiB on, 512 for UInt8) x 8 16-byte
 //    vectors per lane = 128 KiB (96 KiB, 64 KiB; 1, 2 or 4 vectors for
 //    arrays too small to make 120 such tiles), so 2^28 Float32 is 10923
 //    tiles and the
