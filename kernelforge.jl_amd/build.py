@@ -13,6 +13,7 @@ REPO = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libkfhip.so")
+DRIVER = os.path.join(HERE, "kf_driver")
 SOURCES = ["kf_api.hip", "kf_scan.hip", "kf_reduce.hip", "kf_copy.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -48,8 +49,18 @@ def build(verbose=True):
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
     os.replace(tmp, LIB)
+    # the plain C-ABI driver (host code only: g++ against the HIP runtime)
+    cmd = ["g++", "-O2", "-std=c++17", "-D__HIP_PLATFORM_AMD__", "-I", "/opt/rocm/include",
+           "-I", os.path.join(REPO, "include"), os.path.join(CSRC, "kf_driver.cpp"), "-o", DRIVER + ".tmp",
+           "-L", HERE, "-lkfhip", "-L", "/opt/rocm/lib", "-lamdhip64", "-Wl,-rpath,$ORIGIN",
+           "-Wl,-rpath,/opt/rocm/lib"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"kf_driver build failed:\n{r.stderr}")
+    os.replace(DRIVER + ".tmp", DRIVER)
     if verbose:
         print(f"built {LIB}")
+        print(f"built {DRIVER}")
     return LIB
 
 
