@@ -7,10 +7,10 @@
 // publish the tile's own PREFIX, apply the prefix and store. The MI355X
 // design differs from the reference in these ways:
 //
-//  * Tile = 1024 threads (768 for Float32 and 8-byte types from 512 MiB on, 512 for UInt8) x 8 16-byte
-//    vectors per lane = 128 KiB (96 KiB, 64 KiB; 1, 2 or 4 vectors for
-//    arrays too small to make 120 such tiles), so 2^28 Float32 is 10923
-//    tiles and the
+//  * Large tiles: 8 16-byte vectors per lane x 1024 threads = 128 KiB (768
+//    threads = 96 KiB for Float32 and 8-byte types from 512 MiB on; 512
+//    threads = 64 KiB for UInt8; 1, 2 or 4 vectors per lane for arrays too
+//    small to make 120 such tiles), so 2^28 Float32 is 10923 tiles and the
 //    per-tile lookback is amortised over a large streaming body. The tile
 //    stays in registers in "striped" order: lane l of wave w holds vector
 //    j*64 + l of the wave's contiguous chunk, so every load and store is a
@@ -45,8 +45,9 @@ namespace kf {
 
 constexpr int kScanBlock = 1024;       // large tiles (default)
 // Tile shapes: 1024 threads x kTierV[t] 16-byte vectors per lane (16 KiB
-// to 128 KiB; 512 threads for UInt8). An array takes the largest shape that still cuts it into at
-// least kMinTiles tiles (scan_tier). Measured on MI355X over shapes of
+// to 128 KiB; 512 threads for UInt8). An array takes the largest shape that
+// still cuts it into at least kMinTiles tiles (scan_tier). Measured on
+// MI355X over shapes of
 // 256-1024 threads x 1-8 vectors: 1024-thread tiles win at every size, and
 // fewer, larger tiles win once there are ~120 of them (Float32: 10^5 3.8 us
 // at 1 vector; 10^6 6.4-6.5 us at 2-4; 2^21 7.7 us at 4, 17.8 us with 64
