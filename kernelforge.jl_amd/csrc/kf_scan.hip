@@ -39,6 +39,8 @@
 //    carry older epochs and read as INVALID, so the scratch buffer needs no
 //    clearing between calls (the reference fill!s its descriptors before
 //    every launch, src/scan/scan.jl:444-470).
+#include <atomic>
+
 #include "kf_common.h"
 
 namespace kf {
@@ -83,13 +85,15 @@ constexpr int kDescWords = 16;             // 128 bytes per tile descriptor
 constexpr uint32_t kSpinLimit = 1u << 24;  // lookback polls before giving up (seconds)
 // Predecessors polled per lookback round (lanes 64-win..63). Each
 // descriptor is its own 128-byte line, and a poll completes only when its
-// slowest line returns, while in the steady state of a long scan the
-// nearest predecessors already hold PREFIX: with >= 512 tiles, 4 lines per
-// poll measured best (2^28 Float32 338 us; 2: 351, 8: 346, 16: 363, 32:
-// 376, 64: ~370; widening the window as the walk moves back only lost).
-// With fewer tiles (all in flight at once, long walks) the full 64-tile
-// window is faster (2^23 Float32: 14.8 vs 15.1 us at 8).
-inline int look_window(int64_t ntiles) { return ntiles >= 512 ? 4 : kWave; }
+// slowest line returns, while in the steady state of a long scan (more
+// tiles than fit on the GPU at once) the nearest predecessors already hold
+// PREFIX: there 4 lines per poll measured best (2^28 Float32 338 us; 2:
+// 351, 8: 346, 16: 363, 32: 376, 64: ~370; widening the window as the walk
+// moves back only lost). When every tile is resident at once they all
+// publish PARTIAL together and walk back towards tile 0, and the full
+// 64-tile window is faster (10^7 UInt8, 611 tiles on 768 slots: 18.3 vs
+// 20.6 us; 3*10^7 Float32, 916 tiles on 512 slots: 49.5 vs 53.5 us at 4).
+inline int look_window(int64_t ntiles, int64_t resident) { return ntiles > resident ? 4 : kWave; }
 
 template <class T, int BLOCK = kScanBlock, int VPL = 8> struct ScanShape {
   static constexpr int EPV = 16 / (int)sizeof(T);   // elements per 16-byte vector
@@ -411,6 +415,18 @@ template <class T> size_t scan_scratch(int64_t n) {
   return kScanHeaderBytes + (size_t)scan_tiles<T>(n, kMaxOff) * kDescWords * sizeof(uint64_t);
 }
 
+// Workgroups of KERNEL the whole GPU holds at once (occupancy x CUs); the
+// occupancy is computed once per kernel.
+template <auto KERNEL> int64_t resident_tiles(int block) {
+  static std::atomic<int> per_cu{0};
+  int b = per_cu.load(std::memory_order_relaxed);
+  if (b == 0) {
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, KERNEL, block, 0) != hipSuccess || b <= 0) b = 1;
+    per_cu.store(b, std::memory_order_relaxed);
+  }
+  return (int64_t)b * kf_device_cu_count();
+}
+
 // `mode` below carries the exclusive flag in bit 0 and the post-map g
 // (kf_post) in the bits above.
 template <class T, class Op, class Map, int TIER>
@@ -418,14 +434,15 @@ void launch_scan_tier(const void* src, int64_t ss, void* dst, int64_t ds, int64_
                       int vec, int off, void* scratch, hipStream_t stream) {
   constexpr int B = scan_block<T>(TIER), V = tier_v(TIER);
   const int post = mode >> 1;
-  if (mode & 1)
-    hipLaunchKernelGGL((scan_kernel<T, Op, Map, true, B, V>), dim3((unsigned)ntiles), dim3(B), 0, stream,
-                       (const T*)src, ss, (T*)dst, ds, n, ntiles, (uint64_t*)scratch, vec, off,
-                       look_window(ntiles), post);
-  else
-    hipLaunchKernelGGL((scan_kernel<T, Op, Map, false, B, V>), dim3((unsigned)ntiles), dim3(B), 0, stream,
-                       (const T*)src, ss, (T*)dst, ds, n, ntiles, (uint64_t*)scratch, vec, off,
-                       look_window(ntiles), post);
+  if (mode & 1) {
+    constexpr auto kernel = scan_kernel<T, Op, Map, true, B, V>;
+    hipLaunchKernelGGL(kernel, dim3((unsigned)ntiles), dim3(B), 0, stream, (const T*)src, ss, (T*)dst, ds, n,
+                       ntiles, (uint64_t*)scratch, vec, off, look_window(ntiles, resident_tiles<kernel>(B)), post);
+  } else {
+    constexpr auto kernel = scan_kernel<T, Op, Map, false, B, V>;
+    hipLaunchKernelGGL(kernel, dim3((unsigned)ntiles), dim3(B), 0, stream, (const T*)src, ss, (T*)dst, ds, n,
+                       ntiles, (uint64_t*)scratch, vec, off, look_window(ntiles, resident_tiles<kernel>(B)), post);
+  }
 }
 
 template <class T, class Op, class Map>

@@ -199,11 +199,11 @@ def test_views_offsets_strides_inplace(kf, oracle, dev):
 @pytest.mark.parametrize("dt", [np.float32, np.float64, np.int32, np.int64, np.uint8])
 def test_tile_size_switchover(kf, oracle, dev, dt):
     # tiles are 1024 threads (512 for uint8; 768 for float32 and 8-byte
-    # types from 512 MiB on)
-    # x V 16-byte vectors, V in (1, 2, 4, 8): the largest V that still makes >= 120
-    # tiles (480 for uint8); from 512 tiles on the lookback polls 4 tiles per round. Check
-    # both sides of every switch (float32: sparse 0/1 values, so every
-    # partial sum is an integer below 2^24 and exact in any order).
+    # types from 512 MiB on) x V 16-byte vectors, V in (1, 2, 4, 8): the
+    # largest V that still makes >= 120 tiles (480 for uint8); with more
+    # tiles than fit on the GPU at once the lookback polls 4 tiles per
+    # round, else 64. Check both sides of every switch (floats: sparse 0/1
+    # values, so every partial sum is an integer and exact in any order).
     epv = 16 // np.dtype(dt).itemsize
     block = {np.uint8: 512}.get(dt, 1024)
     min_tiles = 480 if dt == np.uint8 else 120
