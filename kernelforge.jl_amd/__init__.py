@@ -40,6 +40,7 @@ from . import _lib as _L
 __all__ = [
     "ArgumentError", "KernelBuffer", "AffineOp", "affine", "identity", "abs2", "sqdiff",
     "scan", "scan_", "mapreduce", "mapreduce_", "get_allocation", "vcopy_", "setvalue_", "scan_status",
+    "maximum", "maximum_", "minimum",
     "Scan1D", "MapReduce1D", "MapReduce2D", "matvec", "matvec_", "vecmat", "vecmat_",
 ]
 
@@ -733,6 +734,35 @@ def get_allocation(kind, f, op, src, *args, **kwargs):
     else:
         raise ArgumentError(f"unknown allocation kind {kind!r}")
     return KernelBuffer(kind, need, src.device)
+
+
+def _rel_op(rel):
+    """The reduction operator of maximum!(rel, ...): `<` keeps the larger, `>` the smaller."""
+    if rel is operator.lt or rel == "<":
+        return "max"
+    if rel is operator.gt or rel == ">":
+        return "min"
+    raise ArgumentError(f"maximum!: the relation must be < or > (got {rel!r})")
+
+
+def maximum_(rel, dst, src, tmp=None):
+    """maximum!(rel, dst, src) (reference src/mapreduce/reductions.jl:3-6): the
+    full reduction with op(x, y) = rel(x, y) ? y : x, i.e. max for `<`, min
+    for `>`. Equal to the reference's on every input without NaN or a signed
+    zero tie; there it follows Base max/min (NaN-propagating, -0.0 < +0.0)
+    where the reference's select depends on its combine order."""
+    return mapreduce_(identity, _rel_op(rel), dst, src, tmp=tmp)
+
+
+def maximum(*args, tmp=None):
+    """maximum([rel,] src) -> host scalar (reference src/mapreduce/reductions.jl:8-15)."""
+    rel, (src,) = (operator.lt, args) if len(args) == 1 else (args[0], args[1:])
+    return mapreduce(identity, _rel_op(rel), src, tmp=tmp)
+
+
+def minimum(src, tmp=None):
+    """minimum(src) = maximum(>, src) (reference src/mapreduce/reductions.jl:16)."""
+    return maximum(operator.gt, src, tmp=tmp)
 
 
 def vcopy_(dst, src):

@@ -376,3 +376,24 @@ def test_scan_buffer_is_refused_for_reductions(kf, dev):
     rbuf = kf.KernelBuffer(kf.MapReduce1D, 1 << 20, dev)
     with pytest.raises(kf.ArgumentError):
         kf.scan_("+", torch.empty_like(x), x, tmp=rbuf)
+
+
+@pytest.mark.parametrize("dt", [np.float32, np.float64, np.int32, np.uint8])
+def test_maximum_minimum(kf, oracle, dev, dt):
+    # reference src/mapreduce/reductions.jl (maximum(src), minimum(src),
+    # maximum!(rel, dst, src)), on views as test/tests/views/views_test.jl:62-63
+    # does with min; exact: max/min select an input
+    import operator
+    rng = np.random.default_rng(151)
+    for n in (1, 33, 10001, 1_000_003):
+        x = gen(rng, dt, n + 2)
+        t = torch.from_numpy(x).to(dev)
+        assert kf.maximum(t) == x.max()
+        assert kf.minimum(t) == x.min()
+        assert kf.minimum(t[2:]) == x[2:].min()
+        assert kf.maximum(operator.gt, t[1:-1]) == x[1:-1].min()
+        out = torch.empty(1, dtype=t.dtype, device=dev)
+        kf.maximum_(operator.lt, out, t)
+        assert out.item() == x.max()
+    with pytest.raises(kf.ArgumentError):
+        kf.maximum(operator.le, torch.ones(3, device=dev))
