@@ -40,7 +40,8 @@ from . import _lib as _L
 __all__ = [
     "ArgumentError", "KernelBuffer", "AffineOp", "affine", "identity", "abs2", "sqdiff",
     "scan", "scan_", "mapreduce", "mapreduce_", "get_allocation", "vcopy_", "setvalue_", "scan_status",
-    "maximum", "maximum_", "minimum",
+    "maximum", "maximum_", "minimum", "mapreduce1d", "mapreduce1d_", "mapreduce2d", "mapreduce2d_",
+    "mapreducedims", "mapreducedims_",
     "Scan1D", "MapReduce1D", "MapReduce2D", "matvec", "matvec_", "vecmat", "vecmat_",
 ]
 
@@ -479,13 +480,22 @@ def _mapreduce_multi(f, op, srcs, dims, g, tmp):
     full reduction only, f(x, y) = x*y or (x-y)^2, equal-length vectors."""
     if dims is not None and dims != ":" and dims is not Ellipsis:
         raise ArgumentError("Multi-array mapreduce only supports full reduction (dims=nothing)")
+    _require_device(*srcs)
+    out = torch.empty(1, dtype=srcs[0].dtype, device=srcs[0].device)
+    _reduce2_into(f, op, out, srcs, tmp)
+    val = _to_scalar(out)
+    return g(val) if g is not None else val
+
+
+def _reduce2_into(f, op, out, srcs, tmp):
+    """out[0] = op_i f(x[i], y[i]) through kf_reduce2."""
     if len(srcs) != 2:
         raise ArgumentError(f"multi-array mapreduce takes two arrays here, got {len(srcs)}")
     x, y = srcs
     fc, opc = _map2_code(f), _op_code(op)
-    _require_device(x, y)
-    if x.dtype != y.dtype or x.dtype not in _DTYPES:
-        raise ArgumentError(f"element types {x.dtype} and {y.dtype}: expected one supported type")
+    _require_device(out, x, y)
+    if x.dtype != y.dtype or x.dtype not in _DTYPES or out.dtype != x.dtype:
+        raise ArgumentError(f"element types {x.dtype}, {y.dtype} -> {out.dtype}: expected one supported type")
     if x.dim() != 1 or y.dim() != 1 or x.shape[0] != y.shape[0]:
         raise ArgumentError("multi-array mapreduce takes vectors of equal length")
     if opc == _L.OP_AFFINE:
@@ -495,15 +505,66 @@ def _mapreduce_multi(f, op, srcs, dims, g, tmp):
         raise ArgumentError("reducing over an empty collection is not allowed")
     L = _L.lib()
     dt = _DTYPES[x.dtype]
-    out = torch.empty(1, dtype=x.dtype, device=x.device)
     buf = _scratch(MapReduce1D, L.kf_reduce2_scratch_bytes(dt, n), x.device, tmp)
     with _on(x.device):
         rc = L.kf_reduce2(opc, fc, dt, ctypes_void(x.data_ptr()), x.stride(0) if n > 1 else 1,
                           ctypes_void(y.data_ptr()), y.stride(0) if n > 1 else 1, n, ctypes_void(out.data_ptr()),
                           ctypes_void(buf.ptr), buf.nbytes, _stream_ptr(x))
     _L.check(rc, "mapreduce")
-    val = _to_scalar(out)
-    return g(val) if g is not None else val
+
+
+def mapreduce1d(f, op, src, g=None, tmp=None, to_cpu=True, **tuning):
+    """mapreduce1d(f, op, src_or_srcs; g, tmp, to_cpu=true) (reference
+    src/mapreduce/1D/mapreduce1d.jl:177-209): a host scalar, or with
+    to_cpu=False the 1-element device array holding it."""
+    if to_cpu:
+        return mapreduce(f, op, src, g=g, tmp=tmp)
+    first = src[0] if isinstance(src, (tuple, list)) else src
+    _require_device(first)
+    dst = torch.empty(1, dtype=first.dtype, device=first.device)
+    return mapreduce1d_(f, op, dst, src, g=g, tmp=tmp)
+
+
+def mapreduce1d_(f, op, dst, src, g=None, tmp=None, **tuning):
+    """mapreduce1d!(f, op, dst, src_or_srcs; g, tmp) (reference
+    src/mapreduce/1D/mapreduce1d.jl:211-345): dst[1] = g(op_i f(src[i]))."""
+    if not isinstance(src, (tuple, list)):
+        return mapreduce_(f, op, dst, src, g=g, tmp=tmp)
+    if _post_code(g) is None:
+        raise ArgumentError(f"mapreduce1d!: unsupported post-map g={g!r}: expected identity, sqrt or abs2")
+    if dst.numel() < 1:
+        raise ArgumentError("dst must hold at least one element")
+    _reduce2_into(f, op, dst.as_strided((1,), (1,)), src, tmp)
+    _apply_post(g, dst, 1, 1)
+    return dst
+
+
+def mapreduce2d(f, op, src, dim, g=None, tmp=None, **tuning):
+    """mapreduce2d(f, op, A, dim; g, tmp) (reference src/mapreduce/2D/mapreduce2d.jl:49-64):
+    the vector of column (dim=1) or row (dim=2) reductions of a matrix."""
+    if dim not in (1, 2):
+        raise ArgumentError(f"dim must be 1 or 2, got {dim}")
+    return vecmat(f, op, None, src, g=g, tmp=tmp) if dim == 1 else matvec(f, op, src, None, g=g, tmp=tmp)
+
+
+def mapreduce2d_(f, op, dst, src, dim, g=None, tmp=None, **tuning):
+    """mapreduce2d!(f, op, dst, A, dim; g, tmp) (reference src/mapreduce/2D/mapreduce2d.jl:111-126)."""
+    if dim not in (1, 2):
+        raise ArgumentError(f"dim must be 1 or 2, got {dim}")
+    if dim == 1:
+        return vecmat_(f, op, dst, None, src, g=g, tmp=tmp)
+    return matvec_(f, op, dst, src, None, g=g, tmp=tmp)
+
+
+def mapreducedims(f, op, src, dims, g=None, tmp=None, **tuning):
+    """mapreducedims(f, op, src, dims; g) (reference src/mapreduce/ND/mapreducedims.jl:117-140):
+    size 1 along `dims`, the source size elsewhere."""
+    return mapreduce(f, op, src, dims=dims, g=g, tmp=tmp)
+
+
+def mapreducedims_(f, op, dst, src, dims, g=None, tmp=None, **tuning):
+    """mapreducedims!(f, op, dst, src, dims; g) (reference src/mapreduce/ND/mapreducedims.jl:146-163)."""
+    return mapreduce_(f, op, dst, src, dims=dims, g=g, tmp=tmp)
 
 
 def mapreduce_(f, op, dst, src, dims=None, g=None, tmp=None, **tuning):

@@ -397,3 +397,39 @@ def test_maximum_minimum(kf, oracle, dev, dt):
         assert out.item() == x.max()
     with pytest.raises(kf.ArgumentError):
         kf.maximum(operator.le, torch.ones(3, device=dev))
+
+
+def test_lower_level_entry_points(kf, oracle, dev):
+    # the names the reference's tests call besides mapreduce/mapreduce!:
+    # mapreduce1d(!), mapreduce2d(!), mapreducedims(!) (mapreduce1d_test.jl,
+    # mapreduce2d_test.jl, mapreducedims_test.jl); exact on Int32
+    import operator
+    rng = np.random.default_rng(163)
+    x = gen(rng, np.int32, 100_003)
+    y = gen(rng, np.int32, 100_003)
+    tx, ty = torch.from_numpy(x).to(dev), torch.from_numpy(y).to(dev)
+    assert kf.mapreduce1d(kf.identity, "+", tx) == int(oracle.reduce(x, "+"))
+    d = kf.mapreduce1d(kf.abs2, "max", tx, to_cpu=False)
+    assert d.device.type == "cuda" and d.shape == (1,) and d.item() == int(oracle.reduce(x, "max", "abs2"))
+    out = torch.zeros(3, dtype=torch.int32, device=dev)
+    kf.mapreduce1d_(operator.mul, "+", out, (tx, ty))
+    assert out[0].item() == int(oracle.reduce2(x, y, "+", "mul")) and out[1:].eq(0).all()
+    assert kf.mapreduce1d(operator.mul, "+", (tx, ty)) == int(oracle.reduce2(x, y, "+", "mul"))
+    rows, cols = 300, 170
+    a = gen(rng, np.int32, rows * cols)
+    A = torch.from_numpy(a).to(dev).view(cols, rows).T
+    for dim in (1, 2):
+        ref = oracle.reduce_dim(a, rows, cols, rows, dim, "+")
+        assert np.array_equal(kf.mapreduce2d(kf.identity, "+", A, dim).cpu().numpy(), ref), dim
+        dst = torch.empty(ref.shape[0], dtype=torch.int32, device=dev)
+        kf.mapreduce2d_(kf.identity, "+", dst, A, dim)
+        assert np.array_equal(dst.cpu().numpy(), ref), dim
+    with pytest.raises(kf.ArgumentError):
+        kf.mapreduce2d(kf.identity, "+", A, 3)
+    B = torch.from_numpy(gen(rng, np.int32, 6 * 7 * 8)).to(dev).view(8, 7, 6).permute(2, 1, 0)  # column-major 6x7x8
+    ref = B.cpu().numpy().astype(np.int64).sum(axis=(0, 2), keepdims=True).astype(np.int32)
+    got = kf.mapreducedims(kf.identity, "+", B, (1, 3))
+    assert tuple(got.shape) == (1, 7, 1) and np.array_equal(got.cpu().numpy(), ref)
+    dst = torch.empty(1, 7, 1, dtype=torch.int32, device=dev)
+    kf.mapreducedims_(kf.identity, "+", dst, B, (1, 3))
+    assert np.array_equal(dst.cpu().numpy(), ref)
