@@ -42,7 +42,7 @@ __all__ = [
     "scan", "scan_", "mapreduce", "mapreduce_", "get_allocation", "vcopy_", "setvalue_", "scan_status",
     "maximum", "maximum_", "minimum", "mapreduce1d", "mapreduce1d_", "mapreduce2d", "mapreduce2d_",
     "mapreducedims", "mapreducedims_",
-    "Scan1D", "MapReduce1D", "MapReduce2D", "matvec", "matvec_", "vecmat", "vecmat_",
+    "Scan1D", "MapReduce1D", "MapReduce2D", "MatVec", "VecMat", "matvec", "matvec_", "vecmat", "vecmat_",
 ]
 
 
@@ -91,6 +91,7 @@ def _map2_code(f):
 
 # Allocation kinds (reference src/algorithms.jl:16-31 tags).
 Scan1D, MapReduce1D, MapReduce2D = "Scan1D", "MapReduce1D", "MapReduce2D"
+MatVec, VecMat = "MatVec", "VecMat"
 
 _OPS = {"+": _L.OP_ADD, "max": _L.OP_MAX, "min": _L.OP_MIN, "affine": _L.OP_AFFINE}
 _MAPS = {"identity": _L.MAP_IDENTITY, "abs2": _L.MAP_ABS2}
@@ -776,25 +777,47 @@ def vecmat_(*args, f=operator.mul, op="+", g=None, tmp=None, **tuning):
 
 
 def get_allocation(kind, f, op, src, *args, **kwargs):
-    """Scratch for a later call with the same operands
-    (reference src/scan/scan.jl:156-211, src/mapreduce/1D/mapreduce1d.jl:140-170).
-    kind: Scan1D, MapReduce1D or MapReduce2D (then pass dims=1 or 2)."""
+    """Scratch for a later call with the same operands (reference
+    src/scan/scan.jl:121-211, src/mapreduce/1D/mapreduce1d.jl:113-170,
+    src/mapreduce/2D/matvec.jl:182, src/mapreduce/2D/vecmat.jl:265).
+
+    kind: Scan1D (src), MapReduce1D (src, or a tuple (x, y) of two arrays),
+    MatVec (A, x) and VecMat (x, A) as the reference orders them, or
+    MapReduce2D (A, dims=1 or 2). Extra positional tuning arguments
+    (workgroup, blocks, arch) are accepted and ignored."""
     L = _L.lib()
     opc = _op_code(op)
-    _map_code(f)
-    _require_device(src)
     if kind == Scan1D:
+        _map_code(f)
+        _require_device(src)
         dt, n, _ = _scan_operand(src, opc)
         need = L.kf_scan_scratch_bytes(dt, opc, n)
+        device = src.device
     elif kind == MapReduce1D:
-        need = L.kf_reduce_scratch_bytes(_DTYPES[src.dtype], src.numel())
-    elif kind == MapReduce2D:
-        dim = int(kwargs.get("dims", args[0] if args else 1))
-        rows, cols, _ = _as_matrix(src, 1) if src.dim() == 2 else (src.numel(), 1, src.numel())
-        need = L.kf_reduce_dim_scratch_bytes(_DTYPES[src.dtype], rows, cols, dim)
+        if isinstance(src, (tuple, list)):
+            _map2_code(f)
+            _require_device(*src)
+            need = L.kf_reduce2_scratch_bytes(_DTYPES[src[0].dtype], src[0].numel())
+            device = src[0].device
+        else:
+            _map_code(f)
+            _require_device(src)
+            need = L.kf_reduce_scratch_bytes(_DTYPES[src.dtype], src.numel())
+            device = src.device
+    elif kind in (MatVec, VecMat, MapReduce2D):
+        if kind == MatVec:
+            A, dim = src, 2
+        elif kind == VecMat:
+            A, dim = (args[0] if args else kwargs["A"]), 1
+        else:
+            A, dim = src, int(kwargs.get("dims", args[0] if args else 1))
+        _require_device(A)
+        rows, cols, _ = _as_matrix(A, 1) if A.dim() == 2 else (A.numel(), 1, A.numel())
+        need = L.kf_reduce_dim_scratch_bytes(_DTYPES[A.dtype], rows, cols, dim)
+        device = A.device
     else:
         raise ArgumentError(f"unknown allocation kind {kind!r}")
-    return KernelBuffer(kind, need, src.device)
+    return KernelBuffer(kind, need, device)
 
 
 def _rel_op(rel):

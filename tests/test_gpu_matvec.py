@@ -72,3 +72,29 @@ def test_api_forms_and_errors(kf, dev):
         kf.matvec(A, y)                                        # wrong length
     with pytest.raises(kf.ArgumentError):
         kf.matvec(A, x.float())                                # mixed types
+
+
+def test_get_allocation_kinds_reference_order(kf, oracle, dev):
+    # reference get_allocation(MatVec, f, op, A, x), get_allocation(VecMat, f, op, x, A)
+    # (matvec.jl:182, vecmat.jl:265) and get_allocation(MapReduce1D, f, op, (x, y), blocks)
+    # (mapreduce1d_test.jl:161); each buffer is reused for several calls
+    rng = np.random.default_rng(173)
+    rows, cols = 3000, 40
+    a = rng.integers(-20, 20, (cols, rows)).astype(np.int32)
+    A = torch.from_numpy(a).to(dev).T                  # column-major rows x cols
+    xr = torch.from_numpy(rng.integers(-20, 20, rows).astype(np.int32)).to(dev)
+    xc = torch.from_numpy(rng.integers(-20, 20, cols).astype(np.int32)).to(dev)
+    tmv = kf.get_allocation(kf.MatVec, operator.mul, "+", A, xc)
+    tvm = kf.get_allocation(kf.VecMat, operator.mul, "+", xr, A)
+    M = a.T.astype(np.int64)
+    for _ in range(3):
+        got = kf.matvec(operator.mul, "+", A, xc, tmp=tmv).cpu().numpy()
+        assert np.array_equal(got, (M @ xc.cpu().numpy().astype(np.int64)).astype(np.int32))
+        got = kf.vecmat(operator.mul, "+", xr, A, tmp=tvm).cpu().numpy()
+        assert np.array_equal(got, (xr.cpu().numpy().astype(np.int64) @ M).astype(np.int32))
+    x = torch.from_numpy(rng.integers(-9, 9, 100_001).astype(np.int32)).to(dev)
+    y = torch.from_numpy(rng.integers(-9, 9, 100_001).astype(np.int32)).to(dev)
+    t2 = kf.get_allocation(kf.MapReduce1D, operator.mul, "+", (x, y), 1000)
+    ref = int((x.cpu().numpy().astype(np.int64) * y.cpu().numpy()).sum())
+    for _ in range(3):
+        assert kf.mapreduce(operator.mul, "+", (x, y), tmp=t2) == ref
