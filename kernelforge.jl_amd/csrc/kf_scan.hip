@@ -273,13 +273,25 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
       }
     }
   } else {
+    // partial tile (the last one, or the first of a misaligned view) or a
+    // strided operand: vectors wholly inside [0, n) of a contiguous operand
+    // still stream; the others go element by element
+    const uint4* g = reinterpret_cast<const uint4*>(srcv + wbase);
 #pragma unroll
     for (int j = 0; j < V; ++j) {
+      const int64_t e0 = wbase + (int64_t)(j * kWave + lane) * EPV - off;  // real index of element 0
       T x[EPV];
+      if (vec && e0 >= 0 && e0 + EPV <= n) {
+        const uint4 w = ld_stream(g + j * kWave + lane);
+        __builtin_memcpy(x, &w, 16);
 #pragma unroll
-      for (int k = 0; k < EPV; ++k) {
-        const int64_t idx = wbase + (int64_t)(j * kWave + lane) * EPV + k - off;  // real index
-        x[k] = (idx >= 0 && idx < n) ? Map::apply(src[idx * src_stride]) : id;
+        for (int k = 0; k < EPV; ++k) x[k] = Map::apply(x[k]);
+      } else {
+#pragma unroll
+        for (int k = 0; k < EPV; ++k) {
+          const int64_t idx = e0 + k;
+          x[k] = (idx >= 0 && idx < n) ? Map::apply(src[idx * src_stride]) : id;
+        }
       }
       __builtin_memcpy(&r[j], x, 16);
       pin_packed<T>(r[j]);
@@ -376,14 +388,15 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
 #pragma unroll
       for (int k = 0; k < EPV; ++k) o[k] = post_apply(post, o[k]);
     }
-    if (full) {
+    const int64_t e0 = wbase + (int64_t)(j * kWave + lane) * EPV - off;  // real index of element 0
+    if (full || (vec && e0 >= 0 && e0 + EPV <= n)) {
       uint4 w;
       __builtin_memcpy(&w, o, 16);
       st_stream(reinterpret_cast<uint4*>(dstv + wbase) + j * kWave + lane, w);
     } else {
 #pragma unroll
       for (int k = 0; k < EPV; ++k) {
-        const int64_t idx = wbase + (int64_t)(j * kWave + lane) * EPV + k - off;
+        const int64_t idx = e0 + k;
         if (idx >= 0 && idx < n) dst[idx * dst_stride] = o[k];
       }
     }
