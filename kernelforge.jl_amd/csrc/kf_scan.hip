@@ -276,14 +276,21 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
     // partial tile (the last one, or the first of a misaligned view) or a
     // strided operand: vectors wholly inside [0, n) of a contiguous operand
     // still stream; the others go element by element
+    // (all vector loads are issued before any is used, as in the full path)
     const uint4* g = reinterpret_cast<const uint4*>(srcv + wbase);
+    bool inside[V];
 #pragma unroll
     for (int j = 0; j < V; ++j) {
       const int64_t e0 = wbase + (int64_t)(j * kWave + lane) * EPV - off;  // real index of element 0
+      inside[j] = vec && e0 >= 0 && e0 + EPV <= n;
+      if (inside[j]) r[j] = ld_stream(g + j * kWave + lane);
+    }
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      const int64_t e0 = wbase + (int64_t)(j * kWave + lane) * EPV - off;
       T x[EPV];
-      if (vec && e0 >= 0 && e0 + EPV <= n) {
-        const uint4 w = ld_stream(g + j * kWave + lane);
-        __builtin_memcpy(x, &w, 16);
+      if (inside[j]) {
+        __builtin_memcpy(x, &r[j], 16);
 #pragma unroll
         for (int k = 0; k < EPV; ++k) x[k] = Map::apply(x[k]);
       } else {
