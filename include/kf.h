@@ -46,12 +46,15 @@ typedef enum {
 
 /* Binary operator `op` of scan!/mapreduce. KF_OP_AFFINE is the
  * non-commutative composition (a1,b1) o (a2,b2) = (a2*a1, a2*b1 + b2) on
- * KF_F32X2 pairs; it is accepted by kf_scan only. */
+ * KF_F32X2 pairs; it is accepted by kf_scan only. KF_OP_MUL is Julia `*`
+ * (IEEE product for floats, wrap-around for integers), the operator of the
+ * reference's product-scan tests (test/tests/scan/scan_test.jl:1-19). */
 typedef enum {
   KF_OP_ADD = 0,
   KF_OP_MAX = 1,
   KF_OP_MIN = 2,
-  KF_OP_AFFINE = 3
+  KF_OP_AFFINE = 3,
+  KF_OP_MUL = 4
 } kf_op;
 
 /* Element map `f` (applied to each element before `op`). */

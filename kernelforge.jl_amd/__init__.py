@@ -93,7 +93,7 @@ def _map2_code(f):
 Scan1D, MapReduce1D, MapReduce2D = "Scan1D", "MapReduce1D", "MapReduce2D"
 MatVec, VecMat = "MatVec", "VecMat"
 
-_OPS = {"+": _L.OP_ADD, "max": _L.OP_MAX, "min": _L.OP_MIN, "affine": _L.OP_AFFINE}
+_OPS = {"+": _L.OP_ADD, "max": _L.OP_MAX, "min": _L.OP_MIN, "affine": _L.OP_AFFINE, "*": _L.OP_MUL}
 _MAPS = {"identity": _L.MAP_IDENTITY, "abs2": _L.MAP_ABS2}
 _DTYPES = {torch.float32: _L.F32, torch.float64: _L.F64, torch.int32: _L.I32,
            torch.int64: _L.I64, torch.uint8: _L.U8}
@@ -102,6 +102,8 @@ _DTYPES = {torch.float32: _L.F32, torch.float64: _L.F64, torch.int32: _L.I32,
 def _op_code(op):
     if op is operator.add or op is operator.iadd or op is sum:
         return _L.OP_ADD
+    if op is operator.mul or op is operator.imul:
+        return _L.OP_MUL
     if op is max:
         return _L.OP_MAX
     if op is min:
@@ -110,7 +112,7 @@ def _op_code(op):
         return _L.OP_AFFINE
     if isinstance(op, str) and op in _OPS:
         return _OPS[op]
-    raise ArgumentError(f"unsupported operator {op!r}: expected +, max, min or affine")
+    raise ArgumentError(f"unsupported operator {op!r}: expected +, *, max, min or affine")
 
 
 def _map_code(f):

@@ -12,7 +12,7 @@ LIB_PATH = os.path.join(HERE, "libkfhip.so")
 
 # enums mirrored from include/kf.h
 KF_OK, KF_EINVAL, KF_ENOSCRATCH, KF_EHIP = 0, 1, 2, 3
-OP_ADD, OP_MAX, OP_MIN, OP_AFFINE = 0, 1, 2, 3
+OP_ADD, OP_MAX, OP_MIN, OP_AFFINE, OP_MUL = 0, 1, 2, 3, 4
 MAP_IDENTITY, MAP_ABS2 = 0, 1
 MAP2_MUL, MAP2_SQDIFF = 0, 1
 POST_IDENTITY, POST_SQRT, POST_ABS2 = 0, 1, 2

@@ -47,7 +47,7 @@ int kf_validate_op(kf_op op, kf_map f, kf_dtype dt, int allow_affine) {
     if (f != KF_MAP_IDENTITY) return kf_set_error(KF_EINVAL, "abs2 is not defined on affine pairs");
     return KF_OK;
   }
-  if (op != KF_OP_ADD && op != KF_OP_MAX && op != KF_OP_MIN)
+  if (op != KF_OP_ADD && op != KF_OP_MAX && op != KF_OP_MIN && op != KF_OP_MUL)
     return kf_set_error(KF_EINVAL, "unknown op %d", (int)op);
   return KF_OK;
 }

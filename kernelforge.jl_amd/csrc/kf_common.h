@@ -81,6 +81,16 @@ template <> __device__ inline int32_t OpMin::identity<int32_t>() { return INT32_
 template <> __device__ inline int64_t OpMin::identity<int64_t>() { return INT64_MAX; }
 template <> __device__ inline uint8_t OpMin::identity<uint8_t>() { return 255; }
 
+// Julia `*`: IEEE products; integers wrap (computed unsigned).
+struct OpMul {
+  template <class T> __device__ static T identity() { return T(1); }
+  __device__ static float combine(float x, float y) { return x * y; }
+  __device__ static double combine(double x, double y) { return x * y; }
+  __device__ static int32_t combine(int32_t x, int32_t y) { return (int32_t)((uint32_t)x * (uint32_t)y); }
+  __device__ static int64_t combine(int64_t x, int64_t y) { return (int64_t)((uint64_t)x * (uint64_t)y); }
+  __device__ static uint8_t combine(uint8_t x, uint8_t y) { return (uint8_t)(x * y); }
+};
+
 // Composition of affine maps, older map on the left. Non-commutative: every
 // combine site in the kernels keeps the older operand first.
 struct OpAffine {

@@ -655,12 +655,14 @@ int dispatch_op_map(kf_op op, kf_map f, A... args) {
     switch (op) {
       case KF_OP_ADD: return L<T, OpAdd, MapAbs2>::run(args...);
       case KF_OP_MAX: return L<T, OpMax, MapAbs2>::run(args...);
+      case KF_OP_MUL: return L<T, OpMul, MapAbs2>::run(args...);
       default: return L<T, OpMin, MapAbs2>::run(args...);
     }
   }
   switch (op) {
     case KF_OP_ADD: return L<T, OpAdd, MapIdentity>::run(args...);
     case KF_OP_MAX: return L<T, OpMax, MapIdentity>::run(args...);
+    case KF_OP_MUL: return L<T, OpMul, MapIdentity>::run(args...);
     default: return L<T, OpMin, MapIdentity>::run(args...);
   }
 }
@@ -751,12 +753,14 @@ template <class T, class... A> int dispatch_reduce2(kf_op op, kf_map2 f, A... ar
     switch (op) {
       case KF_OP_ADD: return Reduce2L<T, OpAdd, Map2SqDiff>::run(args...);
       case KF_OP_MAX: return Reduce2L<T, OpMax, Map2SqDiff>::run(args...);
+      case KF_OP_MUL: return Reduce2L<T, OpMul, Map2SqDiff>::run(args...);
       default: return Reduce2L<T, OpMin, Map2SqDiff>::run(args...);
     }
   }
   switch (op) {
     case KF_OP_ADD: return Reduce2L<T, OpAdd, Map2Mul>::run(args...);
     case KF_OP_MAX: return Reduce2L<T, OpMax, Map2Mul>::run(args...);
+    case KF_OP_MUL: return Reduce2L<T, OpMul, Map2Mul>::run(args...);
     default: return Reduce2L<T, OpMin, Map2Mul>::run(args...);
   }
 }
@@ -871,12 +875,14 @@ template <class T, class... A> int dispatch_dim_x(kf_op op, kf_map2 f, A... args
     switch (op) {
       case KF_OP_ADD: return launch_reduce_dim<T, OpAdd, Map2SqDiff>(args...);
       case KF_OP_MAX: return launch_reduce_dim<T, OpMax, Map2SqDiff>(args...);
+      case KF_OP_MUL: return launch_reduce_dim<T, OpMul, Map2SqDiff>(args...);
       default: return launch_reduce_dim<T, OpMin, Map2SqDiff>(args...);
     }
   }
   switch (op) {
     case KF_OP_ADD: return launch_reduce_dim<T, OpAdd, Map2Mul>(args...);
     case KF_OP_MAX: return launch_reduce_dim<T, OpMax, Map2Mul>(args...);
+    case KF_OP_MUL: return launch_reduce_dim<T, OpMul, Map2Mul>(args...);
     default: return launch_reduce_dim<T, OpMin, Map2Mul>(args...);
   }
 }

@@ -25,7 +25,8 @@
  *      cpu_baseline figure.
  *
  * Codes: dtype 0 f32, 1 f64, 2 i32, 3 i64, 4 u8, 5 (a,b) f32 pairs;
- *        op 0 +, 1 max, 2 min, 3 affine; map 0 identity, 1 abs2.
+ *        op 0 +, 1 max, 2 min, 3 affine, 4 * (Julia `*`: IEEE product,
+ *        integers wrap); map 0 identity, 1 abs2.
  */
 #include <math.h>
 #include <stdint.h>
@@ -35,7 +36,7 @@
 #endif
 
 enum { D_F32 = 0, D_F64 = 1, D_I32 = 2, D_I64 = 3, D_U8 = 4, D_F32X2 = 5 };
-enum { OP_ADD = 0, OP_MAX = 1, OP_MIN = 2, OP_AFFINE = 3 };
+enum { OP_ADD = 0, OP_MAX = 1, OP_MIN = 2, OP_AFFINE = 3, OP_MUL = 4 };
 
 /* Julia `max`/`min` on IEEE floats: NaN-propagating, -0.0 < +0.0. */
 static double jl_max(double x, double y) {
@@ -53,6 +54,7 @@ static double fop(int op, double x, double y) {
   switch (op) {
     case OP_ADD: return x + y;
     case OP_MAX: return jl_max(x, y);
+    case OP_MUL: return x * y;
     default: return jl_min(x, y);
   }
 }
@@ -84,6 +86,7 @@ static uint64_t iload(const void* p, int dt, int64_t i, int map) {
 }
 static uint64_t iop(int dt, int op, uint64_t x, uint64_t y) {
   if (op == OP_ADD) return wrap(dt, x + y);
+  if (op == OP_MUL) return wrap(dt, x * y);
   if (dt == D_U8) {
     if (op == OP_MAX) return x > y ? x : y;
     return x < y ? x : y;
@@ -93,6 +96,7 @@ static uint64_t iop(int dt, int op, uint64_t x, uint64_t y) {
 }
 static uint64_t iidentity(int dt, int op) {
   if (op == OP_ADD) return 0;
+  if (op == OP_MUL) return 1;
   if (dt == D_U8) return op == OP_MAX ? 0 : 255;
   if (dt == D_I32) return op == OP_MAX ? (uint64_t)(int64_t)INT32_MIN : (uint64_t)(int64_t)INT32_MAX;
   return op == OP_MAX ? (uint64_t)INT64_MIN : (uint64_t)INT64_MAX;
@@ -108,10 +112,10 @@ static void istore(void* p, int dt, int64_t i, uint64_t v) {
 /* ---------------------------------------------------------------- scan ---- */
 
 /* Float scan, double accumulation. Exclusive: out[0] = identity (+0.0 for
- * +, -Inf for max, +Inf for min), out[i] = inclusive[i-1]. */
+ * +, -Inf for max, +Inf for min, 1 for *), out[i] = inclusive[i-1]. */
 void kfo_scan_f(const void* src, int dt, int64_t n, int64_t stride, int op, int map, int excl, double* out) {
   double acc = 0.0;
-  const double id = op == OP_ADD ? 0.0 : (op == OP_MAX ? -INFINITY : INFINITY);
+  const double id = op == OP_ADD ? 0.0 : op == OP_MUL ? 1.0 : (op == OP_MAX ? -INFINITY : INFINITY);
   for (int64_t i = 0; i < n; ++i) {
     const double v = fload(src, dt, i * stride, map);
     const double prev = i == 0 ? id : acc;

@@ -19,7 +19,7 @@ LIB = os.path.join(HERE, "liboracle.so")
 
 DT = {np.dtype(np.float32): 0, np.dtype(np.float64): 1, np.dtype(np.int32): 2,
       np.dtype(np.int64): 3, np.dtype(np.uint8): 4}
-OPS = {"+": 0, "max": 1, "min": 2, "affine": 3}
+OPS = {"+": 0, "max": 1, "min": 2, "affine": 3, "*": 4}
 MAPS = {"identity": 0, "abs2": 1}
 
 _lib = None

@@ -46,3 +46,29 @@ def assert_mixed(got, ref, tol, what=""):
         i = bad[0]
         raise AssertionError(f"{what}: {bad.size} out of tolerance {tol}; first at {i}: "
                              f"got {got[i]!r}, expected {ref[i]!r}")
+
+
+def pow2_factors(rng, n, dt, contiguous=True):
+    """Factors +-2^k whose products are exact in Float32 and Float64, so a
+    product scan or reduction can be compared bit for bit. contiguous=True
+    (scans, which only multiply contiguous runs): every factor is 2 or 1/2
+    and the running exponent is a triangle wave in [-20, 20], so any dropped,
+    repeated or reordered factor changes an exponent. contiguous=False
+    (reductions, whose partial products cover strided subsets): about 8
+    factors are +-2 or +-1/2, the rest +-1. Signs are random."""
+    i = np.arange(n + 1)
+    if contiguous:
+        e = 20 - np.abs(((i + 20) % 80) - 40)   # e[0] = 0
+        k = np.diff(e)
+    else:
+        k = rng.choice([-1, 1], n) * (rng.random(n) < 8.0 / n)
+    return (rng.choice([-1.0, 1.0], n) * np.exp2(k)).astype(dt)
+
+
+def product_rtol(dt, n):
+    """Forward error bound of any product of n floating-point factors
+    (n - 1 roundings): |computed - exact| <= gamma_{n-1} |exact| with
+    gamma_m = m u / (1 - m u), u = 2^-24 (Float32) or 2^-53 (Float64)."""
+    u = 2.0 ** -24 if np.dtype(dt) == np.float32 else 2.0 ** -53
+    m = max(n - 1, 1)
+    return m * u / (1 - m * u)

@@ -63,6 +63,8 @@ def test_invalid_arguments_rejected_without_gpu(kf):
     # affine needs the pair type and vice versa
     assert L.kf_scan(K.OP_AFFINE, 0, 0, K.F32, 0, p, 1, p, 1, 10, p, 1 << 20, None) == K.KF_EINVAL
     assert L.kf_scan(K.OP_ADD, 0, 0, K.F32X2, 0, p, 1, p, 1, 10, p, 1 << 20, None) == K.KF_EINVAL
+    # the multiply operator takes the scalar types only
+    assert L.kf_scan(K.OP_MUL, 0, 0, K.F32X2, 0, p, 1, p, 1, 10, p, 1 << 20, None) == K.KF_EINVAL
     # affine is scan-only
     assert L.kf_reduce(K.OP_AFFINE, 0, K.F32X2, p, 10, 1, p, p, 1 << 20, None) == K.KF_EINVAL
     # post-map g: unknown code, sqrt on integers, any g on the affine scan

@@ -6,7 +6,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import NP, assert_close, dec
+from helpers import NP, assert_close, dec, pow2_factors, product_rtol
 
 pytestmark = pytest.mark.gpu
 
@@ -52,6 +52,37 @@ def test_full_reduce(kf, oracle, dev, dt, op, f):
             assert dt(got) == dt(ref), (n, got, ref)
         else:
             assert got == int(ref), (n, got, ref)
+
+
+@pytest.mark.parametrize("dt", [np.float32, np.float64, np.int32, np.int64, np.uint8])
+def test_product_reduce(kf, oracle, dev, dt):
+    # mapreduce(identity, *, x): odd integer factors (wrapping, exact);
+    # float factors +-2^k (exact products, compared bit for bit) and factors
+    # in [0.999, 1.001] within the forward error bound gamma_{n-1} of a
+    # product in any association order
+    rng = np.random.default_rng(37)
+    for n in SIZES:
+        if np.dtype(dt).kind == "f":
+            x = pow2_factors(rng, n, dt, contiguous=False)
+            got = kf.mapreduce(kf.identity, "*", torch.from_numpy(x).to(dev))
+            assert got == oracle.reduce(x, "*"), n
+            x = rng.uniform(0.999, 1.001, n).astype(dt)
+            got = kf.mapreduce(kf.identity, "*", torch.from_numpy(x).to(dev))
+            ref = oracle.reduce(x, "*")
+            assert abs(got - ref) <= product_rtol(dt, n) * abs(ref), (n, got, ref)
+        else:
+            x = 2 * rng.integers(-3, 3, n) + 1
+            x = (x % 256).astype(dt) if dt == np.uint8 else x.astype(dt)
+            got = kf.mapreduce(kf.identity, "*", torch.from_numpy(x).to(dev))
+            assert got == int(oracle.reduce(x, "*")), n
+    # along dims, on a column view
+    rows, cols = 300, 70
+    buf = rng.uniform(0.99, 1.01, (2 * cols, rows)).reshape(-1)
+    A = torch.from_numpy(buf).to(dev).as_strided((rows, cols), (1, 2 * rows))
+    for dim in (1, 2):
+        got = kf.mapreduce(kf.identity, "*", A, dims=dim).reshape(-1).cpu().numpy()
+        ref = oracle.reduce_dim(buf, rows, cols, 2 * rows, dim, "*")
+        assert_close(got, ref, product_rtol(np.float64, rows if dim == 1 else cols), what=f"dims={dim}")
 
 
 @pytest.mark.parametrize("dt", [np.float32, np.float64, np.int32])

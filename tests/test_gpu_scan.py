@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import NP, assert_close, assert_mixed, dec
+from helpers import NP, assert_close, assert_mixed, dec, pow2_factors, product_rtol
 
 pytestmark = pytest.mark.gpu
 
@@ -91,6 +91,59 @@ def test_float_add_scan(kf, oracle, dev, dt, rtol):
             assert_close(got, ref, rtol, atol=1e-30, what=f"{dt.__name__} + n={n} excl={exclusive}")
             if exclusive:
                 assert got[0] == 0 and not np.signbit(got[0])
+
+
+@pytest.mark.parametrize("dt", [np.int32, np.int64, np.uint8])
+@pytest.mark.parametrize("exclusive", [False, True])
+def test_int_product_scan_exact(kf, oracle, dev, dt, exclusive):
+    # Julia `*` wraps on integers; odd factors never reach 0 modulo 2^bits,
+    # so every prefix stays informative across all tile sizes
+    rng = np.random.default_rng(zlib.crc32(f"mul{dt.__name__}{exclusive}".encode()))
+    for n in SIZES:
+        x = 2 * rng.integers(-3, 3, n) + 1
+        x = (x % 256).astype(dt) if dt == np.uint8 else x.astype(dt)
+        got = run(kf, dev, x, "*", exclusive=exclusive)
+        ref = oracle.scan(x, "*", exclusive=exclusive)
+        assert np.array_equal(got, ref), f"{dt.__name__} * excl={exclusive} n={n}: first diff at " \
+            f"{np.nonzero(got != ref)[0][:1]}"
+
+
+@pytest.mark.parametrize("dt", [np.float32, np.float64])
+def test_float_product_scan(kf, oracle, dev, dt):
+    # exact: +-2 / +-1/2 factors (every prefix is a power of two), bit for bit;
+    # rounded: factors in [0.999, 1.001] within the forward error bound
+    # gamma_{i-1} of a product of i factors, whatever the association order
+    rng = np.random.default_rng(19)
+    for n in SIZES:
+        x = pow2_factors(rng, n, dt)
+        for exclusive in (False, True):
+            got = run(kf, dev, x, "*", exclusive=exclusive)
+            ref = oracle.scan(x, "*", exclusive=exclusive)
+            assert np.array_equal(got.astype(np.float64), ref), f"{dt.__name__} * n={n} excl={exclusive}"
+            if exclusive:
+                assert got[0] == 1
+        x = rng.uniform(0.999, 1.001, n).astype(dt)
+        got = run(kf, dev, x, "*")
+        assert_close(got, oracle.scan(x, "*"), product_rtol(dt, n), what=f"{dt.__name__} * n={n}")
+
+
+def test_product_scan_reference_cases(kf, oracle, dev):
+    # reference test/tests/scan/scan_test.jl:1-19: scan!(*, dst, src) on
+    # Float32 U[0,1) at n = 10^7 and scan!(identity, *, dst, src) on Float64
+    # at n = 1005, both against accumulate(*); the Float32 products underflow
+    # within ~100 elements, hence the mixed criterion
+    import operator
+    rng = np.random.default_rng(20)
+    x = rng.random(10**7).astype(np.float32)
+    t = torch.from_numpy(x).to(dev)
+    d = torch.zeros_like(t)
+    kf.scan_(operator.mul, d, t)
+    assert_mixed(d.cpu().numpy(), oracle.scan(x, "*"), 1e-5, what="scan!(*) Float32 10^7")
+    y = rng.random(1005)
+    t = torch.from_numpy(y).to(dev)
+    d = torch.zeros_like(t)
+    kf.scan_(kf.identity, operator.mul, d, t)
+    assert_mixed(d.cpu().numpy(), oracle.scan(y, "*"), 1e-12, what="scan!(identity, *) Float64 1005")
 
 
 def test_golden_vectors(kf, dev, golden):

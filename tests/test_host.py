@@ -12,8 +12,9 @@ def test_operator_and_map_resolution(kf):
     assert kf._op_code(max) == L.OP_MAX and kf._op_code(min) == L.OP_MIN
     assert kf._op_code(kf.affine) == L.OP_AFFINE
     assert kf._map_code(kf.identity) == L.MAP_IDENTITY and kf._map_code(kf.abs2) == L.MAP_ABS2
+    assert kf._op_code(operator.mul) == L.OP_MUL == kf._op_code("*")
     with pytest.raises(kf.ArgumentError):
-        kf._op_code(operator.mul)
+        kf._op_code(operator.truediv)
     with pytest.raises(kf.ArgumentError):
         kf._map_code(lambda x: x)
 

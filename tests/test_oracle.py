@@ -75,6 +75,75 @@ def test_scan_int_wraps(oracle):
                                                     (250 * 250 + 100 + 255 * 255) % 256]
 
 
+def _wrap_signed(v, bits):
+    v %= 1 << bits
+    return v - (1 << bits) if v >= 1 << (bits - 1) else v
+
+
+@pytest.mark.parametrize("n", [1, 2, 12, 13, 21, 40, 1000])
+def test_product_scan_closed_forms(oracle, n):
+    # scan!(*) of 1:n is n!, exact in Python integers and then wrapped to the
+    # element width (Julia Int32/Int64/UInt8 `*` wrap around)
+    facts, f = [], 1
+    for k in range(1, n + 1):
+        f *= k
+        facts.append(f)
+    for dt, bits, signed in ((np.int32, 32, True), (np.int64, 64, True), (np.uint8, 8, False)):
+        x = np.arange(1, n + 1).astype(dt)
+        want = [(_wrap_signed(v, bits) if signed else v % (1 << bits)) for v in facts]
+        assert oracle.scan(x, "*").tolist() == want, (dt, n)
+        exc = oracle.scan(x, "*", exclusive=True)
+        assert exc[0] == 1 and exc[1:].tolist() == want[:-1]
+        assert int(oracle.reduce(x, "*")) == want[-1]
+    # powers of two are exact in binary floating point
+    for dt in (np.float32, np.float64):
+        k = min(n, 1000)
+        got = oracle.scan(np.full(k, 2.0, dt), "*")
+        assert np.array_equal(got, 2.0 ** np.arange(1, k + 1, dtype=np.float64))
+        got = oracle.scan(np.full(k, 0.5, dt), "*", exclusive=True)
+        assert np.array_equal(got, 0.5 ** np.arange(0, k, dtype=np.float64))
+
+
+def test_product_scan_matches_numpy(oracle):
+    # the reference's product-scan test draws U[0, 1) (scan_test.jl:1-19); numpy's
+    # cumprod in Float64 is an independent left-to-right product
+    rng = np.random.default_rng(5)
+    x = rng.uniform(0.9, 1.1, 4097)
+    assert np.allclose(oracle.scan(x, "*"), np.cumprod(x), rtol=1e-12, atol=0)
+    assert np.isclose(oracle.reduce(x, "*"), np.prod(x), rtol=1e-12)
+    xf = x.astype(np.float32)
+    assert np.allclose(oracle.scan(xf, "*"), np.cumprod(xf.astype(np.float64)), rtol=1e-12, atol=0)
+
+
+def test_pow2_product_fixtures_are_exact(oracle):
+    # the GPU product tests compare bit for bit on these factors: every
+    # prefix (scan) or subset (reduction) product must be a representable
+    # power of two, here checked against the exponent and sign sums
+    import sys, os
+    sys.path.insert(0, os.path.dirname(__file__))
+    from helpers import pow2_factors, product_rtol
+    rng = np.random.default_rng(3)
+    for dt in (np.float32, np.float64):
+        for n in (1, 7, 4097, 1_000_000):
+            x = pow2_factors(rng, n, dt)
+            e = np.cumsum(np.log2(np.abs(x.astype(np.float64))))
+            sgn = np.cumprod(np.sign(x.astype(np.float64)))
+            assert np.abs(e).max() <= 20
+            assert np.array_equal(oracle.scan(x, "*"), sgn * np.exp2(e))
+            y = pow2_factors(rng, n, dt, contiguous=False)
+            assert np.abs(np.log2(np.abs(y.astype(np.float64)))).sum() <= 60
+            assert oracle.reduce(y, "*") == np.prod(np.sign(y)) * np.exp2(np.log2(np.abs(y.astype(np.float64))).sum())
+    # the error bound covers a float32 pairwise tree of near-1 factors (whose
+    # rounding drifts one way: about -8e-5 at 10^5)
+    x = rng.uniform(0.999, 1.001, 100_000).astype(np.float32)
+    y = x.copy()
+    while y.size > 1:
+        y = np.append(y, np.float32(1)) if y.size % 2 else y
+        y = (y[0::2] * y[1::2]).astype(np.float32)
+    exact = oracle.reduce(x, "*")
+    assert abs(float(y[0]) - exact) <= product_rtol(np.float32, x.size) * abs(exact)
+
+
 def test_exclusive_is_shifted_inclusive(oracle):
     rng = np.random.default_rng(1)
     for dt, op, ident in ((np.int32, "max", np.iinfo(np.int32).min), (np.int32, "min", np.iinfo(np.int32).max),
