@@ -76,14 +76,21 @@ typedef enum {
   KF_MAP2_SQDIFF = 1  /* (x - y)^2   (squared distance)  */
 } kf_map2;
 
-/* Element types. KF_F32X2 is an interleaved (a, b) pair of float32. */
+/* Element types. KF_F32X2 is an interleaved (a, b) pair of float32.
+ * KF_Q32 / KF_Q64 are quaternions (s, v1, v2, v3) of float32 / float64, the
+ * memory layout of Julia's QuaternionF32 / QuaternionF64 (Quaternions.jl,
+ * used by the reference's non-commutative scan test,
+ * test/tests/scan/scan_test.jl:22-33); they take KF_OP_MUL (the Hamilton
+ * product) in kf_scan only. */
 typedef enum {
   KF_F32 = 0,
   KF_F64 = 1,
   KF_I32 = 2,
   KF_I64 = 3,
   KF_U8 = 4,
-  KF_F32X2 = 5
+  KF_F32X2 = 5,
+  KF_Q32 = 6,
+  KF_Q64 = 7
 } kf_dtype;
 
 int kf_version(void);

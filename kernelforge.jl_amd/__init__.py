@@ -19,9 +19,13 @@ Arrays are torch tensors on a ROCm device, read with Julia's conventions:
 tensor dim k is Julia dim k+1, `dims` are 1-based, and a Julia column-major
 matrix is a tensor whose first dim has stride 1 (e.g. `torch.empty(n, m).T`
 is an m x n column-major matrix; `A[:, ::2]` is `view(A, :, 1:2:end)`).
-Affine pairs are float32 tensors of shape (n, 2) holding (a, b).
+Affine pairs are float32 tensors of shape (n, 2) holding (a, b); a vector
+of quaternions (Julia's QuaternionF32 / QuaternionF64) is a float32 /
+float64 tensor of shape (n, 4) holding (s, v1, v2, v3).
 
-Operators: `+` (operator.add or "+"), `max`, `min`, `affine` (scan only);
+Operators: `+` (operator.add or "+"), `*` (operator.mul or "*"; on
+quaternions the Hamilton product, scan only), `max`, `min`, `affine` (scan
+only);
 maps: `identity`, `abs2`. Anything else raises ArgumentError, as does a
 shape/dtype mismatch. Tuning keywords of the reference (Nitem, workgroup,
 blocks, family, arch) are accepted and ignored: launch shapes are fixed for
@@ -251,6 +255,12 @@ def _scan_operand(t, op):
         if t.shape[0] > 0 and (t.stride(1) != 1 or t.stride(0) % 2 != 0):
             raise ArgumentError("affine pairs must be stored as adjacent (a, b) float32 values")
         return _L.F32X2, t.shape[0], max(t.stride(0) // 2, 1)
+    if op == _L.OP_MUL and t.dim() == 2 and t.shape[1] == 4 and t.dtype in (torch.float32, torch.float64):
+        # a vector of quaternions (s, v1, v2, v3), the layout of Julia's
+        # QuaternionF32 / QuaternionF64; `*` is the Hamilton product
+        if t.shape[0] > 0 and (t.stride(1) != 1 or t.stride(0) % 4 != 0):
+            raise ArgumentError("quaternions must be stored as 4 adjacent (s, v1, v2, v3) values")
+        return (_L.Q32 if t.dtype == torch.float32 else _L.Q64), t.shape[0], max(t.stride(0) // 4, 1)
     if t.dim() != 1:
         raise ArgumentError(f"scan! takes vectors; got a {t.dim()}-d tensor")
     if t.dtype not in _DTYPES:
@@ -274,7 +284,7 @@ def scan_(*args, exclusive=False, tmp=None, g=None, **tuning):
     dst[i] = inclusive[i-1]. In place (dst is src) is allowed."""
     f, op, (dst, src) = _split_f_op(args, 2, "scan!")
     opc, fc = _op_code(op), _map_code(f)
-    if _post_code(g) is None or (g not in (None, identity) and opc == _L.OP_AFFINE):
+    if _post_code(g) is None or (g not in (None, identity) and (opc == _L.OP_AFFINE or src.dim() == 2)):
         raise ArgumentError(f"scan!: unsupported post-map g={g!r}: expected identity, sqrt or abs2")
     _require_device(dst, src)
     dt, n, ss = _scan_operand(src, opc)

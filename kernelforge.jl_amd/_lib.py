@@ -16,7 +16,7 @@ OP_ADD, OP_MAX, OP_MIN, OP_AFFINE, OP_MUL = 0, 1, 2, 3, 4
 MAP_IDENTITY, MAP_ABS2 = 0, 1
 MAP2_MUL, MAP2_SQDIFF = 0, 1
 POST_IDENTITY, POST_SQRT, POST_ABS2 = 0, 1, 2
-F32, F64, I32, I64, U8, F32X2 = 0, 1, 2, 3, 4, 5
+F32, F64, I32, I64, U8, F32X2, Q32, Q64 = 0, 1, 2, 3, 4, 5, 6, 7
 
 # Every symbol include/kf.h declares, with its ctypes signature.
 _P, _I, _I64, _SZ = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_size_t

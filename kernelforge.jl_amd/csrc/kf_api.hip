@@ -32,6 +32,8 @@ size_t kf_dtype_size(kf_dtype dt) {
     case KF_I64: return 8;
     case KF_U8: return 1;
     case KF_F32X2: return 8;
+    case KF_Q32: return 16;
+    case KF_Q64: return 32;
   }
   return 0;
 }
@@ -45,6 +47,13 @@ int kf_validate_op(kf_op op, kf_map f, kf_dtype dt, int allow_affine) {
     if (op != KF_OP_AFFINE || dt != KF_F32X2)
       return kf_set_error(KF_EINVAL, "the affine operator requires KF_F32X2 elements and vice versa");
     if (f != KF_MAP_IDENTITY) return kf_set_error(KF_EINVAL, "abs2 is not defined on affine pairs");
+    return KF_OK;
+  }
+  if (dt == KF_Q32 || dt == KF_Q64) {
+    if (!allow_affine)
+      return kf_set_error(KF_EINVAL, "the quaternion product is non-commutative and is supported by kf_scan only");
+    if (op != KF_OP_MUL) return kf_set_error(KF_EINVAL, "quaternion elements take KF_OP_MUL only");
+    if (f != KF_MAP_IDENTITY) return kf_set_error(KF_EINVAL, "abs2 is not defined on quaternions here");
     return KF_OK;
   }
   if (op != KF_OP_ADD && op != KF_OP_MAX && op != KF_OP_MIN && op != KF_OP_MUL)

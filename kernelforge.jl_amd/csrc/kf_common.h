@@ -29,6 +29,15 @@ struct __attribute__((aligned(8))) f32x2 {
   float a, b;
 };
 
+// Quaternions s + v1 i + v2 j + v3 k, laid out as Julia's Quaternion{T}
+// (fields s, v1, v2, v3): QuaternionF32 16 bytes, QuaternionF64 32 bytes.
+template <class F> struct quat {
+  F s, v1, v2, v3;
+};
+using q32 = quat<float>;
+using q64 = quat<double>;
+template <class T> constexpr bool is_quat = __is_same(T, q32) || __is_same(T, q64);
+
 // ---------------------------------------------------------------------------
 // Operators. Each provides identity<T>() and combine(older, newer).
 // ---------------------------------------------------------------------------
@@ -81,9 +90,23 @@ template <> __device__ inline int32_t OpMin::identity<int32_t>() { return INT32_
 template <> __device__ inline int64_t OpMin::identity<int64_t>() { return INT64_MAX; }
 template <> __device__ inline uint8_t OpMin::identity<uint8_t>() { return 255; }
 
-// Julia `*`: IEEE products; integers wrap (computed unsigned).
+// Julia `*`: IEEE products; integers wrap (computed unsigned); quaternions
+// multiply by the Hamilton product, older operand on the left.
 struct OpMul {
-  template <class T> __device__ static T identity() { return T(1); }
+  template <class T> __device__ static T identity() {
+    if constexpr (is_quat<T>)
+      return T{1, 0, 0, 0};
+    else
+      return T(1);
+  }
+  template <class F> __device__ static quat<F> combine(quat<F> p, quat<F> q) {
+    quat<F> o;
+    o.s = p.s * q.s - p.v1 * q.v1 - p.v2 * q.v2 - p.v3 * q.v3;
+    o.v1 = p.s * q.v1 + p.v1 * q.s + p.v2 * q.v3 - p.v3 * q.v2;
+    o.v2 = p.s * q.v2 - p.v1 * q.v3 + p.v2 * q.s + p.v3 * q.v1;
+    o.v3 = p.s * q.v3 + p.v1 * q.v2 - p.v2 * q.v1 + p.v3 * q.s;
+    return o;
+  }
   __device__ static float combine(float x, float y) { return x * y; }
   __device__ static double combine(double x, double y) { return x * y; }
   __device__ static int32_t combine(int32_t x, int32_t y) { return (int32_t)((uint32_t)x * (uint32_t)y); }
@@ -222,6 +245,8 @@ template <> struct DT<KF_I32> { using T = int32_t; };
 template <> struct DT<KF_I64> { using T = int64_t; };
 template <> struct DT<KF_U8> { using T = uint8_t; };
 template <> struct DT<KF_F32X2> { using T = f32x2; };
+template <> struct DT<KF_Q32> { using T = q32; };
+template <> struct DT<KF_Q64> { using T = q64; };
 
 }  // namespace kf
 

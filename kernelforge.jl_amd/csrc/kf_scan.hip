@@ -95,8 +95,27 @@ constexpr uint32_t kSpinLimit = 1u << 24;  // lookback polls before giving up (s
 // 20.6 us; 3*10^7 Float32, 916 tiles on 512 slots: 49.5 vs 53.5 us at 4).
 inline int look_window(int64_t ntiles, int64_t resident) { return ntiles > resident ? 4 : kWave; }
 
+// The unit a lane loads and stores: 16 bytes, or one element of a wider
+// type (a 32-byte QuaternionF64 moves as two 16-byte halves).
+template <class T> constexpr int kVecBytes = sizeof(T) > 16 ? (int)sizeof(T) : 16;
+struct uint4x2 {
+  uint4 lo, hi;
+};
+template <class T> using VecT = __typeof__(__builtin_choose_expr(sizeof(T) > 16, uint4x2{}, uint4{}));
+__device__ inline uint4 ld_vec(const uint4* p) { return ld_stream(p); }
+__device__ inline uint4x2 ld_vec(const uint4x2* p) {
+  const uint4* q = reinterpret_cast<const uint4*>(p);
+  return uint4x2{ld_stream(q), ld_stream(q + 1)};
+}
+__device__ inline void st_vec(uint4* p, uint4 v) { st_stream(p, v); }
+__device__ inline void st_vec(uint4x2* p, uint4x2 v) {
+  uint4* q = reinterpret_cast<uint4*>(p);
+  st_stream(q, v.lo);
+  st_stream(q + 1, v.hi);
+}
+
 template <class T, int BLOCK = kScanBlock, int VPL = 8> struct ScanShape {
-  static constexpr int EPV = 16 / (int)sizeof(T);   // elements per 16-byte vector
+  static constexpr int EPV = kVecBytes<T> / (int)sizeof(T);  // elements per vector
   static constexpr int V = VPL;                     // vectors per lane
   static constexpr int WAVE_ELEMS = kWave * V * EPV;
   static constexpr int TILE = BLOCK * V * EPV;
@@ -186,7 +205,7 @@ template <class T, int BLOCK> constexpr bool kStashForLookback = sizeof(T) == 8 
 // The post-map g on a stored value: sqrt or abs2 for floats, abs2
 // (wrapping) for integers; kf_scan rejects anything else.
 template <class T> __device__ inline T post_apply(int post, T v) {
-  if constexpr (__is_same(T, f32x2)) {
+  if constexpr (__is_same(T, f32x2) || is_quat<T>) {
     return v;
   } else if constexpr (__is_same(T, float)) {
     return post == KF_POST_SQRT ? __builtin_sqrtf(v) : v * v;
@@ -207,7 +226,7 @@ template <class T, class Op> __device__ inline T exclusive_first() {
 // For sub-dword T, make the packed dwords of a vector the only live copy at
 // this point; the compiler would otherwise keep all V*EPV unpacked values
 // in registers between the phases of the scan (and spill).
-template <class T> __device__ inline void pin_packed(uint4& v) {
+template <class T, class VV> __device__ inline void pin_packed(VV& v) {
   if constexpr (sizeof(T) < 4) asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w));
 }
 
@@ -265,7 +284,8 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
   __shared__ T wave_pre[kScanWaves];
   __shared__ uint64_t s_ticket;
   constexpr bool kLdsRows = kLdsRowsFor<Op, V>;
-  __shared__ uint4 s_stash[kStashForLookback<T, BLOCK> ? V : 1][kWave];
+  using Vec = VecT<T>;
+  __shared__ Vec s_stash[kStashForLookback<T, BLOCK> ? V : 1][kWave];
   __shared__ T s_rowpre[kStashForLookback<T, BLOCK> && !kLdsRows ? V : 1][kWave];
   __shared__ __align__(16) T s_rows[kLdsRows ? kScanWaves : 1][kLdsRows ? V * kWave : 1];
 
@@ -296,19 +316,19 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
   // The tile stays packed in registers (4 dwords per vector whatever T is,
   // so 16 uint8 elements cost what 4 floats do); each vector is unpacked
   // only while it is being combined.
-  uint4 r[V];
+  Vec r[V];
   if (full) {
-    const uint4* g = reinterpret_cast<const uint4*>(srcv + wbase);
+    const Vec* g = reinterpret_cast<const Vec*>(srcv + wbase);
 #pragma unroll
-    for (int j = 0; j < V; ++j) r[j] = ld_stream(g + j * kWave + lane);
+    for (int j = 0; j < V; ++j) r[j] = ld_vec(g + j * kWave + lane);
     if constexpr (!__is_same(Map, MapIdentity)) {
 #pragma unroll
       for (int j = 0; j < V; ++j) {
         T x[EPV];
-        __builtin_memcpy(x, &r[j], 16);
+        __builtin_memcpy(x, &r[j], sizeof(Vec));
 #pragma unroll
         for (int k = 0; k < EPV; ++k) x[k] = Map::apply(x[k]);
-        __builtin_memcpy(&r[j], x, 16);
+        __builtin_memcpy(&r[j], x, sizeof(Vec));
         pin_packed<T>(r[j]);
       }
     }
@@ -317,20 +337,20 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
     // strided operand: vectors wholly inside [0, n) of a contiguous operand
     // still stream; the others go element by element
     // (all vector loads are issued before any is used, as in the full path)
-    const uint4* g = reinterpret_cast<const uint4*>(srcv + wbase);
+    const Vec* g = reinterpret_cast<const Vec*>(srcv + wbase);
     bool inside[V];
 #pragma unroll
     for (int j = 0; j < V; ++j) {
       const int64_t e0 = wbase + (int64_t)(j * kWave + lane) * EPV - off;  // real index of element 0
       inside[j] = vec && e0 >= 0 && e0 + EPV <= n;
-      if (inside[j]) r[j] = ld_stream(g + j * kWave + lane);
+      if (inside[j]) r[j] = ld_vec(g + j * kWave + lane);
     }
 #pragma unroll
     for (int j = 0; j < V; ++j) {
       const int64_t e0 = wbase + (int64_t)(j * kWave + lane) * EPV - off;
       T x[EPV];
       if (inside[j]) {
-        __builtin_memcpy(x, &r[j], 16);
+        __builtin_memcpy(x, &r[j], sizeof(Vec));
 #pragma unroll
         for (int k = 0; k < EPV; ++k) x[k] = Map::apply(x[k]);
       } else {
@@ -340,7 +360,7 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
           x[k] = (idx >= 0 && idx < n) ? Map::apply(src[idx * src_stride]) : id;
         }
       }
-      __builtin_memcpy(&r[j], x, 16);
+      __builtin_memcpy(&r[j], x, sizeof(Vec));
       pin_packed<T>(r[j]);
     }
   }
@@ -354,10 +374,10 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
 #pragma unroll
   for (int j = 0; j < V; ++j) {
     T x[EPV];
-    __builtin_memcpy(x, &r[j], 16);
+    __builtin_memcpy(x, &r[j], sizeof(Vec));
 #pragma unroll
     for (int k = 1; k < EPV; ++k) x[k] = Op::combine(x[k - 1], x[k]);
-    __builtin_memcpy(&r[j], x, 16);
+    __builtin_memcpy(&r[j], x, sizeof(Vec));
     pin_packed<T>(r[j]);
     if constexpr (kLdsRows) {
       tot[j] = x[EPV - 1];
@@ -431,7 +451,7 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
       }
     }
     T x[EPV], o[EPV];
-    __builtin_memcpy(x, &r[j], 16);
+    __builtin_memcpy(x, &r[j], sizeof(Vec));
     const T p = Op::combine(prefix, rowpre[j]);
     if constexpr (EXCL) {
       o[0] = p;
@@ -448,9 +468,9 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
     }
     const int64_t e0 = wbase + (int64_t)(j * kWave + lane) * EPV - off;  // real index of element 0
     if (full || (vec && e0 >= 0 && e0 + EPV <= n)) {
-      uint4 w;
-      __builtin_memcpy(&w, o, 16);
-      st_stream(reinterpret_cast<uint4*>(dstv + wbase) + j * kWave + lane, w);
+      Vec w;
+      __builtin_memcpy(&w, o, sizeof(Vec));
+      st_vec(reinterpret_cast<Vec*>(dstv + wbase) + j * kWave + lane, w);
     } else {
 #pragma unroll
       for (int k = 0; k < EPV; ++k) {
@@ -463,16 +483,20 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
 
 // Tile shape for n elements of T: a pure function of (T, n) so that the
 // scratch query and the launch agree.
+// Elements wider than 8 bytes carry 4-8 VGPRs per vector and per row
+// prefix: they stop at 4 (16-byte) or 2 (32-byte) vectors per lane.
+template <class T> constexpr int max_tier() { return sizeof(T) > 16 ? 1 : sizeof(T) > 8 ? 2 : kTiers - 1; }
+
 template <class T> int scan_tier(int64_t n) {
   const int64_t bytes = n * (int64_t)sizeof(T);
   if (has_wide_tier<T>() && bytes >= kWideBytes) return kTierWide;
-  int t = kTiers - 1;
-  while (t > 0 && bytes < min_tiles<T>() * (int64_t)scan_block<T>(t) * kTierV[t] * 16) --t;
+  int t = max_tier<T>();
+  while (t > 0 && bytes < min_tiles<T>() * (int64_t)scan_block<T>(t) * kTierV[t] * kVecBytes<T>) --t;
   return t;
 }
 
 template <class T> int64_t tier_tile(int tier) {
-  return (int64_t)scan_block<T>(tier) * tier_v(tier) * (16 / (int64_t)sizeof(T));
+  return (int64_t)scan_block<T>(tier) * tier_v(tier) * ScanShape<T>::EPV;
 }
 
 // Tiles for n elements starting `off` elements after a 16-byte boundary.
@@ -521,15 +545,22 @@ int launch_scan(const void* src, int64_t ss, void* dst, int64_t ds, int64_t n, i
                 void* scratch, hipStream_t stream) {
   // Vector path when both operands are contiguous and equally misaligned
   // (e.g. views src[k:], dst[k:] of aligned buffers); `off` shifts the tiles.
+  // (elements of 16 bytes or more need 16-byte aligned operands for it)
   const int vec = ss == 1 && ds == 1 && ((uintptr_t)src % 16 == (uintptr_t)dst % 16) &&
-                  ((uintptr_t)src % sizeof(T) == 0);
+                  ((uintptr_t)src % 16 % sizeof(T) == 0);
   const int off = vec ? (int)(((uintptr_t)src % 16) / sizeof(T)) : 0;
   const int64_t ntiles = scan_tiles<T>(n, off);
   switch (scan_tier<T>(n)) {
     case 0: launch_scan_tier<T, Op, Map, 0>(src, ss, dst, ds, n, excl, ntiles, vec, off, scratch, stream); break;
     case 1: launch_scan_tier<T, Op, Map, 1>(src, ss, dst, ds, n, excl, ntiles, vec, off, scratch, stream); break;
-    case 2: launch_scan_tier<T, Op, Map, 2>(src, ss, dst, ds, n, excl, ntiles, vec, off, scratch, stream); break;
-    case 3: launch_scan_tier<T, Op, Map, 3>(src, ss, dst, ds, n, excl, ntiles, vec, off, scratch, stream); break;
+    case 2:
+      if constexpr (max_tier<T>() >= 2)
+        launch_scan_tier<T, Op, Map, 2>(src, ss, dst, ds, n, excl, ntiles, vec, off, scratch, stream);
+      break;
+    case 3:
+      if constexpr (max_tier<T>() >= 3)
+        launch_scan_tier<T, Op, Map, 3>(src, ss, dst, ds, n, excl, ntiles, vec, off, scratch, stream);
+      break;
     default:
       if constexpr (has_wide_tier<T>())
         launch_scan_tier<T, Op, Map, kTierWide>(src, ss, dst, ds, n, excl, ntiles, vec, off, scratch, stream);
@@ -540,7 +571,7 @@ int launch_scan(const void* src, int64_t ss, void* dst, int64_t ds, int64_t n, i
 template <class T, class Op>
 int scan_map(kf_map f, const void* src, int64_t ss, void* dst, int64_t ds, int64_t n, int excl,
              void* scratch, hipStream_t stream) {
-  if constexpr (__is_same(T, f32x2)) {
+  if constexpr (__is_same(T, f32x2) || is_quat<T>) {
     return launch_scan<T, Op, MapIdentity>(src, ss, dst, ds, n, excl, scratch, stream);
   } else {
     if (f == KF_MAP_ABS2) return launch_scan<T, Op, MapAbs2>(src, ss, dst, ds, n, excl, scratch, stream);
@@ -553,6 +584,8 @@ int scan_op(kf_op op, kf_map f, const void* src, int64_t ss, void* dst, int64_t 
             int excl, void* scratch, hipStream_t stream) {
   if constexpr (__is_same(T, f32x2)) {
     return scan_map<T, OpAffine>(f, src, ss, dst, ds, n, excl, scratch, stream);
+  } else if constexpr (is_quat<T>) {
+    return scan_map<T, OpMul>(f, src, ss, dst, ds, n, excl, scratch, stream);
   } else {
     switch (op) {
       case KF_OP_ADD: return scan_map<T, OpAdd>(f, src, ss, dst, ds, n, excl, scratch, stream);
@@ -594,6 +627,8 @@ extern "C" size_t kf_scan_scratch_bytes(kf_dtype dt, kf_op op, int64_t n) {
     case KF_I64: return scan_scratch<int64_t>(n);
     case KF_U8: return scan_scratch<uint8_t>(n);
     case KF_F32X2: return scan_scratch<f32x2>(n);
+    case KF_Q32: return scan_scratch<q32>(n);
+    case KF_Q64: return scan_scratch<q64>(n);
   }
   return 0;
 }
@@ -605,8 +640,8 @@ extern "C" int kf_scan(kf_op op, kf_map f, kf_post g, kf_dtype dt, int exclusive
   if (rc) return rc;
   if (g != KF_POST_IDENTITY && g != KF_POST_SQRT && g != KF_POST_ABS2)
     return kf_set_error(KF_EINVAL, "kf_scan: unknown post-map g = %d", (int)g);
-  if (g != KF_POST_IDENTITY && dt == KF_F32X2)
-    return kf_set_error(KF_EINVAL, "kf_scan: the affine scan takes no post-map");
+  if (g != KF_POST_IDENTITY && (dt == KF_F32X2 || dt == KF_Q32 || dt == KF_Q64))
+    return kf_set_error(KF_EINVAL, "kf_scan: the affine and quaternion scans take no post-map");
   if (g == KF_POST_SQRT && dt != KF_F32 && dt != KF_F64)
     return kf_set_error(KF_EINVAL, "kf_scan: sqrt post-map needs a floating-point type");
   if (n < 0) return kf_set_error(KF_EINVAL, "kf_scan: n = %lld < 0", (long long)n);
@@ -616,7 +651,7 @@ extern "C" int kf_scan(kf_op op, kf_map f, kf_post g, kf_dtype dt, int exclusive
     return kf_set_error(KF_EINVAL, "kf_scan: strides must be >= 1 (got %lld, %lld)",
                         (long long)src_stride, (long long)dst_stride);
   const size_t es = kf_dtype_size(dt);
-  const size_t align = dt == KF_F32X2 ? 4 : es;
+  const size_t align = dt == KF_F32X2 || dt == KF_Q32 ? 4 : dt == KF_Q64 ? 8 : es;
   if ((uintptr_t)src % align || (uintptr_t)dst % align)
     return kf_set_error(KF_EINVAL, "kf_scan: src/dst not aligned to the element type");
   // Overlap other than exact in-place aliasing would make tiles read data
@@ -633,7 +668,10 @@ extern "C" int kf_scan(kf_op op, kf_map f, kf_post g, kf_dtype dt, int exclusive
                         scratch ? scratch_bytes : (size_t)0);
   if ((uintptr_t)scratch % 256)
     return kf_set_error(KF_EINVAL, "kf_scan: scratch must be 256-byte aligned");
-  if (scan_tiles<f32x2>(n) * kScanBlock > (int64_t)0xffffffffLL)
+  // tiles of this dtype (an upper bound: the scratch query allows for the
+  // largest misalignment shift) times threads per tile must fit the grid
+  const int64_t tiles = (int64_t)((need - kScanHeaderBytes) / (kDescWords * sizeof(uint64_t)));
+  if (tiles * kScanBlock > (int64_t)0xffffffffLL)
     return kf_set_error(KF_EINVAL, "kf_scan: n = %lld exceeds the grid limit", (long long)n);
   hipStream_t s = (hipStream_t)stream;
   const int mode = (exclusive ? 1 : 0) | ((int)g << 1);
@@ -644,6 +682,8 @@ extern "C" int kf_scan(kf_op op, kf_map f, kf_post g, kf_dtype dt, int exclusive
     case KF_I64: return scan_op<int64_t>(op, f, src, src_stride, dst, dst_stride, n, mode, scratch, s);
     case KF_U8: return scan_op<uint8_t>(op, f, src, src_stride, dst, dst_stride, n, mode, scratch, s);
     case KF_F32X2: return scan_op<f32x2>(op, f, src, src_stride, dst, dst_stride, n, mode, scratch, s);
+    case KF_Q32: return scan_op<q32>(op, f, src, src_stride, dst, dst_stride, n, mode, scratch, s);
+    case KF_Q64: return scan_op<q64>(op, f, src, src_stride, dst, dst_stride, n, mode, scratch, s);
   }
   return kf_set_error(KF_EINVAL, "kf_scan: bad dtype");
 }

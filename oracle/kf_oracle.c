@@ -158,6 +158,32 @@ void kfo_scan_affine(const float* ab, int64_t n, int excl, double* out) {
   }
 }
 
+/* Quaternion product scan in double: q[4*i .. 4*i+3] = (s, v1, v2, v3) as
+ * float (f64 == 0) or double (f64 == 1); prefixes multiply older on the
+ * left (Base.accumulate(*, x) on Quaternions.jl values, reference
+ * test/tests/scan/scan_test.jl:22-33), by the Hamilton product
+ * (s1 + v1 i + ...)(s2 + w1 i + ...) with i^2 = j^2 = k^2 = ijk = -1.
+ * Exclusive: out[0] = (1, 0, 0, 0). */
+void kfo_scan_quat(const void* q, int f64, int64_t n, int excl, double* out) {
+  double p[4] = {1.0, 0.0, 0.0, 0.0};
+  for (int64_t i = 0; i < n; ++i) {
+    double x[4];
+    for (int c = 0; c < 4; ++c) x[c] = f64 ? ((const double*)q)[4 * i + c] : (double)((const float*)q)[4 * i + c];
+    if (excl)
+      for (int c = 0; c < 4; ++c) out[4 * i + c] = p[c];
+    const double s = p[0] * x[0] - p[1] * x[1] - p[2] * x[2] - p[3] * x[3];
+    const double a = p[0] * x[1] + p[1] * x[0] + p[2] * x[3] - p[3] * x[2];
+    const double b = p[0] * x[2] - p[1] * x[3] + p[2] * x[0] + p[3] * x[1];
+    const double c = p[0] * x[3] + p[1] * x[2] - p[2] * x[1] + p[3] * x[0];
+    p[0] = s;
+    p[1] = a;
+    p[2] = b;
+    p[3] = c;
+    if (!excl)
+      for (int k = 0; k < 4; ++k) out[4 * i + k] = p[k];
+  }
+}
+
 /* -------------------------------------------------------------- reduce ---- */
 
 double kfo_reduce_f(const void* src, int dt, int64_t n, int64_t stride, int op, int map) {

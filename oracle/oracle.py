@@ -41,6 +41,7 @@ def lib():
         L.kfo_scan_f.argtypes = [P, I, I64, I64, I, I, I, P]
         L.kfo_scan_i.argtypes = [P, I, I64, I64, I, I, I, P]
         L.kfo_scan_affine.argtypes = [P, I64, I, P]
+        L.kfo_scan_quat.argtypes = [P, I, I64, I, P]
         L.kfo_reduce_f.argtypes = [P, I, I64, I64, I, I]
         L.kfo_reduce_f.restype = D
         L.kfo_reduce_i.argtypes = [P, I, I64, I64, I, I, P]
@@ -72,8 +73,16 @@ def _is_float(a):
 
 def scan(x, op="+", f="identity", exclusive=False):
     """Base.accumulate(op, f.(x)) (exclusive: shifted right, identity first).
-    x: 1-D numpy array (any stride); (n, 2) float32 pairs for op='affine'."""
+    x: 1-D numpy array (any stride); (n, 2) float32 pairs for op='affine';
+    (n, 4) float32/float64 quaternions (s, v1, v2, v3) for op='*' (Hamilton
+    product)."""
     L = lib()
+    if op == "*" and x.ndim == 2:
+        q = np.ascontiguousarray(x)
+        assert q.shape[1] == 4 and q.dtype in (np.float32, np.float64)
+        out = np.empty((q.shape[0], 4), np.float64)
+        L.kfo_scan_quat(_p(q), int(q.dtype == np.float64), q.shape[0], int(exclusive), _p(out))
+        return out
     if op == "affine":
         ab = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, 2)
         out = np.empty((ab.shape[0], 2), np.float64)

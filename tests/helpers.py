@@ -72,3 +72,32 @@ def product_rtol(dt, n):
     u = 2.0 ** -24 if np.dtype(dt) == np.float32 else 2.0 ** -53
     m = max(n - 1, 1)
     return m * u / (1 - m * u)
+
+
+# The quaternion group Q8 = {+-1, +-i, +-j, +-k} as (s, v1, v2, v3): its
+# products stay in the group and are exact in any float type, and it is
+# non-commutative (i j = k, j i = -k), so a scan of Q8 elements checks the
+# order of every product bit for bit.
+Q8 = np.array([[1, 0, 0, 0], [-1, 0, 0, 0], [0, 1, 0, 0], [0, -1, 0, 0],
+               [0, 0, 1, 0], [0, 0, -1, 0], [0, 0, 0, 1], [0, 0, 0, -1]], np.float64)
+
+
+def q8_sequence(rng, n, dt):
+    return Q8[rng.integers(0, 8, n)].astype(dt)
+
+
+def quat_as_complex2(q):
+    """2x2 complex matrices of quaternions (s, v1, v2, v3): s + v1 i + v2 j
+    + v3 k -> [[s + v1 i, v2 + v3 i], [-v2 + v3 i, s - v1 i]], an algebra
+    homomorphism, so matrix products are quaternion products."""
+    q = np.asarray(q, np.float64)
+    m = np.empty(q.shape[:-1] + (2, 2), np.complex128)
+    m[..., 0, 0] = q[..., 0] + 1j * q[..., 1]
+    m[..., 0, 1] = q[..., 2] + 1j * q[..., 3]
+    m[..., 1, 0] = -q[..., 2] + 1j * q[..., 3]
+    m[..., 1, 1] = q[..., 0] - 1j * q[..., 1]
+    return m
+
+
+def complex2_as_quat(m):
+    return np.stack([m[..., 0, 0].real, m[..., 0, 0].imag, m[..., 0, 1].real, m[..., 0, 1].imag], -1)

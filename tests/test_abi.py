@@ -63,8 +63,15 @@ def test_invalid_arguments_rejected_without_gpu(kf):
     # affine needs the pair type and vice versa
     assert L.kf_scan(K.OP_AFFINE, 0, 0, K.F32, 0, p, 1, p, 1, 10, p, 1 << 20, None) == K.KF_EINVAL
     assert L.kf_scan(K.OP_ADD, 0, 0, K.F32X2, 0, p, 1, p, 1, 10, p, 1 << 20, None) == K.KF_EINVAL
-    # the multiply operator takes the scalar types only
+    # the multiply operator takes the scalar types and the quaternions
     assert L.kf_scan(K.OP_MUL, 0, 0, K.F32X2, 0, p, 1, p, 1, 10, p, 1 << 20, None) == K.KF_EINVAL
+    # quaternions: the product only, no map or post-map, scan only
+    for q in (K.Q32, K.Q64):
+        assert L.kf_scan(K.OP_ADD, 0, 0, q, 0, p, 1, p, 1, 10, p, 1 << 20, None) == K.KF_EINVAL
+        assert L.kf_scan(K.OP_MUL, K.MAP_ABS2, 0, q, 0, p, 1, p, 1, 10, p, 1 << 20, None) == K.KF_EINVAL
+        assert L.kf_scan(K.OP_MUL, 0, K.POST_ABS2, q, 0, p, 1, p, 1, 10, p, 1 << 20, None) == K.KF_EINVAL
+        assert L.kf_reduce(K.OP_MUL, 0, q, p, 10, 1, p, p, 1 << 20, None) == K.KF_EINVAL
+        assert "scan only" in _err(kf) or "kf_scan only" in _err(kf)
     # affine is scan-only
     assert L.kf_reduce(K.OP_AFFINE, 0, K.F32X2, p, 10, 1, p, p, 1 << 20, None) == K.KF_EINVAL
     # post-map g: unknown code, sqrt on integers, any g on the affine scan

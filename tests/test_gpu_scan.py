@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import NP, assert_close, assert_mixed, dec, pow2_factors, product_rtol
+from helpers import NP, assert_close, assert_mixed, dec, pow2_factors, product_rtol, q8_sequence
 
 pytestmark = pytest.mark.gpu
 
@@ -144,6 +144,49 @@ def test_product_scan_reference_cases(kf, oracle, dev):
     d = torch.zeros_like(t)
     kf.scan_(kf.identity, operator.mul, d, t)
     assert_mixed(d.cpu().numpy(), oracle.scan(y, "*"), 1e-12, what="scan!(identity, *) Float64 1005")
+
+
+@pytest.mark.parametrize("dt", [np.float32, np.float64])
+def test_quaternion_scan_q8_exact(kf, oracle, dev, dt):
+    # random elements of the quaternion group {+-1, +-i, +-j, +-k}: every
+    # product is exact and i j = -j i, so any reordered, dropped or repeated
+    # factor shows bit for bit, at every tile shape
+    import operator
+    rng = np.random.default_rng(41)
+    for n in SIZES:
+        q = q8_sequence(rng, n, dt)
+        t = torch.from_numpy(q).to(dev)
+        for exclusive in (False, True):
+            got = kf.scan(operator.mul, t, exclusive=exclusive).cpu().numpy()
+            ref = oracle.scan(q, "*", exclusive=exclusive)
+            assert np.array_equal(got.astype(np.float64), ref), f"{dt.__name__} n={n} excl={exclusive}: " \
+                f"first diff at {np.nonzero((got != ref).any(1))[0][:1]}"
+    # a strided view (every 3rd quaternion) takes the element-wise path
+    q = q8_sequence(rng, 3 * 5001, dt)
+    t = torch.from_numpy(q).to(dev)[::3]
+    assert np.array_equal(kf.scan("*", t).cpu().numpy().astype(np.float64), oracle.scan(q[::3], "*"))
+
+
+@pytest.mark.parametrize("dt,n", [(np.float64, 10**6), (np.float32, 10**4)])
+def test_quaternion_scan_reference_case(kf, oracle, dev, dt, n):
+    # reference test/tests/scan/scan_test.jl:22-33: scan!(identity, *, dst,
+    # src) over 10^6 unit QuaternionF64 (normalised randn) against
+    # accumulate(*). Bound: one Hamilton product of quaternions of norm ~1
+    # adds at most gamma_4 * 2 <= 8u (normwise) and products by the identity
+    # are exact, so output i (a product of i factors in some association) is
+    # within 10 i u of the exact product.
+    import operator
+    rng = np.random.default_rng(43)
+    x = rng.standard_normal((n, 4))
+    q = (x / np.linalg.norm(x, axis=1, keepdims=True)).astype(dt)
+    t = torch.from_numpy(q).to(dev)
+    d = torch.zeros_like(t)
+    kf.scan_(kf.identity, operator.mul, d, t)
+    err = np.linalg.norm(d.cpu().numpy().astype(np.float64) - oracle.scan(q, "*"), axis=1)
+    u = 2.0 ** -53 if dt == np.float64 else 2.0 ** -24
+    bound = 10 * u * np.arange(1, n + 1)
+    bad = np.nonzero(err > bound)[0]
+    assert bad.size == 0, f"{bad.size} outside the bound; first at {bad[0]}: {err[bad[0]]} > {bound[bad[0]]}"
 
 
 def test_golden_vectors(kf, dev, golden):

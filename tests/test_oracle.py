@@ -144,6 +144,44 @@ def test_pow2_product_fixtures_are_exact(oracle):
     assert abs(float(y[0]) - exact) <= product_rtol(np.float32, x.size) * abs(exact)
 
 
+def test_quaternion_scan_pins(oracle):
+    import sys, os
+    sys.path.insert(0, os.path.dirname(__file__))
+    from helpers import Q8, q8_sequence, quat_as_complex2, complex2_as_quat
+    one, i, j, k = Q8[0], Q8[2], Q8[4], Q8[6]
+    # Hamilton's rules: i j = k, j k = i, k i = j, j i = -k, i^2 = -1
+    for a, b, want in ((i, j, k), (j, k, i), (k, i, j), (j, i, -k), (i, i, -one), (k, j, -i)):
+        assert np.array_equal(oracle.scan(np.stack([a, b]), "*")[1], want)
+    # Q8 sequences: exact, and equal to running products of the 2x2 complex
+    # representation (an independent formula for the same algebra)
+    rng = np.random.default_rng(9)
+    for dt in (np.float32, np.float64):
+        q = q8_sequence(rng, 2000, dt)
+        got = oracle.scan(q, "*")
+        m = quat_as_complex2(q)
+        run = np.eye(2, dtype=np.complex128)
+        want = np.empty((len(q), 4))
+        for t in range(len(q)):
+            run = run @ m[t]
+            want[t] = complex2_as_quat(run)
+        assert np.array_equal(got, want)
+        exc = oracle.scan(q, "*", exclusive=True)
+        assert np.array_equal(exc[0], one) and np.array_equal(exc[1:], got[:-1])
+    # random quaternions: matrix representation within rounding, norms
+    # multiply, and the order matters
+    q = rng.standard_normal((500, 4))
+    q *= rng.uniform(0.9, 1.1, (500, 1)) / np.linalg.norm(q, axis=1, keepdims=True)
+    got = oracle.scan(q, "*")
+    m = quat_as_complex2(q)
+    run = np.eye(2, dtype=np.complex128)
+    norms = np.cumprod(np.linalg.norm(q, axis=1))
+    for t in range(len(q)):
+        run = run @ m[t]
+        assert np.linalg.norm(got[t] - complex2_as_quat(run)) <= 1e-12 * norms[t]
+    assert np.allclose(np.linalg.norm(got, axis=1), norms, rtol=1e-12)
+    assert not np.allclose(oracle.scan(q[::-1], "*")[-1], got[-1])
+
+
 def test_exclusive_is_shifted_inclusive(oracle):
     rng = np.random.default_rng(1)
     for dt, op, ident in ((np.int32, "max", np.iinfo(np.int32).min), (np.int32, "min", np.iinfo(np.int32).max),
