@@ -11,7 +11,7 @@
  * the kernels keep it valid themselves (epoch-tagged tile descriptors and
  * self-resetting counters), so one scratch buffer may be reused across calls,
  * dtypes, operators and sizes without clearing. A buffer serves one family:
- * scan calls (kf_scan), or reduction calls (kf_reduce, kf_reduce2,
+ * scan calls (kf_scan), or reduction calls (kf_reduce, kf_reduce2, kf_reduce3,
  * kf_reduce_dim*). Reduction partials written over scan descriptors could
  * read as current ones, so never share one buffer between the two.
  * Calls that share a scratch buffer must be ordered on one stream;
@@ -75,6 +75,11 @@ typedef enum {
   KF_MAP2_MUL = 0,    /* x * y       (dot product)       */
   KF_MAP2_SQDIFF = 1  /* (x - y)^2   (squared distance)  */
 } kf_map2;
+
+/* Three-argument element map of kf_reduce3: f(x, y, z). */
+typedef enum {
+  KF_MAP3_MUL = 0     /* x * y * z */
+} kf_map3;
 
 /* Element types. KF_F32X2 is an interleaved (a, b) pair of float32.
  * KF_Q32 / KF_Q64 are quaternions (s, v1, v2, v3) of float32 / float64, the
@@ -160,6 +165,19 @@ size_t kf_reduce2_scratch_bytes(kf_dtype dt, int64_t n);
 
 int kf_reduce2(kf_op op, kf_map2 f, kf_dtype dt,
                const void* x, int64_t x_stride, const void* y, int64_t y_stride, int64_t n,
+               void* dst, void* scratch, size_t scratch_bytes, void* stream);
+
+/* ------------------------------------------------------------- reduce3 ----
+ * dst[0] = f(x[0], y[0], z[0]) op ... op f(x[n-1], y[n-1], z[n-1]) with
+ * f = x*y*z: the three-array form of the same reference entry point
+ *   mapreduce1d(f, op, srcs::NTuple)  src/mapreduce/1D/mapreduce1d.jl:186-204
+ * (its test: sum(a .* b .* c), test/tests/mapreduce/mapreduce1d_test.jl:180-194).
+ * Scratch as kf_reduce2. */
+size_t kf_reduce3_scratch_bytes(kf_dtype dt, int64_t n);
+
+int kf_reduce3(kf_op op, kf_map3 f, kf_dtype dt,
+               const void* x, int64_t x_stride, const void* y, int64_t y_stride,
+               const void* z, int64_t z_stride, int64_t n,
                void* dst, void* scratch, size_t scratch_bytes, void* stream);
 
 /* ---------------------------------------------------------- reduce_dim ----

@@ -76,6 +76,11 @@ class AffineOp:
 affine = AffineOp()
 
 
+def prod3(a, b, c):
+    """a * b * c: the three-array map of mapreduce(prod3, +, (a, b, c))."""
+    return a * b * c
+
+
 def sqdiff(a, b):
     """(a - b)^2: the two-array map of a squared Euclidean distance."""
     return (a - b) * (a - b)
@@ -489,8 +494,9 @@ def mapreduce(f, op, src, dims=None, g=None, tmp=None, **tuning):
 
 
 def _mapreduce_multi(f, op, srcs, dims, g, tmp):
-    """mapreduce(f, op, (x, y)) (reference src/mapreduce/mapreduce.jl:228-239):
-    full reduction only, f(x, y) = x*y or (x-y)^2, equal-length vectors."""
+    """mapreduce(f, op, (x, y[, z])) (reference src/mapreduce/mapreduce.jl:228-239):
+    full reduction only, f(x, y) = x*y or (x-y)^2, f(x, y, z) = x*y*z,
+    equal-length vectors."""
     if dims is not None and dims != ":" and dims is not Ellipsis:
         raise ArgumentError("Multi-array mapreduce only supports full reduction (dims=nothing)")
     _require_device(*srcs)
@@ -500,16 +506,24 @@ def _mapreduce_multi(f, op, srcs, dims, g, tmp):
     return g(val) if g is not None else val
 
 
+def _map3_code(f):
+    if f is operator.mul or f is prod3 or (isinstance(f, str) and f in ("mul", "*")):
+        return _L.MAP3_MUL
+    raise ArgumentError(f"unsupported three-array map {f!r}: expected prod3 (x*y*z) or operator.mul")
+
+
 def _reduce2_into(f, op, out, srcs, tmp):
-    """out[0] = op_i f(x[i], y[i]) through kf_reduce2."""
-    if len(srcs) != 2:
-        raise ArgumentError(f"multi-array mapreduce takes two arrays here, got {len(srcs)}")
-    x, y = srcs
-    fc, opc = _map2_code(f), _op_code(op)
-    _require_device(out, x, y)
-    if x.dtype != y.dtype or x.dtype not in _DTYPES or out.dtype != x.dtype:
-        raise ArgumentError(f"element types {x.dtype}, {y.dtype} -> {out.dtype}: expected one supported type")
-    if x.dim() != 1 or y.dim() != 1 or x.shape[0] != y.shape[0]:
+    """out[0] = op_i f(x[i], y[i]) through kf_reduce2, or op_i f(x[i], y[i],
+    z[i]) through kf_reduce3 for three arrays."""
+    if len(srcs) not in (2, 3):
+        raise ArgumentError(f"multi-array mapreduce takes two or three arrays, got {len(srcs)}")
+    fc = _map2_code(f) if len(srcs) == 2 else _map3_code(f)
+    opc = _op_code(op)
+    _require_device(out, *srcs)
+    x = srcs[0]
+    if any(a.dtype != x.dtype for a in srcs) or x.dtype not in _DTYPES or out.dtype != x.dtype:
+        raise ArgumentError(f"element types {[a.dtype for a in srcs]} -> {out.dtype}: expected one supported type")
+    if any(a.dim() != 1 or a.shape[0] != x.shape[0] for a in srcs):
         raise ArgumentError("multi-array mapreduce takes vectors of equal length")
     if opc == _L.OP_AFFINE:
         raise ArgumentError("mapreduce needs a commutative operator; the affine operator is scan-only")
@@ -518,11 +532,18 @@ def _reduce2_into(f, op, out, srcs, tmp):
         raise ArgumentError("reducing over an empty collection is not allowed")
     L = _L.lib()
     dt = _DTYPES[x.dtype]
-    buf = _scratch(MapReduce1D, L.kf_reduce2_scratch_bytes(dt, n), x.device, tmp)
+    args = []
+    for a in srcs:
+        args += [ctypes_void(a.data_ptr()), a.stride(0) if n > 1 else 1]
+    if len(srcs) == 2:
+        buf = _scratch(MapReduce1D, L.kf_reduce2_scratch_bytes(dt, n), x.device, tmp)
+        entry = L.kf_reduce2
+    else:
+        buf = _scratch(MapReduce1D, L.kf_reduce3_scratch_bytes(dt, n), x.device, tmp)
+        entry = L.kf_reduce3
     with _on(x.device):
-        rc = L.kf_reduce2(opc, fc, dt, ctypes_void(x.data_ptr()), x.stride(0) if n > 1 else 1,
-                          ctypes_void(y.data_ptr()), y.stride(0) if n > 1 else 1, n, ctypes_void(out.data_ptr()),
-                          ctypes_void(buf.ptr), buf.nbytes, _stream_ptr(x))
+        rc = entry(opc, fc, dt, *args, n, ctypes_void(out.data_ptr()), ctypes_void(buf.ptr), buf.nbytes,
+                   _stream_ptr(x))
     _L.check(rc, "mapreduce")
 
 
@@ -807,7 +828,7 @@ def get_allocation(kind, f, op, src, *args, **kwargs):
         device = src.device
     elif kind == MapReduce1D:
         if isinstance(src, (tuple, list)):
-            _map2_code(f)
+            _map2_code(f) if len(src) == 2 else _map3_code(f)
             _require_device(*src)
             need = L.kf_reduce2_scratch_bytes(_DTYPES[src[0].dtype], src[0].numel())
             device = src[0].device

@@ -15,6 +15,7 @@ KF_OK, KF_EINVAL, KF_ENOSCRATCH, KF_EHIP = 0, 1, 2, 3
 OP_ADD, OP_MAX, OP_MIN, OP_AFFINE, OP_MUL = 0, 1, 2, 3, 4
 MAP_IDENTITY, MAP_ABS2 = 0, 1
 MAP2_MUL, MAP2_SQDIFF = 0, 1
+MAP3_MUL = 0
 POST_IDENTITY, POST_SQRT, POST_ABS2 = 0, 1, 2
 F32, F64, I32, I64, U8, F32X2, Q32, Q64 = 0, 1, 2, 3, 4, 5, 6, 7
 
@@ -32,6 +33,8 @@ SIGNATURES = {
     "kf_reduce_dim": ([_I, _I, _I, _P, _I64, _I64, _I64, _I, _P, _I64, _P, _SZ, _P], _I),
     "kf_reduce2_scratch_bytes": ([_I, _I64], _SZ),
     "kf_reduce2": ([_I, _I, _I, _P, _I64, _P, _I64, _I64, _P, _P, _SZ, _P], _I),
+    "kf_reduce3_scratch_bytes": ([_I, _I64], _SZ),
+    "kf_reduce3": ([_I, _I, _I, _P, _I64, _P, _I64, _P, _I64, _I64, _P, _P, _SZ, _P], _I),
     "kf_reduce_dim_batched_scratch_bytes": ([_I, _I64, _I64, _I64], _SZ),
     "kf_reduce_dim_batched": ([_I, _I, _I, _P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P, _SZ, _P], _I),
     "kf_reduce_dim_x": ([_I, _I, _I, _P, _I64, _I64, _I64, _I, _P, _I64, _P, _I64, _P, _SZ, _P], _I),

@@ -305,77 +305,107 @@ struct Map2SqDiff {
   __device__ static uint8_t apply(uint8_t a, uint8_t b) { const uint8_t d = (uint8_t)(a - b); return (uint8_t)(d * d); }
 };
 
-template <class T, class Op, class M2>
-__global__ __launch_bounds__(kRedBlock) void reduce2_once_kernel(const T* x, const T* y, int64_t n, T* out) {
+// x * y * z, the three-array map (wrapping for integers).
+struct Map3Mul {
+  template <class T> __device__ static T apply(T a, T b, T c) { return Map2Mul::apply(Map2Mul::apply(a, b), c); }
+};
+
+// K operand arrays of one multi-array reduction (K = 2 or 3), passed by value.
+template <class T, int K> struct Operands {
+  const T* p[K];
+  int64_t s[K];
+};
+template <class M, class T, int K> __device__ inline T apply_k(const T (&v)[K]) {
+  if constexpr (K == 2)
+    return M::apply(v[0], v[1]);
+  else
+    return M::apply(v[0], v[1], v[2]);
+}
+
+// Multi-array reduction, vector path: the one-shot workgroups of
+// reduce_once_kernel, each loading the same 16-byte vectors of all K arrays.
+template <class T, class Op, class M, int K>
+__global__ __launch_bounds__(kRedBlock) void reducek_once_kernel(Operands<T, K> a, int64_t n, T* out) {
   constexpr int EPV = 16 / (int)sizeof(T);
   __shared__ T s_wave[kRedWaves];
   const T id = Op::template identity<T>();
   const int tid = threadIdx.x;
   const int64_t nvec = n / EPV;
-  const uint4* vx = reinterpret_cast<const uint4*>(x);
-  const uint4* vy = reinterpret_cast<const uint4*>(y);
   const int64_t base = (int64_t)blockIdx.x * kOnceVecs + tid;
-  uint4 rx[kOnceUnroll], ry[kOnceUnroll];
+  uint4 r[kOnceUnroll][K];
 #pragma unroll
   for (int u = 0; u < kOnceUnroll; ++u)
     if (base + u * kRedBlock < nvec) {
-      rx[u] = ld_stream(vx + base + u * kRedBlock);
-      ry[u] = ld_stream(vy + base + u * kRedBlock);
-    }
-  T a[EPV];
 #pragma unroll
-  for (int e = 0; e < EPV; ++e) a[e] = id;
+      for (int k = 0; k < K; ++k) r[u][k] = ld_stream(reinterpret_cast<const uint4*>(a.p[k]) + base + u * kRedBlock);
+    }
+  T acc_e[EPV];
+#pragma unroll
+  for (int e = 0; e < EPV; ++e) acc_e[e] = id;
 #pragma unroll
   for (int u = 0; u < kOnceUnroll; ++u)
     if (base + u * kRedBlock < nvec) {
-      T p[EPV], q[EPV];
-      __builtin_memcpy(p, &rx[u], 16);
-      __builtin_memcpy(q, &ry[u], 16);
+      T x[K][EPV];
 #pragma unroll
-      for (int e = 0; e < EPV; ++e) a[e] = Op::combine(a[e], M2::apply(p[e], q[e]));
+      for (int k = 0; k < K; ++k) __builtin_memcpy(x[k], &r[u][k], 16);
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) {
+        T v[K];
+#pragma unroll
+        for (int k = 0; k < K; ++k) v[k] = x[k][e];
+        acc_e[e] = Op::combine(acc_e[e], apply_k<M, T, K>(v));
+      }
     }
-  T acc = a[0];
+  T acc = acc_e[0];
 #pragma unroll
-  for (int e = 1; e < EPV; ++e) acc = Op::combine(acc, a[e]);
-  if (blockIdx.x == 0 && nvec * EPV + tid < n) acc = Op::combine(acc, M2::apply(x[nvec * EPV + tid], y[nvec * EPV + tid]));
+  for (int e = 1; e < EPV; ++e) acc = Op::combine(acc, acc_e[e]);
+  if (blockIdx.x == 0 && nvec * EPV + tid < n) {
+    T v[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) v[k] = a.p[k][nvec * EPV + tid];
+    acc = Op::combine(acc, apply_k<M, T, K>(v));
+  }
   const T part = block_reduce<T, Op>(acc, s_wave);
   if (tid == 0) out[blockIdx.x] = part;
 }
 
-template <class T, class Op, class M2>
-__global__ __launch_bounds__(kRedBlock) void reduce2_kernel(const T* x, int64_t xs, const T* y, int64_t ys, int64_t n,
-                                                            T* out) {
+// Multi-array reduction, strided operands: grid-stride loop.
+template <class T, class Op, class M, int K>
+__global__ __launch_bounds__(kRedBlock) void reducek_kernel(Operands<T, K> a, int64_t n, T* out) {
   __shared__ T s_wave[kRedWaves];
   T acc = Op::template identity<T>();
   const int64_t gsize = (int64_t)gridDim.x * kRedBlock;
-  for (int64_t i = (int64_t)blockIdx.x * kRedBlock + threadIdx.x; i < n; i += gsize)
-    acc = Op::combine(acc, M2::apply(x[i * xs], y[i * ys]));
+  for (int64_t i = (int64_t)blockIdx.x * kRedBlock + threadIdx.x; i < n; i += gsize) {
+    T v[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) v[k] = a.p[k][i * a.s[k]];
+    acc = Op::combine(acc, apply_k<M, T, K>(v));
+  }
   const T part = block_reduce<T, Op>(acc, s_wave);
   if (threadIdx.x == 0) out[blockIdx.x] = part;
 }
 
-template <class T, class Op, class M2>
-int launch_reduce2(const void* x, int64_t xs, const void* y, int64_t ys, int64_t n, void* dst, void* scratch,
-                   hipStream_t stream) {
+template <class T, class Op, class M, int K>
+int launch_reducek(const Operands<T, K>& a, int64_t n, void* dst, void* scratch, hipStream_t stream) {
   constexpr int EPV = 16 / (int)sizeof(T);
-  const bool vec = xs == 1 && ys == 1 && (uintptr_t)x % 16 == 0 && (uintptr_t)y % 16 == 0;
+  bool vec = true;
+  for (int k = 0; k < K; ++k) vec = vec && a.s[k] == 1 && (uintptr_t)a.p[k] % 16 == 0;
   if (!vec) {
     const int grid = reduce_grid<T>(n);
     T* out = grid == 1 ? (T*)dst : (T*)scratch;
-    hipLaunchKernelGGL((reduce2_kernel<T, Op, M2>), dim3(grid), dim3(kRedBlock), 0, stream, (const T*)x, xs,
-                       (const T*)y, ys, n, out);
+    hipLaunchKernelGGL((reducek_kernel<T, Op, M, K>), dim3(grid), dim3(kRedBlock), 0, stream, a, n, out);
     if (grid > 1)
       hipLaunchKernelGGL((combine_all_kernel<T, Op>), dim3(1), dim3(kCombineBlock), 0, stream,
                          (const T*)scratch, grid, (T*)dst);
-    return kf_check_launch("reduce2_kernel");
+    return kf_check_launch("reducek_kernel");
   }
   const OnceLevels L = once_levels(n / EPV, EPV);
   size_t abytes = 0;
   for (int i = 0; i < L.nlev; i += 2) abytes = kmax(abytes, round256((size_t)L.count[i] * sizeof(T) + 16));
   T* buf[2] = {(T*)scratch, (T*)((uint8_t*)scratch + abytes)};
   T* out0 = (L.nlev == 1 && L.count[0] == 1) ? (T*)dst : buf[0];
-  hipLaunchKernelGGL((reduce2_once_kernel<T, Op, M2>), dim3((unsigned)L.count[0]), dim3(kRedBlock), 0, stream,
-                     (const T*)x, (const T*)y, n, out0);
+  hipLaunchKernelGGL((reducek_once_kernel<T, Op, M, K>), dim3((unsigned)L.count[0]), dim3(kRedBlock), 0, stream,
+                     a, n, out0);
   for (int i = 1; i < L.nlev; ++i) {
     const int64_t m = L.count[i - 1];
     hipLaunchKernelGGL((reduce_once_kernel<T, Op, MapIdentity>), dim3((unsigned)L.count[i]), dim3(kRedBlock), 0,
@@ -384,7 +414,14 @@ int launch_reduce2(const void* x, int64_t xs, const void* y, int64_t ys, int64_t
   if (out0 != (T*)dst)
     hipLaunchKernelGGL((combine_all_kernel<T, Op>), dim3(1), dim3(kCombineBlock), 0, stream,
                        (const T*)buf[(L.nlev - 1) % 2], (int)L.count[L.nlev - 1], (T*)dst);
-  return kf_check_launch("reduce2_once_kernel");
+  return kf_check_launch("reducek_once_kernel");
+}
+
+template <class T, class Op, class M2>
+int launch_reduce2(const void* x, int64_t xs, const void* y, int64_t ys, int64_t n, void* dst, void* scratch,
+                   hipStream_t stream) {
+  return launch_reducek<T, Op, M2, 2>(Operands<T, 2>{{(const T*)x, (const T*)y}, {xs, ys}}, n, dst, scratch,
+                                      stream);
 }
 
 // ---------------------------------------------------------------------------
@@ -791,6 +828,51 @@ extern "C" int kf_reduce2(kf_op op, kf_map2 f, kf_dtype dt, const void* x, int64
     case KF_U8: return dispatch_reduce2<uint8_t>(op, f, x, x_stride, y, y_stride, n, dst, scratch, s);
     default: return kf_set_error(KF_EINVAL, "kf_reduce2: bad dtype %d", (int)dt);
   }
+}
+
+extern "C" size_t kf_reduce3_scratch_bytes(kf_dtype dt, int64_t n) { return kf_reduce_scratch_bytes(dt, n); }
+
+template <class T>
+int dispatch_reduce3(kf_op op, const Operands<T, 3>& a, int64_t n, void* dst, void* scratch, hipStream_t s) {
+  switch (op) {
+    case KF_OP_ADD: return launch_reducek<T, OpAdd, Map3Mul, 3>(a, n, dst, scratch, s);
+    case KF_OP_MAX: return launch_reducek<T, OpMax, Map3Mul, 3>(a, n, dst, scratch, s);
+    case KF_OP_MUL: return launch_reducek<T, OpMul, Map3Mul, 3>(a, n, dst, scratch, s);
+    default: return launch_reducek<T, OpMin, Map3Mul, 3>(a, n, dst, scratch, s);
+  }
+}
+
+extern "C" int kf_reduce3(kf_op op, kf_map3 f, kf_dtype dt, const void* x, int64_t x_stride, const void* y,
+                          int64_t y_stride, const void* z, int64_t z_stride, int64_t n, void* dst, void* scratch,
+                          size_t scratch_bytes, void* stream) {
+  int rc = kf_validate_op(op, KF_MAP_IDENTITY, dt, /*allow_affine=*/0);
+  if (rc) return rc;
+  if (f != KF_MAP3_MUL) return kf_set_error(KF_EINVAL, "kf_reduce3: unknown map %d", (int)f);
+  if (n < 0) return kf_set_error(KF_EINVAL, "kf_reduce3: n = %lld < 0", (long long)n);
+  if (n == 0) return KF_OK;
+  if (!x || !y || !z || !dst) return kf_set_error(KF_EINVAL, "kf_reduce3: null pointer");
+  if (x_stride < 1 || y_stride < 1 || z_stride < 1) return kf_set_error(KF_EINVAL, "kf_reduce3: strides must be >= 1");
+  const size_t es = kf_dtype_size(dt);
+  if ((uintptr_t)x % es || (uintptr_t)y % es || (uintptr_t)z % es || (uintptr_t)dst % es)
+    return kf_set_error(KF_EINVAL, "kf_reduce3: pointers not aligned to the element type");
+  const size_t need = kf_reduce3_scratch_bytes(dt, n);
+  if (!scratch || scratch_bytes < need)
+    return kf_set_error(KF_ENOSCRATCH, "kf_reduce3: scratch of %zu bytes needed, %zu given", need,
+                        scratch ? scratch_bytes : (size_t)0);
+  if ((uintptr_t)scratch % 256) return kf_set_error(KF_EINVAL, "kf_reduce3: scratch must be 256-byte aligned");
+  hipStream_t s = (hipStream_t)stream;
+#define KF_R3(T) \
+  dispatch_reduce3<T>(op, Operands<T, 3>{{(const T*)x, (const T*)y, (const T*)z}, {x_stride, y_stride, z_stride}}, \
+                      n, dst, scratch, s)
+  switch (dt) {
+    case KF_F32: return KF_R3(float);
+    case KF_F64: return KF_R3(double);
+    case KF_I32: return KF_R3(int32_t);
+    case KF_I64: return KF_R3(int64_t);
+    case KF_U8: return KF_R3(uint8_t);
+    default: return kf_set_error(KF_EINVAL, "kf_reduce3: bad dtype %d", (int)dt);
+  }
+#undef KF_R3
 }
 
 extern "C" size_t kf_reduce_dim_scratch_bytes(kf_dtype dt, int64_t rows, int64_t cols, int dim) {

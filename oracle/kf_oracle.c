@@ -227,6 +227,27 @@ void kfo_reduce2_i(const void* x, const void* y, int dt, int64_t n, int op, int 
   istore(out, dt, 0, acc);
 }
 
+/* Three-array reduction op_i x[i]*y[i]*z[i] (the reference's
+ * mapreduce1d(f, op, (a, b, c)), src/mapreduce/1D/mapreduce1d.jl:186-204,
+ * tested with f = a*b*c, test/tests/mapreduce/mapreduce1d_test.jl:180-194). */
+double kfo_reduce3_f(const void* x, const void* y, const void* z, int dt, int64_t n, int op) {
+  double acc = 0.0;
+  for (int64_t i = 0; i < n; ++i) {
+    const double v = fload(x, dt, i, 0) * fload(y, dt, i, 0) * fload(z, dt, i, 0);
+    acc = i == 0 ? v : fop(op, acc, v);
+  }
+  return acc;
+}
+
+void kfo_reduce3_i(const void* x, const void* y, const void* z, int dt, int64_t n, int op, void* out) {
+  uint64_t acc = 0;
+  for (int64_t i = 0; i < n; ++i) {
+    const uint64_t v = wrap(dt, wrap(dt, iload(x, dt, i, 0) * iload(y, dt, i, 0)) * iload(z, dt, i, 0));
+    acc = i == 0 ? v : iop(dt, op, acc, v);
+  }
+  istore(out, dt, 0, acc);
+}
+
 /* matvec (dim 2): out[i] = op_j f(A[i,j], x[j]); vecmat (dim 1):
  * out[j] = op_i f(x[i], A[i,j]); f2 = 0 -> product, 1 -> squared difference
  * (reference src/mapreduce/2D/matvec.jl:393-474, vecmat.jl:328-405). */

@@ -48,6 +48,9 @@ def lib():
         L.kfo_reduce2_f.argtypes = [P, P, I, I64, I, I]
         L.kfo_reduce2_f.restype = D
         L.kfo_reduce2_i.argtypes = [P, P, I, I64, I, I, P]
+        L.kfo_reduce3_f.argtypes = [P, P, P, I, I64, I]
+        L.kfo_reduce3_f.restype = D
+        L.kfo_reduce3_i.argtypes = [P, P, P, I, I64, I, P]
         L.kfo_reduce_dim_x_f.argtypes = [P, P, I, I64, I64, I64, I, I, I, P]
         L.kfo_reduce_dim_x_i.argtypes = [P, P, I, I64, I64, I64, I, I, I, P]
         L.kfo_reduce_dim_f.argtypes = [P, I, I64, I64, I64, I, I, I, P]
@@ -122,6 +125,18 @@ def reduce2(x, y, op="+", f2="mul"):
     L.kfo_reduce2_i(_p(x), _p(y), DT[x.dtype], x.shape[0], OPS[op], code, _p(out))
     return out[0]
 
+
+
+def reduce3(x, y, z, op="+"):
+    """Base.mapreduce((a, b, c) -> a*b*c, op, x, y, z); float products in Float64."""
+    L = lib()
+    x, y, z = (np.ascontiguousarray(a) for a in (x, y, z))
+    assert x.dtype == y.dtype == z.dtype and x.shape == y.shape == z.shape and x.ndim == 1
+    if _is_float(x):
+        return L.kfo_reduce3_f(_p(x), _p(y), _p(z), DT[x.dtype], x.shape[0], OPS[op])
+    out = np.empty(1, x.dtype)
+    L.kfo_reduce3_i(_p(x), _p(y), _p(z), DT[x.dtype], x.shape[0], OPS[op], _p(out))
+    return out[0]
 
 def reduce_dim(buf, rows, cols, col_stride, dim, op="+", f="identity"):
     """Base.mapreduce(f, op, A; dims=dim) of the column-major matrix

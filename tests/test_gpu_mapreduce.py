@@ -346,6 +346,43 @@ def test_two_array_mapreduce(kf, oracle, dev, dt):
     assert d == pytest.approx(np.sqrt(np.sum((x - y) ** 2)), rel=1e-12)
 
 
+@pytest.mark.parametrize("dt", [np.float32, np.float64, np.int32, np.int64, np.uint8])
+def test_three_array_mapreduce(kf, oracle, dev, dt):
+    # reference test/tests/mapreduce/mapreduce1d_test.jl:180-194: sum(a .* b .* c)
+    # and cbrt(sum(a .* b .* c)); exact for integers, floats within
+    # 2 roundings of each product plus the sum's rtol * sum|a b c|
+    rng = np.random.default_rng(61)
+    for n in (1, 5, 33, 4097, 12_000, 100_003, (1 << 22) + 3):
+        x, y, z = gen(rng, dt, n), gen(rng, dt, n), gen(rng, dt, n)
+        t = [torch.from_numpy(a).to(dev) for a in (x, y, z)]
+        for op in ("+", "max"):
+            got = kf.mapreduce(kf.prod3, op, tuple(t))
+            ref = oracle.reduce3(x, y, z, op)
+            if np.dtype(dt).kind == "f":
+                bound = np.sum(np.abs(x.astype(np.float64) * y * z)) if op == "+" else abs(ref)
+                tol = 1e-6 if dt == np.float32 else 1e-12
+                assert abs(got - ref) <= tol * bound + 1e-300, (n, op, got, ref)
+            else:
+                assert got == int(ref), (n, op)
+        if n > 8:   # strided operands take the scalar path
+            got = kf.mapreduce(kf.prod3, "+", (t[0][1::2], t[1][:-1:2], t[2][::2][: len(x[1::2])]))
+            ref = oracle.reduce3(x[1::2], y[:-1:2], z[::2][: len(x[1::2])])
+            if np.dtype(dt).kind != "f":
+                assert got == int(ref), n
+    # the reference's cases: U[0,1) of length 12000, g = cbrt; the
+    # lower-level names with a reused buffer
+    import operator
+    a, b, c = (rng.random(12_000) for _ in range(3))
+    ta, tb, tc = (torch.from_numpy(v).to(dev) for v in (a, b, c))
+    assert kf.mapreduce1d(operator.mul, "+", (ta, tb, tc)) == pytest.approx(np.sum(a * b * c), rel=1e-12)
+    tmp = kf.get_allocation(kf.MapReduce1D, kf.prod3, "+", (ta, tb, tc))
+    r = kf.mapreduce1d(kf.prod3, "+", (ta, tb, tc), g=np.cbrt, tmp=tmp)
+    assert r == pytest.approx(np.cbrt(np.sum(a * b * c)), rel=1e-12)
+    d = torch.empty(1, dtype=torch.float64, device=dev)
+    kf.mapreduce1d_(kf.prod3, "+", d, (ta, tb, tc), tmp=tmp)
+    assert d.item() == pytest.approx(np.sum(a * b * c), rel=1e-12)
+
+
 def test_post_map_g(kf, dev):
     # reference test/tests/mapreduce/mapreduce2d_test.jl:30-35: abs2 + g = sqrt row norms
     import math

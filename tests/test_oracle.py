@@ -182,6 +182,22 @@ def test_quaternion_scan_pins(oracle):
     assert not np.allclose(oracle.scan(q[::-1], "*")[-1], got[-1])
 
 
+@pytest.mark.parametrize("n", [1, 2, 100, 1000, 40_000])
+def test_reduce3_closed_forms(oracle, n):
+    # sum_{i<=n} i*i*i = (n(n+1)/2)^2 (Nicomachus), exact in Int64 and, wrapped,
+    # in Int32; max of an increasing product is the last one
+    r = np.arange(1, n + 1, dtype=np.int64)
+    want = (n * (n + 1) // 2) ** 2
+    assert int(oracle.reduce3(r, r, r)) == want
+    r32 = r.astype(np.int32)
+    w32 = want % (1 << 32)
+    assert int(oracle.reduce3(r32, r32, r32)) == (w32 - (1 << 32) if w32 >= 1 << 31 else w32)
+    assert int(oracle.reduce3(r, r, r, "max")) == n ** 3
+    rng = np.random.default_rng(n)
+    a, b, c = rng.random((3, n))
+    assert np.isclose(oracle.reduce3(a, b, c), np.sum(a * b * c), rtol=1e-12)
+
+
 def test_exclusive_is_shifted_inclusive(oracle):
     rng = np.random.default_rng(1)
     for dt, op, ident in ((np.int32, "max", np.iinfo(np.int32).min), (np.int32, "min", np.iinfo(np.int32).max),
