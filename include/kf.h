@@ -72,8 +72,10 @@ typedef enum {
 
 /* Two-argument element map of kf_reduce2: f(x, y). */
 typedef enum {
-  KF_MAP2_MUL = 0,    /* x * y       (dot product)       */
-  KF_MAP2_SQDIFF = 1  /* (x - y)^2   (squared distance)  */
+  KF_MAP2_MUL = 0,     /* x * y       (dot product)       */
+  KF_MAP2_SQDIFF = 1,  /* (x - y)^2   (squared distance)  */
+  KF_MAP2_WSQ = 2,     /* x * y * y   (weighted sum of squares; kf_reduce2 only) */
+  KF_MAP2_EXPDIFF = 3  /* exp(x - y)  (floating-point types; kf_reduce2 only)    */
 } kf_map2;
 
 /* Three-argument element map of kf_reduce3: f(x, y, z). */

@@ -86,7 +86,19 @@ def sqdiff(a, b):
     return (a - b) * (a - b)
 
 
-_MAP2 = {"mul": _L.MAP2_MUL, "*": _L.MAP2_MUL, "sqdiff": _L.MAP2_SQDIFF}
+def wsq(w, x):
+    """w * x^2: the two-array map of a weighted sum of squares."""
+    return w * x * x
+
+
+def expdiff(a, b):
+    """exp(a - b) (floating-point types)."""
+    import math
+    return math.exp(a - b)
+
+
+_MAP2 = {"mul": _L.MAP2_MUL, "*": _L.MAP2_MUL, "sqdiff": _L.MAP2_SQDIFF, "wsq": _L.MAP2_WSQ,
+         "expdiff": _L.MAP2_EXPDIFF}
 
 
 def _map2_code(f):
@@ -94,9 +106,13 @@ def _map2_code(f):
         return _L.MAP2_MUL
     if f is sqdiff:
         return _L.MAP2_SQDIFF
+    if f is wsq:
+        return _L.MAP2_WSQ
+    if f is expdiff:
+        return _L.MAP2_EXPDIFF
     if isinstance(f, str) and f in _MAP2:
         return _MAP2[f]
-    raise ArgumentError(f"unsupported two-array map {f!r}: expected operator.mul or sqdiff")
+    raise ArgumentError(f"unsupported two-array map {f!r}: expected operator.mul, sqdiff, wsq or expdiff")
 
 # Allocation kinds (reference src/algorithms.jl:16-31 tags).
 Scan1D, MapReduce1D, MapReduce2D = "Scan1D", "MapReduce1D", "MapReduce2D"

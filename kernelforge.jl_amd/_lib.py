@@ -14,7 +14,7 @@ LIB_PATH = os.path.join(HERE, "libkfhip.so")
 KF_OK, KF_EINVAL, KF_ENOSCRATCH, KF_EHIP = 0, 1, 2, 3
 OP_ADD, OP_MAX, OP_MIN, OP_AFFINE, OP_MUL = 0, 1, 2, 3, 4
 MAP_IDENTITY, MAP_ABS2 = 0, 1
-MAP2_MUL, MAP2_SQDIFF = 0, 1
+MAP2_MUL, MAP2_SQDIFF, MAP2_WSQ, MAP2_EXPDIFF = 0, 1, 2, 3
 MAP3_MUL = 0
 POST_IDENTITY, POST_SQRT, POST_ABS2 = 0, 1, 2
 F32, F64, I32, I64, U8, F32X2, Q32, Q64 = 0, 1, 2, 3, 4, 5, 6, 7

@@ -305,6 +305,16 @@ struct Map2SqDiff {
   __device__ static uint8_t apply(uint8_t a, uint8_t b) { const uint8_t d = (uint8_t)(a - b); return (uint8_t)(d * d); }
 };
 
+// x * y * y (weighted sum of squares) and exp(x - y), the reference's
+// mapreduce1d tests' other two-array maps (mapreduce1d_test.jl:117-131).
+struct Map2WSq {
+  template <class T> __device__ static T apply(T a, T b) { return Map2Mul::apply(Map2Mul::apply(a, b), b); }
+};
+struct Map2ExpDiff {
+  __device__ static float apply(float a, float b) { return expf(a - b); }
+  __device__ static double apply(double a, double b) { return exp(a - b); }
+};
+
 // x * y * z, the three-array map (wrapping for integers).
 struct Map3Mul {
   template <class T> __device__ static T apply(T a, T b, T c) { return Map2Mul::apply(Map2Mul::apply(a, b), c); }
@@ -785,20 +795,23 @@ extern "C" int kf_reduce(kf_op op, kf_map f, kf_dtype dt, const void* src, int64
 
 extern "C" size_t kf_reduce2_scratch_bytes(kf_dtype dt, int64_t n) { return kf_reduce_scratch_bytes(dt, n); }
 
-template <class T, class... A> int dispatch_reduce2(kf_op op, kf_map2 f, A... args) {
-  if (f == KF_MAP2_SQDIFF) {
-    switch (op) {
-      case KF_OP_ADD: return Reduce2L<T, OpAdd, Map2SqDiff>::run(args...);
-      case KF_OP_MAX: return Reduce2L<T, OpMax, Map2SqDiff>::run(args...);
-      case KF_OP_MUL: return Reduce2L<T, OpMul, Map2SqDiff>::run(args...);
-      default: return Reduce2L<T, OpMin, Map2SqDiff>::run(args...);
-    }
-  }
+template <class T, class M2, class... A> int dispatch_reduce2_op(kf_op op, A... args) {
   switch (op) {
-    case KF_OP_ADD: return Reduce2L<T, OpAdd, Map2Mul>::run(args...);
-    case KF_OP_MAX: return Reduce2L<T, OpMax, Map2Mul>::run(args...);
-    case KF_OP_MUL: return Reduce2L<T, OpMul, Map2Mul>::run(args...);
-    default: return Reduce2L<T, OpMin, Map2Mul>::run(args...);
+    case KF_OP_ADD: return Reduce2L<T, OpAdd, M2>::run(args...);
+    case KF_OP_MAX: return Reduce2L<T, OpMax, M2>::run(args...);
+    case KF_OP_MUL: return Reduce2L<T, OpMul, M2>::run(args...);
+    default: return Reduce2L<T, OpMin, M2>::run(args...);
+  }
+}
+
+template <class T, class... A> int dispatch_reduce2(kf_op op, kf_map2 f, A... args) {
+  switch (f) {
+    case KF_MAP2_SQDIFF: return dispatch_reduce2_op<T, Map2SqDiff>(op, args...);
+    case KF_MAP2_WSQ: return dispatch_reduce2_op<T, Map2WSq>(op, args...);
+    case KF_MAP2_EXPDIFF:
+      if constexpr (__is_same(T, float) || __is_same(T, double)) return dispatch_reduce2_op<T, Map2ExpDiff>(op, args...);
+      return kf_set_error(KF_EINVAL, "kf_reduce2: exp(x - y) needs a floating-point type");
+    default: return dispatch_reduce2_op<T, Map2Mul>(op, args...);
   }
 }
 
@@ -806,7 +819,10 @@ extern "C" int kf_reduce2(kf_op op, kf_map2 f, kf_dtype dt, const void* x, int64
                           int64_t y_stride, int64_t n, void* dst, void* scratch, size_t scratch_bytes, void* stream) {
   int rc = kf_validate_op(op, KF_MAP_IDENTITY, dt, /*allow_affine=*/0);
   if (rc) return rc;
-  if (f != KF_MAP2_MUL && f != KF_MAP2_SQDIFF) return kf_set_error(KF_EINVAL, "kf_reduce2: unknown map %d", (int)f);
+  if (f != KF_MAP2_MUL && f != KF_MAP2_SQDIFF && f != KF_MAP2_WSQ && f != KF_MAP2_EXPDIFF)
+    return kf_set_error(KF_EINVAL, "kf_reduce2: unknown map %d", (int)f);
+  if (f == KF_MAP2_EXPDIFF && dt != KF_F32 && dt != KF_F64)
+    return kf_set_error(KF_EINVAL, "kf_reduce2: exp(x - y) needs a floating-point type");
   if (n < 0) return kf_set_error(KF_EINVAL, "kf_reduce2: n = %lld < 0", (long long)n);
   if (n == 0) return KF_OK;
   if (!x || !y || !dst) return kf_set_error(KF_EINVAL, "kf_reduce2: null pointer");
@@ -974,7 +990,8 @@ extern "C" int kf_reduce_dim_x(kf_op op, kf_map2 f, kf_dtype dt, const void* A, 
                                int64_t dst_stride, void* scratch, size_t scratch_bytes, void* stream) {
   int rc = kf_validate_op(op, KF_MAP_IDENTITY, dt, /*allow_affine=*/0);
   if (rc) return rc;
-  if (f != KF_MAP2_MUL && f != KF_MAP2_SQDIFF) return kf_set_error(KF_EINVAL, "kf_reduce_dim_x: unknown map %d", (int)f);
+  if (f != KF_MAP2_MUL && f != KF_MAP2_SQDIFF)
+    return kf_set_error(KF_EINVAL, "kf_reduce_dim_x: map %d is not one of x*y, (x-y)^2", (int)f);
   if (dim != 1 && dim != 2) return kf_set_error(KF_EINVAL, "kf_reduce_dim_x: dim must be 1 or 2 (got %d)", dim);
   if (rows < 0 || cols < 0) return kf_set_error(KF_EINVAL, "kf_reduce_dim_x: negative shape");
   if ((dim == 1 ? cols : rows) == 0) return KF_OK;

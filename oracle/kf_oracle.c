@@ -199,13 +199,23 @@ void kfo_reduce_i(const void* src, int dt, int64_t n, int64_t stride, int op, in
   istore(out, dt, 0, acc);
 }
 
-/* Two-array reduction: f2 = 0 -> x*y, 1 -> (x-y)^2 (the reference's
+/* Two-array maps: f2 = 0 -> x*y, 1 -> (x-y)^2, 2 -> x*y*y, 3 -> exp(x-y). */
+static double fmap2(int f2, double a, double b) {
+  switch (f2) {
+    case 0: return a * b;
+    case 1: return (a - b) * (a - b);
+    case 2: return a * b * b;
+    default: return exp(a - b);
+  }
+}
+
+/* Two-array reduction op_i f2(x[i], y[i]) (the reference's
  * mapreduce(f, op, (x, y)), src/mapreduce/1D/mapreduce1d.jl:186-204). */
 double kfo_reduce2_f(const void* x, const void* y, int dt, int64_t n, int op, int f2) {
   double acc = 0.0;
   for (int64_t i = 0; i < n; ++i) {
     const double a = fload(x, dt, i, 0), b = fload(y, dt, i, 0);
-    const double v = f2 ? (a - b) * (a - b) : a * b;
+    const double v = fmap2(f2, a, b);
     acc = i == 0 ? v : fop(op, acc, v);
   }
   return acc;
@@ -216,9 +226,11 @@ void kfo_reduce2_i(const void* x, const void* y, int dt, int64_t n, int op, int 
   for (int64_t i = 0; i < n; ++i) {
     const uint64_t a = iload(x, dt, i, 0), b = iload(y, dt, i, 0);
     uint64_t v;
-    if (f2) {
+    if (f2 == 1) {
       const uint64_t d = wrap(dt, a - b);
       v = wrap(dt, d * d);
+    } else if (f2 == 2) {
+      v = wrap(dt, wrap(dt, a * b) * b);
     } else {
       v = wrap(dt, a * b);
     }

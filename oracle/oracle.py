@@ -114,11 +114,11 @@ def reduce(x, op="+", f="identity"):
 
 
 def reduce2(x, y, op="+", f2="mul"):
-    """Base.mapreduce(f2, op, x, y) for f2 in {"mul": x*y, "sqdiff": (x-y)^2}."""
+    """Base.mapreduce(f2, op, x, y) for f2 in {"mul": x*y, "sqdiff": (x-y)^2, "wsq": x*y*y, "expdiff": exp(x-y)}."""
     L = lib()
     x, y = np.ascontiguousarray(x), np.ascontiguousarray(y)
     assert x.dtype == y.dtype and x.shape == y.shape and x.ndim == 1
-    code = {"mul": 0, "sqdiff": 1}[f2]
+    code = {"mul": 0, "sqdiff": 1, "wsq": 2, "expdiff": 3}[f2]
     if _is_float(x):
         return L.kfo_reduce2_f(_p(x), _p(y), DT[x.dtype], x.shape[0], OPS[op], code)
     out = np.empty(1, x.dtype)

@@ -383,6 +383,39 @@ def test_three_array_mapreduce(kf, oracle, dev, dt):
     assert d.item() == pytest.approx(np.sum(a * b * c), rel=1e-12)
 
 
+@pytest.mark.parametrize("dt", [np.float32, np.float64, np.int32, np.int64])
+def test_two_array_weighted_squares_and_expdiff(kf, oracle, dev, dt):
+    # reference test/tests/mapreduce/mapreduce1d_test.jl:117-131:
+    # sum(w .* x .^ 2) (n = 50000) and sum(exp.(a .- b)) (n = 10000, a, b in
+    # [0, 2)); exact for integers, floats within rtol * the sum of |terms|
+    # (each term rounds at most 3 times in the element type, exp within a few ulps)
+    rng = np.random.default_rng(67)
+    tol = 1e-6 if dt == np.float32 else 1e-12
+    for n in (1, 9, 4097, 50_000, (1 << 21) + 1):
+        w, x = gen(rng, dt, n), gen(rng, dt, n)
+        tw, tx = torch.from_numpy(w).to(dev), torch.from_numpy(x).to(dev)
+        got = kf.mapreduce1d(kf.wsq, "+", (tw, tx))
+        ref = oracle.reduce2(w, x, "+", "wsq")
+        if np.dtype(dt).kind == "f":
+            bound = np.sum(np.abs(w.astype(np.float64) * x * x))
+            assert abs(got - ref) <= tol * bound + 1e-300, (n, got, ref)
+        else:
+            assert got == int(ref), n
+    if np.dtype(dt).kind != "f":
+        with pytest.raises(kf.ArgumentError):
+            kf.mapreduce1d(kf.expdiff, "+", (tw, tx))
+        return
+    for n in (1, 10_000, 1 << 20):
+        a, b = (rng.random(n) * 2).astype(dt), (rng.random(n) * 2).astype(dt)
+        got = kf.mapreduce1d(kf.expdiff, "+", (torch.from_numpy(a).to(dev), torch.from_numpy(b).to(dev)))
+        ref = oracle.reduce2(a, b, "+", "expdiff")
+        assert abs(got - ref) <= 4 * tol * ref, (n, got, ref)
+    # the matvec / vecmat entry point takes the symmetric maps only
+    A = torch.ones(8, 4, dtype=torch.from_numpy(a).dtype, device=dev)
+    with pytest.raises(kf.ArgumentError):
+        kf.matvec(kf.wsq, "+", A.T, torch.ones(8, dtype=A.dtype, device=dev))
+
+
 def test_post_map_g(kf, dev):
     # reference test/tests/mapreduce/mapreduce2d_test.jl:30-35: abs2 + g = sqrt row norms
     import math

@@ -198,6 +198,20 @@ def test_reduce3_closed_forms(oracle, n):
     assert np.isclose(oracle.reduce3(a, b, c), np.sum(a * b * c), rtol=1e-12)
 
 
+def test_reduce2_weighted_squares_and_expdiff(oracle):
+    # sum_i i * i^2 = (n(n+1)/2)^2 (exact integers); exp(x - y) against numpy;
+    # exp(x - x) = 1, so the sum is n exactly
+    n = 3000
+    r = np.arange(1, n + 1, dtype=np.int64)
+    assert int(oracle.reduce2(r, r, "+", "wsq")) == (n * (n + 1) // 2) ** 2
+    rng = np.random.default_rng(12)
+    w, x = rng.random((2, n))
+    assert np.isclose(oracle.reduce2(w, x, "+", "wsq"), np.sum(w * x * x), rtol=1e-12)
+    a, b = rng.random((2, n)) * 2
+    assert np.isclose(oracle.reduce2(a, b, "+", "expdiff"), np.sum(np.exp(a - b)), rtol=1e-12)
+    assert oracle.reduce2(a, a, "+", "expdiff") == n
+
+
 def test_exclusive_is_shifted_inclusive(oracle):
     rng = np.random.default_rng(1)
     for dt, op, ident in ((np.int32, "max", np.iinfo(np.int32).min), (np.int32, "min", np.iinfo(np.int32).max),
