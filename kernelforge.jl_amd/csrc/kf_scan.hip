@@ -16,7 +16,10 @@
 //    j*64 + l of the wave's contiguous chunk, so every load and store is a
 //    fully coalesced 16-byte access and no LDS transpose is needed. Each
 //    row j (64 lanes x 16 bytes) is scanned in-lane, then across the wave
-//    with DPP row shifts/broadcasts, and rows are chained with a carry.
+//    with DPP row shifts/broadcasts, and rows are chained with a carry (the
+//    affine pairs instead scan all row totals once through LDS,
+//    wave_row_prefixes). A lane's unit is one 16-byte vector, or one element
+//    for wider types (32-byte Float64 quaternions, moved as two halves).
 //  * The lookback window lives in the top lanes of one wave: lane j reads
 //    the descriptor of tile (t - 64 + j) for the last `win` lanes, so
 //    lane order is tile order and a DPP scan combines the window in the
@@ -40,6 +43,7 @@
 //    clearing between calls (the reference fill!s its descriptors before
 //    every launch, src/scan/scan.jl:444-470).
 #include <atomic>
+#include <type_traits>
 
 #include "kf_common.h"
 
@@ -101,7 +105,7 @@ template <class T> constexpr int kVecBytes = sizeof(T) > 16 ? (int)sizeof(T) : 1
 struct uint4x2 {
   uint4 lo, hi;
 };
-template <class T> using VecT = __typeof__(__builtin_choose_expr(sizeof(T) > 16, uint4x2{}, uint4{}));
+template <class T> using VecT = std::conditional_t<(sizeof(T) > 16), uint4x2, uint4>;
 __device__ inline uint4 ld_vec(const uint4* p) { return ld_stream(p); }
 __device__ inline uint4x2 ld_vec(const uint4x2* p) {
   const uint4* q = reinterpret_cast<const uint4*>(p);
