@@ -42,7 +42,7 @@ import torch
 from . import _lib as _L
 
 __all__ = [
-    "ArgumentError", "KernelBuffer", "AffineOp", "affine", "identity", "abs2", "sqdiff",
+    "ArgumentError", "KernelBuffer", "AffineOp", "affine", "identity", "abs2", "sqdiff", "wsq", "expdiff", "prod3",
     "scan", "scan_", "mapreduce", "mapreduce_", "get_allocation", "vcopy_", "setvalue_", "scan_status",
     "maximum", "maximum_", "minimum", "mapreduce1d", "mapreduce1d_", "mapreduce2d", "mapreduce2d_",
     "mapreducedims", "mapreducedims_",
@@ -417,7 +417,7 @@ def _as_matrix(t, k):
     if r is None or c is None or (r[0] > 1 and r[1] != 1):
         raise NotImplementedError(
             f"layout with shape {tuple(sizes)} and strides {tuple(strides)} cannot be viewed as a "
-            "column-major matrix split at dim {k}")
+            f"column-major matrix split at dim {k}")
     rows, cols = r[0], c[0]
     col_stride = c[1] if cols > 1 else max(rows, 1)
     if cols > 1 and col_stride < rows:
