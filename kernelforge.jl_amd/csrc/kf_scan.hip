@@ -74,15 +74,26 @@ constexpr int64_t kMinTiles = 120;
 // UInt8 tiles carry 4x the elements per byte of work: they need more tiles
 // (480) before a larger shape pays (2^30 unchanged; 10^7: 25.8 -> 18.6 us).
 template <class T> constexpr int64_t min_tiles() { return sizeof(T) == 1 ? 480 : kMinTiles; }
-// Float32 and 8-byte arrays of at least kWideBytes (2^27 Float32 elements)
-// take the 768-thread shape.
+// Arrays of at least kWideBytes take a wider shape: Float32 and the 8-byte
+// types 768 threads x 8 vectors (96 KiB); UInt8 512 threads x 12 vectors
+// (96 KiB), and from kHugeBytes on 512 x 16 (128 KiB). The UInt8 shapes
+// halve or third the lookbacks per byte and still fit two workgroups per
+// CU (96 and 120 VGPRs): 6*10^8 214 -> 207 us, 8*10^8 279 -> 269 us,
+// 10^9 343 -> 329 us at 12; 2^30 361 -> 341 us, 2^31 702 -> 657 us at 16,
+// where 12 gives 350 / 673 (20 and 24 vectors lose 8-10 %; at 32 the
+// compiler no longer keeps the tile in registers).
 constexpr int64_t kWideBytes = 1LL << 29;
-constexpr int kTierWide = kTiers;  // tier index of that shape (8 vectors per lane)
-template <class T> constexpr bool has_wide_tier() { return __is_same(T, float) || sizeof(T) == 8; }
+constexpr int64_t kHugeBytes = 1LL << 30;
+constexpr int kTierWide = kTiers;      // tier index of the wide shape
+constexpr int kTierHuge = kTiers + 1;  // UInt8 from kHugeBytes
+template <class T> constexpr bool has_wide_tier() { return __is_same(T, float) || sizeof(T) == 8 || sizeof(T) == 1; }
+template <class T> constexpr bool has_huge_tier() { return sizeof(T) == 1; }
 template <class T> constexpr int scan_block(int tier) {
   return sizeof(T) == 1 ? 512 : tier == kTierWide ? 768 : kScanBlock;
 }
-constexpr int tier_v(int tier) { return tier == kTierWide ? 8 : kTierV[tier]; }
+template <class T> constexpr int tier_v(int tier) {
+  return tier == kTierHuge ? 16 : tier == kTierWide ? (sizeof(T) == 1 ? 12 : 8) : kTierV[tier];
+}
 constexpr uint32_t kStatePartial = 1, kStatePrefix = 2;
 constexpr size_t kScanHeaderBytes = 256;
 constexpr int kDescWords = 16;             // 128 bytes per tile descriptor
@@ -493,6 +504,7 @@ template <class T> constexpr int max_tier() { return sizeof(T) > 16 ? 1 : sizeof
 
 template <class T> int scan_tier(int64_t n) {
   const int64_t bytes = n * (int64_t)sizeof(T);
+  if (has_huge_tier<T>() && bytes >= kHugeBytes) return kTierHuge;
   if (has_wide_tier<T>() && bytes >= kWideBytes) return kTierWide;
   int t = max_tier<T>();
   while (t > 0 && bytes < min_tiles<T>() * (int64_t)scan_block<T>(t) * kTierV[t] * kVecBytes<T>) --t;
@@ -500,7 +512,7 @@ template <class T> int scan_tier(int64_t n) {
 }
 
 template <class T> int64_t tier_tile(int tier) {
-  return (int64_t)scan_block<T>(tier) * tier_v(tier) * ScanShape<T>::EPV;
+  return (int64_t)scan_block<T>(tier) * tier_v<T>(tier) * ScanShape<T>::EPV;
 }
 
 // Tiles for n elements starting `off` elements after a 16-byte boundary.
@@ -531,7 +543,7 @@ template <auto KERNEL> int64_t resident_tiles(int block) {
 template <class T, class Op, class Map, int TIER>
 void launch_scan_tier(const void* src, int64_t ss, void* dst, int64_t ds, int64_t n, int mode, int64_t ntiles,
                       int vec, int off, void* scratch, hipStream_t stream) {
-  constexpr int B = scan_block<T>(TIER), V = tier_v(TIER);
+  constexpr int B = scan_block<T>(TIER), V = tier_v<T>(TIER);
   const int post = mode >> 1;
   if (mode & 1) {
     constexpr auto kernel = scan_kernel<T, Op, Map, true, B, V>;
@@ -565,9 +577,13 @@ int launch_scan(const void* src, int64_t ss, void* dst, int64_t ds, int64_t n, i
       if constexpr (max_tier<T>() >= 3)
         launch_scan_tier<T, Op, Map, 3>(src, ss, dst, ds, n, excl, ntiles, vec, off, scratch, stream);
       break;
-    default:
+    case kTierWide:
       if constexpr (has_wide_tier<T>())
         launch_scan_tier<T, Op, Map, kTierWide>(src, ss, dst, ds, n, excl, ntiles, vec, off, scratch, stream);
+      break;
+    default:
+      if constexpr (has_huge_tier<T>())
+        launch_scan_tier<T, Op, Map, kTierHuge>(src, ss, dst, ds, n, excl, ntiles, vec, off, scratch, stream);
   }
   return kf_check_launch("scan_kernel");
 }

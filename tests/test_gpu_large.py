@@ -37,6 +37,30 @@ def test_uint8_scan_beyond_2pow31(kf, dev):
     torch.cuda.synchronize()
 
 
+def test_uint8_scan_wide_shape_switchover(kf, dev):
+    # UInt8 arrays switch to 512 x 12-vector tiles at 2^29 bytes and to
+    # 512 x 16 at 2^30: both sides of each switch, inclusive and exclusive,
+    # against the closed-form prefix of x[k] = k mod 256
+    for edge in (1 << 29, 1 << 30):
+        for n in (edge - 1, edge, edge + 1):
+            x = torch.empty(n, dtype=torch.uint8, device=dev)
+            for s in range(0, n, CHUNK):
+                e = min(n, s + CHUNK)
+                x[s:e] = (torch.arange(s, e, device=dev) % 256).to(torch.uint8)
+            for exclusive in (False, True):
+                y = kf.scan("+", x, exclusive=exclusive)
+                for s in range(0, n, CHUNK):
+                    e = min(n, s + CHUNK)
+                    i = torch.arange(s, e, device=dev)
+                    want = u8_ramp_prefix(i - 1 if exclusive else i)
+                    if exclusive and s == 0:
+                        want[0] = 0
+                    assert torch.equal(y[s:e], want), (n, exclusive, s)
+                del y
+            del x
+    torch.cuda.synchronize()
+
+
 def test_int32_reductions_beyond_2pow31(kf, dev):
     n = (1 << 31) + 5
     x = torch.ones(n, dtype=torch.int32, device=dev)
