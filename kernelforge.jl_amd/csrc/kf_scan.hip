@@ -75,8 +75,8 @@ constexpr int64_t kMinTiles = 120;
 // (480) before a larger shape pays (2^30 unchanged; 10^7: 25.8 -> 18.6 us).
 template <class T> constexpr int64_t min_tiles() { return sizeof(T) == 1 ? 480 : kMinTiles; }
 // Arrays of at least kWideBytes take a wider shape: Float32 and the 8-byte
-// types 768 threads x 8 vectors (96 KiB); UInt8 512 threads x 12 vectors
-// (96 KiB), and from kHugeBytes on 512 x 16 (128 KiB). The UInt8 shapes
+// types 768 threads x 8 vectors (96 KiB); UInt8 (from kU8WideBytes) 512
+// threads x 12 vectors (96 KiB), and from kHugeBytes on 512 x 16 (128 KiB). The UInt8 shapes
 // halve or third the lookbacks per byte and still fit two workgroups per
 // CU (96 and 120 VGPRs): 6*10^8 214 -> 207 us, 8*10^8 279 -> 269 us,
 // 10^9 343 -> 329 us at 12; 2^30 361 -> 341 us, 2^31 702 -> 657 us at 16,
@@ -84,6 +84,9 @@ template <class T> constexpr int64_t min_tiles() { return sizeof(T) == 1 ? 480 :
 // compiler no longer keeps the tile in registers).
 constexpr int64_t kWideBytes = 1LL << 29;
 constexpr int64_t kHugeBytes = 1LL << 30;
+// UInt8 takes the 12-vector shape from 256 MiB (3*10^8: 118 -> 116 us; at
+// 10^8 the 8-vector tiles stay ahead, 50.6 vs 53.3 us).
+constexpr int64_t kU8WideBytes = 1LL << 28;
 constexpr int kTierWide = kTiers;      // tier index of the wide shape
 constexpr int kTierHuge = kTiers + 1;  // UInt8 from kHugeBytes
 template <class T> constexpr bool has_wide_tier() { return __is_same(T, float) || sizeof(T) == 8 || sizeof(T) == 1; }
@@ -511,7 +514,7 @@ template <class T> constexpr int max_tier() { return sizeof(T) > 16 ? 1 : sizeof
 template <class T> int scan_tier(int64_t n) {
   const int64_t bytes = n * (int64_t)sizeof(T);
   if (has_huge_tier<T>() && bytes >= kHugeBytes) return kTierHuge;
-  if (has_wide_tier<T>() && bytes >= kWideBytes) return kTierWide;
+  if (has_wide_tier<T>() && bytes >= (sizeof(T) == 1 ? kU8WideBytes : kWideBytes)) return kTierWide;
   int t = max_tier<T>();
   while (t > 0 && bytes < min_tiles<T>() * (int64_t)scan_block<T>(t) * kTierV[t] * kVecBytes<T>) --t;
   return t;

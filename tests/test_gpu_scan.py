@@ -295,7 +295,7 @@ def test_views_offsets_strides_inplace(kf, oracle, dev):
 @pytest.mark.parametrize("dt", [np.float32, np.float64, np.int32, np.int64, np.uint8])
 def test_tile_size_switchover(kf, oracle, dev, dt):
     # tiles are 1024 threads (512 for uint8; 768 for float32 and 8-byte
-    # types from 512 MiB on; uint8's own 12- and 16-vector shapes from 512
+    # types from 512 MiB on; uint8's own 12- and 16-vector shapes from 256
     # MiB and 1 GiB are checked in test_gpu_large.py) x V 16-byte vectors,
     # V in (1, 2, 4, 8): the
     # largest V that still makes >= 120 tiles (480 for uint8); with more
