@@ -9,7 +9,7 @@
  * size it with the matching *_scratch_bytes query and zero-fill it ONCE
  * before its first use (kf_scratch_reset does that on a stream). After that
  * the kernels keep it valid themselves (epoch-tagged tile descriptors and
- * self-resetting counters), so one scratch buffer may be reused across calls,
+ * epoch-tagged reduction fold slots), so one scratch buffer may be reused across calls,
  * dtypes, operators and sizes without clearing. A buffer serves one family:
  * scan calls (kf_scan), or reduction calls (kf_reduce, kf_reduce2, kf_reduce3,
  * kf_reduce_dim*). Reduction partials written over scan descriptors could

@@ -13,7 +13,11 @@
 //    (mapreduce1d_kernel.jl:66-92); a "last workgroup done" ticket was
 //    measured here to serialise thousands of same-address device atomics
 //    at the end of the grid (the full reduction ran at 1.8 TB/s with 8192
-//    workgroups), so stage 2 uses no atomics, fences or flags at all.
+//    workgroups), and fences cost more than the launch they save. Grids of
+//    up to kFoldMax workgroups skip the launch with an atomic-free fold
+//    instead: epoch-tagged partial slots written with relaxed device-scope
+//    stores and gathered by the last workgroup (fold_partial), which saves
+//    a launch's host cost (eager 10^6 Float32: 11.0 -> 8.7 us).
 //  * Combine orders depend only on the shape and pointer alignment, so every
 //    result is bit-for-bit reproducible run to run.
 #include "kf_common.h"
@@ -26,6 +30,16 @@ constexpr int kRedUnroll = 4;
 constexpr int kRedMaxBlocks = 8192;
 
 inline size_t round256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+// Every reduction scratch buffer starts with a reserved area that no other
+// partial buffer overlaps: an 8-byte epoch word (then padding to 256 bytes)
+// and kFoldMax 16-byte slots for the single-level fold of
+// reduce_once_kernel. Partial buffers of all reduction kinds sit after it,
+// so stale partials of other calls can never read as current fold slots.
+constexpr int kFoldMax = 2048;  // workgroups a single-level fold combines
+constexpr bool kUseFold = true;
+constexpr size_t kRedReserved = 256 + (size_t)kFoldMax * 16;
+inline void* red_work(void* scratch) { return scratch ? (uint8_t*)scratch + kRedReserved : nullptr; }
 
 // Block-wide combine in wave order; result valid in thread 0.
 template <class T, class Op> __device__ inline T block_reduce(T x, T* s_wave) {
@@ -123,9 +137,94 @@ __global__ __launch_bounds__(kRedBlock) void reduce_kernel(const T* src, int64_t
 constexpr int kOnceUnroll = 2;
 constexpr int kOnceVecs = kRedBlock * kOnceUnroll;
 
-template <class T, class Op, class Map>
+// Single-level fold, replacing combine_all_kernel's launch for grids of
+// 2..kFoldMax workgroups. Every workgroup but the last publishes its
+// partial into its slot as W 64-bit words, each {tag:32, value bits:32},
+// with relaxed device-scope stores. The last workgroup polls all slots
+// (8 per thread, all in flight together) until every word carries the
+// tag, then combines them in slot order with its own partial last, so
+// the result does not depend on timing. It stores the result and the tag
+// as the new epoch. The tag is epoch + 1, read with a plain load at kernel
+// start: the previous call's last workgroup wrote it before that kernel
+// ended, and within a call every reader loads it before publishing,
+// which the waiter's completion depends on. Slots of older calls never
+// match. Only one workgroup ever waits, so progress needs no co-residency;
+// a bounded spin (only a corrupted or concurrently shared buffer can
+// exhaust it) keeps a bad buffer from hanging the GPU.
+constexpr uint32_t kFoldSpinLimit = 1u << 22;
+template <class T, class Op> __device__ inline void fold_partial(T part, T* out, uint64_t* hdr, T* s_wave) {
+  constexpr int W = Words<T>::W;
+  constexpr int PER = kFoldMax / kRedBlock;
+  __shared__ uint32_t s_tag;
+  const int tid = threadIdx.x;
+  if (tid == 0) {
+    const uint32_t t = (uint32_t)hdr[0] + 1u;
+    s_tag = t == 0 ? 1u : t;
+  }
+  __syncthreads();
+  const uint32_t tag = s_tag;
+  uint64_t* slots = hdr + 256 / sizeof(uint64_t);
+  const int last = (int)gridDim.x - 1;
+  if ((int)blockIdx.x != last) {
+    if (tid == 0) {
+      const Words<T> w = to_words(part);
+#pragma unroll
+      for (int i = 0; i < W; ++i) st_agent(slots + 2 * blockIdx.x + i, ((uint64_t)tag << 32) | w.w[i]);
+    }
+    return;
+  }
+  // the last workgroup: slot k * kRedBlock + tid of every k on this thread
+  const T id = Op::template identity<T>();
+  T v[PER];
+  bool done[PER];
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    v[k] = id;
+    done[k] = k * kRedBlock + tid >= last;
+  }
+  for (uint32_t polls = 0; polls < kFoldSpinLimit; ++polls) {
+    uint64_t d[PER][W];
+#pragma unroll
+    for (int k = 0; k < PER; ++k)
+      if (!done[k]) {
+#pragma unroll
+        for (int i = 0; i < W; ++i) d[k][i] = ld_agent(slots + 2 * (k * kRedBlock + tid) + i);
+      }
+    bool all = true;
+#pragma unroll
+    for (int k = 0; k < PER; ++k)
+      if (!done[k]) {
+        bool ok = true;
+        Words<T> w;
+#pragma unroll
+        for (int i = 0; i < W; ++i) {
+          ok &= (uint32_t)(d[k][i] >> 32) == tag;
+          w.w[i] = (uint32_t)d[k][i];
+        }
+        if (ok) {
+          v[k] = from_words<T>(w);
+          done[k] = true;
+        } else {
+          all = false;
+        }
+      }
+    if (__syncthreads_and(all)) break;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  T acc = v[0];
+#pragma unroll
+  for (int k = 1; k < PER; ++k) acc = Op::combine(acc, v[k]);
+  __syncthreads();  // s_wave still holds this workgroup's own partial sums
+  const T others = block_reduce<T, Op>(acc, s_wave);
+  if (tid == 0) {
+    out[0] = Op::combine(others, part);
+    hdr[0] = tag;
+  }
+}
+
+template <class T, class Op, class Map, bool FOLD = false>
 __global__ __launch_bounds__(kRedBlock) void reduce_once_kernel(const T* src, int64_t n, int64_t head,
-                                                                int64_t nvec, T* out) {
+                                                                int64_t nvec, T* out, uint64_t* fold_hdr) {
   constexpr int EPV = 16 / (int)sizeof(T);
   __shared__ T s_wave[kRedWaves];
   const T id = Op::template identity<T>();
@@ -156,7 +255,11 @@ __global__ __launch_bounds__(kRedBlock) void reduce_once_kernel(const T* src, in
     if (tail0 + tid < n) acc = Op::combine(acc, Map::apply(src[tail0 + tid]));
   }
   const T part = block_reduce<T, Op>(acc, s_wave);
-  if (tid == 0) out[blockIdx.x] = part;
+  if constexpr (!FOLD) {
+    if (tid == 0) out[blockIdx.x] = part;  // a partial, or the result when gridDim.x == 1
+  } else {
+    fold_partial<T, Op>(part, out, fold_hdr, s_wave);  // out is the result
+  }
 }
 
 // Full reduction, stage 2: one 1024-thread workgroup combines `count`
@@ -239,38 +342,45 @@ inline size_t reduce_scratch(size_t es, int64_t n) {
     const size_t bytes = round256((size_t)L.count[i] * es + 16);
     if (i % 2 == 0) a = kmax(a, bytes); else b = kmax(b, bytes);
   }
-  return kmax<size_t>(a + b, round256((size_t)kRedMaxBlocks * es));
+  return kRedReserved + kmax<size_t>(a + b, round256((size_t)kRedMaxBlocks * es));
 }
 
 template <class T, class Op, class Map>
 int launch_reduce(const void* src, int64_t n, int64_t stride, void* dst, void* scratch,
                   hipStream_t stream) {
   constexpr int EPV = 16 / (int)sizeof(T);
+  uint8_t* work = (uint8_t*)red_work(scratch);
   if (stride != 1) {
     const int grid = reduce_grid<T>(n);
-    T* out = grid == 1 ? (T*)dst : (T*)scratch;
+    T* out = grid == 1 ? (T*)dst : (T*)work;
     hipLaunchKernelGGL((reduce_kernel<T, Op, Map>), dim3(grid), dim3(kRedBlock), 0, stream,
                        (const T*)src, n, stride, out, 0);
     if (grid > 1)
       hipLaunchKernelGGL((combine_all_kernel<T, Op>), dim3(1), dim3(kCombineBlock), 0, stream,
-                         (const T*)scratch, grid, (T*)dst);
+                         (const T*)work, grid, (T*)dst);
     return kf_check_launch("reduce_kernel");
   }
   const int64_t head = kmin<int64_t>(n, (int64_t)(((16 - ((uintptr_t)src & 15)) & 15) / sizeof(T)));
   const int64_t nvec = (n - head) / EPV;
   const OnceLevels L = once_levels(nvec, EPV);
+  if (kUseFold && L.nlev == 1 && L.count[0] > 1 && L.count[0] <= kFoldMax) {
+    // one launch: the last workgroup folds the others' partials (fold_partial)
+    hipLaunchKernelGGL((reduce_once_kernel<T, Op, Map, true>), dim3((unsigned)L.count[0]), dim3(kRedBlock), 0,
+                       stream, (const T*)src, n, head, nvec, (T*)dst, (uint64_t*)scratch);
+    return kf_check_launch("reduce_once_kernel");
+  }
   size_t abytes = 0;
   for (int i = 0; i < L.nlev; i += 2) abytes = kmax(abytes, round256((size_t)L.count[i] * sizeof(T) + 16));
-  T* buf[2] = {(T*)scratch, (T*)((uint8_t*)scratch + abytes)};
+  T* buf[2] = {(T*)work, (T*)(work + abytes)};
   // level 0 reads the input (with map, head and tail); later levels reduce partials
   T* out0 = (L.nlev == 1 && L.count[0] == 1) ? (T*)dst : buf[0];
   hipLaunchKernelGGL((reduce_once_kernel<T, Op, Map>), dim3((unsigned)L.count[0]), dim3(kRedBlock), 0, stream,
-                     (const T*)src, n, head, nvec, out0);
+                     (const T*)src, n, head, nvec, out0, (uint64_t*)nullptr);
   for (int i = 1; i < L.nlev; ++i) {
     const int64_t m = L.count[i - 1];
     const int64_t mv = m / EPV;
     hipLaunchKernelGGL((reduce_once_kernel<T, Op, MapIdentity>), dim3((unsigned)L.count[i]), dim3(kRedBlock), 0,
-                       stream, (const T*)buf[(i - 1) % 2], m, (int64_t)0, mv, buf[i % 2]);
+                       stream, (const T*)buf[(i - 1) % 2], m, (int64_t)0, mv, buf[i % 2], (uint64_t*)nullptr);
   }
   if (out0 != (T*)dst)
     hipLaunchKernelGGL((combine_all_kernel<T, Op>), dim3(1), dim3(kCombineBlock), 0, stream,
@@ -334,8 +444,9 @@ template <class M, class T, int K> __device__ inline T apply_k(const T (&v)[K]) 
 
 // Multi-array reduction, vector path: the one-shot workgroups of
 // reduce_once_kernel, each loading the same 16-byte vectors of all K arrays.
-template <class T, class Op, class M, int K>
-__global__ __launch_bounds__(kRedBlock) void reducek_once_kernel(Operands<T, K> a, int64_t n, T* out) {
+template <class T, class Op, class M, int K, bool FOLD = false>
+__global__ __launch_bounds__(kRedBlock) void reducek_once_kernel(Operands<T, K> a, int64_t n, T* out,
+                                                                 uint64_t* fold_hdr) {
   constexpr int EPV = 16 / (int)sizeof(T);
   __shared__ T s_wave[kRedWaves];
   const T id = Op::template identity<T>();
@@ -376,7 +487,11 @@ __global__ __launch_bounds__(kRedBlock) void reducek_once_kernel(Operands<T, K> 
     acc = Op::combine(acc, apply_k<M, T, K>(v));
   }
   const T part = block_reduce<T, Op>(acc, s_wave);
-  if (tid == 0) out[blockIdx.x] = part;
+  if constexpr (!FOLD) {
+    if (tid == 0) out[blockIdx.x] = part;
+  } else {
+    fold_partial<T, Op>(part, out, fold_hdr, s_wave);  // out is the result
+  }
 }
 
 // Multi-array reduction, strided operands: grid-stride loop.
@@ -396,8 +511,9 @@ __global__ __launch_bounds__(kRedBlock) void reducek_kernel(Operands<T, K> a, in
 }
 
 template <class T, class Op, class M, int K>
-int launch_reducek(const Operands<T, K>& a, int64_t n, void* dst, void* scratch, hipStream_t stream) {
+int launch_reducek(const Operands<T, K>& a, int64_t n, void* dst, void* scratch_base, hipStream_t stream) {
   constexpr int EPV = 16 / (int)sizeof(T);
+  void* scratch = red_work(scratch_base);
   bool vec = true;
   for (int k = 0; k < K; ++k) vec = vec && a.s[k] == 1 && (uintptr_t)a.p[k] % 16 == 0;
   if (!vec) {
@@ -410,16 +526,21 @@ int launch_reducek(const Operands<T, K>& a, int64_t n, void* dst, void* scratch,
     return kf_check_launch("reducek_kernel");
   }
   const OnceLevels L = once_levels(n / EPV, EPV);
+  if (kUseFold && L.nlev == 1 && L.count[0] > 1 && L.count[0] <= kFoldMax) {
+    hipLaunchKernelGGL((reducek_once_kernel<T, Op, M, K, true>), dim3((unsigned)L.count[0]), dim3(kRedBlock), 0,
+                       stream, a, n, (T*)dst, (uint64_t*)scratch_base);
+    return kf_check_launch("reducek_once_kernel");
+  }
   size_t abytes = 0;
   for (int i = 0; i < L.nlev; i += 2) abytes = kmax(abytes, round256((size_t)L.count[i] * sizeof(T) + 16));
   T* buf[2] = {(T*)scratch, (T*)((uint8_t*)scratch + abytes)};
   T* out0 = (L.nlev == 1 && L.count[0] == 1) ? (T*)dst : buf[0];
   hipLaunchKernelGGL((reducek_once_kernel<T, Op, M, K>), dim3((unsigned)L.count[0]), dim3(kRedBlock), 0, stream,
-                     a, n, out0);
+                     a, n, out0, (uint64_t*)nullptr);
   for (int i = 1; i < L.nlev; ++i) {
     const int64_t m = L.count[i - 1];
     hipLaunchKernelGGL((reduce_once_kernel<T, Op, MapIdentity>), dim3((unsigned)L.count[i]), dim3(kRedBlock), 0,
-                       stream, (const T*)buf[(i - 1) % 2], m, (int64_t)0, m / EPV, buf[i % 2]);
+                       stream, (const T*)buf[(i - 1) % 2], m, (int64_t)0, m / EPV, buf[i % 2], (uint64_t*)nullptr);
   }
   if (out0 != (T*)dst)
     hipLaunchKernelGGL((combine_all_kernel<T, Op>), dim3(1), dim3(kCombineBlock), 0, stream,
@@ -740,7 +861,8 @@ template <class T, class Op, class Map2> struct Reduce2L {
 template <class T, class Op, class Map> struct ReduceDimL {
   static int run(const void* A, int64_t rows, int64_t cols, int64_t cs, int dim, void* dst, int64_t ds,
                  void* scratch, hipStream_t s, int64_t batch, int64_t a_bstride) {
-    return launch_reduce_dim<T, Op, Unary<Map>>(A, rows, cols, cs, dim, dst, ds, scratch, s, batch, a_bstride);
+    return launch_reduce_dim<T, Op, Unary<Map>>(A, rows, cols, cs, dim, dst, ds, red_work(scratch), s, batch,
+                                                a_bstride);
   }
 };
 
@@ -896,7 +1018,7 @@ extern "C" size_t kf_reduce_dim_scratch_bytes(kf_dtype dt, int64_t rows, int64_t
   if (es == 0 || rows <= 0 || cols <= 0 || (dim != 1 && dim != 2)) return 256;
   // the plan depends on alignment: reserve for the larger of the two
   const DimPlan pv = plan_dim(es, rows, cols, dim, true), ps = plan_dim(es, rows, cols, dim, false);
-  return kmax<size_t>(256, kmax<size_t>(pv.partial_bytes, ps.partial_bytes));
+  return kRedReserved + kmax<size_t>(256, kmax<size_t>(pv.partial_bytes, ps.partial_bytes));
 }
 
 extern "C" int kf_reduce_dim(kf_op op, kf_map f, kf_dtype dt, const void* A, int64_t rows, int64_t cols,
@@ -934,7 +1056,7 @@ extern "C" size_t kf_reduce_dim_batched_scratch_bytes(kf_dtype dt, int64_t rows,
   const size_t es = kf_dtype_size(dt);
   if (es == 0 || rows <= 0 || cols <= 0 || batch <= 0) return 256;
   const DimPlan pv = plan_dim(es, rows, cols, 2, true, batch), ps = plan_dim(es, rows, cols, 2, false, batch);
-  return kmax<size_t>(256, kmax<size_t>(pv.partial_bytes, ps.partial_bytes));
+  return kRedReserved + kmax<size_t>(256, kmax<size_t>(pv.partial_bytes, ps.partial_bytes));
 }
 
 extern "C" int kf_reduce_dim_batched(kf_op op, kf_map f, kf_dtype dt, const void* A, int64_t rows, int64_t cols,
@@ -1015,11 +1137,11 @@ extern "C" int kf_reduce_dim_x(kf_op op, kf_map2 f, kf_dtype dt, const void* A, 
   hipStream_t s = (hipStream_t)stream;
   const int64_t one = 1, zero = 0;
   switch (dt) {
-    case KF_F32: return dispatch_dim_x<float>(op, f, A, rows, cols, col_stride, dim, dst, dst_stride, scratch, s, one, zero, x, x_stride);
-    case KF_F64: return dispatch_dim_x<double>(op, f, A, rows, cols, col_stride, dim, dst, dst_stride, scratch, s, one, zero, x, x_stride);
-    case KF_I32: return dispatch_dim_x<int32_t>(op, f, A, rows, cols, col_stride, dim, dst, dst_stride, scratch, s, one, zero, x, x_stride);
-    case KF_I64: return dispatch_dim_x<int64_t>(op, f, A, rows, cols, col_stride, dim, dst, dst_stride, scratch, s, one, zero, x, x_stride);
-    case KF_U8: return dispatch_dim_x<uint8_t>(op, f, A, rows, cols, col_stride, dim, dst, dst_stride, scratch, s, one, zero, x, x_stride);
+    case KF_F32: return dispatch_dim_x<float>(op, f, A, rows, cols, col_stride, dim, dst, dst_stride, red_work(scratch), s, one, zero, x, x_stride);
+    case KF_F64: return dispatch_dim_x<double>(op, f, A, rows, cols, col_stride, dim, dst, dst_stride, red_work(scratch), s, one, zero, x, x_stride);
+    case KF_I32: return dispatch_dim_x<int32_t>(op, f, A, rows, cols, col_stride, dim, dst, dst_stride, red_work(scratch), s, one, zero, x, x_stride);
+    case KF_I64: return dispatch_dim_x<int64_t>(op, f, A, rows, cols, col_stride, dim, dst, dst_stride, red_work(scratch), s, one, zero, x, x_stride);
+    case KF_U8: return dispatch_dim_x<uint8_t>(op, f, A, rows, cols, col_stride, dim, dst, dst_stride, red_work(scratch), s, one, zero, x, x_stride);
     default: return kf_set_error(KF_EINVAL, "kf_reduce_dim_x: bad dtype %d", (int)dt);
   }
 }

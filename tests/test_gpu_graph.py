@@ -1,6 +1,8 @@
 """The kernels record into HIP graphs (no memset nodes; scratch is kept valid
 by the kernels themselves) and every replay matches eager execution, with
 eager work and synchronisations between replays."""
+import operator
+
 import numpy as np
 import pytest
 import torch
@@ -15,6 +17,7 @@ def test_graph_replays_match_eager(kf, oracle, dev):
     A = torch.from_numpy(rng.integers(-8, 9, (300, 5000)).astype(np.int32)).to(dev).T  # 5000 x 300 col-major
     y = torch.empty_like(x)
     tot = torch.empty(1, dtype=torch.int32, device=dev)
+    dot = torch.empty(1, dtype=torch.int32, device=dev)
     rows = torch.empty(5000, dtype=torch.int32, device=dev)
     t_scan = kf.get_allocation(kf.Scan1D, kf.identity, "+", x)
     t_red = kf.get_allocation(kf.MapReduce1D, kf.identity, "+", x)
@@ -22,7 +25,8 @@ def test_graph_replays_match_eager(kf, oracle, dev):
 
     def work():
         kf.scan_("+", y, x, tmp=t_scan, exclusive=True)
-        kf.mapreduce_(kf.identity, max, tot, x, tmp=t_red)
+        kf.mapreduce_(kf.identity, max, tot, x, tmp=t_red)         # single-level fold (489 workgroups)
+        kf.mapreduce1d_(operator.mul, "+", dot, (x, x), tmp=t_red)  # the same, two arrays
         kf.mapreduce_(kf.identity, "+", rows, A, dims=2, tmp=t_dim)
 
     work()  # eager warm-up
@@ -39,6 +43,7 @@ def test_graph_replays_match_eager(kf, oracle, dev):
         xs, As = x.cpu().numpy(), A.cpu().numpy()
         assert np.array_equal(y.cpu().numpy(), oracle.scan(xs, "+", exclusive=True)), rep
         assert tot.item() == xs.max(), rep
+        assert dot.item() == int(np.sum(xs.astype(np.int64) ** 2) % 2**32 - (2**32 if np.sum(xs.astype(np.int64) ** 2) % 2**32 >= 2**31 else 0)), rep
         assert np.array_equal(rows.cpu().numpy(), As.sum(axis=1).astype(np.int32)), rep
         # the same calls eagerly agree with the replay
         y2 = torch.empty_like(y)
