@@ -162,7 +162,8 @@ int kf_reduce(kf_op op, kf_map f, kf_dtype dt,
  *   mapreduce(f, op, (x, y))  src/mapreduce/mapreduce.jl:228-239 ->
  *   mapreduce1d(f, op, srcs::NTuple)  src/mapreduce/1D/mapreduce1d.jl:186-204
  * for the maps x*y and (x-y)^2 (its tests' dot products and distances,
- * test/tests/mapreduce/mapreduce1d_test.jl:231-319). */
+ * test/tests/mapreduce/mapreduce1d_test.jl:231-319), x*y*y and exp(x-y)
+ * (its weighted sum of squares and sum(exp(a - b)), same file :117-131). */
 size_t kf_reduce2_scratch_bytes(kf_dtype dt, int64_t n);
 
 int kf_reduce2(kf_op op, kf_map2 f, kf_dtype dt,
