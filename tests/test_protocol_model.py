@@ -2,7 +2,10 @@
 
 A randomized scheduler interleaves, one memory word at a time, what the
 tiles of one scan do in kernelforge.jl_amd/csrc/kf_scan.hip:
-  * a tile takes a ticket, "loads" its aggregate, publishes PARTIAL (W tagged
+  * tiles are numbered by workgroup id and start in dispatch order: tile t
+    queues on XCD t mod X, each XCD starts its queue in increasing order and
+    holds at most a few tiles at once (a tile leaves when it is done);
+  * a started tile "loads" its aggregate, publishes PARTIAL (W tagged
     words, written one by one in random order), looks back, publishes PREFIX;
   * a lookback poll reads the descriptors of a window of predecessors, each
     word separately (so a reader can observe a half-written descriptor), and
@@ -99,7 +102,11 @@ def tile_program(t, agg, mem, epoch, W, window, rng, result, accept=classify):
     yield from publish(PREFIX, run + agg)
 
 
-def run_schedule(seed, W, accept=classify):
+class Stuck(Exception):
+    """No tile can make progress: the dispatch order deadlocked."""
+
+
+def run_schedule(seed, W, accept=classify, reverse_xcd_order=False, max_steps=400_000):
     rng = random.Random(seed * 7 + W)
     ntiles = rng.randint(1, 40)
     window = rng.choice([1, 2, 8, 64])
@@ -107,22 +114,31 @@ def run_schedule(seed, W, accept=classify):
     mem = Memory(ntiles, W, epoch - rng.randint(1, 3), rng)
     aggs = [f"[{t}]" for t in range(ntiles)]
     result = {}
-    # tiles start in ticket order (a tile only starts after every earlier
-    # ticket was handed out) but then run at arbitrary relative speeds
-    progs, started = {}, 0
+    nxcd = rng.choice([1, 2, 8])
+    slots = rng.randint(1, 3)   # tiles one XCD holds at once
+    queues = [[t for t in range(ntiles) if t % nxcd == x] for x in range(nxcd)]
+    if reverse_xcd_order:
+        queues = [q[::-1] for q in queues]
+    running = [set() for _ in range(nxcd)]
+    progs = {}
     steps = 0
-    while started < ntiles or progs:
+    while any(queues) or progs:
         steps += 1
-        assert steps < 2_000_000, "schedule did not terminate"
-        if started < ntiles and (not progs or rng.random() < 0.3):
-            progs[started] = tile_program(started, aggs[started], mem, epoch, W, window, rng, result, accept)
-            started += 1
+        if steps > max_steps:
+            raise Stuck(f"seed {seed}: {len(progs)} tiles waiting, {sum(map(len, queues))} not started")
+        free = [x for x in range(nxcd) if queues[x] and len(running[x]) < slots]
+        if free and (not progs or rng.random() < 0.3):
+            x = rng.choice(free)
+            t = queues[x].pop(0)
+            running[x].add(t)
+            progs[t] = tile_program(t, aggs[t], mem, epoch, W, window, rng, result, accept)
             continue
         t = rng.choice(list(progs))
         try:
             next(progs[t])
         except StopIteration:
             del progs[t]
+            running[t % nxcd].discard(t)
     return ntiles, epoch, aggs, result, mem
 
 
@@ -147,6 +163,19 @@ def test_model_detects_a_broken_acceptance_rule():
         ntiles, _, aggs, result, _ = run_schedule(seed, 2, accept=classify_word0_only)
         wrong += any(result[t] != "".join(aggs[:t]) for t in range(ntiles))
     assert wrong > 0
+
+
+def test_model_detects_out_of_order_dispatch():
+    # negative control for the progress argument: if an XCD started its
+    # workgroups in decreasing id order, a full XCD of tiles waiting on a
+    # lower tile it has not started would never drain
+    stuck = 0
+    for seed in range(30):
+        try:
+            run_schedule(seed, 1, reverse_xcd_order=True, max_steps=20_000)
+        except Stuck:
+            stuck += 1
+    assert stuck > 0
 
 
 def test_torn_descriptor_is_rejected():
