@@ -60,31 +60,31 @@
 namespace kf {
 
 constexpr int kScanBlock = 1024;       // large tiles (default)
-// Tile shapes: 1024 threads x kTierV[t] 16-byte vectors per lane (16 KiB
+// Tile shapes: 1024 threads x kTierV[t] 16-byte vectors per lane (32 KiB
 // to 128 KiB; 512 threads for UInt8). An array takes the largest shape that
-// still cuts it into at least kMinTiles tiles (scan_tier). Measured on
-// MI355X over shapes of
-// 256-1024 threads x 1-8 vectors: 1024-thread tiles win at every size, and
-// fewer, larger tiles win once there are ~120 of them (Float32: 10^5 3.8 us
-// at 1 vector; 10^6 6.4-6.5 us at 2-4; 2^21 7.7 us at 4, 17.8 us with 64
-// tiles of 8; from 4*10^6 on 8 vectors).
-// Threads per tile by element type, measured at 2^28 Float32 / Int32,
-// 2^27 Float64, 2^26 affine pairs and 2^30 UInt8 over 512, 768 and 1024:
-// UInt8 (16 elements per vector, long in-tile work) gains most from two
-// co-resident workgroups per CU, one computing while the other streams
-// (512: 5.74 vs 5.43 TB/s at 1024). Large Float32 and 8-byte arrays take
-// 768-thread tiles, two workgroups per CU (the 8-byte types once wave 0
-// parks its tile in LDS during the lookback, 72-74 VGPRs): Float32 6.18 vs
-// 6.11 TB/s at 2^28, Float64 6.22 vs 5.95 at 2^27, affine 5.91 vs 5.70 at
-// 2^26; below 2^27 Float32 (-2.5 % at 2^26, -20 % at 2^24) and 10^7
-// Float64 (-4 %) they lose. Int32 is equal at 768 and 1024.
+// still cuts it into at least min_tiles() tiles (scan_tier), but never fewer
+// than 2 vectors per lane (UInt8: 1). Measured on MI355X with tiles
+// numbered by workgroup id: 240 tiles rather than 120 gives Float32 2^21
+// 7.68 -> 6.80 us, 2*10^6 7.55 -> 7.04 us, 4*10^6 10.4 -> 8.8 us, 10^6 6.06
+// -> 6.16 us. Letting 10^6 drop to 16 KiB tiles to reach 240 cost 9 %,
+// hence the floor.
+// Threads per tile by element type (2^28 Float32 / Int32, 2^27 Float64,
+// 2^26 affine pairs, 2^30 UInt8 over 512, 768 and 1024): UInt8 (16
+// elements per vector, long in-tile work) gains most from co-resident
+// workgroups, one computing while another streams (512: 5.74 vs 5.43 TB/s
+// at 1024). Large Float32, Int32 and 8-byte arrays take 768-thread tiles,
+// two workgroups per CU (the 8-byte types once wave 0 parks its tile in LDS
+// during the lookback): Float32 2^28 320 vs 329 us at 1024, Int32 322 vs
+// 335 us, Float64 2^27 324 vs 353 us.
 constexpr int kTiers = 4;
 constexpr int kTierV[kTiers] = {1, 2, 4, 8};
-constexpr int64_t kMinTiles = 120;
+constexpr int64_t kMinTiles = 240;
 // UInt8 tiles carry 4x the elements per byte of work: they need more tiles
-// (480) before a larger shape pays (2^30 unchanged; 10^7: 25.8 -> 18.6 us).
+// (480) before a larger shape pays (10^7 9.7 us at 480, 10.7 at 240, 18.2
+// at 960).
 template <class T> constexpr int64_t min_tiles() { return sizeof(T) == 1 ? 480 : kMinTiles; }
-// Arrays of at least kWideBytes take a wider shape: Float32 and the 8-byte
+template <class T> constexpr int kMinTier = sizeof(T) == 1 ? 0 : 1;
+// Arrays of at least kWideBytes take a wider shape: the 4- and 8-byte
 // types 768 threads x 8 vectors (96 KiB); UInt8 (from kU8WideBytes) 512
 // threads x 12 vectors (96 KiB), and from kHugeBytes on 512 x 16 (128 KiB). The UInt8 shapes
 // halve or third the lookbacks per byte and still fit two workgroups per
@@ -99,7 +99,9 @@ constexpr int64_t kHugeBytes = 1LL << 30;
 constexpr int64_t kU8WideBytes = 1LL << 28;
 constexpr int kTierWide = kTiers;      // tier index of the wide shape
 constexpr int kTierHuge = kTiers + 1;  // UInt8 from kHugeBytes
-template <class T> constexpr bool has_wide_tier() { return __is_same(T, float) || sizeof(T) == 8 || sizeof(T) == 1; }
+template <class T> constexpr bool has_wide_tier() {
+  return sizeof(T) == 4 || sizeof(T) == 8 || sizeof(T) == 1;
+}
 template <class T> constexpr bool has_huge_tier() { return sizeof(T) == 1; }
 // (Float32 and the 8-byte types measured 0.5-10 % slower at 512 x 12 or 16.)
 constexpr int kWideBlockF32 = 768, kWideVF32 = 8, kWideBlock8 = 768, kWideV8 = 8;
@@ -118,16 +120,22 @@ constexpr size_t kScanHeaderBytes = 256;
 constexpr int kDescWords = 16;             // 128 bytes per tile descriptor
 constexpr uint32_t kSpinLimit = 1u << 24;  // lookback polls before giving up (seconds)
 // Predecessors polled per lookback round (lanes 64-win..63). Each
-// descriptor is its own 128-byte line, and a poll completes only when its
+// descriptor is its own 128-byte line and a poll completes only when its
 // slowest line returns, while in the steady state of a long scan (more
-// tiles than fit on the GPU at once) the nearest predecessors already hold
-// PREFIX: there 4 lines per poll measured best (2^28 Float32 338 us; 2:
-// 351, 8: 346, 16: 363, 32: 376, 64: ~370; widening the window as the walk
-// moves back only lost). When every tile is resident at once they all
+// tiles than fit on the GPU at once) the nearest predecessors mostly hold
+// PREFIX already: the larger the tile, the fewer lines a poll needs.
+// Measured with tiles numbered by workgroup id: 96 KiB tiles 4 (2^28
+// Float32 320 us; 2: 330, 8: 333); 128 KiB tiles over 4+ generations 2
+// (Float32 10^8 126.7 vs 129.6 us at 4); tiles of 64 KiB or less 8 (UInt8
+// 10^8 40.9 vs 41.7 us). When every tile is resident at once they all
 // publish PARTIAL together and walk back towards tile 0, and the full
-// 64-tile window is faster (10^7 UInt8, 611 tiles on 768 slots: 18.3 vs
-// 20.6 us; 3*10^7 Float32, 916 tiles on 512 slots: 49.5 vs 53.5 us at 4).
-inline int look_window(int64_t ntiles, int64_t resident) { return ntiles > resident ? 4 : kWave; }
+// 64-tile window is faster.
+inline int look_window(int64_t ntiles, int64_t resident, int64_t tile_bytes) {
+  if (ntiles <= resident) return kWave;
+  if (tile_bytes >= (128 << 10) && ntiles > 4 * resident) return 2;
+  if (tile_bytes <= (64 << 10)) return 8;
+  return 4;
+}
 
 // The unit a lane loads and stores: 16 bytes, or one element of a wider
 // type (a 32-byte QuaternionF64 moves as two 16-byte halves).
@@ -522,7 +530,7 @@ template <class T> int scan_tier(int64_t n) {
   if (has_huge_tier<T>() && bytes >= kHugeBytes) return kTierHuge;
   if (has_wide_tier<T>() && bytes >= (sizeof(T) == 1 ? kU8WideBytes : kWideBytes)) return kTierWide;
   int t = max_tier<T>();
-  while (t > 0 && bytes < min_tiles<T>() * (int64_t)scan_block<T>(t) * kTierV[t] * kVecBytes<T>) --t;
+  while (t > kMinTier<T> && bytes < min_tiles<T>() * (int64_t)scan_block<T>(t) * kTierV[t] * kVecBytes<T>) --t;
   return t;
 }
 
@@ -563,11 +571,11 @@ void launch_scan_tier(const void* src, int64_t ss, void* dst, int64_t ds, int64_
   if (mode & 1) {
     constexpr auto kernel = scan_kernel<T, Op, Map, true, B, V>;
     hipLaunchKernelGGL(kernel, dim3((unsigned)ntiles), dim3(B), 0, stream, (const T*)src, ss, (T*)dst, ds, n,
-                       ntiles, (uint64_t*)scratch, vec, off, look_window(ntiles, resident_tiles<kernel>(B)), post);
+                       ntiles, (uint64_t*)scratch, vec, off, look_window(ntiles, resident_tiles<kernel>(B), (int64_t)B * V * kVecBytes<T>), post);
   } else {
     constexpr auto kernel = scan_kernel<T, Op, Map, false, B, V>;
     hipLaunchKernelGGL(kernel, dim3((unsigned)ntiles), dim3(B), 0, stream, (const T*)src, ss, (T*)dst, ds, n,
-                       ntiles, (uint64_t*)scratch, vec, off, look_window(ntiles, resident_tiles<kernel>(B)), post);
+                       ntiles, (uint64_t*)scratch, vec, off, look_window(ntiles, resident_tiles<kernel>(B), (int64_t)B * V * kVecBytes<T>), post);
   }
 }
 

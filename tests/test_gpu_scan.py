@@ -294,20 +294,23 @@ def test_views_offsets_strides_inplace(kf, oracle, dev):
 
 @pytest.mark.parametrize("dt", [np.float32, np.float64, np.int32, np.int64, np.uint8])
 def test_tile_size_switchover(kf, oracle, dev, dt):
-    # tiles are 1024 threads (512 for uint8; 768 for float32 and 8-byte
-    # types from 512 MiB on; uint8's own 12- and 16-vector shapes from 256
-    # MiB and 1 GiB are checked in test_gpu_large.py) x V 16-byte vectors,
-    # V in (1, 2, 4, 8): the
-    # largest V that still makes >= 120 tiles (480 for uint8); with more
-    # tiles than fit on the GPU at once the lookback polls 4 tiles per
-    # round, else 64. Check both sides of every switch (floats: sparse 0/1
-    # values, so every partial sum is an integer and exact in any order).
+    # tiles are 1024 threads (512 for uint8; 768 for 4- and 8-byte types
+    # from 512 MiB on; uint8's own 12- and 16-vector shapes from 256 MiB and
+    # 1 GiB are checked in test_gpu_large.py) x V 16-byte vectors, V in
+    # (1, 2, 4, 8): the largest V that still makes >= 240 tiles (480 for
+    # uint8), never below 2 except for uint8. The lookback polls 64 tiles
+    # while every tile is resident, else 2, 4 or 8 by tile size (2 for
+    # 128 KiB tiles from 4 generations on). Check both sides of every switch
+    # (floats: sparse 0/1 values, so every partial sum is an integer and
+    # exact in any order).
     epv = 16 // np.dtype(dt).itemsize
     block = {np.uint8: 512}.get(dt, 1024)
-    min_tiles = 480 if dt == np.uint8 else 120
+    min_tiles = 480 if dt == np.uint8 else 240
     rng = np.random.default_rng(23)
     edges = [min_tiles * block * v * epv for v in (2, 4, 8)] + [512 * block * 8 * epv]
-    if dt in (np.float32, np.float64, np.int64):
+    if dt != np.uint8:
+        edges.append(4 * 512 * block * 8 * epv)        # window 2 from 4 generations of 128 KiB tiles
+    if dt in (np.float32, np.float64, np.int32, np.int64):
         edges.append(2**29 // np.dtype(dt).itemsize)   # 768-thread tiles from 512 MiB on
     for e in edges:
         for n in (e - 1, e, e + 1):
