@@ -130,8 +130,17 @@ constexpr uint32_t kSpinLimit = 1u << 24;  // lookback polls before giving up (s
 // 10^8 40.9 vs 41.7 us). When every tile is resident at once they all
 // publish PARTIAL together and walk back towards tile 0, and the full
 // 64-tile window is faster.
-inline int look_window(int64_t ntiles, int64_t resident, int64_t tile_bytes) {
-  if (ntiles <= resident) return kWave;
+// Grids of at most kWave * kAllChunk + 1 tiles, all resident at once, read
+// every predecessor in one poll round (lookback_all, window code 0) instead
+// of walking back one 64-tile window per round: Float32 10^6 6.09 -> 5.72
+// us, 2*10^6 7.03 -> 6.70 us, 2^21 6.90 -> 6.53 us, affine 2^22 13.6 ->
+// 13.2 us. Only for types of up to 4 bytes: the 8-byte types lost 1-3 %
+// from the extra registers (Float64 10^6 8.41 -> 8.70 us), and a chunk of
+// 8 lost 5 % at 10^7 Float32.
+constexpr int kAllChunk = 4;
+template <class T> constexpr bool kLookAllFor = sizeof(T) <= 4;
+inline int look_window(int64_t ntiles, int64_t resident, int64_t tile_bytes, bool look_all) {
+  if (ntiles <= resident) return look_all && ntiles <= (int64_t)kWave * kAllChunk + 1 ? 0 : kWave;
   if (tile_bytes >= (128 << 10) && ntiles > 4 * resident) return 2;
   if (tile_bytes <= (64 << 10)) return 8;
   return 4;
@@ -225,6 +234,73 @@ __device__ inline T lookback(const uint64_t* desc, int64_t tile, uint32_t epoch3
     }
     __builtin_amdgcn_s_sleep(1);
   }
+}
+
+// Lookback when every tile of the grid is resident at once: lane L reads
+// the descriptors of its contiguous chunk [L*c, L*c + c) of all `tile`
+// predecessors (c <= CH) with every load in flight together, folds them in
+// tile order (restarting at a PREFIX), and an ordered wave reduction from
+// the newest lane holding a PREFIX gives the exclusive prefix; a lane
+// whose chunk still holds an unpublished descriptor re-reads it.
+template <class T, class Op, int CH>
+__device__ inline T lookback_all(const uint64_t* desc, int64_t tile, uint32_t epoch30) {
+  constexpr int W = ScanShape<T>::W;
+  const int lane = lane_id();
+  const T id = Op::template identity<T>();
+  const int64_t c = (tile + kWave - 1) / kWave;
+  const int64_t t0 = (int64_t)lane * c;
+  const int cnt = (int)kmax<int64_t>(0, kmin<int64_t>(c, tile - t0));
+  T val = id;
+  bool has_prefix = false;
+  bool done = cnt == 0;
+  for (uint32_t polls = 0;; ++polls) {
+    if (polls == kSpinLimit) {
+      __hip_atomic_fetch_or(const_cast<uint64_t*>(desc) - kScanHeaderBytes / sizeof(uint64_t) + 1,
+                            (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      break;
+    }
+    if (!done) {
+      uint64_t d[CH][W];
+#pragma unroll
+      for (int k = 0; k < CH; ++k)
+        if (k < cnt) {
+#pragma unroll
+          for (int i = 0; i < W; ++i) d[k][i] = ld_agent(desc + (t0 + k) * kDescWords + i);
+        }
+      bool ok = true;
+      T run = id;
+      bool pre = false;
+#pragma unroll
+      for (int k = 0; k < CH; ++k)
+        if (k < cnt) {
+          const uint32_t tag = (uint32_t)(d[k][0] >> 32);
+          bool good = (tag >> 2) == epoch30 && (tag & 3u) != 0;
+#pragma unroll
+          for (int i = 1; i < W; ++i) good &= (uint32_t)(d[k][i] >> 32) == tag;
+          ok &= good;
+          Words<T> w;
+#pragma unroll
+          for (int i = 0; i < W; ++i) w.w[i] = (uint32_t)d[k][i];
+          const T v = from_words<T>(w);
+          if ((tag & 3u) == kStatePrefix) {
+            run = v;
+            pre = true;
+          } else {
+            run = Op::combine(run, v);
+          }
+        }
+      if (ok) {
+        val = run;
+        has_prefix = pre;
+        done = true;
+      }
+    }
+    if (__builtin_amdgcn_ballot_w64(!done) == 0) break;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  const uint64_t pm = __builtin_amdgcn_ballot_w64(has_prefix);
+  const int m = pm ? 63 - __builtin_clzll(pm) : 0;
+  return wave_reduce<Op>(lane >= m ? val : id);
 }
 
 // Byte-wise a + b (mod 256 in every byte) of four packed bytes.
@@ -451,7 +527,10 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
       if (lane == 0) publish(desc, tile, (epoch30 << 2) | kStatePrefix, agg);
     } else {
       if (lane == 0) publish(desc, tile, (epoch30 << 2) | kStatePartial, agg);
-      excl = lookback<T, Op>(desc, tile, epoch30, win);
+      if constexpr (kLookAllFor<T>)
+        excl = win == 0 ? lookback_all<T, Op, kAllChunk>(desc, tile, epoch30) : lookback<T, Op>(desc, tile, epoch30, win);
+      else
+        excl = lookback<T, Op>(desc, tile, epoch30, win);
       if (lane == 0) publish(desc, tile, (epoch30 << 2) | kStatePrefix, Op::combine(excl, agg));
     }
     if (lane == 0 && tile == ntiles - 1) st_agent(scratch, ((tk >> 32) + 1) << 32);  // next call's epoch
@@ -571,11 +650,11 @@ void launch_scan_tier(const void* src, int64_t ss, void* dst, int64_t ds, int64_
   if (mode & 1) {
     constexpr auto kernel = scan_kernel<T, Op, Map, true, B, V>;
     hipLaunchKernelGGL(kernel, dim3((unsigned)ntiles), dim3(B), 0, stream, (const T*)src, ss, (T*)dst, ds, n,
-                       ntiles, (uint64_t*)scratch, vec, off, look_window(ntiles, resident_tiles<kernel>(B), (int64_t)B * V * kVecBytes<T>), post);
+                       ntiles, (uint64_t*)scratch, vec, off, look_window(ntiles, resident_tiles<kernel>(B), (int64_t)B * V * kVecBytes<T>, kLookAllFor<T>), post);
   } else {
     constexpr auto kernel = scan_kernel<T, Op, Map, false, B, V>;
     hipLaunchKernelGGL(kernel, dim3((unsigned)ntiles), dim3(B), 0, stream, (const T*)src, ss, (T*)dst, ds, n,
-                       ntiles, (uint64_t*)scratch, vec, off, look_window(ntiles, resident_tiles<kernel>(B), (int64_t)B * V * kVecBytes<T>), post);
+                       ntiles, (uint64_t*)scratch, vec, off, look_window(ntiles, resident_tiles<kernel>(B), (int64_t)B * V * kVecBytes<T>, kLookAllFor<T>), post);
   }
 }
 
