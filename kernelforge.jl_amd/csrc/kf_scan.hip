@@ -8,9 +8,9 @@
 // design differs from the reference in these ways:
 //
 //  * Large tiles: 8 16-byte vectors per lane x 1024 threads = 128 KiB (768
-//    threads = 96 KiB for Float32 and 8-byte types from 512 MiB on; 512
-//    threads = 64 KiB for UInt8; 1, 2 or 4 vectors per lane for arrays too
-//    small to make 120 such tiles), so 2^28 Float32 is 10923 tiles and the
+//    threads = 96 KiB for 4- and 8-byte types from 512 MiB on; 512 threads
+//    x 8/12/16 vectors for UInt8; 2 or 4 vectors per lane for arrays too
+//    small to make 240 such tiles), so 2^28 Float32 is 10923 tiles and the
 //    per-tile lookback is amortised over a large streaming body. The tile
 //    stays in registers in "striped" order: lane l of wave w holds vector
 //    j*64 + l of the wave's contiguous chunk, so every load and store is a
@@ -23,7 +23,8 @@
 //  * The lookback window lives in the top lanes of one wave: lane j reads
 //    the descriptor of tile (t - 64 + j) for the last `win` lanes, so
 //    lane order is tile order and a DPP scan combines the window in the
-//    order a non-commutative op needs.
+//    order a non-commutative op needs (lookback_all, for fully resident
+//    grids, gives each lane a contiguous chunk of predecessors instead).
 //  * Each tile descriptor owns a 128-byte line (kDescWords words): tiles are
 //    published from different XCDs, and packing several descriptors per line
 //    made those writers and the pollers contend for one line (measured: 5.0
