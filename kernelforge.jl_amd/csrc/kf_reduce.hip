@@ -572,9 +572,20 @@ constexpr int kDimBlock = 256;
 constexpr int kDimWaves = kDimBlock / kWave;
 constexpr int kDimUnroll = 4;
 constexpr int kDimMaxSplit = 64;
-constexpr int kRowVecsDefault = 2;    // dim 2: 16-byte vectors per thread per column
-constexpr int kColUnrollDefault = 8;  // dim 2: columns in flight per thread
+constexpr int kRowVecsDefault = 2;    // dim 2, unaligned path: elements per thread per column / 1
+constexpr int kColUnrollDefault = 8;  // dim 2, unaligned path: columns per pass
 constexpr int kDim2Blocks = 256;      // dim 2: target workgroups (one per CU)
+// dim 2, aligned path: the widest strip (16-byte vectors per thread per
+// column) that still gives kDim2Blocks workgroups; columns in flight per
+// thread for each strip width.
+constexpr int kDim2MaxRowVecs = 8;
+constexpr int kColUnrollRv1 = 16;
+constexpr int kColUnrollRv2 = 8;
+constexpr int kColUnrollRv4 = 4;
+constexpr int kColUnrollRv8 = 4;
+constexpr int col_unroll_for(int rv) {
+  return rv == 1 ? kColUnrollRv1 : rv == 2 ? kColUnrollRv2 : rv == 4 ? kColUnrollRv4 : kColUnrollRv8;
+}
 
 template <class T, class Op, class F>
 __global__ __launch_bounds__(kDimBlock) void reduce_cols_kernel(
@@ -645,11 +656,11 @@ __global__ __launch_bounds__(kDimBlock) void reduce_cols_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// dim = 2: a workgroup owns a strip of 256*kRowVecs*EPV rows (8 KiB of each
-// column; thread t holds vectors t, t+256, ... of the strip) and a range of
-// columns, which it walks kColUnroll at a time, so every load is part of a
-// 8 KiB contiguous run. Strips are split over S column ranges whose
-// partials stage 2 combines.
+// dim = 2: a workgroup owns a strip of 256*kRowVecs*EPV rows (4-32 KiB of
+// each column; thread t holds vectors t, t+256, ... of the strip) and a range
+// of columns, which it walks kColUnroll at a time, so every load is part of a
+// contiguous run of the strip's width. Strips are split over S column ranges
+// whose partials stage 2 combines.
 // ---------------------------------------------------------------------------
 template <class T, class Op, class F, bool VEC, int kRowVecs = kRowVecsDefault, int kColUnroll = kColUnrollDefault>
 __global__ __launch_bounds__(kDimBlock) void reduce_rows_kernel(
@@ -729,6 +740,7 @@ __global__ __launch_bounds__(kDimBlock) void reduce_rows_kernel(
 struct DimPlan {
   int64_t groups;  // column groups (dim 1) or row strips (dim 2)
   int split;       // S workgroups cooperating on one group
+  int row_vecs;    // dim 2: strip width in vectors (elements on the unaligned path) per thread
   size_t partial_bytes;
 };
 
@@ -751,15 +763,31 @@ inline DimPlan plan_dim(size_t es, int64_t rows, int64_t cols, int dim, bool vec
     }
     p.split = (int)S;
   } else {
-    const int64_t rs = (int64_t)kDimBlock * kRowVecsDefault * epv;
+    // Aligned path: the widest strip that still leaves one workgroup per
+    // CU, so each workgroup streams the longest contiguous runs; with too
+    // few rows even for 1-vector strips, columns are split instead.
+    // Float32: 4M x 64 6.8 TB/s at 8 vectors (512 workgroups) against 5.7
+    // at 2; 1M x 256 7.1 at 4 against 5.6 at 2; 65536 x 4096 6.8 at 1 (S = 4)
+    // against 6.6 at 2 (S = 8) and 6.1 at 4 (S = 16).
+    int rv = kRowVecsDefault;
+    if (vec) {
+      rv = 1;
+      for (int c = kDim2MaxRowVecs; c > 1; c /= 2) {
+        const int64_t rsc = (int64_t)kDimBlock * c * epv;
+        if ((rows + rsc - 1) / rsc * nb >= kDim2Blocks) {
+          rv = c;
+          break;
+        }
+      }
+    }
+    p.row_vecs = rv;
+    const int cu = vec ? col_unroll_for(rv) : kColUnrollDefault;
+    const int64_t rs = (int64_t)kDimBlock * rv * epv;
     p.groups = (rows + rs - 1) / rs;
-    // Few workgroups with 16 loads in flight per thread beat many
-    // workgroups with more split partials (65536 x 4096 Float32: 6.6 TB/s at
-    // 256 workgroups, 5.4 TB/s at 1024 with 4 loads per thread).
     int64_t S = 1;
     if (p.groups * nb < kDim2Blocks) {
       S = (kDim2Blocks + p.groups * nb - 1) / (p.groups * nb);
-      S = kmin<int64_t>(S, kmax<int64_t>(cols / (2 * kColUnrollDefault), 1));
+      S = kmin<int64_t>(S, kmax<int64_t>(cols / (2 * cu), 1));
       S = kmin<int64_t>(S, 256);
     }
     p.split = (int)S;
@@ -801,16 +829,24 @@ int launch_reduce_dim(const void* A, int64_t rows, int64_t cols, int64_t cs, int
     T* dz = (T*)dst + z0 * dst_bstride;
     T* out = p.split > 1 ? (T*)scratch : dz;
     const dim3 grid((unsigned)p.groups, p.split, nz);
-    if (vec)
-      hipLaunchKernelGGL((reduce_rows_kernel<T, Op, F, true>), grid, dim3(kDimBlock), 0, stream, Az, rows, cols, cs,
-                         out, ds, seg, a_bstride, dst_bstride, (const T*)x, xs);
-    else
+#define KF_ROWS_VEC(RV)                                                                                  \
+  hipLaunchKernelGGL((reduce_rows_kernel<T, Op, F, true, RV, col_unroll_for(RV)>), grid, dim3(kDimBlock), 0, stream, \
+                     Az, rows, cols, cs, out, ds, seg, a_bstride, dst_bstride, (const T*)x, xs)
+    if (vec) {
+      switch (p.row_vecs) {
+        case 1: KF_ROWS_VEC(1); break;
+        case 2: KF_ROWS_VEC(2); break;
+        case 4: KF_ROWS_VEC(4); break;
+        default: KF_ROWS_VEC(8); break;
+      }
+    } else
       hipLaunchKernelGGL((reduce_rows_kernel<T, Op, F, false>), grid, dim3(kDimBlock), 0, stream, Az, rows, cols,
                          cs, out, ds, seg, a_bstride, dst_bstride, (const T*)x, xs);
     if (p.split > 1)
       hipLaunchKernelGGL((combine_split_kernel<T, Op>), dim3((unsigned)((rows + kRedBlock - 1) / kRedBlock), nz),
                          dim3(kRedBlock), 0, stream, (const T*)scratch, p.split, rows, dz, ds, dst_bstride);
   }
+#undef KF_ROWS_VEC
   return kf_check_launch("reduce_rows_kernel");
 }
 

@@ -177,6 +177,31 @@ def test_dims_2d(kf, oracle, dev, dt, shape, view):
                 assert np.array_equal(g, ref), (dim, op, f)
 
 
+@pytest.mark.parametrize("dt", [np.int32, np.int64, np.uint8])
+@pytest.mark.parametrize("shape", [
+    (2_100_000, 5),        # 4-byte: 8-vector strips, 257 of them; column tail
+    (1_048_580, 9),        # 4-byte: 4-vector strips, the last one ragged
+    (1_000_003, 6),        # 4-byte: 2-vector strips, fewer columns than one pass
+    (300_000, 37),         # 1-vector strips, no split
+    (70_000, 300),         # 1-vector strips split over column ranges
+    (8197, 11, 130),       # batched: 8-vector strips reached through the batch count
+])
+def test_dims2_strip_widths(kf, dev, dt, shape):
+    # The dims=2 launch picks its strip width (16-byte vectors per thread per
+    # column) from rows x batch; these shapes reach every width for each
+    # element size, with ragged last strips and column tails. Exact: integer
+    # sums wrap in the element type, max is order-free.
+    rng = np.random.default_rng(sum(shape))
+    hi = 256 if dt == np.uint8 else 1 << 20
+    a = rng.integers(0, hi, shape[::-1]).astype(dt)            # C order == Julia column-major shape
+    x = torch.from_numpy(a).to(dev).permute(*reversed(range(len(shape))))
+    xn = x.cpu().numpy()
+    for op in ("+", "max"):
+        got = kf.mapreduce(kf.identity, op, x, dims=2).cpu().numpy()
+        ref = xn.sum(axis=1, keepdims=True, dtype=dt) if op == "+" else xn.max(axis=1, keepdims=True)
+        assert got.shape == ref.shape and np.array_equal(got, ref), (shape, op)
+
+
 def test_dims_golden(kf, dev, golden):
     for c in golden["reduce_dim"]:
         buf = dec(c["buf"], np.float64)
