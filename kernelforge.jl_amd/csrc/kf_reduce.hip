@@ -571,7 +571,8 @@ template <class Map> struct Unary {
 constexpr int kDimBlock = 256;
 constexpr int kDimWaves = kDimBlock / kWave;
 constexpr int kDimUnroll = 4;
-constexpr int kDimMaxSplit = 64;
+constexpr int kDimMaxSplit = 64;          // dim 1 splits combined by combine_split_kernel
+constexpr int kDimMaxSplitNarrow = 4096;  // dim 1 splits combined by reduce_rows_narrow_kernel
 constexpr int kRowVecsDefault = 2;    // dim 2, unaligned path: elements per thread per column / 1
 constexpr int kColUnrollDefault = 8;  // dim 2, unaligned path: columns per pass
 constexpr int kDim2Blocks = 256;      // dim 2: target workgroups (one per CU)
@@ -595,9 +596,9 @@ __global__ __launch_bounds__(kDimBlock) void reduce_cols_kernel(
   const T id = Op::template identity<T>();
   const int lane = lane_id();
   const int wave = threadIdx.x / kWave;
-  const int64_t col = (int64_t)blockIdx.x * kDimWaves + wave;
   const int s = blockIdx.y;
-  if (col >= cols) return;  // whole wave leaves together
+  // grid-stride over blocks of kDimWaves columns (the grid is capped)
+  for (int64_t col = (int64_t)blockIdx.x * kDimWaves + wave; col < cols; col += (int64_t)gridDim.x * kDimWaves) {
   T acc = id;
   const T* c = A + col * col_stride;
   const int64_t r0 = (int64_t)s * seg_rows;
@@ -653,6 +654,109 @@ __global__ __launch_bounds__(kDimBlock) void reduce_cols_kernel(
   acc = wave_reduce<Op>(acc);
   // S == 1: out is dst; otherwise out is partials[s*cols + col]
   if (lane == 0) out[gridDim.y == 1 ? col * out_stride : (int64_t)s * cols + col] = acc;
+  }
+}
+
+// Combine of x over aligned groups of L lanes (L a power of two <= 64),
+// lower lanes on the left; the result is valid in each group's first lane.
+template <class T> __device__ inline T shfl_xor_t(T v, int m) {
+  Words<T> w = to_words(v), r;
+#pragma unroll
+  for (int i = 0; i < Words<T>::W; ++i) r.w[i] = (uint32_t)__shfl_xor((int)w.w[i], m, kWave);
+  return from_words<T>(r);
+}
+template <class Op, int L, class T> __device__ inline T group_reduce(T x) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int m = 1; m < L; m <<= 1) {
+    const T y = shfl_xor_t(x, m);
+    x = (lane & m) ? Op::combine(y, x) : Op::combine(x, y);
+  }
+  return x;
+}
+
+// dim = 1, short columns: L lanes per column (kDimBlock / L columns per
+// workgroup pass), each lane combining units j, j+L, ... of its column
+// (16-byte vectors when VEC: rows % EPV == 0 and aligned columns; elements
+// otherwise), then a combine over the L lanes. Grid-stride over column
+// blocks, so any column count fits one capped grid.
+constexpr int kSegUnits = 4;      // target units per lane
+constexpr int kSegMaxBlocks = 8192;
+template <class T, class Op, class F, bool VEC, int L>
+__global__ __launch_bounds__(kDimBlock) void reduce_cols_seg_kernel(const T* A, int64_t rows, int64_t cols,
+                                                                    int64_t col_stride, T* out, int64_t out_stride,
+                                                                    const T* xv, int64_t xs) {
+  constexpr int EPV = VEC ? 16 / (int)sizeof(T) : 1;
+  constexpr int CPB = kDimBlock / L;
+  constexpr int U = kSegUnits;
+  const T id = Op::template identity<T>();
+  const int j = threadIdx.x % L;
+  const int64_t nu = rows / EPV;  // VEC: rows % EPV == 0
+  for (int64_t cb = (int64_t)blockIdx.x * CPB; cb < cols; cb += (int64_t)gridDim.x * CPB) {
+    const int64_t col = cb + threadIdx.x / L;
+    T acc = id;
+    if (col < cols) {
+      const T* c = A + col * col_stride;
+      T a[EPV];
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) a[e] = id;
+      int64_t i = j;
+      for (; i + (U - 1) * L < nu; i += U * L) {
+        if constexpr (VEC) {
+          uint4 r[U], rx[U];
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            r[u] = ld_stream(reinterpret_cast<const uint4*>(c) + i + u * L);
+            if constexpr (F::kHasX) rx[u] = reinterpret_cast<const uint4*>(xv)[i + u * L];
+          }
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            T x[EPV], w[EPV];
+            __builtin_memcpy(x, &r[u], 16);
+            if constexpr (F::kHasX) __builtin_memcpy(w, &rx[u], 16);
+#pragma unroll
+            for (int e = 0; e < EPV; ++e) a[e] = Op::combine(a[e], F::apply(x[e], F::kHasX ? w[e] : x[e]));
+          }
+        } else {
+          T x[U], w[U];
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            x[u] = c[i + u * L];
+            if constexpr (sizeof(T) == 1) {
+              // one byte per register: keeps adjacent byte loads from being
+              // fused into a sub-dword vector the backend cannot split
+              uint32_t b = x[u];
+              __asm__ volatile("" : "+v"(b));
+              x[u] = (T)b;
+            }
+            w[u] = F::kHasX ? xv[(i + u * L) * xs] : x[u];
+          }
+#pragma unroll
+          for (int u = 0; u < U; ++u) a[0] = Op::combine(a[0], F::apply(x[u], w[u]));
+        }
+      }
+      for (; i < nu; i += L) {
+        if constexpr (VEC) {
+          const uint4 r = ld_stream(reinterpret_cast<const uint4*>(c) + i);
+          T x[EPV], w[EPV];
+          __builtin_memcpy(x, &r, 16);
+          if constexpr (F::kHasX) {
+            const uint4 q = reinterpret_cast<const uint4*>(xv)[i];
+            __builtin_memcpy(w, &q, 16);
+          }
+#pragma unroll
+          for (int e = 0; e < EPV; ++e) a[e] = Op::combine(a[e], F::apply(x[e], F::kHasX ? w[e] : x[e]));
+        } else {
+          a[0] = Op::combine(a[0], F::apply(c[i], F::kHasX ? xv[i * xs] : c[i]));
+        }
+      }
+      acc = a[0];
+#pragma unroll
+      for (int e = 1; e < EPV; ++e) acc = Op::combine(acc, a[e]);
+    }
+    acc = group_reduce<Op, L>(acc);
+    if (j == 0 && col < cols) out[col * out_stride] = acc;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -737,10 +841,97 @@ __global__ __launch_bounds__(kDimBlock) void reduce_rows_kernel(
 }
 
 
+// dim = 2, narrow matrices (at most kDimBlock row units: 16-byte vectors
+// when VEC, i.e. rows % EPV == 0 and aligned columns, else elements): the
+// workgroup is split into P = kDimBlock / units column phases; thread
+// (unit, phase) walks columns phase, phase + P, ... of its column range, kNarrowUnroll
+// loads in flight, and the phases are combined in order through LDS. Also
+// the second stage of split reductions: the S partial columns are a
+// rows x S matrix reduced along dim 2 the same way.
+constexpr int kNarrowUnroll = 8;
+constexpr int kNarrowBlocks = 512;  // target workgroups over batch x column ranges
+template <class T, class Op, class F, bool VEC>
+__global__ __launch_bounds__(kDimBlock) void reduce_rows_narrow_kernel(
+    const T* A, int64_t rows, int64_t cols, int64_t col_stride, T* out, int64_t out_stride, int64_t seg_cols,
+    int64_t a_bstride, int64_t out_bstride, const T* xv, int64_t xs) {
+  constexpr int EPV = VEC ? 16 / (int)sizeof(T) : 1;
+  constexpr int U = kNarrowUnroll;
+  __shared__ T s_acc[kDimBlock * EPV];
+  A += (int64_t)blockIdx.z * a_bstride;
+  out += gridDim.y == 1 ? (int64_t)blockIdx.z * out_bstride : (int64_t)blockIdx.z * gridDim.y * rows;
+  const T id = Op::template identity<T>();
+  const int nunits = (int)(rows / EPV);  // <= kDimBlock (host-checked)
+  const int P = kDimBlock / nunits;
+  const int t = threadIdx.x;
+  const int unit = t % nunits, ph = t / nunits;
+  const int64_t c0 = (int64_t)blockIdx.y * seg_cols;
+  const int64_t c1 = kmin<int64_t>(cols, c0 + seg_cols);
+  T a[EPV];
+#pragma unroll
+  for (int e = 0; e < EPV; ++e) a[e] = id;
+  if (ph < P) {
+    const T* p = A + (int64_t)unit * EPV;
+    int64_t c = c0 + ph;
+    for (; c + (int64_t)(U - 1) * P < c1; c += (int64_t)U * P) {
+      if constexpr (VEC) {
+        uint4 r[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) r[u] = ld_stream(reinterpret_cast<const uint4*>(p + (c + (int64_t)u * P) * col_stride));
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const T w = F::kHasX ? xv[(c + (int64_t)u * P) * xs] : id;
+          T x[EPV];
+          __builtin_memcpy(x, &r[u], 16);
+#pragma unroll
+          for (int e = 0; e < EPV; ++e) a[e] = Op::combine(a[e], F::apply(x[e], w));
+        }
+      } else {
+        T x[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) x[u] = p[(c + (int64_t)u * P) * col_stride];
+#pragma unroll
+        for (int u = 0; u < U; ++u) a[0] = Op::combine(a[0], F::apply(x[u], F::kHasX ? xv[(c + (int64_t)u * P) * xs] : id));
+      }
+    }
+    for (; c < c1; c += P) {
+      const T w = F::kHasX ? xv[c * xs] : id;
+      if constexpr (VEC) {
+        const uint4 r = ld_stream(reinterpret_cast<const uint4*>(p + c * col_stride));
+        T x[EPV];
+        __builtin_memcpy(x, &r, 16);
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) a[e] = Op::combine(a[e], F::apply(x[e], w));
+      } else {
+        a[0] = Op::combine(a[0], F::apply(p[c * col_stride], w));
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) s_acc[t * EPV + e] = a[e];
+  }
+  __syncthreads();
+  if (t < nunits) {
+    // phases in column order: phase q holds columns q, q + P, ...; every op
+    // here is commutative, and phase order keeps the combine deterministic
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) a[e] = s_acc[t * EPV + e];
+    for (int q = 1; q < P; ++q)
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) a[e] = Op::combine(a[e], s_acc[(q * nunits + t) * EPV + e]);
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) {
+      const int64_t r = (int64_t)t * EPV + e;
+      out[gridDim.y == 1 ? r * out_stride : (int64_t)blockIdx.y * rows + r] = a[e];
+    }
+  }
+}
+
 struct DimPlan {
   int64_t groups;  // column groups (dim 1) or row strips (dim 2)
   int split;       // S workgroups cooperating on one group
   int row_vecs;    // dim 2: strip width in vectors (elements on the unaligned path) per thread
+  int seg_lanes;   // dim 1: lanes per column of reduce_cols_seg_kernel (0: one wave per column)
+  bool narrow;     // dim 2: reduce_rows_narrow_kernel
+  bool unit_vec;   // seg / narrow kernels: 16-byte units (rows % EPV == 0, aligned columns)
   size_t partial_bytes;
 };
 
@@ -748,20 +939,54 @@ struct DimPlan {
 // the scratch query and the launch agree.
 constexpr int64_t kMaxBatchPerLaunch = 65535;  // grid.z limit
 
+// Row units of an m-row operand for the seg / narrow kernels: 16-byte
+// vectors when m is a multiple of the vector width (and the columns are
+// aligned), else elements.
+inline int64_t row_units(size_t es, int64_t m, bool aligned) {
+  const int64_t ev = (int64_t)(16 / es);
+  return aligned && m % ev == 0 ? m / ev : m;
+}
+constexpr int64_t kColsMaxBlocks = 65536;  // wave-per-column grid cap (grid-stride beyond)
+
 inline DimPlan plan_dim(size_t es, int64_t rows, int64_t cols, int dim, bool vec, int64_t batch = 1) {
   const int64_t nb = kmin<int64_t>(kmax<int64_t>(batch, 1), kMaxBatchPerLaunch);
   DimPlan p{};
   const int epv = vec ? (int)(16 / es) : 1;
   if (dim == 1) {
-    p.groups = (cols + kDimWaves - 1) / kDimWaves;
-    int64_t S = 1;
-    if (cols < 16384) {
-      S = (16384 + cols - 1) / cols;
-      const int64_t by_rows = rows / ((int64_t)kWave * 4 * kDimUnroll * 4);  // >= 4 unrolled passes each
-      S = kmin<int64_t>(S, kmax<int64_t>(by_rows, 1));
-      S = kmin<int64_t>(S, kDimMaxSplit);
+    // Short columns: L lanes per column with about kSegUnits units each.
+    const int64_t nu = row_units(es, rows, vec);
+    int L = 1;
+    while (L < kWave && (int64_t)L * kSegUnits < nu) L <<= 1;
+    if (L < kWave) {
+      p.seg_lanes = L;
+      p.unit_vec = vec && nu != rows;
+      p.groups = kmin<int64_t>((cols + kDimBlock / L - 1) / (kDimBlock / L), kSegMaxBlocks);
+      p.split = 1;
+    } else {
+      p.groups = kmin<int64_t>((cols + kDimWaves - 1) / kDimWaves, kColsMaxBlocks);
+      int64_t S = 1;
+      if (cols < 16384) {
+        // The split partials are a cols x S matrix; when it is narrow its
+        // combine is reduce_rows_narrow_kernel and S may be large (few long
+        // columns), else the serial combine_split_kernel keeps S small.
+        const bool narrow2 = row_units(es, cols, true) <= kDimBlock;
+        S = (16384 + cols - 1) / cols;
+        const int64_t by_rows = rows / ((int64_t)kWave * 4 * kDimUnroll * 4);  // >= 4 unrolled passes each
+        S = kmin<int64_t>(S, kmax<int64_t>(by_rows, 1));
+        S = kmin<int64_t>(S, narrow2 ? kDimMaxSplitNarrow : kDimMaxSplit);
+      }
+      p.split = (int)S;
     }
-    p.split = (int)S;
+  } else if (row_units(es, rows, vec) <= kDimBlock) {
+    // Narrow: one strip covers every row; column ranges fill the GPU.
+    const int64_t nu = row_units(es, rows, vec);
+    p.narrow = true;
+    p.unit_vec = vec && nu != rows;
+    p.groups = 1;
+    const int64_t P = kDimBlock / nu;
+    int64_t S = (kNarrowBlocks + nb - 1) / nb;
+    S = kmin<int64_t>(S, kmax<int64_t>(cols / (2 * kNarrowUnroll * P), 1));
+    p.split = (int)kmin<int64_t>(S, 65535);
   } else {
     // Aligned path: the widest strip that still leaves one workgroup per
     // CU, so each workgroup streams the longest contiguous runs; with too
@@ -801,6 +1026,32 @@ inline bool dim_vec_ok(const void* A, int64_t cs, size_t es) {
 }
 
 template <class T, class Op, class F>
+void launch_narrow(bool unit_vec, dim3 grid, const T* A, int64_t rows, int64_t cols, int64_t cs, T* out, int64_t ods,
+                   int64_t seg, int64_t a_bstride, int64_t out_bstride, const T* x, int64_t xs, hipStream_t stream) {
+  if (unit_vec)
+    hipLaunchKernelGGL((reduce_rows_narrow_kernel<T, Op, F, true>), grid, dim3(kDimBlock), 0, stream, A, rows, cols,
+                       cs, out, ods, seg, a_bstride, out_bstride, x, xs);
+  else
+    hipLaunchKernelGGL((reduce_rows_narrow_kernel<T, Op, F, false>), grid, dim3(kDimBlock), 0, stream, A, rows, cols,
+                       cs, out, ods, seg, a_bstride, out_bstride, x, xs);
+}
+
+// Second stage of a split dims reduction: nz batches of an m x S partial
+// matrix (column s at s*m, batch z at z*S*m; the scratch is 256-byte
+// aligned) reduced along dim 2 into dst[i*ds + z*dst_bstride].
+template <class T, class Op>
+void launch_combine(const T* part, int S, int64_t m, T* dst, int64_t ds, int64_t dst_bstride, unsigned nz,
+                    hipStream_t stream) {
+  const int64_t nu = row_units(sizeof(T), m, true);
+  if (nu <= kDimBlock)
+    launch_narrow<T, Op, Unary<MapIdentity>>(nu != m, dim3(1, 1, nz), part, m, S, m, dst, ds, S, (int64_t)S * m,
+                                             dst_bstride, nullptr, 0, stream);
+  else
+    hipLaunchKernelGGL((combine_split_kernel<T, Op>), dim3((unsigned)((m + kRedBlock - 1) / kRedBlock), nz),
+                       dim3(kRedBlock), 0, stream, part, S, m, dst, ds, dst_bstride);
+}
+
+template <class T, class Op, class F>
 int launch_reduce_dim(const void* A, int64_t rows, int64_t cols, int64_t cs, int dim, void* dst,
                       int64_t ds, void* scratch, hipStream_t stream, int64_t batch = 1, int64_t a_bstride = 0,
                       const void* x = nullptr, int64_t xs = 0) {
@@ -809,15 +1060,36 @@ int launch_reduce_dim(const void* A, int64_t rows, int64_t cols, int64_t cs, int
   if (F::kHasX && dim == 1) vec = vec && xs == 1 && (uintptr_t)x % 16 == 0;
   const DimPlan p = plan_dim(sizeof(T), rows, cols, dim, vec, batch);
   if (dim == 1) {
+    if (p.seg_lanes) {
+      const dim3 grid((unsigned)p.groups);
+#define KF_SEG(V, L)                                                                                          \
+  hipLaunchKernelGGL((reduce_cols_seg_kernel<T, Op, F, V, L>), grid, dim3(kDimBlock), 0, stream, (const T*)A, rows, \
+                     cols, cs, (T*)dst, ds, (const T*)x, xs)
+#define KF_SEG_L(V)                    \
+  switch (p.seg_lanes) {               \
+    case 1: KF_SEG(V, 1); break;       \
+    case 2: KF_SEG(V, 2); break;       \
+    case 4: KF_SEG(V, 4); break;       \
+    case 8: KF_SEG(V, 8); break;       \
+    case 16: KF_SEG(V, 16); break;     \
+    default: KF_SEG(V, 32); break;     \
+  }
+      if (p.unit_vec) {
+        KF_SEG_L(true)
+      } else {
+        KF_SEG_L(false)
+      }
+#undef KF_SEG_L
+#undef KF_SEG
+      return kf_check_launch("reduce_cols_seg_kernel");
+    }
     T* out = p.split > 1 ? (T*)scratch : (T*)dst;
     constexpr int EPV = 16 / (int)sizeof(T);
     int64_t seg = (rows + p.split - 1) / p.split;
     seg = (seg + EPV - 1) / EPV * EPV;
     hipLaunchKernelGGL((reduce_cols_kernel<T, Op, F>), dim3((unsigned)p.groups, p.split), dim3(kDimBlock), 0,
                        stream, (const T*)A, rows, cols, cs, out, ds, seg, (int)vec, (const T*)x, xs);
-    if (p.split > 1)
-      hipLaunchKernelGGL((combine_split_kernel<T, Op>), dim3((unsigned)((cols + kRedBlock - 1) / kRedBlock), 1),
-                         dim3(kRedBlock), 0, stream, (const T*)scratch, p.split, cols, (T*)dst, ds, (int64_t)0);
+    if (p.split > 1) launch_combine<T, Op>((const T*)scratch, p.split, cols, (T*)dst, ds, 0, 1, stream);
     return kf_check_launch("reduce_cols_kernel");
   }
   // dim 2, batched: dst[(i + z*rows)*ds] = op_j f(A[i + j*cs + z*a_bstride])
@@ -829,6 +1101,12 @@ int launch_reduce_dim(const void* A, int64_t rows, int64_t cols, int64_t cs, int
     T* dz = (T*)dst + z0 * dst_bstride;
     T* out = p.split > 1 ? (T*)scratch : dz;
     const dim3 grid((unsigned)p.groups, p.split, nz);
+    if (p.narrow) {
+      launch_narrow<T, Op, F>(p.unit_vec, grid, Az, rows, cols, cs, out, ds, seg, a_bstride, dst_bstride, (const T*)x,
+                              xs, stream);
+      if (p.split > 1) launch_combine<T, Op>((const T*)scratch, p.split, rows, dz, ds, dst_bstride, nz, stream);
+      continue;
+    }
 #define KF_ROWS_VEC(RV)                                                                                  \
   hipLaunchKernelGGL((reduce_rows_kernel<T, Op, F, true, RV, col_unroll_for(RV)>), grid, dim3(kDimBlock), 0, stream, \
                      Az, rows, cols, cs, out, ds, seg, a_bstride, dst_bstride, (const T*)x, xs)
@@ -842,9 +1120,7 @@ int launch_reduce_dim(const void* A, int64_t rows, int64_t cols, int64_t cs, int
     } else
       hipLaunchKernelGGL((reduce_rows_kernel<T, Op, F, false>), grid, dim3(kDimBlock), 0, stream, Az, rows, cols,
                          cs, out, ds, seg, a_bstride, dst_bstride, (const T*)x, xs);
-    if (p.split > 1)
-      hipLaunchKernelGGL((combine_split_kernel<T, Op>), dim3((unsigned)((rows + kRedBlock - 1) / kRedBlock), nz),
-                         dim3(kRedBlock), 0, stream, (const T*)scratch, p.split, rows, dz, ds, dst_bstride);
+    if (p.split > 1) launch_combine<T, Op>((const T*)scratch, p.split, rows, dz, ds, dst_bstride, nz, stream);
   }
 #undef KF_ROWS_VEC
   return kf_check_launch("reduce_rows_kernel");

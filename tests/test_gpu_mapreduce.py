@@ -202,6 +202,74 @@ def test_dims2_strip_widths(kf, dev, dt, shape):
         assert got.shape == ref.shape and np.array_equal(got, ref), (shape, op)
 
 
+def _exact_dims_case(kf, dev, rng, dt, rows, cols, dim, pad=0, ops=("+", "max")):
+    # column-major rows x cols with column stride rows + pad; integer sums
+    # wrap in the element type, max is order-free: both exact
+    hi = 256 if dt == np.uint8 else 1 << 20
+    cs = rows + pad
+    buf = rng.integers(0, hi, cs * cols).astype(dt)
+    A = torch.from_numpy(buf).to(dev).as_strided((rows, cols), (1, cs))
+    M = buf.reshape(cols, cs)[:, :rows].T
+    for op in ops:
+        got = kf.mapreduce(kf.identity, op, A, dims=dim).cpu().numpy().reshape(-1)
+        ref = M.sum(axis=dim - 1, dtype=dt) if op == "+" else M.max(axis=dim - 1)
+        assert np.array_equal(got, ref), (rows, cols, pad, dim, op)
+
+
+@pytest.mark.parametrize("dt", [np.int32, np.int64, np.uint8])
+def test_dims1_short_columns(kf, dev, dt):
+    # Columns of up to 128 row units take L = 1..32 lanes per column
+    # (16-byte units when rows is a multiple of the vector width and the
+    # columns are aligned, elements otherwise); longer ones one wave each.
+    rng = np.random.default_rng(11)
+    for rows in (1, 2, 3, 4, 5, 8, 12, 16, 31, 32, 64, 100, 128, 255, 256, 512, 513, 1000, 2048, 2064):
+        for pad in (0, 1, 16):
+            _exact_dims_case(kf, dev, rng, dt, rows, 3001, 1, pad)
+
+
+@pytest.mark.parametrize("dt", [np.int32, np.uint8])
+@pytest.mark.parametrize("shape", [(1_000_003, 3), (1 << 20, 2), (777_777, 5), (300_001, 17), (65536, 100)])
+def test_dims1_few_long_columns(kf, dev, dt, shape):
+    # few long columns split into up to 4096 row segments per column; the
+    # cols x S partials are combined by the narrow dims=2 kernel
+    _exact_dims_case(kf, dev, np.random.default_rng(sum(shape)), dt, *shape, 1)
+
+
+@pytest.mark.parametrize("dt", [np.int32, np.int64, np.uint8])
+def test_dims2_narrow(kf, dev, dt):
+    # At most 256 row units: thread (unit, phase) over column phases, split
+    # over column ranges whose partials the same kernel combines.
+    rng = np.random.default_rng(12)
+    for rows in (1, 2, 3, 4, 7, 16, 64, 100, 256, 257, 1000, 1024):
+        for cols in (1, 5, 1000, 100_003):
+            for pad in (0, 3):
+                if rows * cols > 30_000_000:
+                    continue
+                _exact_dims_case(kf, dev, rng, dt, rows, cols, 2, pad)
+
+
+@pytest.mark.parametrize("shape", [(16, 1000, 7), (3, 5000, 4), (64, 33, 300), (2, 100_000, 3)])
+def test_dims2_narrow_batched(kf, dev, shape):
+    # middle-dims reductions with narrow rows: batch in grid.z, split partials per batch
+    rng = np.random.default_rng(sum(shape))
+    a = rng.integers(-1000, 1000, shape[::-1]).astype(np.int32)
+    x = torch.from_numpy(a).to(dev).permute(2, 1, 0)
+    xn = x.cpu().numpy()
+    for op in ("+", "max"):
+        got = kf.mapreduce(kf.identity, op, x, dims=2).cpu().numpy()
+        ref = xn.sum(axis=1, keepdims=True, dtype=np.int32) if op == "+" else xn.max(axis=1, keepdims=True)
+        assert np.array_equal(got, ref), (shape, op)
+
+
+def test_dims1_column_count_beyond_one_grid(kf, dev):
+    # more columns than one capped grid covers: both dims=1 kernels
+    # grid-stride over column blocks (1-lane columns past 8192 x 256 columns;
+    # wave-per-column past 65536 x 4)
+    rng = np.random.default_rng(13)
+    _exact_dims_case(kf, dev, rng, np.uint8, 1, (1 << 26) + 5, 1, ops=("+",))
+    _exact_dims_case(kf, dev, rng, np.uint8, 2064, 270_000, 1, ops=("max",))
+
+
 def test_dims_golden(kf, dev, golden):
     for c in golden["reduce_dim"]:
         buf = dec(c["buf"], np.float64)

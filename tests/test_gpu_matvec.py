@@ -11,7 +11,8 @@ import torch
 pytestmark = pytest.mark.gpu
 
 SHAPES = [(1, 1), (3, 3), (101, 101), (512, 512), (1000, 1000), (1024, 10), (4096, 32), (65536, 16),
-          (3, 10_000), (32, 50_000), (4, 1000), (63, 1000), (2048, 1000), (32768, 50)]
+          (3, 10_000), (32, 50_000), (4, 1000), (63, 1000), (2048, 1000), (32768, 50),
+          (8, 300_000), (12, 100_000), (300_000, 3), (100, 20_000)]
 
 
 def mk(rng, dt, shape):
