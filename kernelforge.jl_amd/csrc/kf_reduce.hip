@@ -571,6 +571,7 @@ template <class Map> struct Unary {
 constexpr int kDimBlock = 256;
 constexpr int kDimWaves = kDimBlock / kWave;
 constexpr int kDimUnroll = 4;
+constexpr int kScalarUnroll = 8;  // element (unaligned) paths: loads in flight per thread
 constexpr int kDimMaxSplit = 64;          // dim 1 splits combined by combine_split_kernel
 constexpr int kDimMaxSplitNarrow = 4096;  // dim 1 splits combined by reduce_rows_narrow_kernel
 constexpr int kRowVecsDefault = 2;    // dim 2, unaligned path: elements per thread per column / 1
@@ -648,8 +649,19 @@ __global__ __launch_bounds__(kDimBlock) void reduce_cols_kernel(
     const int64_t t = r0 + nv * EPV + lane;
     if (t < r1) acc = Op::combine(acc, F::apply(c[t], F::kHasX ? xv[t] : c[t]));
   } else {
-    for (int64_t r = r0 + lane; r < r1; r += kWave)
-      acc = Op::combine(acc, F::apply(c[r], F::kHasX ? xv[r * xs] : c[r]));
+    // element path: kScalarUnroll loads in flight per lane
+    int64_t r = r0 + lane;
+    for (; r + (kScalarUnroll - 1) * kWave < r1; r += kScalarUnroll * kWave) {
+      T x[kScalarUnroll], w[kScalarUnroll];
+#pragma unroll
+      for (int u = 0; u < kScalarUnroll; ++u) {
+        x[u] = c[r + u * kWave];
+        w[u] = F::kHasX ? xv[(r + u * kWave) * xs] : x[u];
+      }
+#pragma unroll
+      for (int u = 0; u < kScalarUnroll; ++u) acc = Op::combine(acc, F::apply(x[u], w[u]));
+    }
+    for (; r < r1; r += kWave) acc = Op::combine(acc, F::apply(c[r], F::kHasX ? xv[r * xs] : c[r]));
   }
   acc = wave_reduce<Op>(acc);
   // S == 1: out is dst; otherwise out is partials[s*cols + col]
@@ -680,7 +692,9 @@ template <class Op, int L, class T> __device__ inline T group_reduce(T x) {
 // (16-byte vectors when VEC: rows % EPV == 0 and aligned columns; elements
 // otherwise), then a combine over the L lanes. Grid-stride over column
 // blocks, so any column count fits one capped grid.
-constexpr int kSegUnits = 4;      // target units per lane
+constexpr int kSegElemsPerLane = 4;  // target element units per lane (16-byte units: 1)
+constexpr int kSegMaxLanesVec = 8, kSegMaxLanesElem = 16;
+constexpr int kSegMaxUnitsVec = 128, kSegMaxUnitsElem = 256;  // longer columns take one wave each
 constexpr int kSegMaxBlocks = 8192;
 template <class T, class Op, class F, bool VEC, int L>
 __global__ __launch_bounds__(kDimBlock) void reduce_cols_seg_kernel(const T* A, int64_t rows, int64_t cols,
@@ -688,7 +702,7 @@ __global__ __launch_bounds__(kDimBlock) void reduce_cols_seg_kernel(const T* A, 
                                                                     const T* xv, int64_t xs) {
   constexpr int EPV = VEC ? 16 / (int)sizeof(T) : 1;
   constexpr int CPB = kDimBlock / L;
-  constexpr int U = kSegUnits;
+  constexpr int U = 4;
   const T id = Op::template identity<T>();
   const int j = threadIdx.x % L;
   const int64_t nu = rows / EPV;  // VEC: rows % EPV == 0
@@ -822,7 +836,34 @@ __global__ __launch_bounds__(kDimBlock) void reduce_rows_kernel(
       }
     }
   } else {
-    for (int64_t c = c0; c < c1; ++c)
+    // element path (unaligned, or the ragged last strip): kColUnroll
+    // columns of loads in flight; rows past the end read row 0's element and
+    // drop it
+    int64_t c = c0;
+    if constexpr (!VEC)  // the aligned kernel takes this branch only for its one ragged strip
+    for (; c + kColUnroll <= c1; c += kColUnroll) {
+      T x[kColUnroll][kRowVecs][EPV];
+#pragma unroll
+      for (int q = 0; q < kColUnroll; ++q)
+#pragma unroll
+        for (int u = 0; u < kRowVecs; ++u)
+#pragma unroll
+          for (int e = 0; e < EPV; ++e) {
+            const int64_t r = strip + (int64_t)(u * kDimBlock + tid) * EPV + e;
+            x[q][u][e] = A[(r < rows ? r : 0) + (c + q) * col_stride];
+          }
+#pragma unroll
+      for (int q = 0; q < kColUnroll; ++q) {
+        const T w = F::kHasX ? xv[(c + q) * xs] : id;
+#pragma unroll
+        for (int u = 0; u < kRowVecs; ++u)
+#pragma unroll
+          for (int e = 0; e < EPV; ++e)
+            if (strip + (int64_t)(u * kDimBlock + tid) * EPV + e < rows)
+              a[u][e] = Op::combine(a[u][e], F::apply(x[q][u][e], w));
+      }
+    }
+    for (; c < c1; ++c)
 #pragma unroll
       for (int u = 0; u < kRowVecs; ++u)
 #pragma unroll
@@ -953,13 +994,22 @@ inline DimPlan plan_dim(size_t es, int64_t rows, int64_t cols, int dim, bool vec
   DimPlan p{};
   const int epv = vec ? (int)(16 / es) : 1;
   if (dim == 1) {
-    // Short columns: L lanes per column with about kSegUnits units each.
+    // Short columns: L lanes per column, one 16-byte unit or about
+    // kSegElemsPerLane elements each, at most 8 (16) lanes. Float32, 1 GiB:
+    // 16 rows 5.7 TB/s at 4 lanes against 3.5 at 1; 64 rows 6.2 at 8 lanes
+    // against 5.7 at 16; unaligned 16 rows 5.4 at 4 lanes against 2.5 at
+    // 16; unaligned 128 rows 5.8 at 16 lanes against 5.1 at 8; unaligned
+    // 256 rows 6.1 here against 3.3 with a wave per column, while aligned
+    // 1024 rows stay faster with a wave per column (6.8 against 6.4).
     const int64_t nu = row_units(es, rows, vec);
+    const bool uv = vec && nu != rows;
+    const int64_t per = uv ? 1 : kSegElemsPerLane;
+    const int max_lanes = uv ? kSegMaxLanesVec : kSegMaxLanesElem;
     int L = 1;
-    while (L < kWave && (int64_t)L * kSegUnits < nu) L <<= 1;
-    if (L < kWave) {
+    while (L < max_lanes && (int64_t)L * per < nu) L <<= 1;
+    if (nu <= (uv ? kSegMaxUnitsVec : kSegMaxUnitsElem)) {
       p.seg_lanes = L;
-      p.unit_vec = vec && nu != rows;
+      p.unit_vec = uv;
       p.groups = kmin<int64_t>((cols + kDimBlock / L - 1) / (kDimBlock / L), kSegMaxBlocks);
       p.split = 1;
     } else {
@@ -1071,8 +1121,7 @@ int launch_reduce_dim(const void* A, int64_t rows, int64_t cols, int64_t cs, int
     case 2: KF_SEG(V, 2); break;       \
     case 4: KF_SEG(V, 4); break;       \
     case 8: KF_SEG(V, 8); break;       \
-    case 16: KF_SEG(V, 16); break;     \
-    default: KF_SEG(V, 32); break;     \
+    default: KF_SEG(V, 16); break;     \
   }
       if (p.unit_vec) {
         KF_SEG_L(true)

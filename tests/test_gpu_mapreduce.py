@@ -218,7 +218,7 @@ def _exact_dims_case(kf, dev, rng, dt, rows, cols, dim, pad=0, ops=("+", "max"))
 
 @pytest.mark.parametrize("dt", [np.int32, np.int64, np.uint8])
 def test_dims1_short_columns(kf, dev, dt):
-    # Columns of up to 128 row units take L = 1..32 lanes per column
+    # Columns of up to 128 vector (256 element) units take L = 1..16 lanes per column
     # (16-byte units when rows is a multiple of the vector width and the
     # columns are aligned, elements otherwise); longer ones one wave each.
     rng = np.random.default_rng(11)
