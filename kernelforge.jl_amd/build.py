@@ -14,7 +14,7 @@ CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libkfhip.so")
 DRIVER = os.path.join(HERE, "kf_driver")
-SOURCES = ["kf_api.hip", "kf_scan.hip", "kf_reduce.hip", "kf_copy.hip"]
+SOURCES = ["kf_api.hip", "kf_scan.hip", "kf_reduce.hip", "kf_reduce_dims.hip", "kf_matvec.hip", "kf_copy.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [

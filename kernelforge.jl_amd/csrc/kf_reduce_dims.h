@@ -1,0 +1,756 @@
+// Reduction-along-dims kernels and their launch plan, shared by
+// kf_reduce_dims.hip (mapreduce with dims) and kf_matvec.hip (matvec /
+// vecmat with a vector operand) so the two instantiation sets compile in
+// parallel. Reference src/mapreduce/2D/vecmat_kernel.jl:1-169 (dims=1),
+// src/mapreduce/2D/matvec_kernel.jl:1-239 (dims=2): partial results per
+// workgroup, then a combine when columns or rows are split.
+#pragma once
+#include "kf_reduce.h"
+
+namespace kf {
+
+
+// Stage 2 of the split dims reductions: out[i*ds] = op_s partials[s*m + i],
+// for batch z = blockIdx.y: partials at z*S*m, outputs at z*dst_bstride.
+template <class T, class Op>
+__global__ __launch_bounds__(kRedBlock) void combine_split_kernel(const T* partials, int S, int64_t m, T* dst,
+                                                                  int64_t ds, int64_t dst_bstride) {
+  const int64_t i = (int64_t)blockIdx.x * kRedBlock + threadIdx.x;
+  if (i >= m) return;
+  partials += (int64_t)blockIdx.y * S * m;
+  dst += (int64_t)blockIdx.y * dst_bstride;
+  T x = partials[i];
+  for (int s = 1; s < S; ++s) x = Op::combine(x, partials[(int64_t)s * m + i]);
+  dst[i * ds] = x;
+}
+
+// ---------------------------------------------------------------------------
+// dim = 1: one wave per column (a column of a column-major matrix is
+// contiguous), optionally split into S row segments when there are too few
+// columns to fill the GPU.
+// ---------------------------------------------------------------------------
+// Element function of the dims kernels: f(a) for a plain reduction, or
+// f(a, x) with a vector operand x (matvec: x[j] per column; vecmat: x[i]
+// per row).
+template <class Map> struct Unary {
+  static constexpr bool kHasX = false;
+  template <class T> __device__ static T apply(T a, T) { return Map::apply(a); }
+};
+
+constexpr int kDimBlock = 256;
+constexpr int kDimWaves = kDimBlock / kWave;
+constexpr int kDimUnroll = 4;
+constexpr int kScalarUnroll = 8;  // element (unaligned) paths: loads in flight per thread
+constexpr int kDimMaxSplit = 64;          // dim 1 splits combined by combine_split_kernel
+constexpr int kDimMaxSplitNarrow = 4096;  // dim 1 splits combined by reduce_rows_narrow_kernel
+constexpr int kRowVecsDefault = 2;    // dim 2, unaligned path: elements per thread per column / 1
+constexpr int kColUnrollDefault = 8;  // dim 2, unaligned path: columns per pass
+constexpr int kDim2Blocks = 256;      // dim 2: target workgroups (one per CU)
+// dim 2, aligned path: the widest strip (16-byte vectors per thread per
+// column) that still gives kDim2Blocks workgroups; columns in flight per
+// thread for each strip width.
+constexpr int kDim2MaxRowVecs = 8;
+constexpr int kColUnrollRv1 = 16;
+constexpr int kColUnrollRv2 = 8;
+constexpr int kColUnrollRv4 = 4;
+constexpr int kColUnrollRv8 = 4;
+constexpr int col_unroll_for(int rv) {
+  return rv == 1 ? kColUnrollRv1 : rv == 2 ? kColUnrollRv2 : rv == 4 ? kColUnrollRv4 : kColUnrollRv8;
+}
+
+template <class T, class Op, class F>
+__global__ __launch_bounds__(kDimBlock) void reduce_cols_kernel(
+    const T* A, int64_t rows, int64_t cols, int64_t col_stride, T* out, int64_t out_stride,
+    int64_t seg_rows, int vec, const T* xv, int64_t xs) {
+  constexpr int EPV = 16 / (int)sizeof(T);
+  const T id = Op::template identity<T>();
+  const int lane = lane_id();
+  const int wave = threadIdx.x / kWave;
+  const int s = blockIdx.y;
+  // grid-stride over blocks of kDimWaves columns (the grid is capped)
+  for (int64_t col = (int64_t)blockIdx.x * kDimWaves + wave; col < cols; col += (int64_t)gridDim.x * kDimWaves) {
+  T acc = id;
+  const T* c = A + col * col_stride;
+  const int64_t r0 = (int64_t)s * seg_rows;
+  const int64_t r1 = kmin<int64_t>(rows, r0 + seg_rows);
+  if (vec) {
+    // seg_rows is a multiple of EPV and columns are 16-byte aligned.
+    const int64_t nv = r1 > r0 ? (r1 - r0) / EPV : 0;
+    const uint4* v = reinterpret_cast<const uint4*>(c + r0);
+    const uint4* vx = reinterpret_cast<const uint4*>(xv + r0);  // used only with an operand (16-B aligned, xs = 1)
+    T a[kDimUnroll][EPV];
+#pragma unroll
+    for (int u = 0; u < kDimUnroll; ++u)
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) a[u][e] = id;
+    int64_t i = lane;
+    for (; i + (kDimUnroll - 1) * kWave < nv; i += kDimUnroll * kWave) {
+      uint4 r[kDimUnroll], rx[kDimUnroll];
+#pragma unroll
+      for (int u = 0; u < kDimUnroll; ++u) {
+        r[u] = ld_stream(v + i + u * kWave);
+        if constexpr (F::kHasX) rx[u] = vx[i + u * kWave];
+      }
+#pragma unroll
+      for (int u = 0; u < kDimUnroll; ++u) {
+        T x[EPV], w[EPV];
+        __builtin_memcpy(x, &r[u], 16);
+        if constexpr (F::kHasX) __builtin_memcpy(w, &rx[u], 16);
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) a[u][e] = Op::combine(a[u][e], F::apply(x[e], F::kHasX ? w[e] : x[e]));
+      }
+    }
+    for (; i < nv; i += kWave) {
+      const uint4 r = ld_stream(v + i);
+      T x[EPV], w[EPV];
+      __builtin_memcpy(x, &r, 16);
+      if constexpr (F::kHasX) {
+        const uint4 q = vx[i];
+        __builtin_memcpy(w, &q, 16);
+      }
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) a[0][e] = Op::combine(a[0][e], F::apply(x[e], F::kHasX ? w[e] : x[e]));
+    }
+#pragma unroll
+    for (int u = 0; u < kDimUnroll; ++u)
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) acc = Op::combine(acc, a[u][e]);
+    const int64_t t = r0 + nv * EPV + lane;
+    if (t < r1) acc = Op::combine(acc, F::apply(c[t], F::kHasX ? xv[t] : c[t]));
+  } else {
+    // element path: kScalarUnroll loads in flight per lane
+    int64_t r = r0 + lane;
+    for (; r + (kScalarUnroll - 1) * kWave < r1; r += kScalarUnroll * kWave) {
+      T x[kScalarUnroll], w[kScalarUnroll];
+#pragma unroll
+      for (int u = 0; u < kScalarUnroll; ++u) {
+        x[u] = c[r + u * kWave];
+        w[u] = F::kHasX ? xv[(r + u * kWave) * xs] : x[u];
+      }
+#pragma unroll
+      for (int u = 0; u < kScalarUnroll; ++u) acc = Op::combine(acc, F::apply(x[u], w[u]));
+    }
+    for (; r < r1; r += kWave) acc = Op::combine(acc, F::apply(c[r], F::kHasX ? xv[r * xs] : c[r]));
+  }
+  acc = wave_reduce<Op>(acc);
+  // S == 1: out is dst; otherwise out is partials[s*cols + col]
+  if (lane == 0) out[gridDim.y == 1 ? col * out_stride : (int64_t)s * cols + col] = acc;
+  }
+}
+
+// Combine of x over aligned groups of L lanes (L a power of two <= 64),
+// lower lanes on the left; the result is valid in each group's first lane.
+template <class T> __device__ inline T shfl_xor_t(T v, int m) {
+  Words<T> w = to_words(v), r;
+#pragma unroll
+  for (int i = 0; i < Words<T>::W; ++i) r.w[i] = (uint32_t)__shfl_xor((int)w.w[i], m, kWave);
+  return from_words<T>(r);
+}
+template <class Op, int L, class T> __device__ inline T group_reduce(T x) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int m = 1; m < L; m <<= 1) {
+    const T y = shfl_xor_t(x, m);
+    x = (lane & m) ? Op::combine(y, x) : Op::combine(x, y);
+  }
+  return x;
+}
+
+// dim = 1, short columns: L lanes per column (kDimBlock / L columns per
+// workgroup pass), each lane combining units j, j+L, ... of its column
+// (16-byte vectors when VEC: rows % EPV == 0 and aligned columns; elements
+// otherwise), then a combine over the L lanes. Grid-stride over column
+// blocks, so any column count fits one capped grid.
+constexpr int kSegElemsPerLane = 4;  // target element units per lane (16-byte units: 1)
+constexpr int kSegMaxLanesVec = 8, kSegMaxLanesElem = 16;
+constexpr int kSegMaxUnitsVec = 128, kSegMaxUnitsElem = 256;  // longer columns take one wave each
+constexpr int kSegMaxBlocks = 8192;
+template <class T, class Op, class F, bool VEC, int L>
+__global__ __launch_bounds__(kDimBlock) void reduce_cols_seg_kernel(const T* A, int64_t rows, int64_t cols,
+                                                                    int64_t col_stride, T* out, int64_t out_stride,
+                                                                    const T* xv, int64_t xs) {
+  constexpr int EPV = VEC ? 16 / (int)sizeof(T) : 1;
+  constexpr int CPB = kDimBlock / L;
+  constexpr int U = 4;
+  const T id = Op::template identity<T>();
+  const int j = threadIdx.x % L;
+  const int64_t nu = rows / EPV;  // VEC: rows % EPV == 0
+  for (int64_t cb = (int64_t)blockIdx.x * CPB; cb < cols; cb += (int64_t)gridDim.x * CPB) {
+    const int64_t col = cb + threadIdx.x / L;
+    T acc = id;
+    if (col < cols) {
+      const T* c = A + col * col_stride;
+      T a[EPV];
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) a[e] = id;
+      int64_t i = j;
+      for (; i + (U - 1) * L < nu; i += U * L) {
+        if constexpr (VEC) {
+          uint4 r[U], rx[U];
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            r[u] = ld_stream(reinterpret_cast<const uint4*>(c) + i + u * L);
+            if constexpr (F::kHasX) rx[u] = reinterpret_cast<const uint4*>(xv)[i + u * L];
+          }
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            T x[EPV], w[EPV];
+            __builtin_memcpy(x, &r[u], 16);
+            if constexpr (F::kHasX) __builtin_memcpy(w, &rx[u], 16);
+#pragma unroll
+            for (int e = 0; e < EPV; ++e) a[e] = Op::combine(a[e], F::apply(x[e], F::kHasX ? w[e] : x[e]));
+          }
+        } else {
+          T x[U], w[U];
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            x[u] = c[i + u * L];
+            if constexpr (sizeof(T) == 1) {
+              // one byte per register: keeps adjacent byte loads from being
+              // fused into a sub-dword vector the backend cannot split
+              uint32_t b = x[u];
+              __asm__ volatile("" : "+v"(b));
+              x[u] = (T)b;
+            }
+            w[u] = F::kHasX ? xv[(i + u * L) * xs] : x[u];
+          }
+#pragma unroll
+          for (int u = 0; u < U; ++u) a[0] = Op::combine(a[0], F::apply(x[u], w[u]));
+        }
+      }
+      for (; i < nu; i += L) {
+        if constexpr (VEC) {
+          const uint4 r = ld_stream(reinterpret_cast<const uint4*>(c) + i);
+          T x[EPV], w[EPV];
+          __builtin_memcpy(x, &r, 16);
+          if constexpr (F::kHasX) {
+            const uint4 q = reinterpret_cast<const uint4*>(xv)[i];
+            __builtin_memcpy(w, &q, 16);
+          }
+#pragma unroll
+          for (int e = 0; e < EPV; ++e) a[e] = Op::combine(a[e], F::apply(x[e], F::kHasX ? w[e] : x[e]));
+        } else {
+          a[0] = Op::combine(a[0], F::apply(c[i], F::kHasX ? xv[i * xs] : c[i]));
+        }
+      }
+      acc = a[0];
+#pragma unroll
+      for (int e = 1; e < EPV; ++e) acc = Op::combine(acc, a[e]);
+    }
+    acc = group_reduce<Op, L>(acc);
+    if (j == 0 && col < cols) out[col * out_stride] = acc;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dim = 2: a workgroup owns a strip of 256*kRowVecs*EPV rows (4-32 KiB of
+// each column; thread t holds vectors t, t+256, ... of the strip) and a range
+// of columns, which it walks kColUnroll at a time, so every load is part of a
+// contiguous run of the strip's width. Strips are split over S column ranges
+// whose partials stage 2 combines.
+// ---------------------------------------------------------------------------
+template <class T, class Op, class F, bool VEC, int kRowVecs = kRowVecsDefault, int kColUnroll = kColUnrollDefault>
+__global__ __launch_bounds__(kDimBlock) void reduce_rows_kernel(
+    const T* A, int64_t rows, int64_t cols, int64_t col_stride, T* out, int64_t out_stride, int64_t seg_cols,
+    int64_t a_bstride, int64_t out_bstride, const T* xv, int64_t xs) {
+  constexpr int EPV = VEC ? 16 / (int)sizeof(T) : 1;
+  // batch z = blockIdx.z: one (rows x cols) matrix per batch entry
+  A += (int64_t)blockIdx.z * a_bstride;
+  out += gridDim.y == 1 ? (int64_t)blockIdx.z * out_bstride : (int64_t)blockIdx.z * gridDim.y * rows;
+  constexpr int RS = kDimBlock * kRowVecs * EPV;
+  const T id = Op::template identity<T>();
+  const int tid = threadIdx.x;
+  const int s = blockIdx.y;
+  const int64_t strip = (int64_t)blockIdx.x * RS;
+  const int64_t c0 = (int64_t)s * seg_cols;
+  const int64_t c1 = kmin<int64_t>(cols, c0 + seg_cols);
+
+  T a[kRowVecs][EPV];
+#pragma unroll
+  for (int u = 0; u < kRowVecs; ++u)
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) a[u][e] = id;
+  if constexpr (VEC) {
+  {  // vector launches cover whole strips only (the host splits off the rest)
+    const T* p = A + strip;
+    int64_t c = c0;
+    for (; c + kColUnroll <= c1; c += kColUnroll) {
+      uint4 r[kColUnroll][kRowVecs];
+#pragma unroll
+      for (int q = 0; q < kColUnroll; ++q)
+#pragma unroll
+        for (int u = 0; u < kRowVecs; ++u)
+          r[q][u] = ld_stream(reinterpret_cast<const uint4*>(p + (c + q) * col_stride) + u * kDimBlock + tid);
+#pragma unroll
+      for (int q = 0; q < kColUnroll; ++q) {
+        const T w = F::kHasX ? xv[(c + q) * xs] : id;
+#pragma unroll
+        for (int u = 0; u < kRowVecs; ++u) {
+          T x[EPV];
+          __builtin_memcpy(x, &r[q][u], sizeof(x));
+#pragma unroll
+          for (int e = 0; e < EPV; ++e) a[u][e] = Op::combine(a[u][e], F::apply(x[e], w));
+        }
+      }
+    }
+    for (; c < c1; ++c) {
+      const T w = F::kHasX ? xv[c * xs] : id;
+#pragma unroll
+      for (int u = 0; u < kRowVecs; ++u) {
+        const uint4 r = ld_stream(reinterpret_cast<const uint4*>(p + c * col_stride) + u * kDimBlock + tid);
+        T x[EPV];
+        __builtin_memcpy(x, &r, sizeof(x));
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) a[u][e] = Op::combine(a[u][e], F::apply(x[e], w));
+      }
+    }
+  }
+  } else {
+    // element path (unaligned): kColUnroll columns of loads in flight; rows
+    // past the end read row 0's element and drop it
+    int64_t c = c0;
+    for (; c + kColUnroll <= c1; c += kColUnroll) {
+      T x[kColUnroll][kRowVecs][EPV];
+#pragma unroll
+      for (int q = 0; q < kColUnroll; ++q)
+#pragma unroll
+        for (int u = 0; u < kRowVecs; ++u)
+#pragma unroll
+          for (int e = 0; e < EPV; ++e) {
+            const int64_t r = strip + (int64_t)(u * kDimBlock + tid) * EPV + e;
+            x[q][u][e] = A[(r < rows ? r : 0) + (c + q) * col_stride];
+          }
+#pragma unroll
+      for (int q = 0; q < kColUnroll; ++q) {
+        const T w = F::kHasX ? xv[(c + q) * xs] : id;
+#pragma unroll
+        for (int u = 0; u < kRowVecs; ++u)
+#pragma unroll
+          for (int e = 0; e < EPV; ++e)
+            if (strip + (int64_t)(u * kDimBlock + tid) * EPV + e < rows)
+              a[u][e] = Op::combine(a[u][e], F::apply(x[q][u][e], w));
+      }
+    }
+    for (; c < c1; ++c)
+#pragma unroll
+      for (int u = 0; u < kRowVecs; ++u)
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) {
+          const int64_t r = strip + (int64_t)(u * kDimBlock + tid) * EPV + e;
+          if (r < rows) a[u][e] = Op::combine(a[u][e], F::apply(A[r + c * col_stride], F::kHasX ? xv[c * xs] : id));
+        }
+  }
+#pragma unroll
+  for (int u = 0; u < kRowVecs; ++u)
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) {
+      const int64_t r = strip + (int64_t)(u * kDimBlock + tid) * EPV + e;
+      if (r < rows) out[gridDim.y == 1 ? r * out_stride : (int64_t)s * rows + r] = a[u][e];
+    }
+}
+
+
+// dim = 2, narrow matrices (at most kDimBlock row units: 16-byte vectors
+// when VEC, i.e. rows % EPV == 0 and aligned columns, else elements): the
+// workgroup is split into P = kDimBlock / units column phases; thread
+// (unit, phase) walks columns phase, phase + P, ... of its column range, kNarrowUnroll
+// loads in flight, and the phases are combined in order through LDS. Also
+// the second stage of split reductions: the S partial columns are a
+// rows x S matrix reduced along dim 2 the same way.
+constexpr int kNarrowUnroll = 8;
+constexpr int kNarrowBlocks = 512;  // target workgroups over batch x column ranges
+template <class T, class Op, class F, bool VEC>
+__global__ __launch_bounds__(kDimBlock) void reduce_rows_narrow_kernel(
+    const T* A, int64_t rows, int64_t cols, int64_t col_stride, T* out, int64_t out_stride, int64_t seg_cols,
+    int64_t a_bstride, int64_t out_bstride, const T* xv, int64_t xs) {
+  constexpr int EPV = VEC ? 16 / (int)sizeof(T) : 1;
+  constexpr int U = kNarrowUnroll;
+  __shared__ T s_acc[kDimBlock * EPV];
+  A += (int64_t)blockIdx.z * a_bstride;
+  out += gridDim.y == 1 ? (int64_t)blockIdx.z * out_bstride : (int64_t)blockIdx.z * gridDim.y * rows;
+  const T id = Op::template identity<T>();
+  const int nunits = (int)(rows / EPV);  // <= kDimBlock (host-checked)
+  const int P = kDimBlock / nunits;
+  const int t = threadIdx.x;
+  const int unit = t % nunits, ph = t / nunits;
+  const int64_t c0 = (int64_t)blockIdx.y * seg_cols;
+  const int64_t c1 = kmin<int64_t>(cols, c0 + seg_cols);
+  T a[EPV];
+#pragma unroll
+  for (int e = 0; e < EPV; ++e) a[e] = id;
+  if (ph < P) {
+    const T* p = A + (int64_t)unit * EPV;
+    int64_t c = c0 + ph;
+    for (; c + (int64_t)(U - 1) * P < c1; c += (int64_t)U * P) {
+      if constexpr (VEC) {
+        uint4 r[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) r[u] = ld_stream(reinterpret_cast<const uint4*>(p + (c + (int64_t)u * P) * col_stride));
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const T w = F::kHasX ? xv[(c + (int64_t)u * P) * xs] : id;
+          T x[EPV];
+          __builtin_memcpy(x, &r[u], 16);
+#pragma unroll
+          for (int e = 0; e < EPV; ++e) a[e] = Op::combine(a[e], F::apply(x[e], w));
+        }
+      } else {
+        T x[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) x[u] = p[(c + (int64_t)u * P) * col_stride];
+#pragma unroll
+        for (int u = 0; u < U; ++u) a[0] = Op::combine(a[0], F::apply(x[u], F::kHasX ? xv[(c + (int64_t)u * P) * xs] : id));
+      }
+    }
+    for (; c < c1; c += P) {
+      const T w = F::kHasX ? xv[c * xs] : id;
+      if constexpr (VEC) {
+        const uint4 r = ld_stream(reinterpret_cast<const uint4*>(p + c * col_stride));
+        T x[EPV];
+        __builtin_memcpy(x, &r, 16);
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) a[e] = Op::combine(a[e], F::apply(x[e], w));
+      } else {
+        a[0] = Op::combine(a[0], F::apply(p[c * col_stride], w));
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) s_acc[t * EPV + e] = a[e];
+  }
+  __syncthreads();
+  if (t < nunits) {
+    // phases in column order: phase q holds columns q, q + P, ...; every op
+    // here is commutative, and phase order keeps the combine deterministic
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) a[e] = s_acc[t * EPV + e];
+    for (int q = 1; q < P; ++q)
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) a[e] = Op::combine(a[e], s_acc[(q * nunits + t) * EPV + e]);
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) {
+      const int64_t r = (int64_t)t * EPV + e;
+      out[gridDim.y == 1 ? r * out_stride : (int64_t)blockIdx.y * rows + r] = a[e];
+    }
+  }
+}
+
+struct DimPlan {
+  int64_t groups;  // column groups (dim 1) or row strips (dim 2)
+  int split;       // S workgroups cooperating on one group
+  int row_vecs;    // dim 2: strip width in vectors (elements on the unaligned path) per thread
+  int seg_lanes;   // dim 1: lanes per column of reduce_cols_seg_kernel (0: one wave per column)
+  bool narrow;     // dim 2: reduce_rows_narrow_kernel
+  bool unit_vec;   // seg / narrow kernels: 16-byte units (rows % EPV == 0, aligned columns)
+  size_t partial_bytes;
+};
+
+// Launch plan; a pure function of (element size, shape, dim, alignment) so
+// the scratch query and the launch agree.
+constexpr int64_t kMaxBatchPerLaunch = 65535;  // grid.z limit
+
+// Row units of an m-row operand for the seg / narrow kernels: 16-byte
+// vectors when m is a multiple of the vector width (and the columns are
+// aligned), else elements.
+inline int64_t row_units(size_t es, int64_t m, bool aligned) {
+  const int64_t ev = (int64_t)(16 / es);
+  return aligned && m % ev == 0 ? m / ev : m;
+}
+constexpr int64_t kColsMaxBlocks = 65536;  // wave-per-column grid cap (grid-stride beyond)
+
+inline DimPlan plan_dim(size_t es, int64_t rows, int64_t cols, int dim, bool vec, int64_t batch = 1) {
+  const int64_t nb = kmin<int64_t>(kmax<int64_t>(batch, 1), kMaxBatchPerLaunch);
+  DimPlan p{};
+  const int epv = vec ? (int)(16 / es) : 1;
+  if (dim == 1) {
+    // Short columns: L lanes per column, one 16-byte unit or about
+    // kSegElemsPerLane elements each, at most 8 (16) lanes. Float32, 1 GiB:
+    // 16 rows 5.7 TB/s at 4 lanes against 3.5 at 1; 64 rows 6.2 at 8 lanes
+    // against 5.7 at 16; unaligned 16 rows 5.4 at 4 lanes against 2.5 at
+    // 16; unaligned 128 rows 5.8 at 16 lanes against 5.1 at 8; unaligned
+    // 256 rows 6.1 here against 3.3 with a wave per column, while aligned
+    // 1024 rows stay faster with a wave per column (6.8 against 6.4).
+    const int64_t nu = row_units(es, rows, vec);
+    const bool uv = vec && nu != rows;
+    const int64_t per = uv ? 1 : kSegElemsPerLane;
+    const int max_lanes = uv ? kSegMaxLanesVec : kSegMaxLanesElem;
+    int L = 1;
+    while (L < max_lanes && (int64_t)L * per < nu) L <<= 1;
+    if (nu <= (uv ? kSegMaxUnitsVec : kSegMaxUnitsElem)) {
+      p.seg_lanes = L;
+      p.unit_vec = uv;
+      p.groups = kmin<int64_t>((cols + kDimBlock / L - 1) / (kDimBlock / L), kSegMaxBlocks);
+      p.split = 1;
+    } else {
+      p.groups = kmin<int64_t>((cols + kDimWaves - 1) / kDimWaves, kColsMaxBlocks);
+      int64_t S = 1;
+      if (cols < 16384) {
+        // The split partials are a cols x S matrix; when it is narrow its
+        // combine is reduce_rows_narrow_kernel and S may be large (few long
+        // columns), else the serial combine_split_kernel keeps S small.
+        const bool narrow2 = row_units(es, cols, true) <= kDimBlock;
+        S = (16384 + cols - 1) / cols;
+        const int64_t by_rows = rows / ((int64_t)kWave * 4 * kDimUnroll * 4);  // >= 4 unrolled passes each
+        S = kmin<int64_t>(S, kmax<int64_t>(by_rows, 1));
+        S = kmin<int64_t>(S, narrow2 ? kDimMaxSplitNarrow : kDimMaxSplit);
+      }
+      p.split = (int)S;
+    }
+  } else if (row_units(es, rows, vec) <= kDimBlock) {
+    // Narrow: one strip covers every row; column ranges fill the GPU.
+    const int64_t nu = row_units(es, rows, vec);
+    p.narrow = true;
+    p.unit_vec = vec && nu != rows;
+    p.groups = 1;
+    const int64_t P = kDimBlock / kmax<int64_t>(nu, 1);
+    int64_t S = (kNarrowBlocks + nb - 1) / nb;
+    S = kmin<int64_t>(S, kmax<int64_t>(cols / (2 * kNarrowUnroll * P), 1));
+    p.split = (int)kmin<int64_t>(S, 65535);
+  } else {
+    // Aligned path: the widest strip that still leaves one workgroup per
+    // CU, so each workgroup streams the longest contiguous runs; with too
+    // few rows even for 1-vector strips, columns are split instead.
+    // Float32: 4M x 64 6.8 TB/s at 8 vectors (512 workgroups) against 5.7
+    // at 2; 1M x 256 7.1 at 4 against 5.6 at 2; 65536 x 4096 6.8 at 1 (S = 4)
+    // against 6.6 at 2 (S = 8) and 6.1 at 4 (S = 16).
+    int rv = kRowVecsDefault;
+    if (vec) {
+      rv = 1;
+      for (int c = kDim2MaxRowVecs; c > 1; c /= 2) {
+        const int64_t rsc = (int64_t)kDimBlock * c * epv;
+        if (rows / rsc * nb >= kDim2Blocks) {  // whole strips only
+          rv = c;
+          break;
+        }
+      }
+    }
+    p.row_vecs = rv;
+    const int cu = vec ? col_unroll_for(rv) : kColUnrollDefault;
+    const int64_t rs = (int64_t)kDimBlock * rv * epv;
+    p.groups = (rows + rs - 1) / rs;
+    int64_t S = 1;
+    if (p.groups * nb < kDim2Blocks) {
+      S = (kDim2Blocks + p.groups * nb - 1) / (p.groups * nb);
+      S = kmin<int64_t>(S, kmax<int64_t>(cols / (2 * cu), 1));
+      S = kmin<int64_t>(S, 256);
+    }
+    p.split = (int)S;
+  }
+  if (p.split > 1) p.partial_bytes = round256((size_t)p.split * (size_t)(dim == 1 ? cols : rows) * es * (size_t)nb);
+  return p;
+}
+
+inline bool dim_vec_ok(const void* A, int64_t cs, size_t es) {
+  return ((uintptr_t)A % 16 == 0) && ((cs * (int64_t)es) % 16 == 0);
+}
+
+// Alignment decisions of a dims launch, shared by the entry-point scratch
+// checks and the launch itself. vec: 16-byte paths. peel (dim 2): A is
+// misaligned but every column (and batch entry) shares its misalignment, so
+// the first `peel` rows go to an element-path launch and the rest, from an
+// aligned A + peel, to the vector paths.
+// Shorter columns stay on the element path: split-off head and tail rows
+// would fetch each column's first and last lines again (16 rows: 2.0 TB/s
+// split against 2.9 unsplit).
+constexpr int64_t kPeelMinColumnBytes = 2048;
+struct DimVec {
+  bool vec;
+  int64_t head, tail;  // dim 2 rows split off to element-path launches
+};
+inline DimVec dim_vec(const void* A, int64_t rows, int64_t cs, size_t es, int dim, int64_t batch,
+                      int64_t a_bstride, bool has_x, const void* x, int64_t xs) {
+  const bool strides16 = (cs * (int64_t)es) % 16 == 0 && (batch <= 1 || (a_bstride * (int64_t)es) % 16 == 0);
+  DimVec v{strides16 && (uintptr_t)A % 16 == 0, 0, 0};
+  // vecmat (dim 1 with an operand) reads x along the rows: vector path only if x is too
+  if (has_x && dim == 1) v.vec = v.vec && xs == 1 && (uintptr_t)x % 16 == 0;
+  if (dim == 2 && strides16) {
+    // head: rows before the first 16-byte boundary; tail: rows after the
+    // last whole vector. The vector launch in between has rows % EPV == 0.
+    const int64_t ev = (int64_t)(16 / es);
+    const int64_t h = (int64_t)(((16 - (uintptr_t)A % 16) % 16) / es);
+    if (h < rows && rows * (int64_t)es >= kPeelMinColumnBytes) {
+      const int64_t t = (rows - h) % ev;
+      if (rows - h - t > 0 && (h > 0 || t > 0)) v = {true, h, t};
+    }
+  }
+  // an unsplit dim-2 vector launch needs rows % EPV == 0
+  if (dim == 2 && v.vec && !v.head && !v.tail && rows % (int64_t)(16 / es) != 0) v.vec = false;
+  return v;
+}
+
+// A dim-2 vector launch covers whole strips only: rows past the last whole
+// strip go to further launches under the same rule (ending in the narrow
+// kernel). Partial bytes of that decomposition:
+inline size_t dim2_vec_need(size_t es, int64_t rows, int64_t cols, int64_t batch) {
+  const DimPlan p = plan_dim(es, rows, cols, 2, true, batch);
+  if (p.narrow) return p.partial_bytes;
+  const int64_t rs = (int64_t)kDimBlock * p.row_vecs * (int64_t)(16 / es);
+  const int64_t whole = rows / rs * rs;
+  if (whole == rows || whole == 0) return p.partial_bytes;
+  return kmax(dim2_vec_need(es, whole, cols, batch), dim2_vec_need(es, rows - whole, cols, batch));
+}
+
+// Partial bytes the launch will use for this alignment (0: no scratch).
+inline size_t dim_need(size_t es, int64_t rows, int64_t cols, int dim, int64_t batch, DimVec v) {
+  if (v.head || v.tail) {
+    size_t b = dim2_vec_need(es, rows - v.head - v.tail, cols, batch);
+    if (v.head) b = kmax(b, plan_dim(es, v.head, cols, 2, false, batch).partial_bytes);
+    if (v.tail) b = kmax(b, plan_dim(es, v.tail, cols, 2, false, batch).partial_bytes);
+    return b;
+  }
+  if (dim == 2 && v.vec) return dim2_vec_need(es, rows, cols, batch);
+  return plan_dim(es, rows, cols, dim, v.vec, batch).partial_bytes;
+}
+// Scratch query: the largest need over every alignment case.
+inline size_t dim_query(size_t es, int64_t rows, int64_t cols, int dim, int64_t batch) {
+  size_t b = kmax(plan_dim(es, rows, cols, dim, true, batch).partial_bytes,
+                  plan_dim(es, rows, cols, dim, false, batch).partial_bytes);
+  if (dim == 2) {
+    const int64_t ev = (int64_t)(16 / es);
+    if (rows % ev == 0) b = kmax(b, dim2_vec_need(es, rows, cols, batch));
+    for (int64_t h = 0; h < ev && h < rows; ++h) {
+      const int64_t t = (rows - h) % ev;  // the tail a head of h rows leaves
+      if (rows - h - t > 0 && (h > 0 || t > 0)) b = kmax(b, dim_need(es, rows, cols, 2, batch, {true, h, t}));
+    }
+  }
+  return kRedReserved + kmax<size_t>(256, b);
+}
+
+template <class T, class Op, class F>
+void launch_narrow(bool unit_vec, dim3 grid, const T* A, int64_t rows, int64_t cols, int64_t cs, T* out, int64_t ods,
+                   int64_t seg, int64_t a_bstride, int64_t out_bstride, const T* x, int64_t xs, hipStream_t stream) {
+  if (unit_vec)
+    hipLaunchKernelGGL((reduce_rows_narrow_kernel<T, Op, F, true>), grid, dim3(kDimBlock), 0, stream, A, rows, cols,
+                       cs, out, ods, seg, a_bstride, out_bstride, x, xs);
+  else
+    hipLaunchKernelGGL((reduce_rows_narrow_kernel<T, Op, F, false>), grid, dim3(kDimBlock), 0, stream, A, rows, cols,
+                       cs, out, ods, seg, a_bstride, out_bstride, x, xs);
+}
+
+// Second stage of a split dims reduction: nz batches of an m x S partial
+// matrix (column s at s*m, batch z at z*S*m; the scratch is 256-byte
+// aligned) reduced along dim 2 into dst[i*ds + z*dst_bstride].
+template <class T, class Op>
+void launch_combine(const T* part, int S, int64_t m, T* dst, int64_t ds, int64_t dst_bstride, unsigned nz,
+                    hipStream_t stream) {
+  const int64_t nu = row_units(sizeof(T), m, true);
+  if (nu <= kDimBlock)
+    launch_narrow<T, Op, Unary<MapIdentity>>(nu != m, dim3(1, 1, nz), part, m, S, m, dst, ds, S, (int64_t)S * m,
+                                             dst_bstride, nullptr, 0, stream);
+  else
+    hipLaunchKernelGGL((combine_split_kernel<T, Op>), dim3((unsigned)((m + kRedBlock - 1) / kRedBlock), nz),
+                       dim3(kRedBlock), 0, stream, part, S, m, dst, ds, dst_bstride);
+}
+
+template <class T, class Op, class F>
+int launch_reduce_dim(const void* A, int64_t rows, int64_t cols, int64_t cs, int dim, void* dst,
+                      int64_t ds, void* scratch, hipStream_t stream, int64_t batch = 1, int64_t a_bstride = 0,
+                      const void* x = nullptr, int64_t xs = 0, int64_t dst_bstride = -1, bool may_peel = true) {
+  if (dst_bstride < 0) dst_bstride = rows * ds;
+  const DimVec dv = dim_vec(A, rows, cs, sizeof(T), dim, batch, a_bstride, F::kHasX, x, xs);
+  if (may_peel && (dv.head || dv.tail)) {
+    // element-path launches for the head and tail rows around the vector
+    // launch; stream order lets all of them use the same scratch
+    const int64_t body = rows - dv.head - dv.tail;
+    int rc = KF_OK;
+    if (dv.head)
+      rc = launch_reduce_dim<T, Op, F>(A, dv.head, cols, cs, 2, dst, ds, scratch, stream, batch, a_bstride, x, xs,
+                                       dst_bstride, false);
+    if (!rc)
+      rc = launch_reduce_dim<T, Op, F>((const T*)A + dv.head, body, cols, cs, 2, (T*)dst + dv.head * ds, ds, scratch,
+                                       stream, batch, a_bstride, x, xs, dst_bstride, false);
+    if (!rc && dv.tail)
+      rc = launch_reduce_dim<T, Op, F>((const T*)A + dv.head + body, dv.tail, cols, cs, 2,
+                                       (T*)dst + (dv.head + body) * ds, ds, scratch, stream, batch, a_bstride, x, xs,
+                                       dst_bstride, false);
+    return rc;
+  }
+  const bool vec = dv.vec;
+  const DimPlan p = plan_dim(sizeof(T), rows, cols, dim, vec, batch);
+  if (dim == 2 && vec && !p.narrow) {
+    // the vector kernel takes whole strips only; the rest is launched under
+    // the same rule (stream order lets the launches share the scratch)
+    const int64_t rs = (int64_t)kDimBlock * p.row_vecs * (int64_t)(16 / sizeof(T));
+    const int64_t whole = rows / rs * rs;
+    if (whole != rows && whole > 0) {
+      int rc = launch_reduce_dim<T, Op, F>(A, whole, cols, cs, 2, dst, ds, scratch, stream, batch, a_bstride, x, xs,
+                                           dst_bstride, false);
+      if (!rc)
+        rc = launch_reduce_dim<T, Op, F>((const T*)A + whole, rows - whole, cols, cs, 2, (T*)dst + whole * ds, ds,
+                                         scratch, stream, batch, a_bstride, x, xs, dst_bstride, false);
+      return rc;
+    }
+  }
+  if (dim == 1) {
+    if (p.seg_lanes) {
+      const dim3 grid((unsigned)p.groups);
+#define KF_SEG(V, L)                                                                                          \
+  hipLaunchKernelGGL((reduce_cols_seg_kernel<T, Op, F, V, L>), grid, dim3(kDimBlock), 0, stream, (const T*)A, rows, \
+                     cols, cs, (T*)dst, ds, (const T*)x, xs)
+#define KF_SEG_L(V)                    \
+  switch (p.seg_lanes) {               \
+    case 1: KF_SEG(V, 1); break;       \
+    case 2: KF_SEG(V, 2); break;       \
+    case 4: KF_SEG(V, 4); break;       \
+    case 8: KF_SEG(V, 8); break;       \
+    default: KF_SEG(V, 16); break;     \
+  }
+      if (p.unit_vec) {
+        KF_SEG_L(true)
+      } else {
+        KF_SEG_L(false)
+      }
+#undef KF_SEG_L
+#undef KF_SEG
+      return kf_check_launch("reduce_cols_seg_kernel");
+    }
+    T* out = p.split > 1 ? (T*)scratch : (T*)dst;
+    constexpr int EPV = 16 / (int)sizeof(T);
+    int64_t seg = (rows + p.split - 1) / p.split;
+    seg = (seg + EPV - 1) / EPV * EPV;
+    hipLaunchKernelGGL((reduce_cols_kernel<T, Op, F>), dim3((unsigned)p.groups, p.split), dim3(kDimBlock), 0,
+                       stream, (const T*)A, rows, cols, cs, out, ds, seg, (int)vec, (const T*)x, xs);
+    if (p.split > 1) launch_combine<T, Op>((const T*)scratch, p.split, cols, (T*)dst, ds, 0, 1, stream);
+    return kf_check_launch("reduce_cols_kernel");
+  }
+  // dim 2, batched: dst[i*ds + z*dst_bstride] = op_j f(A[i + j*cs + z*a_bstride])
+  const int64_t seg = (cols + p.split - 1) / p.split;
+  for (int64_t z0 = 0; z0 < batch; z0 += kMaxBatchPerLaunch) {
+    const unsigned nz = (unsigned)kmin<int64_t>(kMaxBatchPerLaunch, batch - z0);
+    const T* Az = (const T*)A + z0 * a_bstride;
+    T* dz = (T*)dst + z0 * dst_bstride;
+    T* out = p.split > 1 ? (T*)scratch : dz;
+    const dim3 grid((unsigned)p.groups, p.split, nz);
+    if (p.narrow) {
+      launch_narrow<T, Op, F>(p.unit_vec, grid, Az, rows, cols, cs, out, ds, seg, a_bstride, dst_bstride, (const T*)x,
+                              xs, stream);
+      if (p.split > 1) launch_combine<T, Op>((const T*)scratch, p.split, rows, dz, ds, dst_bstride, nz, stream);
+      continue;
+    }
+#define KF_ROWS_VEC(RV)                                                                                  \
+  hipLaunchKernelGGL((reduce_rows_kernel<T, Op, F, true, RV, col_unroll_for(RV)>), grid, dim3(kDimBlock), 0, stream, \
+                     Az, rows, cols, cs, out, ds, seg, a_bstride, dst_bstride, (const T*)x, xs)
+    if (vec) {
+      switch (p.row_vecs) {
+        case 1: KF_ROWS_VEC(1); break;
+        case 2: KF_ROWS_VEC(2); break;
+        case 4: KF_ROWS_VEC(4); break;
+        default: KF_ROWS_VEC(8); break;
+      }
+    } else
+      hipLaunchKernelGGL((reduce_rows_kernel<T, Op, F, false>), grid, dim3(kDimBlock), 0, stream, Az, rows, cols,
+                         cs, out, ds, seg, a_bstride, dst_bstride, (const T*)x, xs);
+    if (p.split > 1) launch_combine<T, Op>((const T*)scratch, p.split, rows, dz, ds, dst_bstride, nz, stream);
+  }
+#undef KF_ROWS_VEC
+  return kf_check_launch("reduce_rows_kernel");
+}
+
+template <class T, class Op, class Map> struct ReduceDimL {
+  static int run(const void* A, int64_t rows, int64_t cols, int64_t cs, int dim, void* dst, int64_t ds,
+                 void* scratch, hipStream_t s, int64_t batch, int64_t a_bstride) {
+    return launch_reduce_dim<T, Op, Unary<Map>>(A, rows, cols, cs, dim, dst, ds, red_work(scratch), s, batch,
+                                                a_bstride);
+  }
+};
+
+}  // namespace kf

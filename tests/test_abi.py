@@ -51,6 +51,22 @@ def test_scratch_queries(kf):
     assert L.kf_reduce_dim_scratch_bytes(kf._lib.F32, 2**24, 2, 1) > 256
 
 
+def test_dims_scratch_queries_over_shapes(kf):
+    # host-only plan walk (no GPU): every dtype, both dims, plain and
+    # batched, over row counts around the vector width, the narrow limit and
+    # whole-strip boundaries; each query returns a positive size (the
+    # largest need over every alignment case) without faulting on the host
+    L = kf._lib.lib()
+    rows_set = sorted({1, 2, 3, 5, 15, 16, 17, 255, 256, 257, 511, 512, 513, 1000, 1023, 1024, 1025, 2047,
+                       4093, 4096, 4099, 8191, 8192, 8195, 65535, 65536, 1048572, 1048575, 2_100_003})
+    for dt in (kf._lib.F32, kf._lib.F64, kf._lib.I32, kf._lib.I64, kf._lib.U8):
+        for rows in rows_set:
+            for cols in (1, 3, 40, 4096, 100_003):
+                for dim in (1, 2):
+                    assert L.kf_reduce_dim_scratch_bytes(dt, rows, cols, dim) >= 256
+                assert L.kf_reduce_dim_batched_scratch_bytes(dt, rows, cols, 7) >= 256
+
+
 def _err(kf):
     return kf._lib.lib().kf_last_error().decode()
 

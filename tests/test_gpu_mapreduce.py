@@ -2,6 +2,8 @@
 against the pinned CPU oracle. Integers and max/min are exact; float sums
 are checked against a Float64 host sum with |err| <= rtol * sum(|f(x)|)
 (the error bound of any summation order), rtol stated per test."""
+import sys
+
 import numpy as np
 import pytest
 import torch
@@ -268,6 +270,67 @@ def test_dims1_column_count_beyond_one_grid(kf, dev):
     rng = np.random.default_rng(13)
     _exact_dims_case(kf, dev, rng, np.uint8, 1, (1 << 26) + 5, 1, ops=("+",))
     _exact_dims_case(kf, dev, rng, np.uint8, 2064, 270_000, 1, ops=("max",))
+
+
+@pytest.mark.parametrize("dt", [np.int32, np.int64, np.uint8])
+def test_dims2_misaligned_base_peeled(kf, dev, dt):
+    # A misaligned by k elements with a 16-byte-multiple column stride: the
+    # first 16/es - k rows take an element-path launch, the rest the vector
+    # paths from an aligned base; plain, batched (grid.z) and matvec forms
+    rng = np.random.default_rng(14)
+    ev = 16 // np.dtype(dt).itemsize
+    hi = 256 if dt == np.uint8 else 1 << 20
+    for rows, cols in ((5, 9), (100, 1000), (1000, 77), (5000, 3000), (70_000, 40), (1 << 20, 3)):
+        cs = -(-(rows + ev) // ev) * ev
+        buf = torch.from_numpy(rng.integers(0, hi, cs * cols + ev).astype(dt)).to(dev)
+        for k in sorted({0, 1, ev // 2, ev - 1}):
+            A = buf.as_strided((rows, cols), (1, cs), k)
+            M = A.cpu().numpy()
+            for op in ("+", "max"):
+                got = kf.mapreduce(kf.identity, op, A, dims=2).cpu().numpy().reshape(-1)
+                ref = M.sum(axis=1, dtype=dt) if op == "+" else M.max(axis=1)
+                assert np.array_equal(got, ref), (rows, cols, k, op)
+    # batched: Julia rows x cols x nb with a 16-byte-multiple batch stride
+    rows, cols, nb = 37, 50, 6
+    cs = -(-(rows + ev) // ev) * ev
+    buf = torch.from_numpy(rng.integers(0, hi, cs * cols * nb + ev).astype(dt)).to(dev)
+    X = buf.as_strided((rows, cols, nb), (1, cs, cs * cols), 1)
+    got = kf.mapreduce(kf.identity, "+", X, dims=2).cpu().numpy()
+    assert np.array_equal(got, X.cpu().numpy().sum(axis=1, keepdims=True, dtype=dt))
+    if dt != np.uint8:
+        x = torch.from_numpy(rng.integers(-5, 5, cols).astype(dt)).to(dev)
+        A = buf[: cs * cols + ev].as_strided((rows, cols), (1, cs), 2)
+        got = kf.matvec(A, x).cpu().numpy()
+        ref = (A.cpu().numpy() * x.cpu().numpy()[None, :]).sum(axis=1, dtype=dt)
+        assert np.array_equal(got, ref)
+
+
+def test_vecmat_scratch_contract_with_misaligned_operand(kf, dev):
+    # The C ABI decides scratch from the alignment the launch uses (here the
+    # misaligned x sends vecmat to the element path). A shape whose launch
+    # splits its rows is refused without scratch, on the host, before any
+    # launch; one that does not split runs without scratch; both are exact
+    # with the queried scratch.
+    import ctypes
+    L = sys.modules["kernelforge_amd._lib"]
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    for rows, cols, splits in ((100_000, 40, True), (512, 40, False)):
+        A = torch.randint(-9, 9, (cols, rows), dtype=torch.int32, device=dev).T
+        x = torch.randint(-9, 9, (rows + 1,), dtype=torch.int32, device=dev)[1:]
+        dst = torch.zeros(cols, dtype=torch.int32, device=dev)
+        args = (L.OP_ADD, L.MAP2_MUL, L.I32, P(A), rows, cols, rows, 1, P(x), 1, P(dst), 1)
+        ref = (A.cpu().numpy().astype(np.int64) * x.cpu().numpy()[:, None]).sum(axis=0).astype(np.int32)
+        rc = L.lib().kf_reduce_dim_x(*args, None, 0, stream)
+        if splits:
+            assert rc == L.KF_ENOSCRATCH
+        else:
+            assert rc == L.KF_OK and np.array_equal(dst.cpu().numpy(), ref)
+        need = L.lib().kf_reduce_dim_scratch_bytes(L.I32, rows, cols, 1)
+        tmp = torch.zeros(need, dtype=torch.uint8, device=dev)
+        dst.zero_()
+        assert L.lib().kf_reduce_dim_x(*args, P(tmp), need, stream) == L.KF_OK
+        assert np.array_equal(dst.cpu().numpy(), ref), (rows, cols)
 
 
 def test_dims_golden(kf, dev, golden):
