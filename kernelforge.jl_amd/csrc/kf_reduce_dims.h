@@ -341,12 +341,20 @@ __global__ __launch_bounds__(kDimBlock) void reduce_rows_kernel(
         }
   }
 #pragma unroll
-  for (int u = 0; u < kRowVecs; ++u)
+  for (int u = 0; u < kRowVecs; ++u) {
+    const int64_t r0 = strip + (int64_t)(u * kDimBlock + tid) * EPV;
+    T* o = gridDim.y == 1 ? out + r0 * out_stride : out + (int64_t)s * rows + r0;
+    if (VEC && (gridDim.y > 1 || out_stride == 1) && (uintptr_t)o % 16 == 0) {
+      // whole strip, contiguous aligned outputs: one 16-byte store
+      uint4 v;
+      __builtin_memcpy(&v, a[u], sizeof(v));
+      *reinterpret_cast<uint4*>(o) = v;
+    } else {
 #pragma unroll
-    for (int e = 0; e < EPV; ++e) {
-      const int64_t r = strip + (int64_t)(u * kDimBlock + tid) * EPV + e;
-      if (r < rows) out[gridDim.y == 1 ? r * out_stride : (int64_t)s * rows + r] = a[u][e];
+      for (int e = 0; e < EPV; ++e)
+        if (r0 + e < rows) o[gridDim.y == 1 ? e * out_stride : e] = a[u][e];
     }
+  }
 }
 
 
