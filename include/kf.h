@@ -189,6 +189,11 @@ int kf_reduce3(kf_op op, kf_map3 f, kf_dtype dt,
  *   dim = 1: dst[j * dst_stride] = op_i f(A[i, j])   (cols outputs)
  *   dim = 2: dst[i * dst_stride] = op_j f(A[i, j])   (rows outputs)
  * op must be commutative (ADD, MAX, MIN).
+ * Scratch holds split partials; whether a call splits depends on the shape
+ * and on the alignment of A (and of x for vecmat), and the query returns the
+ * largest need over every alignment, so one buffer of that size serves any
+ * A of this shape. A call that does not split accepts a null scratch; one
+ * that does is refused with KF_ENOSCRATCH before any launch.
  *
  * Replaces the reference's mapreduce2d!(f, op, dst, src, dim)
  *   src/mapreduce/2D/mapreduce2d.jl:111-126, which routes dim=1 to
