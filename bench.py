@@ -11,9 +11,10 @@ events on the stream the kernels run on, the measured copy ceiling, and the
 CPU baseline (the oracle's restatement of Base.accumulate! / Base.mapreduce,
 timed on this host).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--all]
-  --all   also time every BASELINE.json configuration (stderr table and
-          gpurun_out/bench_all.json).
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--all [--all-json PATH]]
+  --all       also time every BASELINE.json configuration (stderr table, and
+              the rows inside the JSON line as "all_configs")
+  --all-json  also write those rows, with the copy ceiling, to PATH
 """
 import argparse
 import json
@@ -102,6 +103,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--all", action="store_true")
+    ap.add_argument("--all-json", default=None)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--sweep", action="store_true",
                     help="the reference's scan/mapreduce size sweep (perfs/julia/benchmarks)")
@@ -211,7 +213,7 @@ def main():
         "wall_s_timed": round(wall, 4),
     }
     if args.all:
-        line["all_configs"] = bench_all(kf, dev, ceiling)
+        line["all_configs"] = bench_all(kf, dev, ceiling, args.all_json)
     if args.sweep:
         line["sweep"] = bench_sweep(kf, dev, ceiling)
     print(json.dumps(line), flush=True)
@@ -262,7 +264,7 @@ def bench_sweep(kf, dev, ceiling):
     return rows
 
 
-def bench_all(kf, dev, ceiling):
+def bench_all(kf, dev, ceiling, json_path=None):
     """Every BASELINE.json configuration: GB/s, % of peak, % of the copy ceiling."""
     rows = []
     g = torch.Generator(device=dev).manual_seed(20261201)
@@ -366,9 +368,10 @@ def bench_all(kf, dev, ceiling):
         ys = torch.empty_like(xs)
         ts = tmp_for(kf.Scan1D, xs)
         rec(f"X7 scan F32 incl n={label}", 8 * n, lambda: kf.scan_("+", ys, xs, tmp=ts))
-    os.makedirs(os.path.join(REPO, "gpurun_out"), exist_ok=True)
-    with open(os.path.join(REPO, "gpurun_out", "bench_all.json"), "w") as fh:
-        json.dump({"copy_ceiling_gbps": ceiling, "rows": rows}, fh, indent=1)
+    if json_path:
+        os.makedirs(os.path.dirname(os.path.abspath(json_path)), exist_ok=True)
+        with open(json_path, "w") as fh:
+            json.dump({"copy_ceiling_gbps": ceiling, "rows": rows}, fh, indent=1)
     return rows
 
 
