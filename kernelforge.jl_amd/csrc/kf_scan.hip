@@ -8,7 +8,7 @@
 // design differs from the reference in these ways:
 //
 //  * Large tiles: 8 16-byte vectors per lane x 1024 threads = 128 KiB (768
-//    threads = 96 KiB for 4- and 8-byte types from 512 MiB on; 512 threads
+//    threads = 96 KiB for 4- and 8-byte types from 20 MiB on; 512 threads
 //    x 8/12/16 vectors for UInt8; 2 or 4 vectors per lane for arrays too
 //    small to make 240 such tiles), so 2^28 Float32 is 10923 tiles and the
 //    per-tile lookback is amortised over a large streaming body. The tile
@@ -93,7 +93,14 @@ template <class T> constexpr int kMinTier = sizeof(T) == 1 ? 0 : 1;
 // 10^9 343 -> 329 us at 12; 2^30 361 -> 341 us, 2^31 702 -> 657 us at 16,
 // where 12 gives 350 / 673 (20 and 24 vectors lose 8-10 %; at 32 the
 // compiler no longer keeps the tile in registers).
-constexpr int64_t kWideBytes = 1LL << 29;
+// The 4- and 8-byte types take it from 20 MiB, where two co-resident 96 KiB
+// tiles per CU balance the last round of tiles better than one 128 KiB tile
+// (HIP graphs, us, 1024 x 8 -> 768 x 8): Float32 6*10^6 11.3 -> 9.9, 10^7
+// 16.4 -> 14.6, 10^8 124.3 -> 122.7; Float64 6*10^6 24.6 -> 17.9, 10^7
+// 35.6 -> 31.5, 2*10^7 64.5 -> 55.1, 5*10^7 142.0 -> 125.4; affine pairs
+// 5*10^6 21.5 -> 17.0, 5*10^7 141.8 -> 125.6. Worst case Float32 2*10^7
+// 29.7 -> 30.6; below 20 MiB (Float32 4*10^6) the 64 KiB tiles stay ahead.
+constexpr int64_t kWideBytes = 20LL << 20;
 constexpr int64_t kHugeBytes = 1LL << 30;
 // UInt8 takes the 12-vector shape from 256 MiB (3*10^8: 118 -> 116 us; at
 // 10^8 the 8-vector tiles stay ahead, 50.6 vs 53.3 us).

@@ -294,8 +294,8 @@ def test_views_offsets_strides_inplace(kf, oracle, dev):
 
 @pytest.mark.parametrize("dt", [np.float32, np.float64, np.int32, np.int64, np.uint8])
 def test_tile_size_switchover(kf, oracle, dev, dt):
-    # tiles are 1024 threads (512 for uint8; 768 for 4- and 8-byte types
-    # from 512 MiB on; uint8's own 12- and 16-vector shapes from 256 MiB and
+    # tiles are 1024 threads (512 for uint8; 768 x 8 vectors for 4- and
+    # 8-byte types from 20 MiB on; uint8's own 12- and 16-vector shapes from 256 MiB and
     # 1 GiB are checked in test_gpu_large.py) x V 16-byte vectors, V in
     # (1, 2, 4, 8): the largest V that still makes >= 240 tiles (480 for
     # uint8), never below 2 except for uint8. The lookback polls 64 tiles
@@ -311,7 +311,7 @@ def test_tile_size_switchover(kf, oracle, dev, dt):
     if dt != np.uint8:
         edges.append(4 * 512 * block * 8 * epv)        # window 2 from 4 generations of 128 KiB tiles
     if dt in (np.float32, np.float64, np.int32, np.int64):
-        edges.append(2**29 // np.dtype(dt).itemsize)   # 768-thread tiles from 512 MiB on
+        edges.append((20 << 20) // np.dtype(dt).itemsize)   # 768-thread tiles from 20 MiB on
     for e in edges:
         for n in (e - 1, e, e + 1):
             x = (rng.random(n) < 1 / 16).astype(dt) if np.dtype(dt).kind == "f" else gen(rng, dt, n)
