@@ -225,6 +225,18 @@ def test_affine_scan(kf, oracle, dev, n):
         assert_mixed(got, oracle.scan(ab, "affine", exclusive=exclusive), 1e-5, what=f"affine n={n} excl={exclusive}")
 
 
+@pytest.mark.parametrize("n", [(20 << 20) // 8 - 1, (20 << 20) // 8, 10**7 + 3])
+def test_affine_scan_wide_tiles(kf, oracle, dev, n):
+    # the affine pairs (8 bytes) switch from 1024 x 4-vector tiles to
+    # 768 x 8-vector tiles at 20 MiB; 10^7 pairs give more tiles than the GPU
+    # holds at once, so the windowed lookback runs as well
+    rng = np.random.default_rng(n)
+    ab = np.stack([rng.uniform(0.9, 1.0, n), rng.standard_normal(n)], 1).astype(np.float32)
+    for exclusive in (False, True):
+        got = kf.scan(kf.affine, torch.from_numpy(ab).to(dev), exclusive=exclusive).cpu().numpy()
+        assert_mixed(got, oracle.scan(ab, "affine", exclusive=exclusive), 1e-5, what=f"affine n={n} excl={exclusive}")
+
+
 def test_affine_is_order_sensitive(kf, oracle, dev):
     # a = 2 on even, 1/2 on odd positions with b = index: any reordering of
     # combines changes the result, exact in binary floating point
