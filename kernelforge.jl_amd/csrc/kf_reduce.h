@@ -19,7 +19,6 @@ inline size_t round256(size_t b) { return (b + 255) & ~(size_t)255; }
 // reduce_once_kernel. Partial buffers of all reduction kinds sit after it,
 // so stale partials of other calls can never read as current fold slots.
 constexpr int kFoldMax = 2048;  // workgroups a single-level fold combines
-constexpr bool kUseFold = true;
 constexpr size_t kRedReserved = 256 + (size_t)kFoldMax * 16;
 inline void* red_work(void* scratch) { return scratch ? (uint8_t*)scratch + kRedReserved : nullptr; }
 

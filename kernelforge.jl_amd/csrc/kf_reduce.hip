@@ -7,16 +7,17 @@
 //  * Stage 1 streams with 16-byte nontemporal loads, several in flight per
 //    lane, every vector element folded into its own accumulator (16
 //    independent Float32 sums per lane: accurate and dependency-free).
-//  * Stage 2 is a second, tiny kernel on the same stream. The reference's
-//    single launch lets workgroup 1 spin on per-workgroup flags
-//    (mapreduce1d_kernel.jl:66-92); a "last workgroup done" ticket was
-//    measured here to serialise thousands of same-address device atomics
-//    at the end of the grid (the full reduction ran at 1.8 TB/s with 8192
-//    workgroups), and fences cost more than the launch they save. Grids of
-//    up to kFoldMax workgroups skip the launch with an atomic-free fold
-//    instead: epoch-tagged partial slots written with relaxed device-scope
-//    stores and gathered by the last workgroup (fold_partial), which saves
-//    a launch's host cost (eager 10^6 Float32: 11.0 -> 8.7 us).
+//  * The combine is an atomic-free fold inside the last launch: the
+//    reference's single launch lets workgroup 1 spin on per-workgroup flags
+//    (mapreduce1d_kernel.jl:66-92); here the last level's workgroups (at
+//    most kFoldMax) publish epoch-tagged partial slots with relaxed
+//    device-scope stores and the last workgroup gathers them
+//    (fold_partial). Arrays of up to 8*256*kFoldMax vectors (64 MiB) take one
+//    launch; larger ones a one-shot level 0 that writes partials and a
+//    folding level 1. A "last workgroup done" ticket was measured to
+//    serialise same-address device atomics at the end of the grid (1.8
+//    TB/s with 8192 workgroups), and fences cost more than the launch they
+//    save.
 //  * Combine orders depend only on the shape and pointer alignment, so every
 //    result is bit-for-bit reproducible run to run.
 #include "kf_reduce.h"
@@ -191,7 +192,7 @@ template <class T, class Op> __device__ inline void fold_partial(T part, T* out,
   }
 }
 
-template <class T, class Op, class Map, bool FOLD = false>
+template <class T, class Op, class Map, bool FOLD = false, int U = kOnceUnroll>
 __global__ __launch_bounds__(kRedBlock) void reduce_once_kernel(const T* src, int64_t n, int64_t head,
                                                                 int64_t nvec, T* out, uint64_t* fold_hdr) {
   constexpr int EPV = 16 / (int)sizeof(T);
@@ -199,16 +200,16 @@ __global__ __launch_bounds__(kRedBlock) void reduce_once_kernel(const T* src, in
   const T id = Op::template identity<T>();
   const int tid = threadIdx.x;
   const uint4* v = reinterpret_cast<const uint4*>(src + head);
-  const int64_t base = (int64_t)blockIdx.x * kOnceVecs + tid;
-  uint4 r[kOnceUnroll];
+  const int64_t base = (int64_t)blockIdx.x * (kRedBlock * U) + tid;
+  uint4 r[U];
 #pragma unroll
-  for (int u = 0; u < kOnceUnroll; ++u)
+  for (int u = 0; u < U; ++u)
     if (base + u * kRedBlock < nvec) r[u] = ld_stream(v + base + u * kRedBlock);
   T a[EPV];
 #pragma unroll
   for (int e = 0; e < EPV; ++e) a[e] = id;
 #pragma unroll
-  for (int u = 0; u < kOnceUnroll; ++u)
+  for (int u = 0; u < U; ++u)
     if (base + u * kRedBlock < nvec) {
       T x[EPV];
       __builtin_memcpy(x, &r[u], 16);
@@ -269,17 +270,39 @@ template <class T> int reduce_grid(int64_t n) {
   return (int)kmax<int64_t>(g, 1);
 }
 
-// Level sizes of the vector path: partial counts after each one-shot level
-// until at most kRedMaxBlocks remain for combine_all_kernel.
+// Level sizes of the vector path. Level 0 reads the input with u0 16-byte
+// vectors per lane; every later level reduces the previous level's partials
+// (read as 16-byte vectors) with kOnceUnroll per lane, until at most
+// kFoldMax partial-producing workgroups remain: the last level folds its
+// partials into the result inside the same launch (fold_partial), so no
+// separate combine launch is needed. u0 is the smallest of 2, 4 and 8 that
+// brings level 0 itself under kFoldMax (one launch in all), else 2.
+// Measured on MI355X (F32 sum): 2^28 157 us in two launches (level 0 at
+// u0 = 2, 4 or 8 within 1 %; before, a third combine_all_kernel launch made
+// it 160-162 us); 10^7 one launch at u0 = 8, 7.0 us in a HIP graph.
+// Single-launch alternatives measured slower at 2^28: 2048 persistent
+// workgroups over contiguous chunks (161 us), one-shot workgroups whose
+// group leaders wait for their group's partials (165 us; 160 us with the
+// groups formed per XCD), and a last-arriver fold by device-scope atomic
+// counters (188 us: the atomics serialise).
 struct OnceLevels {
   int nlev;
+  int u0;
   int64_t count[8];
 };
-inline OnceLevels once_levels(int64_t nvec, int epv) {
+inline OnceLevels once_levels(int64_t nvec, int epv, bool adaptive = true) {
   OnceLevels L{};
-  int64_t c = kmax<int64_t>(1, (nvec + kOnceVecs - 1) / kOnceVecs);
+  L.u0 = kOnceUnroll;
+  if (adaptive) {
+    for (int u = kOnceUnroll; u <= 8; u *= 2)
+      if ((nvec + (int64_t)kRedBlock * u - 1) / ((int64_t)kRedBlock * u) <= kFoldMax) {
+        L.u0 = u;
+        break;
+      }
+  }
+  int64_t c = kmax<int64_t>(1, (nvec + (int64_t)kRedBlock * L.u0 - 1) / ((int64_t)kRedBlock * L.u0));
   L.count[L.nlev++] = c;
-  while (c > kRedMaxBlocks && L.nlev < 8) {
+  while (c > kFoldMax && L.nlev < 8) {
     const int64_t cv = (c + epv - 1) / epv;  // partials read as 16-byte vectors
     c = (cv + kOnceVecs - 1) / kOnceVecs;
     L.count[L.nlev++] = c;
@@ -301,6 +324,21 @@ inline size_t reduce_scratch(size_t es, int64_t n) {
   return kRedReserved + kmax<size_t>(a + b, round256((size_t)kRedMaxBlocks * es));
 }
 
+// Launch of reduce_once_kernel with the level's vectors per lane.
+template <class T, class Op, class Map, bool FOLD>
+void launch_once(int u, unsigned grid, const T* src, int64_t n, int64_t head, int64_t nvec, T* out, uint64_t* hdr,
+                 hipStream_t stream) {
+  if (u == 8)
+    hipLaunchKernelGGL((reduce_once_kernel<T, Op, Map, FOLD, 8>), dim3(grid), dim3(kRedBlock), 0, stream, src, n, head,
+                       nvec, out, hdr);
+  else if (u == 4)
+    hipLaunchKernelGGL((reduce_once_kernel<T, Op, Map, FOLD, 4>), dim3(grid), dim3(kRedBlock), 0, stream, src, n, head,
+                       nvec, out, hdr);
+  else
+    hipLaunchKernelGGL((reduce_once_kernel<T, Op, Map, FOLD, kOnceUnroll>), dim3(grid), dim3(kRedBlock), 0, stream, src,
+                       n, head, nvec, out, hdr);
+}
+
 template <class T, class Op, class Map>
 int launch_reduce(const void* src, int64_t n, int64_t stride, void* dst, void* scratch,
                   hipStream_t stream) {
@@ -319,28 +357,30 @@ int launch_reduce(const void* src, int64_t n, int64_t stride, void* dst, void* s
   const int64_t head = kmin<int64_t>(n, (int64_t)(((16 - ((uintptr_t)src & 15)) & 15) / sizeof(T)));
   const int64_t nvec = (n - head) / EPV;
   const OnceLevels L = once_levels(nvec, EPV);
-  if (kUseFold && L.nlev == 1 && L.count[0] > 1 && L.count[0] <= kFoldMax) {
-    // one launch: the last workgroup folds the others' partials (fold_partial)
-    hipLaunchKernelGGL((reduce_once_kernel<T, Op, Map, true>), dim3((unsigned)L.count[0]), dim3(kRedBlock), 0,
-                       stream, (const T*)src, n, head, nvec, (T*)dst, (uint64_t*)scratch);
-    return kf_check_launch("reduce_once_kernel");
-  }
   size_t abytes = 0;
   for (int i = 0; i < L.nlev; i += 2) abytes = kmax(abytes, round256((size_t)L.count[i] * sizeof(T) + 16));
   T* buf[2] = {(T*)work, (T*)(work + abytes)};
-  // level 0 reads the input (with map, head and tail); later levels reduce partials
-  T* out0 = (L.nlev == 1 && L.count[0] == 1) ? (T*)dst : buf[0];
-  hipLaunchKernelGGL((reduce_once_kernel<T, Op, Map>), dim3((unsigned)L.count[0]), dim3(kRedBlock), 0, stream,
-                     (const T*)src, n, head, nvec, out0, (uint64_t*)nullptr);
-  for (int i = 1; i < L.nlev; ++i) {
-    const int64_t m = L.count[i - 1];
-    const int64_t mv = m / EPV;
-    hipLaunchKernelGGL((reduce_once_kernel<T, Op, MapIdentity>), dim3((unsigned)L.count[i]), dim3(kRedBlock), 0,
-                       stream, (const T*)buf[(i - 1) % 2], m, (int64_t)0, mv, buf[i % 2], (uint64_t*)nullptr);
+  // level 0 reads the input (with map, head and tail); later levels reduce
+  // partials; the last level writes the result (one workgroup) or folds
+  const int last = L.nlev - 1;
+  for (int i = 0; i <= last; ++i) {
+    const unsigned grid = (unsigned)L.count[i];
+    T* out = i == last ? (T*)dst : buf[i % 2];
+    const bool fold = i == last && grid > 1;
+    if (i == 0) {
+      if (fold)
+        launch_once<T, Op, Map, true>(L.u0, grid, (const T*)src, n, head, nvec, out, (uint64_t*)scratch, stream);
+      else
+        launch_once<T, Op, Map, false>(L.u0, grid, (const T*)src, n, head, nvec, out, nullptr, stream);
+    } else {
+      const int64_t m = L.count[i - 1];
+      const T* in = buf[(i - 1) % 2];
+      if (fold)
+        launch_once<T, Op, MapIdentity, true>(kOnceUnroll, grid, in, m, 0, m / EPV, out, (uint64_t*)scratch, stream);
+      else
+        launch_once<T, Op, MapIdentity, false>(kOnceUnroll, grid, in, m, 0, m / EPV, out, nullptr, stream);
+    }
   }
-  if (out0 != (T*)dst)
-    hipLaunchKernelGGL((combine_all_kernel<T, Op>), dim3(1), dim3(kCombineBlock), 0, stream,
-                       (const T*)buf[(L.nlev - 1) % 2], (int)L.count[L.nlev - 1], (T*)dst);
   return kf_check_launch("reduce_once_kernel");
 }
 
@@ -449,8 +489,8 @@ int launch_reducek(const Operands<T, K>& a, int64_t n, void* dst, void* scratch_
                          (const T*)scratch, grid, (T*)dst);
     return kf_check_launch("reducek_kernel");
   }
-  const OnceLevels L = once_levels(n / EPV, EPV);
-  if (kUseFold && L.nlev == 1 && L.count[0] > 1 && L.count[0] <= kFoldMax) {
+  const OnceLevels L = once_levels(n / EPV, EPV, /*adaptive=*/false);
+  if (L.nlev == 1 && L.count[0] > 1) {
     hipLaunchKernelGGL((reducek_once_kernel<T, Op, M, K, true>), dim3((unsigned)L.count[0]), dim3(kRedBlock), 0,
                        stream, a, n, (T*)dst, (uint64_t*)scratch_base);
     return kf_check_launch("reducek_once_kernel");
@@ -458,17 +498,20 @@ int launch_reducek(const Operands<T, K>& a, int64_t n, void* dst, void* scratch_
   size_t abytes = 0;
   for (int i = 0; i < L.nlev; i += 2) abytes = kmax(abytes, round256((size_t)L.count[i] * sizeof(T) + 16));
   T* buf[2] = {(T*)scratch, (T*)((uint8_t*)scratch + abytes)};
-  T* out0 = (L.nlev == 1 && L.count[0] == 1) ? (T*)dst : buf[0];
+  const int last = L.nlev - 1;
   hipLaunchKernelGGL((reducek_once_kernel<T, Op, M, K>), dim3((unsigned)L.count[0]), dim3(kRedBlock), 0, stream,
-                     a, n, out0, (uint64_t*)nullptr);
-  for (int i = 1; i < L.nlev; ++i) {
+                     a, n, last == 0 ? (T*)dst : buf[0], (uint64_t*)nullptr);
+  for (int i = 1; i <= last; ++i) {
     const int64_t m = L.count[i - 1];
-    hipLaunchKernelGGL((reduce_once_kernel<T, Op, MapIdentity>), dim3((unsigned)L.count[i]), dim3(kRedBlock), 0,
-                       stream, (const T*)buf[(i - 1) % 2], m, (int64_t)0, m / EPV, buf[i % 2], (uint64_t*)nullptr);
+    const unsigned grid = (unsigned)L.count[i];
+    T* out = i == last ? (T*)dst : buf[i % 2];
+    if (i == last && grid > 1)
+      launch_once<T, Op, MapIdentity, true>(kOnceUnroll, grid, buf[(i - 1) % 2], m, 0, m / EPV, out,
+                                            (uint64_t*)scratch_base, stream);
+    else
+      launch_once<T, Op, MapIdentity, false>(kOnceUnroll, grid, buf[(i - 1) % 2], m, 0, m / EPV, out, nullptr,
+                                             stream);
   }
-  if (out0 != (T*)dst)
-    hipLaunchKernelGGL((combine_all_kernel<T, Op>), dim3(1), dim3(kCombineBlock), 0, stream,
-                       (const T*)buf[(L.nlev - 1) % 2], (int)L.count[L.nlev - 1], (T*)dst);
   return kf_check_launch("reducek_once_kernel");
 }
 
@@ -677,3 +720,4 @@ extern "C" int kf_scratch_reset(void* scratch, size_t bytes, void* stream) {
                      (int64_t)bytes);
   return kf_check_launch("fill_zero_kernel");
 }
+
