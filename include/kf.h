@@ -183,6 +183,24 @@ int kf_reduce3(kf_op op, kf_map3 f, kf_dtype dt,
                const void* z, int64_t z_stride, int64_t n,
                void* dst, void* scratch, size_t scratch_bytes, void* stream);
 
+/* ------------------------------------------------------ reduce_noalloc ----
+ * No counterpart in the reference: kf_reduce for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). Same arguments and result as
+ * kf_reduce without the scratch pair: the partials live in a static device
+ * array of KF_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends.
+ * Sizes whose kf_reduce_scratch_bytes exceeds it are refused with
+ * KF_EINVAL (Float32 up to about 2^30 elements fits). The call allocates
+ * nothing (its first call on a device looks the array's address up once).
+ * Every call on one GPU shares that GPU's array: calls that overlap on one
+ * GPU (different streams, or host threads, without ordering) race and give
+ * wrong results; order them on one stream. */
+#define KF_NOALLOC_SCRATCH_BYTES ((size_t)4 << 20)
+
+int kf_reduce_noalloc(kf_op op, kf_map f, kf_dtype dt,
+                      const void* src, int64_t n, int64_t stride,
+                      void* dst, void* stream);
+
 /* ---------------------------------------------------------- reduce_dim ----
  * A is a column-major rows x cols matrix: A[i, j] at A + i + j*col_stride
  * (col_stride >= rows; col_stride = 2*rows is the view A[:, 1:2:end]).

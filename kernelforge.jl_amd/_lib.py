@@ -42,6 +42,7 @@ SIGNATURES = {
     "kf_copy": ([_P, _P, _SZ, _P], _I),
     "kf_scan_scratch_status": ([_P, _P, ctypes.POINTER(ctypes.c_int)], _I),
     "kf_fill": ([_P, _I64, _P, _SZ, _P], _I),
+    "kf_reduce_noalloc": ([_I, _I, _I, _P, _I64, _I64, _P, _P], _I),
 }
 
 _lib = None

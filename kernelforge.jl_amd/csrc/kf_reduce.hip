@@ -20,6 +20,8 @@
 //    save.
 //  * Combine orders depend only on the shape and pointer alignment, so every
 //    result is bit-for-bit reproducible run to run.
+#include <mutex>
+
 #include "kf_reduce.h"
 
 namespace kf {
@@ -721,3 +723,64 @@ extern "C" int kf_scratch_reset(void* scratch, size_t bytes, void* stream) {
   return kf_check_launch("fill_zero_kernel");
 }
 
+// ---------------------------------------------------------------------------
+// Allocation-free full reduction: kf_reduce with its scratch in a static
+// device array instead of a caller buffer.
+// ---------------------------------------------------------------------------
+namespace kf {
+constexpr size_t kStaticScratchBytes = KF_NOALLOC_SCRATCH_BYTES;
+}  // namespace kf
+
+// One copy per GPU, alive until the process ends. Zero at load (static
+// storage), which is the initial state the epoch-tagged fold slots need;
+// after that the kernels keep it valid. In host code this name is only a
+// stand-in for the symbol: the device address comes from
+// hipGetSymbolAddress (static_scratch_ptr below).
+static __device__ __align__(256) uint8_t scratch[kf::kStaticScratchBytes];
+
+namespace {
+constexpr int kMaxStaticDevices = 64;
+std::mutex g_static_mu;
+void* g_static_ptr[kMaxStaticDevices] = {};
+
+// Device address of `scratch` on the current device, looked up once per
+// device with that device current.
+int static_scratch_ptr(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxStaticDevices)
+    return kf_set_error(KF_EHIP, "kf_reduce_noalloc: no current HIP device (or device id >= %d)", kMaxStaticDevices);
+  std::lock_guard<std::mutex> lock(g_static_mu);
+  if (!g_static_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return kf_set_error(KF_EHIP, "kf_reduce_noalloc: hipGetSymbolAddress failed: %s", hipGetErrorString(e));
+    g_static_ptr[dev] = p;
+  }
+  *out = g_static_ptr[dev];
+  return KF_OK;
+}
+}  // namespace
+
+extern "C" int kf_reduce_noalloc(kf_op op, kf_map f, kf_dtype dt, const void* src, int64_t n, int64_t stride,
+                                 void* dst, void* stream) {
+  int rc = kf_validate_op(op, f, dt, /*allow_affine=*/0);
+  if (rc) return rc;
+  if (n < 0) return kf_set_error(KF_EINVAL, "kf_reduce_noalloc: n = %lld < 0", (long long)n);
+  if (n == 0) return KF_OK;
+  if (!src || !dst) return kf_set_error(KF_EINVAL, "kf_reduce_noalloc: null src or dst");
+  if (stride < 1) return kf_set_error(KF_EINVAL, "kf_reduce_noalloc: stride must be >= 1");
+  const size_t es = kf_dtype_size(dt);
+  if ((uintptr_t)src % es || (uintptr_t)dst % es)
+    return kf_set_error(KF_EINVAL, "kf_reduce_noalloc: src/dst not aligned to the element type");
+  const size_t need = kf_reduce_scratch_bytes(dt, n);
+  if (need > kStaticScratchBytes)
+    return kf_set_error(KF_EINVAL,
+                        "kf_reduce_noalloc: n = %lld needs %zu bytes of scratch, more than the static %zu; "
+                        "use kf_reduce with a caller buffer",
+                        (long long)n, need, kStaticScratchBytes);
+  void* p = nullptr;
+  rc = static_scratch_ptr(&p);
+  if (rc) return rc;
+  return dispatch_all<ReduceL>(dt, op, f, src, n, stride, dst, p, (hipStream_t)stream);
+}
