@@ -133,13 +133,27 @@ int kf_scan(kf_op op, kf_map f, kf_post g, kf_dtype dt, int exclusive,
             void* dst, int64_t dst_stride, int64_t n,
             void* scratch, size_t scratch_bytes, void* stream);
 
-/* Diagnostics (no counterpart in the reference): *gave_up = 1 if a scan on
- * this scratch since the last query stopped waiting for a predecessor tile
- * (after 2^24 lookback polls; its results are then invalid). That cannot
- * happen unless the scratch was corrupted or shared by overlapping calls.
- * Clears the flag. Synchronises `stream` (the one exception to the
- * no-synchronisation rule above). */
+/* Diagnostics (no counterpart in the reference). KF_OK from kf_scan means
+ * the launch was queued; it does not cover a lookback give-up. Tiles are
+ * numbered by workgroup id, and a tile waits only on lower-numbered tiles,
+ * which is deadlock-free because the GPU dispatches each XCD's workgroups
+ * in increasing id order. Should a predecessor never publish (dispatch out
+ * of that order, a corrupted scratch buffer, or overlapping calls on one
+ * buffer), a tile stops after 2^24 lookback polls and raises the give-up
+ * flag in the scratch header; every waiting tile of that grid then stops
+ * too, no stopped tile stores, and the results are invalid. The flag is
+ * sticky: until it is cleared, every later kf_scan on that scratch is a
+ * no-op (dst untouched). kf_scan_scratch_status synchronises `stream`,
+ * sets *gave_up = 1 if the flag is raised and then clears it and moves the
+ * buffer's epoch past every descriptor of the failed call, so the buffer is
+ * valid again; kf_scratch_reset (a zero fill) also clears it. */
 int kf_scan_scratch_status(void* scratch, void* stream, int* gave_up);
+
+/* Test hook: on the calling host thread, later kf_scan calls leave tile
+ * `tile` unpublished and give up after `spin_limit` polls, so that the
+ * give-up path runs with every kernel exiting normally; tile < 0 restores
+ * normal operation. */
+int kf_debug_scan_giveup(int64_t tile, uint32_t spin_limit);
 
 /* -------------------------------------------------------------- reduce ----
  * dst[0] = f(src[0]) op f(src[stride]) op ... (n terms), written on device.

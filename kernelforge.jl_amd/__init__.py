@@ -297,12 +297,15 @@ def _split_f_op(args, n_arrays, name):
     raise ArgumentError(f"{name} takes ([f,] op, {', '.join(['array'] * n_arrays)})")
 
 
-def scan_(*args, exclusive=False, tmp=None, g=None, **tuning):
-    """scan!([f,] op, dst, src; exclusive=False, tmp=None) -> dst.
+def scan_(*args, exclusive=False, tmp=None, g=None, check=False, **tuning):
+    """scan!([f,] op, dst, src; exclusive=False, tmp=None, check=False) -> dst.
 
     dst[i] = f(src[1]) op ... op f(src[i]) (inclusive, the reference's only
     mode), or the exclusive variant dst[1] = identity(op),
-    dst[i] = inclusive[i-1]. In place (dst is src) is allowed."""
+    dst[i] = inclusive[i-1]. In place (dst is src) is allowed.
+    check=True synchronises after the launch and raises KernelForgeError if
+    the lookback gave up (see scan_status), which a successful launch does
+    not rule out."""
     f, op, (dst, src) = _split_f_op(args, 2, "scan!")
     opc, fc = _op_code(op), _map_code(f)
     if _post_code(g) is None or (g not in (None, identity) and (opc == _L.OP_AFFINE or src.dim() == 2)):
@@ -323,14 +326,20 @@ def scan_(*args, exclusive=False, tmp=None, g=None, **tuning):
         rc = L.kf_scan(opc, fc, _post_code(g), dt, int(bool(exclusive)), ctypes_void(src.data_ptr()), ss,
                        ctypes_void(dst.data_ptr()), ds, n, ctypes_void(buf.ptr), buf.nbytes, _stream_ptr(src))
     _L.check(rc, "scan!")  # g is applied by the kernel as each value is stored
+    if check and scan_status(buf):
+        raise _L.KernelForgeError(
+            "scan!: a tile's lookback gave up waiting for its predecessor; the results are invalid "
+            "(the scratch buffer has been re-validated)")
     return dst
 
 
 def scan_status(tmp):
     """True if a scan! on the Scan1D buffer `tmp` gave up waiting for a
     predecessor tile since the last query (its results are then invalid:
-    only a corrupted or concurrently shared buffer can cause it). Clears the
-    flag; synchronises the current stream. No counterpart in the reference."""
+    only out-of-order workgroup dispatch, a corrupted buffer or overlapping
+    calls can cause it; until the query, later scans on `tmp` do nothing).
+    Clears the flag and re-validates the buffer; synchronises the current
+    stream. No counterpart in the reference."""
     if not isinstance(tmp, KernelBuffer) or tmp.kind != Scan1D:
         raise ArgumentError("scan_status takes the Scan1D KernelBuffer of a scan! call")
     flag = ctypes.c_int(0)
@@ -340,12 +349,12 @@ def scan_status(tmp):
     return bool(flag.value)
 
 
-def scan(*args, exclusive=False, tmp=None, g=None, **tuning):
+def scan(*args, exclusive=False, tmp=None, g=None, check=False, **tuning):
     """scan([f,] op, src) -> new dst (reference src/scan/scan.jl:218-244)."""
     f, op, (src,) = _split_f_op(args, 1, "scan")
     _require_device(src)
     dst = torch.empty_like(src, memory_format=torch.contiguous_format)
-    return scan_(f, op, dst, src, exclusive=exclusive, tmp=tmp, g=g, **tuning)
+    return scan_(f, op, dst, src, exclusive=exclusive, tmp=tmp, g=g, check=check, **tuning)
 
 
 # ---------------------------------------------------------------------------

@@ -43,6 +43,7 @@ SIGNATURES = {
     "kf_scan_scratch_status": ([_P, _P, ctypes.POINTER(ctypes.c_int)], _I),
     "kf_fill": ([_P, _I64, _P, _SZ, _P], _I),
     "kf_reduce_noalloc": ([_I, _I, _I, _P, _I64, _I64, _P, _P], _I),
+    "kf_debug_scan_giveup": ([_I64, ctypes.c_uint32], _I),
 }
 
 _lib = None

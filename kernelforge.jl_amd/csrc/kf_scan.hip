@@ -127,6 +127,7 @@ constexpr uint32_t kStatePartial = 1, kStatePrefix = 2;
 constexpr size_t kScanHeaderBytes = 256;
 constexpr int kDescWords = 16;             // 128 bytes per tile descriptor
 constexpr uint32_t kSpinLimit = 1u << 24;  // lookback polls before giving up (seconds)
+constexpr uint32_t kFlagPollMask = 1023;   // a waiting lookback re-reads the give-up flag every 1024 polls
 // Predecessors polled per lookback round (lanes 64-win..63). Each
 // descriptor is its own 128-byte line and a poll completes only when its
 // slowest line returns, while in the steady state of a long scan (more
@@ -161,10 +162,20 @@ struct uint4x2 {
   uint4 lo, hi;
 };
 template <class T> using VecT = std::conditional_t<(sizeof(T) > 16), uint4x2, uint4>;
-__device__ inline uint4 ld_vec(const uint4* p) { return ld_stream(p); }
+// Loads of a source vector at any element-aligned address: the byte-aligned
+// vector type still compiles to one global_load_dwordx4 (gfx950 serves
+// unaligned global accesses), so a source that is misaligned differently
+// from the destination streams as well (the tiles follow the destination's
+// alignment, which keeps every store a whole aligned vector).
+typedef uint32_t v4u32_u __attribute__((ext_vector_type(4), aligned(1)));
+__device__ inline uint4 ld_stream_u(const void* p) {
+  const v4u32_u v = __builtin_nontemporal_load(reinterpret_cast<const v4u32_u*>(p));
+  return uint4{v.x, v.y, v.z, v.w};
+}
+__device__ inline uint4 ld_vec(const uint4* p) { return ld_stream_u(p); }
 __device__ inline uint4x2 ld_vec(const uint4x2* p) {
   const uint4* q = reinterpret_cast<const uint4*>(p);
-  return uint4x2{ld_stream(q), ld_stream(q + 1)};
+  return uint4x2{ld_stream_u(q), ld_stream_u(q + 1)};
 }
 __device__ inline void st_vec(uint4* p, uint4 v) { st_stream(p, v); }
 __device__ inline void st_vec(uint4x2* p, uint4x2 v) {
@@ -189,22 +200,40 @@ __device__ inline void publish(uint64_t* desc, int64_t tile, uint32_t tag, T v) 
     st_agent(desc + tile * kDescWords + i, ((uint64_t)tag << 32) | w.w[i]);
 }
 
+// Give-up flag: header word 1. A lookback that has polled `limit` times
+// without finding its prefix sets it and stops; so does one that sees it
+// set (it re-reads it every kFlagPollMask + 1 polls), so that one give-up
+// ends every waiting tile of the grid quickly.
+__device__ inline uint64_t* giveup_flag(const uint64_t* desc) {
+  return const_cast<uint64_t*>(desc) - kScanHeaderBytes / sizeof(uint64_t) + 1;
+}
+__device__ inline bool lookback_stop(const uint64_t* desc, uint32_t polls, uint32_t limit) {
+  if (polls >= limit) {
+    __hip_atomic_fetch_or(giveup_flag(desc), (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return true;
+  }
+  if ((polls & kFlagPollMask) != kFlagPollMask) return false;
+  const uint64_t f = ld_agent(giveup_flag(desc));
+  return __builtin_amdgcn_readfirstlane((uint32_t)(f | (f >> 32))) != 0;  // wave-uniform
+}
+
 // Decoupled lookback, executed by one full wave. Returns the combination of
-// every tile before `tile` (tile > 0), in tile order.
+// every tile before `tile` (tile > 0), in tile order; sets gave_up (and
+// returns garbage) when it stopped waiting.
 template <class T, class Op>
-__device__ inline T lookback(const uint64_t* desc, int64_t tile, uint32_t epoch30, int win) {
+__device__ inline T lookback(const uint64_t* desc, int64_t tile, uint32_t epoch30, int win, uint32_t limit,
+                             bool& gave_up) {
   constexpr int W = ScanShape<T>::W;
   const int lane = lane_id();
   const T id = Op::template identity<T>();
   T run = id;
   int64_t newest = tile - 1;  // the window's lane 63
   for (uint32_t polls = 0;; ++polls) {
-    if (polls == kSpinLimit) {
-      // A predecessor never published: impossible unless the scratch buffer
-      // was corrupted or shared by concurrent calls. Record it in header word
-      // 1 and finish the grid (results are then invalid) instead of hanging.
-      __hip_atomic_fetch_or(const_cast<uint64_t*>(desc) - kScanHeaderBytes / sizeof(uint64_t) + 1,
-                            (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (lookback_stop(desc, polls, limit)) {
+      // A predecessor never published: impossible unless tiles were
+      // dispatched out of order, the scratch buffer was corrupted or it is
+      // shared by overlapping calls. The tile stops (results are invalid).
+      gave_up = true;
       return run;
     }
     const int64_t t = newest - (kWave - 1) + lane;
@@ -251,7 +280,8 @@ __device__ inline T lookback(const uint64_t* desc, int64_t tile, uint32_t epoch3
 // the newest lane holding a PREFIX gives the exclusive prefix; a lane
 // whose chunk still holds an unpublished descriptor re-reads it.
 template <class T, class Op, int CH>
-__device__ inline T lookback_all(const uint64_t* desc, int64_t tile, uint32_t epoch30) {
+__device__ inline T lookback_all(const uint64_t* desc, int64_t tile, uint32_t epoch30, uint32_t limit,
+                                 bool& gave_up) {
   constexpr int W = ScanShape<T>::W;
   const int lane = lane_id();
   const T id = Op::template identity<T>();
@@ -262,9 +292,8 @@ __device__ inline T lookback_all(const uint64_t* desc, int64_t tile, uint32_t ep
   bool has_prefix = false;
   bool done = cnt == 0;
   for (uint32_t polls = 0;; ++polls) {
-    if (polls == kSpinLimit) {
-      __hip_atomic_fetch_or(const_cast<uint64_t*>(desc) - kScanHeaderBytes / sizeof(uint64_t) + 1,
-                            (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (lookback_stop(desc, polls, limit)) {
+      gave_up = true;
       break;
     }
     if (!done) {
@@ -397,18 +426,22 @@ template <class Op, int V> constexpr bool kLdsRowsFor = __is_same(Op, OpAffine) 
 template <class T, class Op, class Map, bool EXCL, int BLOCK, int VPL>
 __global__ __launch_bounds__(BLOCK) void scan_kernel(
     const T* src, int64_t src_stride, T* dst, int64_t dst_stride, int64_t n,
-    int64_t ntiles, uint64_t* scratch, int vec, int off, int win, int post) {
+    int64_t ntiles, uint64_t* scratch, int vec, int off, int win, int post, uint32_t limit, int64_t withhold) {
   // Tiles cover the virtual range [0, n + off): element i sits at virtual
-  // position i + off, so that when src and dst share a misalignment of `off`
-  // elements every interior tile starts on a 16-byte boundary. Virtual
-  // positions before `off` and after the end hold the identity and are
-  // never stored.
+  // position i + off, where `off` is dst's misalignment in elements, so
+  // every interior tile stores whole 16-byte vectors at aligned addresses
+  // (the source vectors are then aligned too when src is misaligned the
+  // same way, and unaligned loads otherwise). Virtual positions before
+  // `off` and after the end hold the identity and are never stored.
+  // `limit` is the lookback's poll budget; `withhold` >= 0 makes that tile
+  // publish nothing (a test hook that forces the give-up path).
   using S = ScanShape<T, BLOCK, VPL>;
   constexpr int V = S::V, EPV = S::EPV;
   constexpr int kScanWaves = BLOCK / kWave;
   __shared__ T wave_agg[kScanWaves];
   __shared__ T wave_pre[kScanWaves];
   __shared__ uint64_t s_ticket;
+  __shared__ int s_stop;
   constexpr bool kLdsRows = kLdsRowsFor<Op, V>;
   using Vec = VecT<T>;
   __shared__ Vec s_stash[kStashForLookback<T, BLOCK> ? V : 1][kWave];
@@ -420,8 +453,12 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
   const int wave = tid / kWave;
   const T id = Op::template identity<T>();
 
-  if (tid == 0) s_ticket = ((scratch[0] >> 32) << 32) | (uint64_t)blockIdx.x;  // {epoch, tile}
+  if (tid == 0) {
+    s_ticket = ((scratch[0] >> 32) << 32) | (uint64_t)blockIdx.x;  // {epoch, tile}
+    s_stop = ld_agent(scratch + 1) != 0;  // an earlier give-up: every call is a no-op until cleared
+  }
   __syncthreads();
+  if (s_stop) return;
   const uint64_t tk = s_ticket;
   const int64_t tile = (int64_t)(uint32_t)tk;
   const uint32_t epoch30 = (uint32_t)(tk >> 32) & 0x3fffffffu;
@@ -531,17 +568,24 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
     const T wexcl = wave_shift_right<Op>(wincl);
     const T agg = read_lane(wincl, kScanWaves - 1);
     T excl = id;
+    bool gave_up = false;
+    const bool pub = tile != withhold;
     if (tile == 0) {
-      if (lane == 0) publish(desc, tile, (epoch30 << 2) | kStatePrefix, agg);
+      if (lane == 0 && pub) publish(desc, tile, (epoch30 << 2) | kStatePrefix, agg);
     } else {
-      if (lane == 0) publish(desc, tile, (epoch30 << 2) | kStatePartial, agg);
+      if (lane == 0 && pub) publish(desc, tile, (epoch30 << 2) | kStatePartial, agg);
       if constexpr (kLookAllFor<T>)
-        excl = win == 0 ? lookback_all<T, Op, kAllChunk>(desc, tile, epoch30) : lookback<T, Op>(desc, tile, epoch30, win);
+        excl = win == 0 ? lookback_all<T, Op, kAllChunk>(desc, tile, epoch30, limit, gave_up)
+                        : lookback<T, Op>(desc, tile, epoch30, win, limit, gave_up);
       else
-        excl = lookback<T, Op>(desc, tile, epoch30, win);
-      if (lane == 0) publish(desc, tile, (epoch30 << 2) | kStatePrefix, Op::combine(excl, agg));
+        excl = lookback<T, Op>(desc, tile, epoch30, win, limit, gave_up);
+      if (lane == 0 && pub && !gave_up) publish(desc, tile, (epoch30 << 2) | kStatePrefix, Op::combine(excl, agg));
     }
-    if (lane == 0 && tile == ntiles - 1) st_agent(scratch, ((tk >> 32) + 1) << 32);  // next call's epoch
+    // next call's epoch, once every tile has read this one (the last tile's
+    // completed lookback implies it); not after a give-up, which leaves the
+    // buffer to the status query or a reset
+    if (lane == 0 && tile == ntiles - 1 && !gave_up) st_agent(scratch, ((tk >> 32) + 1) << 32);
+    if (lane == 0) s_stop = gave_up;
     if (lane < kScanWaves) wave_pre[lane] = lane == 0 ? excl : Op::combine(excl, wexcl);
     if constexpr (kStashForLookback<T, BLOCK>) {
       asm volatile("" ::: "memory");
@@ -553,6 +597,7 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
     }
   }
   __syncthreads();
+  if (s_stop) return;  // this tile gave up: it stores nothing
   const T prefix = wave_pre[wave];
   if constexpr (kLdsRows) {
 #pragma unroll
@@ -650,6 +695,11 @@ template <auto KERNEL> int64_t resident_tiles(int block) {
 
 // `mode` below carries the exclusive flag in bit 0 and the post-map g
 // (kf_post) in the bits above.
+// Test hook (kf_debug_scan_giveup): on this host thread, scans withhold the
+// publication of one tile and give up after a short poll budget.
+thread_local int64_t g_withhold = -1;
+thread_local uint32_t g_spin_limit = kSpinLimit;
+
 template <class T, class Op, class Map, int TIER>
 void launch_scan_tier(const void* src, int64_t ss, void* dst, int64_t ds, int64_t n, int mode, int64_t ntiles,
                       int vec, int off, void* scratch, hipStream_t stream) {
@@ -658,23 +708,25 @@ void launch_scan_tier(const void* src, int64_t ss, void* dst, int64_t ds, int64_
   if (mode & 1) {
     constexpr auto kernel = scan_kernel<T, Op, Map, true, B, V>;
     hipLaunchKernelGGL(kernel, dim3((unsigned)ntiles), dim3(B), 0, stream, (const T*)src, ss, (T*)dst, ds, n,
-                       ntiles, (uint64_t*)scratch, vec, off, look_window(ntiles, resident_tiles<kernel>(B), (int64_t)B * V * kVecBytes<T>, kLookAllFor<T>), post);
+                       ntiles, (uint64_t*)scratch, vec, off, look_window(ntiles, resident_tiles<kernel>(B), (int64_t)B * V * kVecBytes<T>, kLookAllFor<T>), post,
+                       g_spin_limit, g_withhold);
   } else {
     constexpr auto kernel = scan_kernel<T, Op, Map, false, B, V>;
     hipLaunchKernelGGL(kernel, dim3((unsigned)ntiles), dim3(B), 0, stream, (const T*)src, ss, (T*)dst, ds, n,
-                       ntiles, (uint64_t*)scratch, vec, off, look_window(ntiles, resident_tiles<kernel>(B), (int64_t)B * V * kVecBytes<T>, kLookAllFor<T>), post);
+                       ntiles, (uint64_t*)scratch, vec, off, look_window(ntiles, resident_tiles<kernel>(B), (int64_t)B * V * kVecBytes<T>, kLookAllFor<T>), post,
+                       g_spin_limit, g_withhold);
   }
 }
 
 template <class T, class Op, class Map>
 int launch_scan(const void* src, int64_t ss, void* dst, int64_t ds, int64_t n, int excl,
                 void* scratch, hipStream_t stream) {
-  // Vector path when both operands are contiguous and equally misaligned
-  // (e.g. views src[k:], dst[k:] of aligned buffers); `off` shifts the tiles.
-  // (elements of 16 bytes or more need 16-byte aligned operands for it)
-  const int vec = ss == 1 && ds == 1 && ((uintptr_t)src % 16 == (uintptr_t)dst % 16) &&
-                  ((uintptr_t)src % 16 % sizeof(T) == 0);
-  const int off = vec ? (int)(((uintptr_t)src % 16) / sizeof(T)) : 0;
+  // Vector path when both operands are contiguous (views src[k:], dst[j:]
+  // of aligned buffers included): `off` shifts the tiles to dst's alignment,
+  // the loads of a differently misaligned src are unaligned vector loads.
+  // (elements of 16 bytes or more need a 16-byte aligned dst for it)
+  const int vec = ss == 1 && ds == 1 && ((uintptr_t)dst % 16 % sizeof(T) == 0);
+  const int off = vec ? (int)(((uintptr_t)dst % 16) / sizeof(T)) : 0;
   const int64_t ntiles = scan_tiles<T>(n, off);
   switch (scan_tier<T>(n)) {
     case 0: launch_scan_tier<T, Op, Map, 0>(src, ss, dst, ds, n, excl, ntiles, vec, off, scratch, stream); break;
@@ -731,7 +783,16 @@ int scan_op(kf_op op, kf_map f, const void* src, int64_t ss, void* dst, int64_t 
 using namespace kf;
 
 namespace kf {
-__global__ void clear_word_kernel(uint64_t* w) { *w = 0; }
+// After a give-up (nothing in flight: the status query synchronised the
+// stream): clear the flag and move the epoch two past the current one, so
+// that no descriptor published by the failed call (tagged with its epoch or,
+// from tiles that started after the last tile advanced it, the next one)
+// can read as current.
+__global__ void reepoch_kernel(uint64_t* hdr) {
+  const uint64_t e = (hdr[0] >> 32) + 2;
+  hdr[0] = (e & 0x3fffffffull) << 32;
+  hdr[1] = 0;
+}
 }  // namespace kf
 
 extern "C" int kf_scan_scratch_status(void* scratch, void* stream, int* gave_up) {
@@ -742,9 +803,21 @@ extern "C" int kf_scan_scratch_status(void* scratch, void* stream, int* gave_up)
   if (hipMemcpyAsync(&w, flag, sizeof w, hipMemcpyDeviceToHost, s) != hipSuccess ||
       hipStreamSynchronize(s) != hipSuccess)
     return kf_check_launch("kf_scan_scratch_status");
-  *gave_up = (w & 1) != 0;
-  if (w != 0) hipLaunchKernelGGL(clear_word_kernel, dim3(1), dim3(1), 0, s, flag);
-  return kf_check_launch("clear_word_kernel");
+  *gave_up = w != 0;
+  if (w != 0) hipLaunchKernelGGL(reepoch_kernel, dim3(1), dim3(1), 0, s, (uint64_t*)scratch);
+  return kf_check_launch("reepoch_kernel");
+}
+
+extern "C" int kf_debug_scan_giveup(int64_t tile, uint32_t spin_limit) {
+  if (tile < 0) {
+    g_withhold = -1;
+    g_spin_limit = kSpinLimit;
+    return KF_OK;
+  }
+  if (spin_limit == 0) return kf_set_error(KF_EINVAL, "kf_debug_scan_giveup: spin_limit must be > 0");
+  g_withhold = tile;
+  g_spin_limit = spin_limit;
+  return KF_OK;
 }
 
 extern "C" size_t kf_scan_scratch_bytes(kf_dtype dt, kf_op op, int64_t n) {

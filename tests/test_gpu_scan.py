@@ -447,3 +447,80 @@ def test_post_map_g_in_the_store(kf, oracle, dev, exclusive):
         assert np.array_equal(got, ref * ref), n        # max selects an input: exact square
     with pytest.raises(kf.ArgumentError):
         kf.scan("+", torch.ones(10, dtype=torch.int32, device=dev), g="sqrt")
+
+
+# ---- the lookback's give-up path, forced from the host -----------------------
+@pytest.mark.parametrize("n", [300_000, 3_000_000])  # all tiles resident / windowed lookback
+def test_lookback_giveup_is_raised_by_the_kernel(kf, oracle, dev, n):
+    # kf_debug_scan_giveup makes tile 3 never publish and gives every
+    # lookback a budget of 4096 polls: the tile after it gives up, raises the
+    # flag, every waiting tile stops, and all kernels exit normally
+    L = kf._lib.lib()
+    rng = np.random.default_rng(41)
+    x = rng.integers(0, 16, n).astype(np.int32)
+    src = torch.from_numpy(x).to(dev)
+    dst = torch.empty_like(src)
+    tmp = kf.get_allocation(kf.Scan1D, kf.identity, "+", src)
+    print(f"give-up test n={n}", flush=True)
+    assert L.kf_debug_scan_giveup(3, 4096) == 0
+    try:
+        kf.scan_("+", dst, src, tmp=tmp)
+        torch.cuda.synchronize()
+    finally:
+        assert L.kf_debug_scan_giveup(-1, 0) == 0
+    # sticky: before the status query, a scan on that buffer stores nothing
+    sentinel = torch.full_like(src, -7)
+    kf.scan_("+", sentinel, src, tmp=tmp)
+    torch.cuda.synchronize()
+    assert bool((sentinel == -7).all())
+    assert kf.scan_status(tmp) is True
+    assert kf.scan_status(tmp) is False
+    # the query re-validated the buffer: the next scans are exact again
+    for excl in (False, True):
+        kf.scan_("+", dst, src, tmp=tmp, exclusive=excl)
+        assert np.array_equal(dst.cpu().numpy(), oracle.scan(x, "+", exclusive=excl))
+    # check=True surfaces a give-up as an exception
+    assert L.kf_debug_scan_giveup(3, 4096) == 0
+    try:
+        with pytest.raises(kf._lib.KernelForgeError):
+            kf.scan_("+", dst, src, tmp=tmp, check=True)
+    finally:
+        assert L.kf_debug_scan_giveup(-1, 0) == 0
+    kf.scan_("+", dst, src, tmp=tmp, check=True)
+    assert np.array_equal(dst.cpu().numpy(), oracle.scan(x, "+"))
+
+
+# ---- source and destination misaligned differently ---------------------------
+@pytest.mark.parametrize("dt", [np.int32, np.int64, np.uint8, np.float64])
+def test_differently_misaligned_views(kf, oracle, dev, dt):
+    # reference test/tests/views/views_test.jl:16-21 scans view(src, 2:n) into
+    # a fresh dst: src and dst then sit at different offsets from a 16-byte
+    # boundary, which the kernel streams with unaligned vector loads
+    rng = np.random.default_rng(43)
+    es = np.dtype(dt).itemsize
+    for n in (5, 1000, 4097, 65536 * 4 + 3, 1_000_003):
+        x = gen(rng, dt, n + 16)
+        src = torch.from_numpy(x).to(dev)
+        out = torch.empty(n + 16, dtype=src.dtype, device=dev)
+        for si, di in ((1, 0), (0, 1), (3, 2), (16 // es - 1 if es < 16 else 0, 0), (2, 7)):
+            if si + n > n + 16 or di + n > n + 16:
+                continue
+            d = out[di:di + n]
+            kf.scan_("+" if dt != np.float64 else "max", d, src[si:si + n])
+            ref = oracle.scan(x[si:si + n], "+" if dt != np.float64 else "max")
+            assert np.array_equal(d.cpu().numpy(), ref), (n, si, di)
+
+
+def test_misaligned_view_headline_size(kf, oracle, dev):
+    # scan!(+, dst, src[2:end]) at 2^28 Float32 with an aligned dst: exact on
+    # sparse 0/1 data (sums stay integers below 2^24)
+    rng = np.random.default_rng(47)
+    n = 2**28
+    x = (rng.random(n + 1) < 2**-6).astype(np.float32)
+    src = torch.from_numpy(x).to(dev)
+    dst = torch.empty(n, dtype=torch.float32, device=dev)
+    kf.scan_("+", dst, src[1:])
+    got = dst.cpu().numpy()
+    ref = np.cumsum(x[1:], dtype=np.float64)
+    assert ref[-1] < 2**24
+    assert np.array_equal(got.astype(np.float64), ref)
