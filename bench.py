@@ -7,14 +7,20 @@ n = 2^28 (BASELINE.json's headline configuration):
 Inputs are resident in HBM before timing starts. `value` is algorithmic GB/s
 of the whole step (12*n bytes / step time). The JSON line also carries the
 per-kernel roofline of the dominant kernel (the scan), measured with HIP
-events on the stream the kernels run on, the measured copy ceiling, and the
-CPU baseline (the oracle's restatement of Base.accumulate! / Base.mapreduce,
-timed on this host).
+events on the stream the kernels run on, the measured copy and read
+ceilings (kf_bw_probe kernels and hipMemcpyDtoD), and the CPU baseline (the
+oracle's restatement of Base.accumulate! / Base.mapreduce, timed on this
+host).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--all [--all-json PATH]]
-  --all       also time every BASELINE.json configuration (stderr table, and
-              the rows inside the JSON line as "all_configs")
-  --all-json  also write those rows, with the copy ceiling, to PATH
+  --all          also time every BASELINE.json configuration (stderr table,
+                 and the rows inside the JSON line as "all_configs")
+  --all-json     also write those rows, with the ceilings, to PATH
+  --sweep        the reference's 10^6..10^9 size sweep
+  --pmc-run      only the marked dispatch sequence of every configuration,
+                 for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs
+  --pmc-summary  FETCH_DIR WRITE_DIR CASES_LOG OUT_JSON: per-configuration
+                 HBM bytes from those two runs (no GPU)
 """
 import argparse
 import json
@@ -64,6 +70,16 @@ def load_traffic():
     return None
 
 
+def load_config_traffic():
+    """{config key: HBM bytes / algorithmic bytes} per BASELINE configuration,
+    from the rocprofv3 --pmc summary in profiles/, if recorded."""
+    p = os.path.join(REPO, "profiles", "traffic_all_configs.json")
+    if os.path.exists(p):
+        with open(p) as fh:
+            return {k: v["ratio"] for k, v in json.load(fh)["configs"].items()}
+    return {}
+
+
 def _cpu_rate(oracle, x, y, threads, budget_s):
     """GB/s of steps (scan + sum over x) on `threads` host threads."""
     n = x.shape[0]
@@ -107,7 +123,14 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--sweep", action="store_true",
                     help="the reference's scan/mapreduce size sweep (perfs/julia/benchmarks)")
+    ap.add_argument("--pmc-run", action="store_true",
+                    help="only the dispatch sequence for rocprofv3 --pmc (see pmc_run)")
+    ap.add_argument("--pmc-summary", nargs=4, metavar=("FETCH_DIR", "WRITE_DIR", "CASES_LOG", "OUT_JSON"),
+                    help="summarise two --pmc-run profiles (FETCH_SIZE, WRITE_SIZE); no GPU needed")
     args = ap.parse_args()
+    if args.pmc_summary:
+        pmc_summary(*args.pmc_summary)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the scan/mapreduce path here is single-GPU "
               "(multi-GPU sharding is a design note only); run with --gpus 1", file=sys.stderr)
@@ -117,6 +140,9 @@ def main():
     kf = __graft_entry__.load_package()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.pmc_run:
+        pmc_run(kf, dev)
+        return
 
     g = torch.Generator(device=dev).manual_seed(20261201)
     src = torch.rand(N, device=dev, generator=g, dtype=torch.float32)
@@ -156,23 +182,13 @@ def main():
     # per-kernel averages over the timed pattern (events on the launch stream)
     scan_s, scan_min = time_calls(do_scan, 20, batches=10, with_min=True)
     red_s, red_min = time_calls(do_reduce, 20, batches=10, with_min=True)
-    cbuf = torch.empty_like(src)
-
-    def do_copy():
-        kf.vcopy_(cbuf, src)
-
-    def do_dtod():
-        cbuf.copy_(src)
-
-    copy_s = time_calls(do_copy, 20)
-    dtod_s = time_calls(do_dtod, 20)
-    copy_gbps = 8 * N / copy_s / 1e9
-    dtod_gbps = 8 * N / dtod_s / 1e9
-    ceiling = max(copy_gbps, dtod_gbps)
+    ceil = measure_ceilings(kf, dev, src)
+    copy_ceiling, read_ceiling = ceil["copy_ceiling_gbps"], ceil["read_ceiling_gbps"]
     scan_gbps = 8 * N / scan_s / 1e9
     red_gbps = 4 * N / red_s / 1e9
-    log(f"scan {scan_s*1e6:.1f} us {scan_gbps:.0f} GB/s | reduce {red_s*1e6:.1f} us {red_gbps:.0f} GB/s | "
-        f"copy kernel {copy_gbps:.0f} GB/s, hipMemcpyDtoD {dtod_gbps:.0f} GB/s")
+    log(f"scan {scan_s*1e6:.1f} us {scan_gbps:.0f} GB/s ({scan_gbps/copy_ceiling*100:.1f}% of copy ceiling) | "
+        f"reduce {red_s*1e6:.1f} us {red_gbps:.0f} GB/s ({red_gbps/read_ceiling*100:.1f}% of read ceiling)")
+    log("ceilings: " + ", ".join(f"{k} {v:.0f}" for k, v in ceil.items()))
 
     cpu = None
     if not args.no_cpu:
@@ -201,22 +217,59 @@ def main():
                      "frac": round(scan_gbps / PEAK_HBM_GBPS, 4), "traffic": load_traffic(),
                      "avg_launch_us": round(scan_s * 1e6, 2), "algorithmic_bytes_per_launch": 8 * N},
         "kernels": {
-            "scan_gbps": round(scan_gbps, 1), "scan_frac_of_copy": round(scan_gbps / ceiling, 4),
-            "mapreduce_gbps": round(red_gbps, 1), "mapreduce_frac_of_copy": round(red_gbps / ceiling, 4),
+            "scan_gbps": round(scan_gbps, 1), "scan_frac_of_copy_ceiling": round(scan_gbps / copy_ceiling, 4),
+            "mapreduce_gbps": round(red_gbps, 1), "mapreduce_frac_of_read_ceiling": round(red_gbps / read_ceiling, 4),
             "mapreduce_frac_of_peak": round(red_gbps / PEAK_HBM_GBPS, 4), "mapreduce_avg_launch_us": round(red_s * 1e6, 2),
             "scan_gbps_best_batch": round(8 * N / scan_min / 1e9, 1),
             "mapreduce_gbps_best_batch": round(4 * N / red_min / 1e9, 1),
-            "copy_kernel_gbps": round(copy_gbps, 1), "hipMemcpyDtoD_gbps": round(dtod_gbps, 1),
-            "copy_ceiling_gbps": round(ceiling, 1),
+            **{k: round(v, 1) for k, v in ceil.items()},
         },
         "cpu_baseline": cpu,
         "wall_s_timed": round(wall, 4),
     }
     if args.all:
-        line["all_configs"] = bench_all(kf, dev, ceiling, args.all_json)
+        line["all_configs"] = bench_all(kf, dev, ceil, args.all_json)
     if args.sweep:
-        line["sweep"] = bench_sweep(kf, dev, ceiling)
+        line["sweep"] = bench_sweep(kf, dev, ceil)
     print(json.dumps(line), flush=True)
+
+
+def measure_ceilings(kf, dev, src):
+    """Copy and read ceilings on the same 1 GiB buffer (2^28 Float32): GB/s
+    of algorithmic bytes (copy 2 x bytes, read 1 x bytes) of every
+    kf_bw_probe kernel and of torch's device-to-device copy
+    (hipMemcpyDtoD); each ceiling is the best of its kind. This plays the
+    part of the reference's vendor memcpy benchmark
+    (perfs/cuda_cpp/cub_nvcc/cub_memcpy_benchmark.cu, bytes = 2N)."""
+    import ctypes
+    L, K = kf._lib.lib(), kf._lib
+    nbytes = src.numel() * src.element_size()
+    cbuf = torch.empty_like(src)
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+    scratch = torch.empty(L.kf_bw_probe_scratch_bytes(nbytes), dtype=torch.uint8, device=dev)
+
+    def probe(kind, dst):
+        def fn():
+            rc = L.kf_bw_probe(kind, ctypes.c_void_p(dst.data_ptr()), ctypes.c_void_p(src.data_ptr()), nbytes,
+                               ctypes.c_void_p(scratch.data_ptr()), scratch.numel(),
+                               ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+            K.check(rc, "kf_bw_probe")
+        return fn
+
+    out = {}
+    for name, kind in (("copy_kernel_gbps", K.BW_COPY), ("copy_tiled_gbps", K.BW_COPY_TILED),
+                       ("copy_ordered_gbps", K.BW_COPY_ORDERED)):
+        out[name] = 2 * nbytes / time_calls(probe(kind, cbuf), 20) / 1e9
+    out["hipMemcpyDtoD_gbps"] = 2 * nbytes / time_calls(lambda: cbuf.copy_(src), 20) / 1e9
+    torch.cuda.synchronize()
+    assert torch.equal(cbuf, src), "copy probe mismatch"
+    for name, kind in (("read_kernel_gbps", K.BW_READ), ("read_tiled_gbps", K.BW_READ_TILED)):
+        out[name] = nbytes / time_calls(probe(kind, sink), 20) / 1e9
+    out["copy_ceiling_gbps"] = max(out[k] for k in ("copy_kernel_gbps", "copy_tiled_gbps", "copy_ordered_gbps",
+                                                    "hipMemcpyDtoD_gbps"))
+    out["read_ceiling_gbps"] = max(out["read_kernel_gbps"], out["read_tiled_gbps"])
+    del cbuf, scratch
+    return out
 
 
 def _graph_time(fn, reps=20):
@@ -232,7 +285,7 @@ def _graph_time(fn, reps=20):
     return time_calls(graph.replay, 1) / reps
 
 
-def bench_sweep(kf, dev, ceiling):
+def bench_sweep(kf, dev, ceil):
     """The reference's own size sweep (perfs/julia/benchmarks/
     scan_perf_comparison.jl:129-131, mapreduce_perf_comparison.jl:121-122):
     n in 10^6..10^9 for Float32, Float64 and UInt8, scan!(+) inclusive and
@@ -255,21 +308,119 @@ def bench_sweep(kf, dev, ceiling):
                     ("mapreduce", es * n, lambda: kf.mapreduce_(kf.identity, "+", o, x, tmp=tr))):
                 sec = _graph_time(fn, reps=20 if n < 10**9 else 5)
                 gb = bytes_ / sec / 1e9
+                c = ceil["copy_ceiling_gbps"] if what == "scan" else ceil["read_ceiling_gbps"]
                 rows.append({"op": what, "n": n, "dtype": str(dt).replace("torch.", ""),
                              "us": round(sec * 1e6, 2), "gbps": round(gb, 1),
-                             "elems_per_s": round(n / sec, 1), "frac_copy": round(gb / ceiling, 4)})
+                             "elems_per_s": round(n / sec, 1), "frac_ceiling": round(gb / c, 4)})
                 log(f"  {what:9s} {str(dt):14s} n={n:>10d} {sec*1e6:10.1f} us {gb:8.0f} GB/s "
-                    f"{gb/ceiling*100:5.1f}% of copy")
+                    f"{gb/c*100:5.1f}% of the {'copy' if what == 'scan' else 'read'} ceiling")
             del x, y, ts, tr
     return rows
 
 
-def bench_all(kf, dev, ceiling, json_path=None):
-    """Every BASELINE.json configuration: GB/s, % of peak, % of the copy ceiling."""
-    rows = []
+def config_cases(kf, dev):
+    """(key, name, algorithmic bytes, fn, reps) for every BASELINE.json
+    configuration (C1-C5) and the extra rows (X1-X8); each case's inputs are
+    alive until the next case is requested."""
+    import operator
     g = torch.Generator(device=dev).manual_seed(20261201)
 
-    def rec(name, bytes_, fn, reps=20):
+    def tmp_for(kind, src):
+        return kf.get_allocation(kind, kf.identity, "+", src)
+
+    x = torch.rand(10**6, device=dev, generator=g)
+    y = torch.empty_like(x)
+    t1 = tmp_for(kf.Scan1D, x)
+    yield "C1", "C1 scan F32 incl n=1e6", 8e6, lambda: kf.scan_("+", y, x, tmp=t1), 20
+    del x, y
+    xi = torch.randint(0, 16, (2**28,), device=dev, generator=g, dtype=torch.int32)
+    yi = torch.empty_like(xi)
+    t2 = tmp_for(kf.Scan1D, xi)
+    yield "C2i", "C2 scan Int32 incl n=2^28", 8 * 2**28, lambda: kf.scan_("+", yi, xi, tmp=t2), 20
+    yield "C2e", "C2 scan Int32 excl n=2^28", 8 * 2**28, lambda: kf.scan_("+", yi, xi, exclusive=True, tmp=t2), 20
+    o = torch.empty(1, device=dev, dtype=torch.int32)
+    xr = torch.randint(-2**31, 2**31 - 1, (2**28,), device=dev, generator=g, dtype=torch.int32)
+    t3 = tmp_for(kf.MapReduce1D, xr)
+    yield "C3c", "C3c mapreduce max Int32 n=2^28", 4 * 2**28, lambda: kf.mapreduce_(kf.identity, max, o, xr, tmp=t3), 20
+    del xi, yi, xr
+    xf = torch.randn(2**30, device=dev, generator=g)
+    of = torch.empty(1, device=dev)
+    t3f = tmp_for(kf.MapReduce1D, xf)
+    yield "C3a", "C3a mapreduce abs2,+ F32 n=2^30", 4 * 2**30, lambda: kf.mapreduce_(kf.abs2, "+", of, xf, tmp=t3f), 10
+    del xf
+    xd = torch.randn(2**28, device=dev, generator=g, dtype=torch.float64)
+    od = torch.empty(1, device=dev, dtype=torch.float64)
+    t3d = tmp_for(kf.MapReduce1D, xd)
+    yield "C3b", "C3b mapreduce abs2,+ F64 n=2^28", 8 * 2**28, lambda: kf.mapreduce_(kf.abs2, "+", od, xd, tmp=t3d), 20
+    del xd
+    ab = torch.empty(2**26, 2, device=dev)
+    ab[:, 0].uniform_(0.9, 1.0, generator=g)
+    ab[:, 1].normal_(generator=g)
+    yab = torch.empty_like(ab)
+    t4 = kf.get_allocation(kf.Scan1D, kf.identity, kf.affine, ab)
+    yield "C4", "C4 affine scan n=2^26", 16 * 2**26, lambda: kf.scan_(kf.affine, yab, ab, tmp=t4), 20
+    del ab, yab
+    t = torch.rand(2**28, device=dev, generator=g) * 2 - 1
+    A1 = t.as_strided((4096, 65536), (1, 4096))
+    t5 = kf.KernelBuffer(kf.MapReduce2D, 64 << 20, dev)  # >= every dims plan below
+    d1 = torch.empty(65536, device=dev)
+    yield "C5a", "C5a dims=1 4096x65536", 4 * 2**28 + 4 * 65536, \
+        lambda: kf.mapreduce_(kf.identity, "+", d1, A1, dims=1, tmp=t5), 20
+    A2 = t.as_strided((65536, 4096), (1, 65536))
+    d2 = torch.empty(65536, device=dev)
+    yield "C5b", "C5b dims=2 65536x4096", 4 * 2**28 + 4 * 65536, \
+        lambda: kf.mapreduce_(kf.identity, "+", d2, A2, dims=2, tmp=t5), 20
+    V1 = A1[:, ::2]
+    d1v = torch.empty(32768, device=dev)
+    yield "C5c", "C5c dims=1 view 4096x(65536/2)", 4 * 2**27 + 4 * 32768, \
+        lambda: kf.mapreduce_(kf.identity, "+", d1v, V1, dims=1, tmp=t5), 20
+    V2 = A2[:, ::2]
+    yield "C5d", "C5d dims=2 view 65536x(4096/2)", 4 * 2**27 + 4 * 65536, \
+        lambda: kf.mapreduce_(kf.identity, "+", d2, V2, dims=2, tmp=t5), 20
+    # beyond the BASELINE configs: vector operands and layouts off the vector path
+    xv = torch.rand(4096, device=dev, generator=g)
+    yield "X1", "X1 matvec 65536x4096 F32", 4 * 2**28 + 8 * 65536 + 4 * 4096, \
+        lambda: kf.matvec_(operator.mul, "+", d2, A2, xv, tmp=t5), 20
+    xr = torch.rand(4096, device=dev, generator=g)
+    yield "X2", "X2 vecmat 4096x65536 F32", 4 * 2**28 + 8 * 65536, \
+        lambda: kf.vecmat_(operator.mul, "+", d1, xr, A1, tmp=t5), 20
+    del t, A1, A2, V1, V2
+    xs = torch.rand(2**28, device=dev, generator=g)
+    ys = torch.empty_like(xs)
+    ts = tmp_for(kf.Scan1D, xs)
+    of1 = torch.empty(1, device=dev)
+    t3s = tmp_for(kf.MapReduce1D, xs)
+    yield "X3", "X3 scan F32 unaligned view x[1:] n=2^28-1", 8 * (2**28 - 1), \
+        lambda: kf.scan_("+", ys[1:], xs[1:], tmp=ts), 20
+    yield "X8", "X8 scan F32 x[1:] -> aligned dst n=2^28-1", 8 * (2**28 - 1), \
+        lambda: kf.scan_("+", ys[:-1], xs[1:], tmp=ts), 20
+    yield "X4", "X4 mapreduce F32 unaligned view x[1:]", 4 * (2**28 - 1), \
+        lambda: kf.mapreduce_(kf.identity, "+", of1, xs[1:], tmp=t3s), 20
+    del xs, ys
+    xd = torch.rand(2**27, device=dev, generator=g, dtype=torch.float64)
+    yd = torch.empty_like(xd)
+    td = tmp_for(kf.Scan1D, xd)
+    yield "X5", "X5 scan F64 incl n=2^27", 16 * 2**27, lambda: kf.scan_("+", yd, xd, tmp=td), 20
+    del xd, yd
+    xb = torch.randint(0, 255, (2**30,), device=dev, generator=g, dtype=torch.uint8)
+    yb = torch.empty_like(xb)
+    tb = tmp_for(kf.Scan1D, xb)
+    yield "X6", "X6 scan UInt8 incl n=2^30", 2 * 2**30, lambda: kf.scan_("+", yb, xb, tmp=tb), 20
+    del xb, yb
+    for n, label in ((10**5, "10^5"), (2**21, "2^21"), (2**23, "2^23")):
+        xs = torch.rand(n, device=dev, generator=g)
+        ys = torch.empty_like(xs)
+        ts = tmp_for(kf.Scan1D, xs)
+        yield f"X7-{label}", f"X7 scan F32 incl n={label}", 8 * n, lambda: kf.scan_("+", ys, xs, tmp=ts), 20
+
+
+def bench_all(kf, dev, ceil, json_path=None):
+    """Every configuration of config_cases: GB/s, % of peak, % of the ceiling
+    of its kind (scans: the copy ceiling; reductions: the read ceiling), and
+    the HBM traffic ratio recorded by rocprofv3 --pmc when profiles/ holds it."""
+    rows = []
+    traffic = load_config_traffic()
+    for key, name, bytes_, fn, reps in config_cases(kf, dev):
         # captured in a HIP graph so that host launch overhead does not hide
         # the kernel time of the small configurations
         fn()
@@ -281,98 +432,134 @@ def bench_all(kf, dev, ceiling, json_path=None):
         graph.replay()
         torch.cuda.synchronize()
         s = time_calls(graph.replay, 1) / reps
+        del graph
         gb = bytes_ / s / 1e9
-        rows.append({"config": name, "us": round(s * 1e6, 2), "gbps": round(gb, 1),
-                     "frac_peak": round(gb / PEAK_HBM_GBPS, 4), "frac_copy": round(gb / ceiling, 4)})
-        log(f"  {name:48s} {s*1e6:10.1f} us {gb:8.0f} GB/s  {gb/ceiling*100:5.1f}% of copy")
-
-    def tmp_for(kind, src, **kw):
-        return kf.get_allocation(kind, kf.identity, "+", src, **kw)
-
-    x = torch.rand(10**6, device=dev, generator=g)
-    y = torch.empty_like(x)
-    t1 = tmp_for(kf.Scan1D, x)
-    rec("C1 scan F32 incl n=1e6", 8e6, lambda: kf.scan_("+", y, x, tmp=t1))
-    del x, y
-    xi = torch.randint(0, 16, (2**28,), device=dev, generator=g, dtype=torch.int32)
-    yi = torch.empty_like(xi)
-    t2 = tmp_for(kf.Scan1D, xi)
-    rec("C2 scan Int32 incl n=2^28", 8 * 2**28, lambda: kf.scan_("+", yi, xi, tmp=t2))
-    rec("C2 scan Int32 excl n=2^28", 8 * 2**28, lambda: kf.scan_("+", yi, xi, exclusive=True, tmp=t2))
-    o = torch.empty(1, device=dev, dtype=torch.int32)
-    xr = torch.randint(-2**31, 2**31 - 1, (2**28,), device=dev, generator=g, dtype=torch.int32)
-    t3 = tmp_for(kf.MapReduce1D, xr)
-    rec("C3c mapreduce max Int32 n=2^28", 4 * 2**28, lambda: kf.mapreduce_(kf.identity, max, o, xr, tmp=t3))
-    del xi, yi, xr
-    xf = torch.randn(2**30, device=dev, generator=g)
-    of = torch.empty(1, device=dev)
-    t3f = tmp_for(kf.MapReduce1D, xf)
-    rec("C3a mapreduce abs2,+ F32 n=2^30", 4 * 2**30, lambda: kf.mapreduce_(kf.abs2, "+", of, xf, tmp=t3f), reps=10)
-    del xf
-    xd = torch.randn(2**28, device=dev, generator=g, dtype=torch.float64)
-    od = torch.empty(1, device=dev, dtype=torch.float64)
-    t3d = tmp_for(kf.MapReduce1D, xd)
-    rec("C3b mapreduce abs2,+ F64 n=2^28", 8 * 2**28, lambda: kf.mapreduce_(kf.abs2, "+", od, xd, tmp=t3d))
-    del xd
-    ab = torch.empty(2**26, 2, device=dev)
-    ab[:, 0].uniform_(0.9, 1.0, generator=g)
-    ab[:, 1].normal_(generator=g)
-    yab = torch.empty_like(ab)
-    t4 = kf.get_allocation(kf.Scan1D, kf.identity, kf.affine, ab)
-    rec("C4 affine scan n=2^26", 16 * 2**26, lambda: kf.scan_(kf.affine, yab, ab, tmp=t4))
-    del ab, yab
-    t = torch.rand(2**28, device=dev, generator=g) * 2 - 1
-    A1 = t.as_strided((4096, 65536), (1, 4096))
-    t5 = kf.KernelBuffer(kf.MapReduce2D, 64 << 20, dev)  # >= every dims plan below
-    d1 = torch.empty(65536, device=dev)
-    rec("C5a dims=1 4096x65536", 4 * 2**28 + 4 * 65536, lambda: kf.mapreduce_(kf.identity, "+", d1, A1, dims=1, tmp=t5))
-    A2 = t.as_strided((65536, 4096), (1, 65536))
-    d2 = torch.empty(65536, device=dev)
-    rec("C5b dims=2 65536x4096", 4 * 2**28 + 4 * 65536, lambda: kf.mapreduce_(kf.identity, "+", d2, A2, dims=2, tmp=t5))
-    V1 = A1[:, ::2]
-    d1v = torch.empty(32768, device=dev)
-    rec("C5c dims=1 view 4096x(65536/2)", 4 * 2**27 + 4 * 32768,
-        lambda: kf.mapreduce_(kf.identity, "+", d1v, V1, dims=1, tmp=t5))
-    V2 = A2[:, ::2]
-    rec("C5d dims=2 view 65536x(4096/2)", 4 * 2**27 + 4 * 65536,
-        lambda: kf.mapreduce_(kf.identity, "+", d2, V2, dims=2, tmp=t5))
-    # beyond the BASELINE configs: vector operands and layouts off the vector path
-    import operator
-    xv = torch.rand(4096, device=dev, generator=g)
-    rec("X1 matvec 65536x4096 F32", 4 * 2**28 + 8 * 65536 + 4 * 4096,
-        lambda: kf.matvec_(operator.mul, "+", d2, A2, xv, tmp=t5))
-    xr = torch.rand(4096, device=dev, generator=g)
-    rec("X2 vecmat 4096x65536 F32", 4 * 2**28 + 8 * 65536,
-        lambda: kf.vecmat_(operator.mul, "+", d1, xr, A1, tmp=t5))
-    xs = torch.rand(2**28, device=dev, generator=g)
-    ys = torch.empty_like(xs)
-    ts = tmp_for(kf.Scan1D, xs)
-    of1 = torch.empty(1, device=dev)
-    t3s = tmp_for(kf.MapReduce1D, xs)
-    rec("X3 scan F32 unaligned view x[1:] n=2^28-1", 8 * (2**28 - 1), lambda: kf.scan_("+", ys[1:], xs[1:], tmp=ts))
-    rec("X4 mapreduce F32 unaligned view x[1:]", 4 * (2**28 - 1),
-        lambda: kf.mapreduce_(kf.identity, "+", of1, xs[1:], tmp=t3s))
-    del xs, ys
-    xd = torch.rand(2**27, device=dev, generator=g, dtype=torch.float64)
-    yd = torch.empty_like(xd)
-    td = tmp_for(kf.Scan1D, xd)
-    rec("X5 scan F64 incl n=2^27", 16 * 2**27, lambda: kf.scan_("+", yd, xd, tmp=td))
-    del xd, yd
-    xb = torch.randint(0, 255, (2**30,), device=dev, generator=g, dtype=torch.uint8)
-    yb = torch.empty_like(xb)
-    tb = tmp_for(kf.Scan1D, xb)
-    rec("X6 scan UInt8 incl n=2^30", 2 * 2**30, lambda: kf.scan_("+", yb, xb, tmp=tb))
-    del xb, yb
-    for n, label in ((10**5, "10^5"), (2**21, "2^21"), (2**23, "2^23")):
-        xs = torch.rand(n, device=dev, generator=g)
-        ys = torch.empty_like(xs)
-        ts = tmp_for(kf.Scan1D, xs)
-        rec(f"X7 scan F32 incl n={label}", 8 * n, lambda: kf.scan_("+", ys, xs, tmp=ts))
+        kind = "copy" if " scan " in f" {name} " else "read"
+        c = ceil[f"{kind}_ceiling_gbps"]
+        row = {"config": name, "us": round(s * 1e6, 2), "gbps": round(gb, 1),
+               "frac_peak": round(gb / PEAK_HBM_GBPS, 4), "ceiling": kind, "frac_ceiling": round(gb / c, 4),
+               "hbm_traffic_ratio": traffic.get(key)}
+        rows.append(row)
+        log(f"  {name:48s} {s*1e6:10.1f} us {gb:8.0f} GB/s  {gb/c*100:5.1f}% of {kind} ceiling"
+            + (f"  traffic {row['hbm_traffic_ratio']:.4f}x" if row["hbm_traffic_ratio"] else ""))
     if json_path:
         os.makedirs(os.path.dirname(os.path.abspath(json_path)), exist_ok=True)
         with open(json_path, "w") as fh:
-            json.dump({"copy_ceiling_gbps": ceiling, "rows": rows}, fh, indent=1)
+            json.dump({"ceilings": ceil, "rows": rows}, fh, indent=1)
     return rows
+
+
+# ---------------------------------------------------------------------------
+# Per-configuration HBM traffic (rocprofv3 --pmc)
+# ---------------------------------------------------------------------------
+PMC_REPS = 3
+CAL_BYTES = 1 << 30
+
+
+def pmc_run(kf, dev):
+    """The dispatch sequence that `rocprofv3 --pmc` counts: a calibration copy
+    of CAL_BYTES (kf_copy, 1 GiB read + 1 GiB written), then every case of
+    config_cases PMC_REPS times, each case preceded by a marker (a 16-byte
+    kf_fill, one fill_kernel workgroup) so that the summary can split the
+    dispatches by case."""
+    marker = torch.zeros(4, dtype=torch.int32, device=dev)
+
+    def begin():  # a 16-byte fill: one fill_kernel workgroup of 256 lanes
+        kf.setvalue_(marker, 1)
+
+    def end():  # a 4-byte fill: one fill_elems_kernel workgroup of 64 lanes
+        kf.setvalue_(marker[:1], 2)
+
+    a = torch.rand(CAL_BYTES // 4, device=dev)
+    b = torch.empty_like(a)
+    cases = [["CAL", "kf_copy calibration, 1 GiB -> 1 GiB", 2 * CAL_BYTES]]
+    begin()
+    kf.vcopy_(b, a)
+    end()
+    torch.cuda.synchronize()
+    del a, b
+    for key, name, bytes_, fn, reps in config_cases(kf, dev):
+        fn()  # outside the counted segment: first-call setup
+        torch.cuda.synchronize()
+        begin()
+        for _ in range(PMC_REPS):
+            fn()
+        end()
+        torch.cuda.synchronize()
+        cases.append([key, name, bytes_])
+        log(f"pmc: {key}")
+    print(json.dumps({"pmc_cases": cases}), flush=True)
+
+
+def _read_counters(path):
+    """[(kernel name, grid size, {counter: value})] in dispatch order from a
+    rocprofv3 counter_collection.csv (one row per dispatch and counter)."""
+    import csv
+    import glob
+    files = glob.glob(os.path.join(path, "**", "*counter_collection.csv"), recursive=True)
+    if not files:
+        raise SystemExit(f"no counter_collection.csv under {path}")
+    disp = {}
+    for f in files:
+        with open(f) as fh:
+            for r in csv.DictReader(fh):
+                k = (int(r["Dispatch_Id"]), r.get("Process_Id", ""))
+                d = disp.setdefault(k, [r["Kernel_Name"], int(r["Grid_Size"]), {}])
+                d[2][r["Counter_Name"]] = d[2].get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+    return [disp[k] for k in sorted(disp)]
+
+
+def _segments(dispatches):
+    """The dispatches between each begin marker (fill_kernel, grid 256) and
+    the following end marker (fill_elems_kernel, grid 64)."""
+    segs, cur = [], None
+    for name, grid, ctr in dispatches:
+        if "fill_kernel" in name and "fill_elems" not in name and grid == 256:
+            cur = []
+            segs.append(cur)
+        elif "fill_elems_kernel" in name and grid == 64:
+            cur = None
+        elif cur is not None:
+            cur.append((name, grid, ctr))
+    return segs
+
+
+def pmc_summary(fetch_dir, write_dir, cases_json, out_json):
+    """Per-case HBM bytes per call from a FETCH_SIZE run and a WRITE_SIZE run
+    of `bench.py --pmc-run`, each scaled by what the counter reads for the
+    calibration copy of known size, against the case's algorithmic bytes."""
+    cases = None
+    with open(cases_json) as fh:
+        for line in fh:
+            if line.startswith('{"pmc_cases"'):
+                cases = json.loads(line)["pmc_cases"]
+    keys = [c[0] for c in cases]
+    algo = {c[0]: c[2] for c in cases}
+    names = {c[0]: c[1] for c in cases}
+    fetch = _segments(_read_counters(fetch_dir))
+    write = _segments(_read_counters(write_dir))
+    if len(fetch) != len(keys) or len(write) != len(keys):
+        raise SystemExit(f"segments: fetch {len(fetch)}, write {len(write)}, cases {len(keys)}")
+
+    def total(seg, ctr):
+        return sum(c.get(ctr, 0.0) for _, _, c in seg) * 1024.0  # counters are KiB per dispatch
+
+    f_cal = CAL_BYTES / total(fetch[0], "FETCH_SIZE")
+    w_cal = CAL_BYTES / total(write[0], "WRITE_SIZE")
+    out = {"calibration": {"fetch_scale": f_cal, "write_scale": w_cal,
+                           "kernel": "kf_copy 1 GiB -> 1 GiB (copy_kernel)"}, "configs": {}}
+    for i, key in enumerate(keys[1:], 1):
+        fb = total(fetch[i], "FETCH_SIZE") * f_cal / PMC_REPS
+        wb = total(write[i], "WRITE_SIZE") * w_cal / PMC_REPS
+        kern = sorted({f"{n.split('(')[0]} (grid {g})" for n, g, _ in fetch[i]})
+        out["configs"][key] = {"name": names.get(key, key), "fetch_bytes": fb, "write_bytes": wb,
+                               "algorithmic_bytes": algo[key], "ratio": (fb + wb) / algo[key],
+                               "dispatches_per_call": len(fetch[i]) / PMC_REPS, "kernels": kern}
+    with open(out_json, "w") as fh:
+        json.dump(out, fh, indent=1)
+    for key, v in out["configs"].items():
+        print(f"{key:8s} {v['name']:48s} fetch {v['fetch_bytes']:.4g} write {v['write_bytes']:.4g} "
+              f"algo {v['algorithmic_bytes']:.4g} ratio {v['ratio']:.4f}")
 
 
 if __name__ == "__main__":

@@ -287,6 +287,29 @@ int kf_copy(void* dst, const void* src, size_t bytes, void* stream);
  * src/copy/copy.jl:52-56 / setvalue_kernel! src/copy/copy_kernel.jl:20-35. */
 int kf_fill(void* dst, int64_t count, const void* value, size_t value_bytes, void* stream);
 
+/* ----------------------------------------------------------- bandwidth ----
+ * Measurement probes (no counterpart in the reference's library; they play
+ * the part of its vendor copy benchmark,
+ * perfs/cuda_cpp/cub_nvcc/cub_memcpy_benchmark.cu, bytes = 2N): the copy
+ * and read ceilings the scan and reduction kernels are measured against.
+ * src, dst and bytes must be multiples of 16. The copies write dst[0:bytes];
+ * the reads load src[0:bytes] and use dst only as a 4-byte sink.
+ * KF_BW_COPY_ORDERED needs kf_bw_probe_scratch_bytes(bytes) of scratch (no
+ * zeroing needed; its epoch comes from a host counter, so it must not be
+ * captured into a graph). */
+typedef enum {
+  KF_BW_COPY = 0,          /* kf_copy: one 16-byte vector per lane, 256 threads    */
+  KF_BW_COPY_TILED = 1,    /* the scan's tile shape: 768 threads x 8 striped vectors */
+  KF_BW_COPY_ORDERED = 2,  /* one vector per lane; tile t stores after tile t-1 loaded */
+  KF_BW_READ = 3,          /* read: one vector per lane                            */
+  KF_BW_READ_TILED = 4     /* read: two vectors per lane, 256 apart (reduction level 0) */
+} kf_bw_kind;
+
+size_t kf_bw_probe_scratch_bytes(size_t bytes);
+
+int kf_bw_probe(int kind, void* dst, const void* src, size_t bytes,
+                void* scratch, size_t scratch_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

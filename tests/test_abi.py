@@ -21,7 +21,8 @@ def test_header_declares_the_expected_surface():
         "kf_reduce_scratch_bytes", "kf_reduce", "kf_reduce_dim_scratch_bytes", "kf_reduce_dim", "kf_copy",
         "kf_reduce2_scratch_bytes", "kf_reduce2", "kf_reduce_dim_batched_scratch_bytes", "kf_reduce_dim_batched", "kf_post_map", "kf_reduce_dim_x",
         "kf_fill", "kf_scan_scratch_status", "kf_reduce3_scratch_bytes", "kf_reduce3",
-        "kf_reduce_noalloc", "kf_debug_scan_giveup"])
+        "kf_reduce_noalloc", "kf_debug_scan_giveup",
+        "kf_bw_probe_scratch_bytes", "kf_bw_probe"])
 
 
 def test_library_exports_every_declared_symbol(kf):
