@@ -17,6 +17,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--all [--all-json PA
                  and the rows inside the JSON line as "all_configs")
   --all-json     also write those rows, with the ceilings, to PATH
   --sweep        the reference's 10^6..10^9 size sweep
+  --timeline     only the per-tile phases of the scan (instrumented library)
   --pmc-run      only the marked dispatch sequence of every configuration,
                  for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs
   --pmc-summary  FETCH_DIR WRITE_DIR CASES_LOG OUT_JSON: per-configuration
@@ -123,6 +124,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--sweep", action="store_true",
                     help="the reference's scan/mapreduce size sweep (perfs/julia/benchmarks)")
+    ap.add_argument("--timeline", action="store_true",
+                    help="only the per-tile scan timeline (libkfhip_timeline.so)")
     ap.add_argument("--pmc-run", action="store_true",
                     help="only the dispatch sequence for rocprofv3 --pmc (see pmc_run)")
     ap.add_argument("--pmc-summary", nargs=4, metavar=("FETCH_DIR", "WRITE_DIR", "CASES_LOG", "OUT_JSON"),
@@ -142,6 +145,9 @@ def main():
     torch.cuda.set_device(dev)
     if args.pmc_run:
         pmc_run(kf, dev)
+        return
+    if args.timeline:
+        print(json.dumps({"scan_timeline": scan_timeline(dev)}), flush=True)
         return
 
     g = torch.Generator(device=dev).manual_seed(20261201)
@@ -446,6 +452,82 @@ def bench_all(kf, dev, ceil, json_path=None):
         os.makedirs(os.path.dirname(os.path.abspath(json_path)), exist_ok=True)
         with open(json_path, "w") as fh:
             json.dump({"ceilings": ceil, "rows": rows}, fh, indent=1)
+    return rows
+
+
+# ---------------------------------------------------------------------------
+# Per-tile timeline of the scan (libkfhip_timeline.so, built with KF_TIMELINE)
+# ---------------------------------------------------------------------------
+TIMELINE_CASES = (("C4 affine n=2^26", 5, 2**26), ("affine n=2^27", 5, 2**27), ("affine n=2^28", 5, 2**28),
+                  ("Float64 n=2^26", 1, 2**26), ("Float64 n=2^27", 1, 2**27), ("Float32 n=2^28", 0, 2**28))
+
+
+def scan_timeline(dev):
+    """Per-tile phases of the decoupled-lookback scan from the instrumented
+    library: each tile's thread 0 stamps the 100 MHz realtime counter at its
+    start, once its tile is scanned (loads done), once its prefix is known
+    (lookback done) and once its stores are issued. Per case: kernel time
+    (events, uninstrumented calls of the same library), tile phases
+    (medians), peak resident tiles, the steady-state bandwidth (bytes of the
+    tiles that finish between full residency and the last tile's start,
+    over that window) and the drain (last tile start to kernel end)."""
+    import ctypes
+    path = os.path.join(REPO, "kernelforge.jl_amd", "libkfhip_timeline.so")
+    L = ctypes.CDLL(path)
+    P, I, I64, SZ = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_size_t
+    L.kf_scan.argtypes = [I, I, I, I, I, P, I64, P, I64, I64, P, SZ, P]
+    L.kf_scan_scratch_bytes.argtypes = [I, I, I64]
+    L.kf_scan_scratch_bytes.restype = SZ
+    L.kf_debug_scan_timeline.argtypes = [P]
+    g = torch.Generator(device=dev).manual_seed(20261201)
+    rows = []
+    for label, dt, n in TIMELINE_CASES:
+        if dt == 5:
+            x = torch.empty(n, 2, device=dev)
+            x[:, 0].uniform_(0.9, 1.0, generator=g)
+            x[:, 1].normal_(generator=g)
+            op, es = 3, 8
+        else:
+            x = torch.rand(n, device=dev, generator=g, dtype=torch.float64 if dt == 1 else torch.float32)
+            op, es = 0, x.element_size()
+        y = torch.empty_like(x)
+        sb = L.kf_scan_scratch_bytes(dt, op, n)
+        scr = torch.zeros(sb, dtype=torch.uint8, device=dev)
+
+        def call():
+            rc = L.kf_scan(op, 0, 0, dt, 0, ctypes.c_void_p(x.data_ptr()), 1, ctypes.c_void_p(y.data_ptr()), 1, n,
+                           ctypes.c_void_p(scr.data_ptr()), sb, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+            assert rc == 0
+        call()
+        torch.cuda.synchronize()
+        t = time_calls(call, 10)
+        tiles_max = (sb - 256) // 128
+        buf = torch.zeros(tiles_max * 6, dtype=torch.int64, device=dev)
+        L.kf_debug_scan_timeline(ctypes.c_void_p(buf.data_ptr()))
+        call()
+        torch.cuda.synchronize()
+        L.kf_debug_scan_timeline(None)
+        a = buf.cpu().numpy().reshape(-1, 6)
+        a = a[a[:, 0] > 0]
+        t0 = a[:, 0].min()
+        st, sc, pf, en = ((a[:, k] - t0) * 0.01 for k in range(4))  # microseconds
+        ev = np.concatenate([np.stack([st, np.ones_like(st)], 1), np.stack([en, -np.ones_like(en)], 1)])
+        ev = ev[np.argsort(ev[:, 0], kind="stable")]
+        active = np.cumsum(ev[:, 1])
+        full = ev[np.argmax(active >= 0.95 * active.max()), 0]
+        last = st.max()
+        tile_bytes = 2 * es * n / len(a)
+        steady = ((en >= full) & (en <= last)).sum() * tile_bytes / (last - full) / 1e3
+        row = {"case": label, "us": round(t * 1e6, 1), "gbps": round(2 * es * n / t / 1e9), "tiles": len(a),
+               "peak_resident": int(active.max()), "span_us": round(float(en.max()), 1),
+               "tile_life_us": round(float(np.median(en - st)), 2), "load_scan_us": round(float(np.median(sc - st)), 2),
+               "lookback_us": round(float(np.median(pf - sc)), 2), "store_issue_us": round(float(np.median(en - pf)), 2),
+               "ramp_us": round(float(full), 2), "steady_gbps": round(float(steady)),
+               "drain_us": round(float(en.max() - last), 1),
+               "tiles_per_xcd": np.bincount(a[:, 4].astype(int) & 15, minlength=8)[:8].tolist()}
+        rows.append(row)
+        log(json.dumps(row))
+        del x, y, scr, buf
     return rows
 
 

@@ -58,6 +58,15 @@
 
 #include "kf_common.h"
 
+#ifdef KF_TIMELINE
+// Instrumented build only (build.py --timeline -> libkfhip_timeline.so):
+// every tile records, by thread 0, four 100 MHz realtime stamps (start,
+// tile scanned, prefix known, stores issued), its XCD and its HW_ID word
+// into kKfTimelineWords words at g_scan_timeline + tile * kKfTimelineWords.
+__device__ uint64_t* g_scan_timeline = nullptr;
+constexpr int kKfTimelineWords = 6;
+#endif
+
 namespace kf {
 
 constexpr int kScanBlock = 1024;       // large tiles (default)
@@ -459,6 +468,9 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
   }
   __syncthreads();
   if (s_stop) return;
+#ifdef KF_TIMELINE
+  const uint64_t tl_start = __builtin_amdgcn_s_memrealtime();
+#endif
   const uint64_t tk = s_ticket;
   const int64_t tile = (int64_t)(uint32_t)tk;
   const uint32_t epoch30 = (uint32_t)(tk >> 32) & 0x3fffffffu;
@@ -548,6 +560,9 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
   if constexpr (kLdsRows) carry = wave_row_prefixes<T, Op, V>(tot, s_rows[wave], lane);
   if (lane == 0) wave_agg[wave] = carry;
   __syncthreads();
+#ifdef KF_TIMELINE
+  const uint64_t tl_scanned = __builtin_amdgcn_s_memrealtime();
+#endif
 
   // ---- publish, look back, publish the inclusive prefix (wave 0) ----------
   // Lane w of wave 0 holds wave w's aggregate; a DPP scan over those lanes
@@ -597,6 +612,9 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
     }
   }
   __syncthreads();
+#ifdef KF_TIMELINE
+  const uint64_t tl_prefix = __builtin_amdgcn_s_memrealtime();
+#endif
   if (s_stop) return;  // this tile gave up: it stores nothing
   const T prefix = wave_pre[wave];
   if constexpr (kLdsRows) {
@@ -649,6 +667,18 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
       }
     }
   }
+#ifdef KF_TIMELINE
+  __syncthreads();
+  if (tid == 0 && g_scan_timeline) {
+    uint64_t* w = g_scan_timeline + tile * kKfTimelineWords;
+    w[0] = tl_start;
+    w[1] = tl_scanned;
+    w[2] = tl_prefix;
+    w[3] = __builtin_amdgcn_s_memrealtime();
+    w[4] = __builtin_amdgcn_s_getreg((3 << 11) | 20);  // HW_REG_XCC_ID[3:0]
+    w[5] = __builtin_amdgcn_s_getreg((31 << 11) | 4);  // HW_REG_HW_ID
+  }
+#endif
 }
 
 // Tile shape for n elements of T: a pure function of (T, n) so that the
@@ -890,3 +920,14 @@ extern "C" int kf_scan(kf_op op, kf_map f, kf_post g, kf_dtype dt, int exclusive
   }
   return kf_set_error(KF_EINVAL, "kf_scan: bad dtype");
 }
+
+#ifdef KF_TIMELINE
+// Points the instrumented scan kernels at a device buffer of
+// kKfTimelineWords words per tile (null: stop recording). Exported by
+// libkfhip_timeline.so only.
+extern "C" int kf_debug_scan_timeline(void* buf) {
+  if (hipMemcpyToSymbol(HIP_SYMBOL(g_scan_timeline), &buf, sizeof(buf)) != hipSuccess)
+    return kf_check_launch("kf_debug_scan_timeline");
+  return KF_OK;
+}
+#endif
