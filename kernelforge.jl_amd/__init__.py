@@ -361,18 +361,22 @@ def scan(*args, exclusive=False, tmp=None, g=None, check=False, **tuning):
 # mapreduce (reference src/mapreduce/mapreduce.jl:51-298)
 # ---------------------------------------------------------------------------
 def _normalize_dims(dims, nd):
+    """Sorted dims tuple; a non-positive d counts from the end (d -> nd + d + 1),
+    then range and duplicate checks with the reference's messages
+    (src/helpers.jl:194-198, src/mapreduce/mapreduce.jl:250-257)."""
     if isinstance(dims, int):
         dims = (dims,)
     try:
         dims = tuple(int(d) for d in dims)
     except TypeError:
         raise ArgumentError(f"dims must be an int or a tuple of ints, got {dims!r}")
+    dims = tuple(sorted(d if d > 0 else nd + d + 1 for d in dims))
     for d in dims:
         if not 1 <= d <= nd:
             raise ArgumentError(f"dimension {d} out of range for {nd}-dimensional array")
     if len(set(dims)) != len(dims):
         raise ArgumentError(f"duplicate dimensions in dims={dims}")
-    return tuple(sorted(dims))
+    return dims
 
 
 def _classify_dims(dims, nd):

@@ -35,6 +35,15 @@ def test_normalize_and_validate_dims(kf):
         kf._normalize_dims(0, 3)
     with pytest.raises(kf.ArgumentError):
         kf._normalize_dims((1, 1), 3)
+    # non-positive dims count from the end (reference src/helpers.jl:194-198):
+    # d -> nd + d + 1, so -1 is the last dim and 0 is one past it
+    assert kf._normalize_dims(-1, 3) == (3,)
+    assert kf._normalize_dims((-1, 1), 3) == (1, 3)
+    assert kf._normalize_dims(-3, 3) == (1,)
+    with pytest.raises(kf.ArgumentError):
+        kf._normalize_dims(-4, 3)
+    with pytest.raises(kf.ArgumentError):
+        kf._normalize_dims((3, -1), 3)
 
 
 @pytest.mark.parametrize("dims,nd,expected", [
