@@ -361,6 +361,16 @@ def test_dims_nd_routing(kf, dev, dims):
     np.testing.assert_allclose(got.cpu().numpy(), ref, rtol=1e-12)
 
 
+@pytest.mark.parametrize("dims,same", [(-1, 3), ((-1, 1), (1, 3)), (-3, 1), ((-2, -1), (2, 3))])
+def test_negative_dims_count_from_the_end(kf, dev, dims, same):
+    # reference src/helpers.jl:194-198: d <= 0 means dim nd + d + 1
+    rng = np.random.default_rng(47)
+    x = torch.from_numpy(rng.integers(-9, 9, (6, 5, 8)).astype(np.int64)).to(dev).permute(2, 1, 0)
+    got = kf.mapreduce(kf.identity, "+", x, dims=dims)
+    ref = kf.mapreduce(kf.identity, "+", x, dims=same)
+    assert torch.equal(got, ref)
+
+
 def test_dims_errors(kf, dev):
     x = torch.zeros(4, 5, device=dev).T
     with pytest.raises(kf.ArgumentError):

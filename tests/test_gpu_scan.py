@@ -413,12 +413,49 @@ def test_config4_affine_2pow26(kf, oracle, dev):
 
 
 def test_headline_f32_2pow28(kf, oracle, dev):
-    # the bench workload; tolerance 1e-4 relative (the lookback chain over
-    # 65536 tiles adds one Float32 rounding per tile to the running prefix)
+    # The bench workload, against the Float64 prefix sums. Bound per element:
+    #   |y_i - s_i| <= lam * sqrt(D) * u * sum_{k<=i} |x_k|,   u = 2^-24,
+    # the probabilistic rounding bound of Higham & Mary (SIAM J. Sci. Comput.
+    # 41(5), 2019) for D roundings, with lam = 6 (each rounding set fails with
+    # probability below 2e-8). Only the roundings of a running prefix are of
+    # the size u * s_i; there are at most two per lookback hop (the window's
+    # predecessor aggregates folded into the prefix found, then the tile's own
+    # aggregate), and at most one hop per tile, so D = 2 * tiles; the tiles'
+    # in-lane, wave and block sums round values a tile's total or smaller.
+    # At 768 x 8 x 4 = 24576 elements per tile, 2^28 elements are 10923
+    # tiles: bound 5.3e-5 relative. A dropped or doubled tile moves every
+    # later prefix by about 12288 (a tile of U[0,1) values), which exceeds
+    # the bound everywhere (at most 5.3e-5 * 1.34e8 = 7.1e3 at the end);
+    # test_headline_exact_sparse checks the same size bit for bit.
     rng = np.random.default_rng(20261201 + 5)
-    x = rng.random(2**28, dtype=np.float32)
+    n = 2**28
+    x = rng.random(n, dtype=np.float32)
     got = run(kf, dev, x, "+")
-    assert_close(got, oracle.scan(x), 1e-4, what="F32 n=2^28")
+    ref = oracle.scan(x)                      # Float64, x >= 0: the sum of |x_k|
+    tiles = -(-n // (768 * 8 * 4))
+    bound = 6.0 * np.sqrt(2.0 * tiles) * 2.0**-24
+    assert bound * ref[-1] < (768 * 8 * 4) * 0.5 * 0.999
+    err = np.abs(got.astype(np.float64) - ref)
+    worst = float(np.max(err / np.maximum(ref, 1.0)))
+    print(f"headline F32 2^28: max relative error {worst:.3e}, bound {bound:.3e}", flush=True)
+    assert np.all(err <= bound * np.maximum(ref, 1.0)), worst
+
+
+def test_headline_exact_sparse(kf, oracle, dev):
+    # 2^28 Float32 values in {0, 1} (one in 64): every prefix is an integer
+    # below 2^24, so every rounding is exact and the scan must match the
+    # integer prefix sums bit for bit; a wrong combine anywhere (a dropped,
+    # doubled or reordered tile, window or row) is an integer mismatch
+    rng = np.random.default_rng(20261201 + 6)
+    n = 2**28
+    x = (rng.random(n) < 2**-6).astype(np.float32)
+    for exclusive in (False, True):
+        got = run(kf, dev, x, "+", exclusive=exclusive)
+        ref = np.cumsum(x, dtype=np.int64)
+        if exclusive:
+            ref = np.concatenate([[0], ref[:-1]])
+        assert ref[-1] < 2**24
+        assert np.array_equal(got.astype(np.int64), ref), exclusive
 
 
 @pytest.mark.parametrize("exclusive", [False, True])
