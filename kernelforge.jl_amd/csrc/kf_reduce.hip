@@ -12,7 +12,7 @@
 //    (mapreduce1d_kernel.jl:66-92); here the last level's workgroups (at
 //    most kFoldMax) publish epoch-tagged partial slots with relaxed
 //    device-scope stores and the last workgroup gathers them
-//    (fold_partial). Arrays of up to 8*256*kFoldMax vectors (64 MiB) take one
+//    (fold_partial). Arrays of up to 16*256*kFoldMax vectors (128 MiB) take one
 //    launch; larger ones a one-shot level 0 that writes partials and a
 //    folding level 1. A "last workgroup done" ticket was measured to
 //    serialise same-address device atomics at the end of the grid (1.8
@@ -277,16 +277,21 @@ template <class T> int reduce_grid(int64_t n) {
 // (read as 16-byte vectors) with kOnceUnroll per lane, until at most
 // kFoldMax partial-producing workgroups remain: the last level folds its
 // partials into the result inside the same launch (fold_partial), so no
-// separate combine launch is needed. u0 is the smallest of 2, 4 and 8 that
-// brings level 0 itself under kFoldMax (one launch in all), else 2.
-// Measured on MI355X (F32 sum): 2^28 157 us in two launches (level 0 at
-// u0 = 2, 4 or 8 within 1 %; before, a third combine_all_kernel launch made
-// it 160-162 us); 10^7 one launch at u0 = 8, 7.0 us in a HIP graph.
+// separate combine launch is needed. u0 is the smallest of 2, 4, 8 and 16
+// that brings level 0 itself under kFoldMax, so arrays of up to 128 MiB
+// reduce in one launch; larger ones take u0 = 2 and a folding level 1.
+// Measured on MI355X (HIP graphs, us; one launch at the adaptive width
+// against level 0 at 2 vectors + a folding level 1): Float32 5*10^6 4.06
+// vs 6.97, 10^7 6.80 vs 10.37, 2*10^7 12.3 vs 14.3; Float64 8*10^6 10.1 vs
+// 14.2; UInt8 1.2*10^8 20.9 vs 20.3 (the one loss); eager calls gain the
+// launch too (Float32 10^7 7.1 vs 10.7). At 2^28 Float32, 157 us in two
+// launches; before, a third combine_all_kernel launch made it 160-162 us.
 // Single-launch alternatives measured slower at 2^28: 2048 persistent
 // workgroups over contiguous chunks (161 us), one-shot workgroups whose
 // group leaders wait for their group's partials (165 us; 160 us with the
 // groups formed per XCD), and a last-arriver fold by device-scope atomic
 // counters (188 us: the atomics serialise).
+constexpr int kOnceMaxUnroll = 16;
 struct OnceLevels {
   int nlev;
   int u0;
@@ -296,7 +301,7 @@ inline OnceLevels once_levels(int64_t nvec, int epv, bool adaptive = true) {
   OnceLevels L{};
   L.u0 = kOnceUnroll;
   if (adaptive) {
-    for (int u = kOnceUnroll; u <= 8; u *= 2)
+    for (int u = kOnceUnroll; u <= kOnceMaxUnroll; u *= 2)
       if ((nvec + (int64_t)kRedBlock * u - 1) / ((int64_t)kRedBlock * u) <= kFoldMax) {
         L.u0 = u;
         break;
@@ -330,7 +335,10 @@ inline size_t reduce_scratch(size_t es, int64_t n) {
 template <class T, class Op, class Map, bool FOLD>
 void launch_once(int u, unsigned grid, const T* src, int64_t n, int64_t head, int64_t nvec, T* out, uint64_t* hdr,
                  hipStream_t stream) {
-  if (u == 8)
+  if (u == 16)
+    hipLaunchKernelGGL((reduce_once_kernel<T, Op, Map, FOLD, 16>), dim3(grid), dim3(kRedBlock), 0, stream, src, n, head,
+                       nvec, out, hdr);
+  else if (u == 8)
     hipLaunchKernelGGL((reduce_once_kernel<T, Op, Map, FOLD, 8>), dim3(grid), dim3(kRedBlock), 0, stream, src, n, head,
                        nvec, out, hdr);
   else if (u == 4)
