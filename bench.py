@@ -295,9 +295,28 @@ def bench_sweep(kf, dev, ceil):
     """The reference's own size sweep (perfs/julia/benchmarks/
     scan_perf_comparison.jl:129-131, mapreduce_perf_comparison.jl:121-122):
     n in 10^6..10^9 for Float32, Float64 and UInt8, scan!(+) inclusive and
-    mapreduce(identity, +). HIP-graph timed; GB/s of algorithmic bytes."""
+    mapreduce(identity, +). HIP-graph timed; GB/s of algorithmic bytes, as a
+    fraction of the 1 GiB ceiling of its kind and of a same-size copy (the
+    best of kf_bw_probe's copies over the scan's bytes) or read (the best
+    read probe over the reduction's bytes): below ~100 MB launch latency and
+    the first tiles' ramp bound copies too."""
+    import ctypes
+    L, K = kf._lib.lib(), kf._lib
     rows = []
     g = torch.Generator(device=dev).manual_seed(20261201)
+
+    def probe_us(kinds, nbytes, dst, src, scratch):
+        best = None
+        for kind in kinds:
+            def fn():
+                K.check(L.kf_bw_probe(kind, ctypes.c_void_p(dst.data_ptr()), ctypes.c_void_p(src.data_ptr()), nbytes,
+                                      ctypes.c_void_p(scratch.data_ptr()), scratch.numel(),
+                                      ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)), "kf_bw_probe")
+            t = _graph_time(fn, reps=20 if nbytes < 10**9 else 5) if kind != K.BW_COPY_ORDERED else \
+                time_calls(fn, 20)  # the ordered copy takes its epoch from a host counter: no graph
+            best = t if best is None else min(best, t)
+        return best
+
     for n in (10**6, 10**7, 10**8, 10**9):
         for dt in (torch.float32, torch.float64, torch.uint8):
             if dt == torch.uint8:
@@ -309,6 +328,11 @@ def bench_sweep(kf, dev, ceil):
             o = torch.empty(1, device=dev, dtype=dt)
             ts = kf.get_allocation(kf.Scan1D, kf.identity, "+", x)
             tr = kf.get_allocation(kf.MapReduce1D, kf.identity, "+", x)
+            nb = n * es // 16 * 16
+            pscr = torch.empty(L.kf_bw_probe_scratch_bytes(nb), dtype=torch.uint8, device=dev)
+            sink = torch.zeros(4, dtype=torch.int32, device=dev)
+            same = {"scan": probe_us((K.BW_COPY, K.BW_COPY_ORDERED), nb, y, x, pscr),
+                    "mapreduce": probe_us((K.BW_READ, K.BW_READ_TILED), nb, sink, x, pscr)}
             for what, bytes_, fn in (
                     ("scan", 2 * es * n, lambda: kf.scan_("+", y, x, tmp=ts)),
                     ("mapreduce", es * n, lambda: kf.mapreduce_(kf.identity, "+", o, x, tmp=tr))):
@@ -317,10 +341,14 @@ def bench_sweep(kf, dev, ceil):
                 c = ceil["copy_ceiling_gbps"] if what == "scan" else ceil["read_ceiling_gbps"]
                 rows.append({"op": what, "n": n, "dtype": str(dt).replace("torch.", ""),
                              "us": round(sec * 1e6, 2), "gbps": round(gb, 1),
-                             "elems_per_s": round(n / sec, 1), "frac_ceiling": round(gb / c, 4)})
+                             "elems_per_s": round(n / sec, 1), "frac_ceiling": round(gb / c, 4),
+                             "same_size_probe_us": round(same[what] * 1e6, 2),
+                             "frac_same_size": round(same[what] / sec, 4)})
                 log(f"  {what:9s} {str(dt):14s} n={n:>10d} {sec*1e6:10.1f} us {gb:8.0f} GB/s "
-                    f"{gb/c*100:5.1f}% of the {'copy' if what == 'scan' else 'read'} ceiling")
-            del x, y, ts, tr
+                    f"{gb/c*100:5.1f}% of the {'copy' if what == 'scan' else 'read'} ceiling, "
+                    f"same-size {'copy' if what == 'scan' else 'read'} {same[what]*1e6:.1f} us "
+                    f"({same[what]/sec*100:.0f}%)")
+            del x, y, ts, tr, pscr
     return rows
 
 
