@@ -22,6 +22,8 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--all [--all-json PA
                  for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs
   --pmc-summary  FETCH_DIR WRITE_DIR CASES_LOG OUT_JSON: per-configuration
                  HBM bytes from those two runs (no GPU)
+  --trace-summary TRACE_DIR BENCH_JSON OUT_MD: per-row kernel tables of a
+                 rocprofv3 --kernel-trace run of --all / --sweep (no GPU)
 """
 import argparse
 import json
@@ -130,7 +132,12 @@ def main():
                     help="only the dispatch sequence for rocprofv3 --pmc (see pmc_run)")
     ap.add_argument("--pmc-summary", nargs=4, metavar=("FETCH_DIR", "WRITE_DIR", "CASES_LOG", "OUT_JSON"),
                     help="summarise two --pmc-run profiles (FETCH_SIZE, WRITE_SIZE); no GPU needed")
+    ap.add_argument("--trace-summary", nargs=3, metavar=("TRACE_DIR", "BENCH_JSON", "OUT_MD"),
+                    help="per-row kernel tables from a rocprofv3 --kernel-trace run of --all/--sweep; no GPU needed")
     args = ap.parse_args()
+    if args.trace_summary:
+        trace_summary(*args.trace_summary)
+        return
     if args.pmc_summary:
         pmc_summary(*args.pmc_summary)
         return
@@ -240,6 +247,19 @@ def main():
     print(json.dumps(line), flush=True)
 
 
+_MARKER = {}
+
+
+def _mark(kf, dev, begin):
+    """Marker fills around each measured row, so that a kernel trace can be
+    split by row: begin = a 16-byte kf_fill (one fill_kernel workgroup of
+    256 lanes), end = a 4-byte one (one fill_elems_kernel workgroup of 64)."""
+    t = _MARKER.get(dev)
+    if t is None:
+        t = _MARKER[dev] = torch.zeros(4, dtype=torch.int32, device=dev)
+    kf.setvalue_(t if begin else t[:1], 1 if begin else 2)
+
+
 def measure_ceilings(kf, dev, src):
     """Copy and read ceilings on the same 1 GiB buffer (2^28 Float32): GB/s
     of algorithmic bytes (copy 2 x bytes, read 1 x bytes) of every
@@ -336,7 +356,9 @@ def bench_sweep(kf, dev, ceil):
             for what, bytes_, fn in (
                     ("scan", 2 * es * n, lambda: kf.scan_("+", y, x, tmp=ts)),
                     ("mapreduce", es * n, lambda: kf.mapreduce_(kf.identity, "+", o, x, tmp=tr))):
+                _mark(kf, dev, True)
                 sec = _graph_time(fn, reps=20 if n < 10**9 else 5)
+                _mark(kf, dev, False)
                 gb = bytes_ / sec / 1e9
                 c = ceil["copy_ceiling_gbps"] if what == "scan" else ceil["read_ceiling_gbps"]
                 rows.append({"op": what, "n": n, "dtype": str(dt).replace("torch.", ""),
@@ -457,6 +479,7 @@ def bench_all(kf, dev, ceil, json_path=None):
     for key, name, bytes_, fn, reps in config_cases(kf, dev):
         # captured in a HIP graph so that host launch overhead does not hide
         # the kernel time of the small configurations
+        _mark(kf, dev, True)
         fn()
         torch.cuda.synchronize()
         graph = torch.cuda.CUDAGraph()
@@ -466,6 +489,7 @@ def bench_all(kf, dev, ceil, json_path=None):
         graph.replay()
         torch.cuda.synchronize()
         s = time_calls(graph.replay, 1) / reps
+        _mark(kf, dev, False)
         del graph
         gb = bytes_ / s / 1e9
         kind = "copy" if " scan " in f" {name} " else "read"
@@ -632,6 +656,52 @@ def _segments(dispatches):
         elif cur is not None:
             cur.append((name, grid, ctr))
     return segs
+
+
+def trace_summary(trace_dir, bench_json, out_md):
+    """Markdown tables of a `rocprofv3 --kernel-trace` run of `bench.py --all
+    [--sweep]`: the dispatches between each row's markers, grouped by kernel
+    and grid, with the kernel time per call of the row (the sum over its
+    kernels of duration x dispatches / calls of its most frequent kernel)
+    and GB/s of the row's algorithmic bytes at that time."""
+    import csv
+    import glob
+    import statistics
+    files = glob.glob(os.path.join(trace_dir, "**", "*kernel_trace.csv"), recursive=True)
+    if not files:
+        raise SystemExit(f"no kernel_trace.csv under {trace_dir}")
+    disp = []
+    for f in files:
+        with open(f) as fh:
+            for r in csv.DictReader(fh):
+                grid = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
+                disp.append((int(r["Start_Timestamp"]), r["Kernel_Name"], grid,
+                             (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3))
+    disp.sort()
+    segs = _segments([(name, grid, {"us": us}) for _, name, grid, us in disp])
+    line = [json.loads(x) for x in open(bench_json) if x.startswith("{")][0]
+    rows = [(r["config"], r["gbps"] * r["us"] * 1e3) for r in line.get("all_configs", [])]
+    rows += [(f"sweep {r['op']} {r['dtype']} n={r['n']}",
+              r["gbps"] * r["us"] * 1e3) for r in line.get("sweep", [])]
+    if len(segs) != len(rows):
+        raise SystemExit(f"{len(segs)} marked segments, {len(rows)} rows")
+    out = ["| row | kernel | grid (work-items) | dispatches | avg µs | min µs | max µs | kernel µs per call | GB/s at that |",
+           "|---|---|---|---|---|---|---|---|---|"]
+    for (label, nbytes), seg in zip(rows, segs):
+        groups = {}
+        for name, grid, c in seg:
+            groups.setdefault((name.split("(")[0].replace("void ", "").replace("kf::", ""), grid), []).append(c["us"])
+        calls = max(len(v) for v in groups.values())
+        per_call = sum(sum(v) for v in groups.values()) / calls
+        first = True
+        for (name, grid), v in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+            out.append(f"| {label if first else ''} | `{name}` | {grid} | {len(v)} | {statistics.mean(v):.2f} | "
+                       f"{min(v):.2f} | {max(v):.2f} | " + (f"{per_call:.2f} | {nbytes / per_call / 1e3:.0f} |"
+                                                              if first else " | |"))
+            first = False
+    with open(out_md, "w") as fh:
+        fh.write("\n".join(out) + "\n")
+    print("\n".join(out))
 
 
 def pmc_summary(fetch_dir, write_dir, cases_json, out_json):
