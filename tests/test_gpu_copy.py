@@ -86,3 +86,46 @@ def test_setvalue_rejects(kf, dev):
         kf.setvalue_(x[:, 0], 1.0)          # not contiguous
     with pytest.raises(kf.ArgumentError):
         kf.setvalue_(x, (1.0, 2.0))         # tuple length does not match the rows
+
+
+# ---- the bandwidth probes behind bench.py's ceilings --------------------------
+@pytest.mark.parametrize("nbytes", [16, 4096, 4096 * 3 + 16, 1 << 20, (96 << 10) * 5 + 48, 64 << 20])
+def test_bw_probe_copies_are_exact(kf, dev, nbytes):
+    # every copy kind moves the bytes exactly (the ordered copy twice in a row:
+    # its flags from the first call must not let the second skip its order)
+    import ctypes
+    L, K = kf._lib.lib(), kf._lib
+    g = torch.Generator(device=dev).manual_seed(nbytes)
+    src = torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device=dev, generator=g)
+    scratch = torch.empty(L.kf_bw_probe_scratch_bytes(nbytes), dtype=torch.uint8, device=dev)
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for kind in (K.BW_COPY, K.BW_COPY_TILED, K.BW_COPY_ORDERED, K.BW_COPY_ORDERED):
+        dst = torch.zeros_like(src)
+        rc = L.kf_bw_probe(kind, ctypes.c_void_p(dst.data_ptr()), ctypes.c_void_p(src.data_ptr()), nbytes,
+                           ctypes.c_void_p(scratch.data_ptr()), scratch.numel(), s)
+        assert rc == K.KF_OK, L.kf_last_error()
+        torch.cuda.synchronize()
+        assert torch.equal(dst, src), (kind, nbytes)
+
+
+def test_bw_probe_reads_write_nothing_but_their_sink(kf, dev):
+    import ctypes
+    L, K = kf._lib.lib(), kf._lib
+    nbytes = 1 << 24
+    src = torch.arange(nbytes // 4, dtype=torch.int32, device=dev)
+    sink = torch.full((4,), 7, dtype=torch.int32, device=dev)
+    before = src.clone()
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for kind in (K.BW_READ, K.BW_READ_TILED):
+        rc = L.kf_bw_probe(kind, ctypes.c_void_p(sink.data_ptr()), ctypes.c_void_p(src.data_ptr()), nbytes, None, 0, s)
+        assert rc == K.KF_OK, L.kf_last_error()
+    torch.cuda.synchronize()
+    assert torch.equal(src, before)
+    assert sink[1:].tolist() == [7, 7, 7]   # the sink's first word is the only one a probe may touch
+    # argument checks: misaligned sizes and a missing scratch for the ordered copy
+    assert L.kf_bw_probe(K.BW_COPY, ctypes.c_void_p(sink.data_ptr()), ctypes.c_void_p(src.data_ptr()), 15, None, 0,
+                         s) == K.KF_EINVAL
+    assert L.kf_bw_probe(K.BW_COPY_ORDERED, ctypes.c_void_p(sink.data_ptr()), ctypes.c_void_p(src.data_ptr()), 16,
+                         None, 0, s) == K.KF_ENOSCRATCH
+    assert L.kf_bw_probe(99, ctypes.c_void_p(sink.data_ptr()), ctypes.c_void_p(src.data_ptr()), 16, None, 0,
+                         s) == K.KF_EINVAL
