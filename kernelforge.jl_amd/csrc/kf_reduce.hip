@@ -12,8 +12,10 @@
 //    (mapreduce1d_kernel.jl:66-92); here the last level's workgroups (at
 //    most kFoldMax) publish epoch-tagged partial slots with relaxed
 //    device-scope stores and the last workgroup gathers them
-//    (fold_partial). Arrays of up to 16*256*kFoldMax vectors (128 MiB) take one
-//    launch; larger ones a one-shot level 0 that writes partials and a
+//    (fold_partial). Every contiguous reduction takes one launch: up to
+//    16*256*kFoldMax vectors (128 MiB) one-shot workgroups of 2-16 vectors
+//    per lane, from 256 MiB kFoldMax persistent workgroups over contiguous
+//    chunks; in between, a one-shot level 0 that writes partials and a
 //    folding level 1. A "last workgroup done" ticket was measured to
 //    serialise same-address device atomics at the end of the grid (1.8
 //    TB/s with 8192 workgroups), and fences cost more than the launch they
@@ -234,6 +236,62 @@ __global__ __launch_bounds__(kRedBlock) void reduce_once_kernel(const T* src, in
   }
 }
 
+// Persistent single-launch reduction for arrays of kChunkMinVecs vectors
+// (256 MiB) or more: kFoldMax workgroups, workgroup b streaming the
+// contiguous chunk [b*chunk, (b+1)*chunk) of vectors with U loads in flight
+// per lane, then the fold. Measured on MI355X against one-shot level 0 +
+// folding level 1 (eager, us): Float32 2^26 41.0 vs 41.9-43.1, 2^28 154.0
+// vs 156.9, 2^30 606 vs 622; Float64 2^26 79.1 vs 80.9, 2^28 305 vs 318;
+// Int32 2^28 153.7 vs 156.7. At 200 MB (5*10^7 Float32, 1.5 loop
+// iterations per lane) it lost (32.5 vs 31.6), hence the threshold; 8 loads
+// in flight instead of 16 were 1-2 % slower.
+constexpr int64_t kChunkMinVecs = (int64_t)1 << 24;
+constexpr int kChunkUnroll = 16;
+template <class T, class Op, class Map, int U>
+__global__ __launch_bounds__(kRedBlock) void reduce_chunk_kernel(const T* src, int64_t n, int64_t head, int64_t nvec,
+                                                                 int64_t chunk, T* out, uint64_t* fold_hdr) {
+  constexpr int EPV = 16 / (int)sizeof(T);
+  __shared__ T s_wave[kRedWaves];
+  const T id = Op::template identity<T>();
+  const int tid = threadIdx.x;
+  const uint4* v = reinterpret_cast<const uint4*>(src + head);
+  const int64_t b0 = (int64_t)blockIdx.x * chunk;
+  const int64_t b1 = kmin<int64_t>(nvec, b0 + chunk);
+  T a[EPV];
+#pragma unroll
+  for (int e = 0; e < EPV; ++e) a[e] = id;
+  int64_t i = b0 + tid;
+  for (; i + (int64_t)(U - 1) * kRedBlock < b1; i += (int64_t)U * kRedBlock) {
+    uint4 r[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) r[u] = ld_stream(v + i + u * kRedBlock);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      T x[EPV];
+      __builtin_memcpy(x, &r[u], 16);
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) a[e] = Op::combine(a[e], Map::apply(x[e]));
+    }
+  }
+  for (; i < b1; i += kRedBlock) {
+    const uint4 r = ld_stream(v + i);
+    T x[EPV];
+    __builtin_memcpy(x, &r, 16);
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) a[e] = Op::combine(a[e], Map::apply(x[e]));
+  }
+  T acc = a[0];
+#pragma unroll
+  for (int e = 1; e < EPV; ++e) acc = Op::combine(acc, a[e]);
+  if (blockIdx.x == 0) {
+    const int64_t tail0 = head + nvec * EPV;
+    if (tid < head) acc = Op::combine(acc, Map::apply(src[tid]));
+    if (tail0 + tid < n) acc = Op::combine(acc, Map::apply(src[tail0 + tid]));
+  }
+  const T part = block_reduce<T, Op>(acc, s_wave);
+  fold_partial<T, Op>(part, out, fold_hdr, s_wave);
+}
+
 // Full reduction, stage 2: one 1024-thread workgroup combines `count`
 // partials; each thread issues all of its (at most kRedMaxBlocks/1024) loads
 // before combining, so the stage costs about one memory latency.
@@ -367,6 +425,14 @@ int launch_reduce(const void* src, int64_t n, int64_t stride, void* dst, void* s
   const int64_t head = kmin<int64_t>(n, (int64_t)(((16 - ((uintptr_t)src & 15)) & 15) / sizeof(T)));
   const int64_t nvec = (n - head) / EPV;
   const OnceLevels L = once_levels(nvec, EPV);
+  if (nvec >= kChunkMinVecs) {
+    // kFoldMax persistent workgroups over contiguous chunks, folded in the
+    // same launch
+    const int64_t chunk = (nvec + kFoldMax - 1) / kFoldMax;
+    hipLaunchKernelGGL((reduce_chunk_kernel<T, Op, Map, kChunkUnroll>), dim3(kFoldMax), dim3(kRedBlock), 0, stream,
+                       (const T*)src, n, head, nvec, chunk, (T*)dst, (uint64_t*)scratch);
+    return kf_check_launch("reduce_chunk_kernel");
+  }
   size_t abytes = 0;
   for (int i = 0; i < L.nlev; i += 2) abytes = kmax(abytes, round256((size_t)L.count[i] * sizeof(T) + 16));
   T* buf[2] = {(T*)work, (T*)(work + abytes)};

@@ -432,11 +432,15 @@ def test_config5_dims(kf, oracle, dev, which):
 
 @pytest.mark.parametrize("dt", [np.int32, np.int64, np.uint8])
 def test_multilevel_full_reduce_exact(kf, oracle, dev, dt):
-    # sizes whose partials need one, two and three combine levels, with
-    # aligned and unaligned starts (exact integer results)
+    # every launch regime of the vector path, at its edges, with aligned and
+    # unaligned starts (exact integer results): one launch of one-shot
+    # workgroups at 2 and 4 vectors per lane (2048 * 256 * 2 vectors), the
+    # same just past 128 MiB (one-shot level 0 + folding level 1), and from
+    # 256 MiB the persistent chunked single launch
     rng = np.random.default_rng(47)
     epv = 16 // np.dtype(dt).itemsize
-    for n in (8192 * 512 * epv - 1, 8192 * 512 * epv + 5, 2**26 + 3):
+    for n in (2048 * 512 * epv - 1, 2048 * 512 * epv + 5, 2048 * 256 * 16 * epv + 5, 2**24 * epv + 3):
+        print(f"multilevel {np.dtype(dt).name} n={n}", flush=True)
         x = gen(rng, dt, n + 3)
         t = torch.from_numpy(x).to(dev)
         for off in (0, 1, 3):
