@@ -407,6 +407,8 @@ void launch_once(int u, unsigned grid, const T* src, int64_t n, int64_t head, in
                        n, head, nvec, out, hdr);
 }
 
+constexpr uintptr_t kHeadAlign = 128;  // head elements, up to 127 (< kRedBlock)
+
 template <class T, class Op, class Map>
 int launch_reduce(const void* src, int64_t n, int64_t stride, void* dst, void* scratch,
                   hipStream_t stream) {
@@ -422,7 +424,13 @@ int launch_reduce(const void* src, int64_t n, int64_t stride, void* dst, void* s
                          (const T*)work, grid, (T*)dst);
     return kf_check_launch("reduce_kernel");
   }
-  const int64_t head = kmin<int64_t>(n, (int64_t)(((16 - ((uintptr_t)src & 15)) & 15) / sizeof(T)));
+  // The vectors start at the first 128-byte line boundary: a vector stream
+  // that starts mid-line makes every workgroup's first and last lines
+  // shared with a neighbour, often on another XCD (and L2), and fetched
+  // twice (2^28 Float32 at x[2:]: 159.9 us with a 16-byte head, 155.0 with a
+  // 128-byte one; aligned 153.7). Workgroup 0 folds in the head elements.
+  const int64_t head = kmin<int64_t>(n, (int64_t)(((kHeadAlign - ((uintptr_t)src & (kHeadAlign - 1))) &
+                                                   (kHeadAlign - 1)) / sizeof(T)));
   const int64_t nvec = (n - head) / EPV;
   const OnceLevels L = once_levels(nvec, EPV);
   if (nvec >= kChunkMinVecs) {
