@@ -17,7 +17,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--all [--all-json PA
                  and the rows inside the JSON line as "all_configs")
   --all-json     also write those rows, with the ceilings, to PATH
   --sweep        the reference's 10^6..10^9 size sweep
-  --timeline     only the per-tile phases of the scan (instrumented library)
+  --timeline [large|mid]  only the per-tile phases of the scan (instrumented library)
   --pmc-run      only the marked dispatch sequence of every configuration,
                  for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs
   --pmc-summary  FETCH_DIR WRITE_DIR CASES_LOG OUT_JSON: per-configuration
@@ -126,8 +126,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--sweep", action="store_true",
                     help="the reference's scan/mapreduce size sweep (perfs/julia/benchmarks)")
-    ap.add_argument("--timeline", action="store_true",
-                    help="only the per-tile scan timeline (libkfhip_timeline.so)")
+    ap.add_argument("--timeline", nargs="?", const="large", choices=("large", "mid"),
+                    help="only the per-tile scan timeline (libkfhip_timeline.so): the large "
+                         "scans (default) or the mid sizes of the reference's sweep")
     ap.add_argument("--pmc-run", action="store_true",
                     help="only the dispatch sequence for rocprofv3 --pmc (see pmc_run)")
     ap.add_argument("--pmc-summary", nargs=4, metavar=("FETCH_DIR", "WRITE_DIR", "CASES_LOG", "OUT_JSON"),
@@ -154,7 +155,8 @@ def main():
         pmc_run(kf, dev)
         return
     if args.timeline:
-        print(json.dumps({"scan_timeline": scan_timeline(dev)}), flush=True)
+        cases = TIMELINE_CASES if args.timeline == "large" else MID_TIMELINE_CASES
+        print(json.dumps({"scan_timeline": scan_timeline(dev, cases)}), flush=True)
         return
 
     g = torch.Generator(device=dev).manual_seed(20261201)
@@ -512,9 +514,15 @@ def bench_all(kf, dev, ceil, json_path=None):
 # ---------------------------------------------------------------------------
 TIMELINE_CASES = (("C4 affine n=2^26", 5, 2**26), ("affine n=2^27", 5, 2**27), ("affine n=2^28", 5, 2**28),
                   ("Float64 n=2^26", 1, 2**26), ("Float64 n=2^27", 1, 2**27), ("Float32 n=2^28", 0, 2**28))
+# Mid sizes: UInt8 and Float32 at equal bytes, from one generation of
+# resident tiles to many.
+MID_TIMELINE_CASES = (("UInt8 n=10^7", 4, 10**7), ("UInt8 n=10^8", 4, 10**8), ("UInt8 n=3*10^8", 4, 3 * 10**8),
+                      ("UInt8 n=2^30", 4, 2**30), ("Float32 n=2.5*10^6", 0, 25 * 10**5),
+                      ("Float32 n=2.5*10^7", 0, 25 * 10**6), ("Float32 n=10^8", 0, 10**8),
+                      ("Float64 n=10^7", 1, 10**7))
 
 
-def scan_timeline(dev):
+def scan_timeline(dev, cases=TIMELINE_CASES):
     """Per-tile phases of the decoupled-lookback scan from the instrumented
     library: each tile's thread 0 stamps the 100 MHz realtime counter at its
     start, once its tile is scanned (loads done), once its prefix is known
@@ -533,12 +541,15 @@ def scan_timeline(dev):
     L.kf_debug_scan_timeline.argtypes = [P]
     g = torch.Generator(device=dev).manual_seed(20261201)
     rows = []
-    for label, dt, n in TIMELINE_CASES:
+    for label, dt, n in cases:
         if dt == 5:
             x = torch.empty(n, 2, device=dev)
             x[:, 0].uniform_(0.9, 1.0, generator=g)
             x[:, 1].normal_(generator=g)
             op, es = 3, 8
+        elif dt == 4:
+            x = torch.randint(0, 256, (n,), device=dev, generator=g, dtype=torch.uint8)
+            op, es = 0, 1
         else:
             x = torch.rand(n, device=dev, generator=g, dtype=torch.float64 if dt == 1 else torch.float32)
             op, es = 0, x.element_size()
