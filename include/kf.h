@@ -133,6 +133,32 @@ int kf_scan(kf_op op, kf_map f, kf_post g, kf_dtype dt, int exclusive,
             void* dst, int64_t dst_stride, int64_t n,
             void* scratch, size_t scratch_bytes, void* stream);
 
+/* kf_scan with the reference's launch-shape keywords: `workgroup` threads
+ * per workgroup and `nitem` elements per thread (reference
+ * src/scan/scan.jl:261-284, where `Nitem` / `workgroup` override
+ * default_nitem / default_workgroup; <= 0 means not given). The kernels are
+ * compiled for a fixed set of tile shapes (1024 threads x 1, 2, 4 or 8
+ * 16-byte vectors per thread, 768 x 8 for 4- and 8-byte elements, 512 x 1,
+ * 2, 4, 8, 12 or 16 for UInt8; elements wider than 8 bytes stop at 4 or 2
+ * vectors), so a request takes the nearest shape: the smallest
+ * |log2(threads / workgroup)| + |log2(elements per thread / nitem)|, a
+ * keyword not given standing for the size-based default shape's value;
+ * ties go to the default shape, then to the smaller tile. kf_scan_shape
+ * reports the shape chosen; the scratch size depends on it
+ * (kf_scan_shaped_scratch_bytes, which replaces the reference's
+ * get_allocation(Scan1D, f, op, src, workgroup, blocks) sizing,
+ * src/scan/scan.jl:187-211). With both keywords <= 0 these are kf_scan and
+ * kf_scan_scratch_bytes. Results do not depend on the shape for integer
+ * elements; floating-point sums are regrouped. */
+size_t kf_scan_shaped_scratch_bytes(kf_dtype dt, kf_op op, int64_t n, int workgroup, int nitem);
+
+int kf_scan_shape(kf_dtype dt, int64_t n, int workgroup, int nitem, int* threads, int* items);
+
+int kf_scan_shaped(kf_op op, kf_map f, kf_post g, kf_dtype dt, int exclusive,
+                   const void* src, int64_t src_stride,
+                   void* dst, int64_t dst_stride, int64_t n, int workgroup, int nitem,
+                   void* scratch, size_t scratch_bytes, void* stream);
+
 /* Diagnostics (no counterpart in the reference). KF_OK from kf_scan means
  * the launch was queued; it does not cover a lookback give-up. Tiles are
  * numbered by workgroup id, and a tile waits only on lower-numbered tiles,

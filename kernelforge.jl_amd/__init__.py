@@ -27,9 +27,11 @@ Operators: `+` (operator.add or "+"), `*` (operator.mul or "*"; on
 quaternions the Hamilton product, scan only), `max`, `min`, `affine` (scan
 only);
 maps: `identity`, `abs2`. Anything else raises ArgumentError, as does a
-shape/dtype mismatch. Tuning keywords of the reference (Nitem, workgroup,
-blocks, family, arch) are accepted and ignored: launch shapes are fixed for
-gfx950. Calls are asynchronous on torch's current stream except the full
+shape/dtype mismatch. The reference's launch-shape keywords of scan!
+(Nitem, workgroup) pick the nearest of the compiled gfx950 tile shapes
+(`scan_shape`); its other tuning keywords (blocks, family, arch, and the
+reductions' Nitem / workgroup) are accepted and ignored: the reduction
+shapes are fixed for gfx950. Calls are asynchronous on torch's current stream except the full
 `mapreduce`, which returns a host scalar (like the reference's
 `Array(dst)[1]`, src/mapreduce/1D/mapreduce1d.jl:203).
 """
@@ -43,6 +45,7 @@ from . import _lib as _L
 
 __all__ = [
     "ArgumentError", "KernelBuffer", "AffineOp", "affine", "identity", "abs2", "sqdiff", "wsq", "expdiff", "prod3",
+    "scan_shape",
     "scan", "scan_", "mapreduce", "mapreduce_", "get_allocation", "vcopy_", "setvalue_", "scan_status",
     "maximum", "maximum_", "minimum", "mapreduce1d", "mapreduce1d_", "mapreduce2d", "mapreduce2d_",
     "mapreducedims", "mapreducedims_",
@@ -297,16 +300,55 @@ def _split_f_op(args, n_arrays, name):
     raise ArgumentError(f"{name} takes ([f,] op, {', '.join(['array'] * n_arrays)})")
 
 
+_SCAN_TUNING = ("Nitem", "workgroup", "family", "arch")
+
+
+def _shape_keywords(tuning, name):
+    """(workgroup, Nitem) of the reference's scan! keywords (0: not given);
+    family and arch are accepted and ignored (the descriptor layout is fixed
+    per element type here)."""
+    for k in tuning:
+        if k not in _SCAN_TUNING:
+            raise ArgumentError(f"{name}: unknown keyword {k}")
+    out = []
+    for k in ("workgroup", "Nitem"):
+        v = tuning.get(k)
+        if v is None:
+            out.append(0)
+        elif isinstance(v, bool) or not isinstance(v, int) or v <= 0:
+            raise ArgumentError(f"{name}: {k} must be a positive integer, got {v!r}")
+        else:
+            out.append(int(v))
+    return tuple(out)
+
+
+def scan_shape(src, op="+", Nitem=None, workgroup=None):
+    """(threads per workgroup, elements per thread) of the tile shape a
+    scan! of `src` takes for these keywords: the compiled shape nearest to
+    the request (kf_scan_shape), the size-based default when neither is
+    given. No counterpart in the reference, which compiles any shape."""
+    wg, ni = _shape_keywords({"Nitem": Nitem, "workgroup": workgroup}, "scan_shape")
+    dt, n, _ = _scan_operand(src, _op_code(op))
+    threads, items = ctypes.c_int(0), ctypes.c_int(0)
+    _L.check(_L.lib().kf_scan_shape(dt, n, wg, ni, ctypes.byref(threads), ctypes.byref(items)), "scan_shape")
+    return threads.value, items.value
+
+
 def scan_(*args, exclusive=False, tmp=None, g=None, check=False, **tuning):
-    """scan!([f,] op, dst, src; exclusive=False, tmp=None, check=False) -> dst.
+    """scan!([f,] op, dst, src; exclusive=False, tmp=None, check=False,
+    Nitem=None, workgroup=None) -> dst.
 
     dst[i] = f(src[1]) op ... op f(src[i]) (inclusive, the reference's only
     mode), or the exclusive variant dst[1] = identity(op),
     dst[i] = inclusive[i-1]. In place (dst is src) is allowed.
     check=True synchronises after the launch and raises KernelForgeError if
     the lookback gave up (see scan_status), which a successful launch does
-    not rule out."""
+    not rule out. Nitem / workgroup select the nearest compiled tile shape
+    (scan_shape); a tmp for such a call comes from
+    get_allocation(Scan1D, f, op, src, workgroup, blocks) or is sized for
+    the shape (ArgumentError if it is too small)."""
     f, op, (dst, src) = _split_f_op(args, 2, "scan!")
+    wg, ni = _shape_keywords(tuning, "scan!")
     opc, fc = _op_code(op), _map_code(f)
     if _post_code(g) is None or (g not in (None, identity) and (opc == _L.OP_AFFINE or src.dim() == 2)):
         raise ArgumentError(f"scan!: unsupported post-map g={g!r}: expected identity, sqrt or abs2")
@@ -320,11 +362,12 @@ def scan_(*args, exclusive=False, tmp=None, g=None, check=False, **tuning):
     if n == 0:
         return dst
     L = _L.lib()
-    need = L.kf_scan_scratch_bytes(dt, opc, n)
+    need = L.kf_scan_shaped_scratch_bytes(dt, opc, n, wg, ni)
     buf = _scratch(Scan1D, need, src.device, tmp)
     with _on(src.device):
-        rc = L.kf_scan(opc, fc, _post_code(g), dt, int(bool(exclusive)), ctypes_void(src.data_ptr()), ss,
-                       ctypes_void(dst.data_ptr()), ds, n, ctypes_void(buf.ptr), buf.nbytes, _stream_ptr(src))
+        rc = L.kf_scan_shaped(opc, fc, _post_code(g), dt, int(bool(exclusive)), ctypes_void(src.data_ptr()), ss,
+                              ctypes_void(dst.data_ptr()), ds, n, wg, ni, ctypes_void(buf.ptr), buf.nbytes,
+                              _stream_ptr(src))
     _L.check(rc, "scan!")  # g is applied by the kernel as each value is stored
     if check and scan_status(buf):
         raise _L.KernelForgeError(
@@ -845,15 +888,29 @@ def get_allocation(kind, f, op, src, *args, **kwargs):
 
     kind: Scan1D (src), MapReduce1D (src, or a tuple (x, y) of two arrays),
     MatVec (A, x) and VecMat (x, A) as the reference orders them, or
-    MapReduce2D (A, dims=1 or 2). Extra positional tuning arguments
-    (workgroup, blocks, arch) are accepted and ignored."""
+    MapReduce2D (A, dims=1 or 2). For Scan1D the reference's positional
+    (workgroup, blocks) are honoured: the buffer fits the tile shape
+    `workgroup` selects and at least `blocks` tiles (get_allocation(Scan1D,
+    f, op, src, blocks) takes blocks alone, as an int). Other tuning
+    arguments (arch, and those of the reductions) are accepted and
+    ignored."""
     L = _L.lib()
     opc = _op_code(op)
     if kind == Scan1D:
         _map_code(f)
         _require_device(src)
         dt, n, _ = _scan_operand(src, opc)
-        need = L.kf_scan_scratch_bytes(dt, opc, n)
+        if len(args) == 1 and isinstance(args[0], int) and not isinstance(args[0], bool):
+            workgroup, blocks = None, args[0]  # get_allocation(Scan1D, f, op, src, blocks; arch)
+        else:
+            workgroup = args[0] if len(args) > 0 else kwargs.get("workgroup")
+            blocks = args[1] if len(args) > 1 else kwargs.get("blocks")
+        wg, _ = _shape_keywords({"workgroup": workgroup}, "get_allocation")
+        if blocks is not None and (isinstance(blocks, bool) or not isinstance(blocks, int) or blocks < 0):
+            raise ArgumentError(f"get_allocation: blocks must be a non-negative integer, got {blocks!r}")
+        need = L.kf_scan_shaped_scratch_bytes(dt, opc, n, wg, 0)
+        if blocks is not None:
+            need = max(need, 256 + 128 * blocks)  # header + one 128-byte descriptor line per tile
         device = src.device
     elif kind == MapReduce1D:
         if isinstance(src, (tuple, list)):

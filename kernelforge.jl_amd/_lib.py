@@ -28,6 +28,9 @@ SIGNATURES = {
     "kf_scratch_reset": ([_P, _SZ, _P], _I),
     "kf_scan_scratch_bytes": ([_I, _I, _I64], _SZ),
     "kf_scan": ([_I, _I, _I, _I, _I, _P, _I64, _P, _I64, _I64, _P, _SZ, _P], _I),
+    "kf_scan_shaped_scratch_bytes": ([_I, _I, _I64, _I, _I], _SZ),
+    "kf_scan_shape": ([_I, _I64, _I, _I, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int)], _I),
+    "kf_scan_shaped": ([_I, _I, _I, _I, _I, _P, _I64, _P, _I64, _I64, _I, _I, _P, _SZ, _P], _I),
     "kf_reduce_scratch_bytes": ([_I, _I64], _SZ),
     "kf_reduce": ([_I, _I, _I, _P, _I64, _I64, _P, _P, _SZ, _P], _I),
     "kf_reduce_dim_scratch_bytes": ([_I, _I64, _I64, _I], _SZ),

@@ -54,6 +54,7 @@
 //    clearing between calls (the reference fill!s its descriptors before
 //    every launch, src/scan/scan.jl:444-470).
 #include <atomic>
+#include <cmath>
 #include <type_traits>
 
 #include "kf_common.h"
@@ -700,15 +701,50 @@ template <class T> int64_t tier_tile(int tier) {
   return (int64_t)scan_block<T>(tier) * tier_v<T>(tier) * ScanShape<T>::EPV;
 }
 
+template <class T> bool tier_exists(int tier) {
+  if (tier >= 0 && tier < kTiers) return tier <= max_tier<T>();
+  if (tier == kTierWide) return has_wide_tier<T>();
+  if (tier == kTierHuge) return has_huge_tier<T>();
+  return false;
+}
+
+// The tile shape for the reference's launch-shape keywords (workgroup =
+// threads per workgroup, Nitem = elements per thread; <= 0: not given).
+// Shapes are compiled ahead of time, so a request takes the shape nearest
+// to it: the smallest sum of |log2(threads / workgroup)| and
+// |log2(elements per lane / Nitem)|, a keyword not given standing for the
+// size-based default shape's value; ties go to the default, then to the
+// smaller tile. No keyword: the default.
+template <class T> int shape_tier(int64_t n, int workgroup, int nitem) {
+  const int def = scan_tier<T>(n);
+  if (workgroup <= 0 && nitem <= 0) return def;
+  const double want_threads = workgroup > 0 ? workgroup : scan_block<T>(def);
+  const double want_items = nitem > 0 ? nitem : tier_v<T>(def) * ScanShape<T>::EPV;
+  int best = -1;
+  double best_d = 0;
+  for (int t = 0; t <= kTierHuge; ++t) {
+    if (!tier_exists<T>(t)) continue;
+    const double d = fabs(log2(scan_block<T>(t) / want_threads)) +
+                     fabs(log2(tier_v<T>(t) * ScanShape<T>::EPV / want_items));
+    const bool tie = best >= 0 && fabs(d - best_d) < 1e-9;
+    if (best < 0 || d < best_d - 1e-9 || (tie && t == def) ||
+        (tie && best != def && tier_tile<T>(t) < tier_tile<T>(best))) {
+      best = t;
+      best_d = d;
+    }
+  }
+  return best;
+}
+
 // Tiles for n elements starting `off` elements after a 16-byte boundary.
-template <class T> int64_t scan_tiles(int64_t n, int off = 0) {
-  const int64_t tile = tier_tile<T>(scan_tier<T>(n));
+template <class T> int64_t scan_tiles(int64_t n, int off, int tier) {
+  const int64_t tile = tier_tile<T>(tier);
   return (n + off + tile - 1) / tile;
 }
 
-template <class T> size_t scan_scratch(int64_t n) {
+template <class T> size_t scan_scratch(int64_t n, int tier) {
   constexpr int kMaxOff = 16 / (int)sizeof(T) - 1 > 0 ? 16 / (int)sizeof(T) - 1 : 0;
-  return kScanHeaderBytes + (size_t)scan_tiles<T>(n, kMaxOff) * kDescWords * sizeof(uint64_t);
+  return kScanHeaderBytes + (size_t)scan_tiles<T>(n, kMaxOff, tier) * kDescWords * sizeof(uint64_t);
 }
 
 // Workgroups of KERNEL the whole GPU holds at once (occupancy x CUs); the
@@ -749,7 +785,7 @@ void launch_scan_tier(const void* src, int64_t ss, void* dst, int64_t ds, int64_
 }
 
 template <class T, class Op, class Map>
-int launch_scan(const void* src, int64_t ss, void* dst, int64_t ds, int64_t n, int excl,
+int launch_scan(const void* src, int64_t ss, void* dst, int64_t ds, int64_t n, int excl, int tier,
                 void* scratch, hipStream_t stream) {
   // Vector path when both operands are contiguous (views src[k:], dst[j:]
   // of aligned buffers included): `off` shifts the tiles to dst's alignment,
@@ -757,8 +793,8 @@ int launch_scan(const void* src, int64_t ss, void* dst, int64_t ds, int64_t n, i
   // (elements of 16 bytes or more need a 16-byte aligned dst for it)
   const int vec = ss == 1 && ds == 1 && ((uintptr_t)dst % 16 % sizeof(T) == 0);
   const int off = vec ? (int)(((uintptr_t)dst % 16) / sizeof(T)) : 0;
-  const int64_t ntiles = scan_tiles<T>(n, off);
-  switch (scan_tier<T>(n)) {
+  const int64_t ntiles = scan_tiles<T>(n, off, tier);
+  switch (tier) {
     case 0: launch_scan_tier<T, Op, Map, 0>(src, ss, dst, ds, n, excl, ntiles, vec, off, scratch, stream); break;
     case 1: launch_scan_tier<T, Op, Map, 1>(src, ss, dst, ds, n, excl, ntiles, vec, off, scratch, stream); break;
     case 2:
@@ -781,31 +817,47 @@ int launch_scan(const void* src, int64_t ss, void* dst, int64_t ds, int64_t n, i
 }
 
 template <class T, class Op>
-int scan_map(kf_map f, const void* src, int64_t ss, void* dst, int64_t ds, int64_t n, int excl,
+int scan_map(kf_map f, const void* src, int64_t ss, void* dst, int64_t ds, int64_t n, int excl, int tier,
              void* scratch, hipStream_t stream) {
   if constexpr (__is_same(T, f32x2) || is_quat<T>) {
-    return launch_scan<T, Op, MapIdentity>(src, ss, dst, ds, n, excl, scratch, stream);
+    return launch_scan<T, Op, MapIdentity>(src, ss, dst, ds, n, excl, tier, scratch, stream);
   } else {
-    if (f == KF_MAP_ABS2) return launch_scan<T, Op, MapAbs2>(src, ss, dst, ds, n, excl, scratch, stream);
-    return launch_scan<T, Op, MapIdentity>(src, ss, dst, ds, n, excl, scratch, stream);
+    if (f == KF_MAP_ABS2) return launch_scan<T, Op, MapAbs2>(src, ss, dst, ds, n, excl, tier, scratch, stream);
+    return launch_scan<T, Op, MapIdentity>(src, ss, dst, ds, n, excl, tier, scratch, stream);
   }
 }
 
 template <class T>
 int scan_op(kf_op op, kf_map f, const void* src, int64_t ss, void* dst, int64_t ds, int64_t n,
-            int excl, void* scratch, hipStream_t stream) {
+            int excl, int workgroup, int nitem, void* scratch, hipStream_t stream) {
+  const int tier = shape_tier<T>(n, workgroup, nitem);
   if constexpr (__is_same(T, f32x2)) {
-    return scan_map<T, OpAffine>(f, src, ss, dst, ds, n, excl, scratch, stream);
+    return scan_map<T, OpAffine>(f, src, ss, dst, ds, n, excl, tier, scratch, stream);
   } else if constexpr (is_quat<T>) {
-    return scan_map<T, OpMul>(f, src, ss, dst, ds, n, excl, scratch, stream);
+    return scan_map<T, OpMul>(f, src, ss, dst, ds, n, excl, tier, scratch, stream);
   } else {
     switch (op) {
-      case KF_OP_ADD: return scan_map<T, OpAdd>(f, src, ss, dst, ds, n, excl, scratch, stream);
-      case KF_OP_MAX: return scan_map<T, OpMax>(f, src, ss, dst, ds, n, excl, scratch, stream);
-      case KF_OP_MUL: return scan_map<T, OpMul>(f, src, ss, dst, ds, n, excl, scratch, stream);
-      default: return scan_map<T, OpMin>(f, src, ss, dst, ds, n, excl, scratch, stream);
+      case KF_OP_ADD: return scan_map<T, OpAdd>(f, src, ss, dst, ds, n, excl, tier, scratch, stream);
+      case KF_OP_MAX: return scan_map<T, OpMax>(f, src, ss, dst, ds, n, excl, tier, scratch, stream);
+      case KF_OP_MUL: return scan_map<T, OpMul>(f, src, ss, dst, ds, n, excl, tier, scratch, stream);
+      default: return scan_map<T, OpMin>(f, src, ss, dst, ds, n, excl, tier, scratch, stream);
     }
   }
+}
+
+// Dispatch of a per-element-type function object over kf_dtype.
+template <class Fn> auto by_dtype(kf_dtype dt, Fn&& fn) -> decltype(fn((float*)nullptr)) {
+  switch (dt) {
+    case KF_F32: return fn((float*)nullptr);
+    case KF_F64: return fn((double*)nullptr);
+    case KF_I32: return fn((int32_t*)nullptr);
+    case KF_I64: return fn((int64_t*)nullptr);
+    case KF_U8: return fn((uint8_t*)nullptr);
+    case KF_F32X2: return fn((f32x2*)nullptr);
+    case KF_Q32: return fn((q32*)nullptr);
+    case KF_Q64: return fn((q64*)nullptr);
+  }
+  return decltype(fn((float*)nullptr))();
 }
 
 }  // namespace kf
@@ -850,25 +902,36 @@ extern "C" int kf_debug_scan_giveup(int64_t tile, uint32_t spin_limit) {
   return KF_OK;
 }
 
-extern "C" size_t kf_scan_scratch_bytes(kf_dtype dt, kf_op op, int64_t n) {
+extern "C" size_t kf_scan_shaped_scratch_bytes(kf_dtype dt, kf_op op, int64_t n, int workgroup, int nitem) {
   (void)op;
   if (n < 0) n = 0;
-  switch (dt) {
-    case KF_F32: return scan_scratch<float>(n);
-    case KF_F64: return scan_scratch<double>(n);
-    case KF_I32: return scan_scratch<int32_t>(n);
-    case KF_I64: return scan_scratch<int64_t>(n);
-    case KF_U8: return scan_scratch<uint8_t>(n);
-    case KF_F32X2: return scan_scratch<f32x2>(n);
-    case KF_Q32: return scan_scratch<q32>(n);
-    case KF_Q64: return scan_scratch<q64>(n);
-  }
-  return 0;
+  return by_dtype(dt, [&](auto* p) -> size_t {
+    using T = std::remove_pointer_t<decltype(p)>;
+    return scan_scratch<T>(n, shape_tier<T>(n, workgroup, nitem));
+  });
 }
 
-extern "C" int kf_scan(kf_op op, kf_map f, kf_post g, kf_dtype dt, int exclusive, const void* src,
-                       int64_t src_stride, void* dst, int64_t dst_stride, int64_t n, void* scratch,
-                       size_t scratch_bytes, void* stream) {
+extern "C" size_t kf_scan_scratch_bytes(kf_dtype dt, kf_op op, int64_t n) {
+  return kf_scan_shaped_scratch_bytes(dt, op, n, 0, 0);
+}
+
+extern "C" int kf_scan_shape(kf_dtype dt, int64_t n, int workgroup, int nitem, int* threads, int* items) {
+  if (!threads || !items) return kf_set_error(KF_EINVAL, "kf_scan_shape: null output pointer");
+  if (kf_dtype_size(dt) == 0) return kf_set_error(KF_EINVAL, "kf_scan_shape: bad dtype %d", (int)dt);
+  if (n < 0) n = 0;
+  by_dtype(dt, [&](auto* p) -> int {
+    using T = std::remove_pointer_t<decltype(p)>;
+    const int t = shape_tier<T>(n, workgroup, nitem);
+    *threads = scan_block<T>(t);
+    *items = tier_v<T>(t) * ScanShape<T>::EPV;
+    return 0;
+  });
+  return KF_OK;
+}
+
+extern "C" int kf_scan_shaped(kf_op op, kf_map f, kf_post g, kf_dtype dt, int exclusive, const void* src,
+                              int64_t src_stride, void* dst, int64_t dst_stride, int64_t n, int workgroup,
+                              int nitem, void* scratch, size_t scratch_bytes, void* stream) {
   int rc = kf_validate_op(op, f, dt, /*allow_affine=*/1);
   if (rc) return rc;
   if (g != KF_POST_IDENTITY && g != KF_POST_SQRT && g != KF_POST_ABS2)
@@ -895,7 +958,7 @@ extern "C" int kf_scan(kf_op op, kf_map f, kf_post g, kf_dtype dt, int exclusive
     if (s0 < d1 && d0 < s1)
       return kf_set_error(KF_EINVAL, "kf_scan: src and dst overlap without being identical");
   }
-  const size_t need = kf_scan_scratch_bytes(dt, op, n);
+  const size_t need = kf_scan_shaped_scratch_bytes(dt, op, n, workgroup, nitem);
   if (!scratch || scratch_bytes < need)
     return kf_set_error(KF_ENOSCRATCH, "kf_scan: scratch of %zu bytes needed, %zu given", need,
                         scratch ? scratch_bytes : (size_t)0);
@@ -908,17 +971,17 @@ extern "C" int kf_scan(kf_op op, kf_map f, kf_post g, kf_dtype dt, int exclusive
     return kf_set_error(KF_EINVAL, "kf_scan: n = %lld exceeds the grid limit", (long long)n);
   hipStream_t s = (hipStream_t)stream;
   const int mode = (exclusive ? 1 : 0) | ((int)g << 1);
-  switch (dt) {
-    case KF_F32: return scan_op<float>(op, f, src, src_stride, dst, dst_stride, n, mode, scratch, s);
-    case KF_F64: return scan_op<double>(op, f, src, src_stride, dst, dst_stride, n, mode, scratch, s);
-    case KF_I32: return scan_op<int32_t>(op, f, src, src_stride, dst, dst_stride, n, mode, scratch, s);
-    case KF_I64: return scan_op<int64_t>(op, f, src, src_stride, dst, dst_stride, n, mode, scratch, s);
-    case KF_U8: return scan_op<uint8_t>(op, f, src, src_stride, dst, dst_stride, n, mode, scratch, s);
-    case KF_F32X2: return scan_op<f32x2>(op, f, src, src_stride, dst, dst_stride, n, mode, scratch, s);
-    case KF_Q32: return scan_op<q32>(op, f, src, src_stride, dst, dst_stride, n, mode, scratch, s);
-    case KF_Q64: return scan_op<q64>(op, f, src, src_stride, dst, dst_stride, n, mode, scratch, s);
-  }
-  return kf_set_error(KF_EINVAL, "kf_scan: bad dtype");
+  return by_dtype(dt, [&](auto* p) -> int {
+    using T = std::remove_pointer_t<decltype(p)>;
+    return scan_op<T>(op, f, src, src_stride, dst, dst_stride, n, mode, workgroup, nitem, scratch, s);
+  });
+}
+
+extern "C" int kf_scan(kf_op op, kf_map f, kf_post g, kf_dtype dt, int exclusive, const void* src,
+                       int64_t src_stride, void* dst, int64_t dst_stride, int64_t n, void* scratch,
+                       size_t scratch_bytes, void* stream) {
+  return kf_scan_shaped(op, f, g, dt, exclusive, src, src_stride, dst, dst_stride, n, 0, 0, scratch,
+                        scratch_bytes, stream);
 }
 
 #ifdef KF_TIMELINE

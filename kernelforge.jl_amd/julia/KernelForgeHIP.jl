@@ -2,9 +2,11 @@
 # scan! / mapreduce hot path. The public functions keep the reference's names,
 # positional arguments and keywords (cited per function); underneath, every call
 # goes through the C ABI of libkfhip.so (include/kf.h) with `ccall`, on the
-# task-local AMDGPU stream. Tuning keywords of the reference (Nitem, workgroup,
-# blocks, family, arch, chunksz, ...) are accepted and ignored: the library
-# picks its own gfx950 launch shapes.
+# task-local AMDGPU stream. scan!'s launch-shape keywords (Nitem, workgroup)
+# select the nearest compiled gfx950 tile shape (kf_scan_shaped); the other
+# tuning keywords of the reference (blocks, family, arch, chunksz, and the
+# reductions' shapes) are accepted and ignored: the library picks its own
+# gfx950 launch shapes there.
 #
 # Supported operands: ROCArrays and strided views of them with eltype Float32,
 # Float64, Int32, Int64, UInt8; NTuple{2,Float32} affine pairs (scan only);
@@ -208,26 +210,50 @@ end
 # ---------------------------------------------------------------------------
 # scan! / scan (reference src/scan/scan.jl:121-284)
 # ---------------------------------------------------------------------------
-_scan_bytes(op, src) = ccall((:kf_scan_scratch_bytes, libkf), Csize_t, (Cint, Cint, Int64),
-                             dtcode(eltype(src)), opcode(op), length(src))
+_shape_kw(v, name) = v === nothing ? Cint(0) :
+    (v isa Integer && v > 0 ? Cint(v) : throw(ArgumentError("$name must be a positive integer, got $v")))
+
+_scan_bytes(op, src, workgroup=nothing, Nitem=nothing) =
+    ccall((:kf_scan_shaped_scratch_bytes, libkf), Csize_t, (Cint, Cint, Int64, Cint, Cint),
+          dtcode(eltype(src)), opcode(op), length(src), _shape_kw(workgroup, "workgroup"), _shape_kw(Nitem, "Nitem"))
 
 """
     get_allocation(::Type{Scan1D}, f, op, src, workgroup=nothing, blocks=nothing, arch=nothing)
     get_allocation(::Type{Scan1D}, f, op, src, blocks::Int; arch=nothing)
 
 A `KernelBuffer` for `scan!` on arrays like `src` (reference
-src/scan/scan.jl:156-211). Its size comes from the element type and length
-(kf_scan_scratch_bytes); `workgroup`, `blocks` and `arch` are accepted for
+src/scan/scan.jl:156-211): the size of the tile shape `workgroup` selects
+(kf_scan_shaped_scratch_bytes), and at least a 256-byte header plus one
+128-byte descriptor per tile of `blocks`. `arch` is accepted for
 compatibility.
 """
 function get_allocation(::Type{Scan1D}, f::F, op::O, src::AbstractArray, blocks::Int;
                         arch=nothing) where {F<:Function,O<:Function}
-    return _buffer(:scan, _scan_bytes(op, src))
+    blocks >= 0 || throw(ArgumentError("blocks must be non-negative, got $blocks"))
+    return _buffer(:scan, max(_scan_bytes(op, src), 256 + 128 * blocks))
 end
 
 function get_allocation(::Type{Scan1D}, f::F, op::O, src::AbstractArray, workgroup=nothing,
                         blocks=nothing, arch=nothing) where {F<:Function,O<:Function}
-    return _buffer(:scan, _scan_bytes(op, src))
+    bytes = _scan_bytes(op, src, workgroup)
+    blocks === nothing || (bytes = max(bytes, 256 + 128 * blocks))
+    return _buffer(:scan, bytes)
+end
+
+"""
+    scan_shape(src, op=+; Nitem=nothing, workgroup=nothing) -> (threads, items)
+
+Threads per workgroup and elements per thread of the compiled tile shape a
+`scan!` of `src` takes for these keywords (kf_scan_shape). No reference
+counterpart: the reference compiles whatever shape it is given.
+"""
+function scan_shape(src::AbstractArray, op::O=+; Nitem=nothing, workgroup=nothing) where {O<:Function}
+    threads, items = Ref{Cint}(0), Ref{Cint}(0)
+    rc = ccall((:kf_scan_shape, libkf), Cint, (Cint, Int64, Cint, Cint, Ptr{Cint}, Ptr{Cint}),
+               dtcode(eltype(src)), length(src), _shape_kw(workgroup, "workgroup"), _shape_kw(Nitem, "Nitem"),
+               threads, items)
+    _check(rc, "scan_shape")
+    return (Int(threads[]), Int(items[]))
 end
 
 """
@@ -237,7 +263,9 @@ end
 `dst[i] = g(f(src[1]) op ... op f(src[i]))` (reference src/scan/scan.jl:251-284).
 `exclusive=true` gives `dst[1] = g(identity of op)`, `dst[i] = g(inclusive[i-1])`
 (no reference counterpart). `check=true` synchronises and throws if a tile's
-lookback gave up (see `scan_status`).
+lookback gave up (see `scan_status`). `Nitem` (elements per thread) and
+`workgroup` (threads per workgroup) select the nearest compiled tile shape
+(`scan_shape`); `family` and `arch` are accepted for compatibility.
 """
 function scan!(op::O, dst::AbstractArray, src::AbstractArray; kwargs...) where {O<:Function}
     return scan!(identity, op, dst, src; kwargs...)
@@ -253,11 +281,13 @@ function scan!(f::F, op::O, dst::AbstractArray, src::AbstractArray; g::G=identit
         throw(ArgumentError("dst eltype $(eltype(dst)) differs from src eltype $(eltype(src))"))
     gc = postcode(g)
     gc === nothing && throw(ArgumentError("unsupported post-map g=$g: expected identity, sqrt or abs2"))
-    buf = _scratch(tmp, :scan, _scan_bytes(op, src))
-    rc = ccall((:kf_scan, libkf), Cint,
-               (Cint, Cint, Cint, Cint, Cint, Ptr{Cvoid}, Int64, Ptr{Cvoid}, Int64, Int64, Ptr{Cvoid}, Csize_t, Ptr{Cvoid}),
+    wg, ni = _shape_kw(workgroup, "workgroup"), _shape_kw(Nitem, "Nitem")
+    buf = _scratch(tmp, :scan, _scan_bytes(op, src, workgroup, Nitem))
+    rc = ccall((:kf_scan_shaped, libkf), Cint,
+               (Cint, Cint, Cint, Cint, Cint, Ptr{Cvoid}, Int64, Ptr{Cvoid}, Int64, Int64, Cint, Cint,
+                Ptr{Cvoid}, Csize_t, Ptr{Cvoid}),
                opcode(op), mapcode(f), gc, dtcode(eltype(src)), Cint(exclusive),
-               devptr(src), _linear(src, "scan!"), devptr(dst), _linear(dst, "scan!"), n,
+               devptr(src), _linear(src, "scan!"), devptr(dst), _linear(dst, "scan!"), n, wg, ni,
                devptr(buf), length(buf), _stream())
     _check(rc, "scan!")
     check && _scan_status(buf) &&

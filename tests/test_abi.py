@@ -22,7 +22,8 @@ def test_header_declares_the_expected_surface():
         "kf_reduce2_scratch_bytes", "kf_reduce2", "kf_reduce_dim_batched_scratch_bytes", "kf_reduce_dim_batched", "kf_post_map", "kf_reduce_dim_x",
         "kf_fill", "kf_scan_scratch_status", "kf_reduce3_scratch_bytes", "kf_reduce3",
         "kf_reduce_noalloc", "kf_debug_scan_giveup",
-        "kf_bw_probe_scratch_bytes", "kf_bw_probe"])
+        "kf_bw_probe_scratch_bytes", "kf_bw_probe",
+        "kf_scan_shaped_scratch_bytes", "kf_scan_shape", "kf_scan_shaped"])
 
 
 def test_library_exports_every_declared_symbol(kf):
@@ -70,6 +71,53 @@ def test_dims_scratch_queries_over_shapes(kf):
                 for dim in (1, 2):
                     assert L.kf_reduce_dim_scratch_bytes(dt, rows, cols, dim) >= 256
                 assert L.kf_reduce_dim_batched_scratch_bytes(dt, rows, cols, 7) >= 256
+
+
+def _shape(kf, dt, n, wg, ni):
+    t, i = ctypes.c_int(0), ctypes.c_int(0)
+    assert kf._lib.lib().kf_scan_shape(dt, n, wg, ni, ctypes.byref(t), ctypes.byref(i)) == kf._lib.KF_OK
+    return t.value, i.value
+
+
+def test_scan_shape_keywords_pick_the_nearest_compiled_shape(kf):
+    # host-only: the shape table, no GPU. Default shapes follow the size.
+    K, L = kf._lib, kf._lib.lib()
+    assert _shape(kf, K.F32, 2**28, 0, 0) == (768, 32)
+    assert _shape(kf, K.F32, 10**6, 0, 0) == (1024, 8)
+    assert _shape(kf, K.U8, 2**30, 0, 0) == (512, 256)
+    assert _shape(kf, K.F64, 2**27, 0, 0) == (768, 16)
+    # exact requests: elements per thread = vectors x elements per vector
+    for ni, want in ((4, 4), (8, 8), (16, 16), (32, 32)):
+        assert _shape(kf, K.F32, 2**28, 1024, ni) == (1024, want)
+    assert _shape(kf, K.F32, 10**6, 768, 32) == (768, 32)
+    assert _shape(kf, K.U8, 10**6, 512, 192) == (512, 192)
+    assert _shape(kf, K.F64, 10**6, 1024, 2) == (1024, 2)
+    # nearest: the reference's 256-thread workgroups take the nearest block
+    # (512 for UInt8, whose only block size it is; 768 is nearer than 1024)
+    assert _shape(kf, K.U8, 10**7, 256, 16) == (512, 16)
+    assert _shape(kf, K.F32, 10**7, 256, 16)[1] == 16
+    # a keyword not given stands for the default's value: workgroup 1024
+    # alone at 2^28 Float32 (default 768 x 32) -> 1024 x 32, Nitem 32 alone
+    # -> the default itself
+    assert _shape(kf, K.F32, 2**28, 1024, 0) == (1024, 32)
+    assert _shape(kf, K.F32, 2**28, 0, 32) == (768, 32)
+    assert _shape(kf, K.F32, 2**28, 0, 8) == (1024, 8)  # 768 threads come with 32 only
+    # Nitem beyond the compiled range clamps to the widest shape
+    assert _shape(kf, K.F32, 2**20, 0, 10**6)[1] == 32
+    assert _shape(kf, K.Q64, 100, 0, 64) == (1024, 2)  # 32-byte elements stop at 2 per thread
+    # scratch follows the shape: one 128-byte line per tile + the header
+    n = 10**6
+    assert L.kf_scan_shaped_scratch_bytes(K.F32, K.OP_ADD, n, 0, 0) == L.kf_scan_scratch_bytes(K.F32, K.OP_ADD, n)
+    assert L.kf_scan_shaped_scratch_bytes(K.F32, K.OP_ADD, n, 1024, 4) == 256 + -(-(n + 3) // 4096) * 128
+    assert L.kf_scan_shaped_scratch_bytes(K.F32, K.OP_ADD, n, 1024, 32) == 256 + -(-(n + 3) // 32768) * 128
+    t = ctypes.c_int(0)
+    assert L.kf_scan_shape(99, 10, 0, 0, ctypes.byref(t), ctypes.byref(t)) == K.KF_EINVAL
+    assert L.kf_scan_shape(K.F32, 10, 0, 0, None, ctypes.byref(t)) == K.KF_EINVAL
+    # a hinted call with a default-sized scratch that is too small is refused
+    p, q = ctypes.c_void_p(4096), ctypes.c_void_p(1 << 24)
+    small = L.kf_scan_scratch_bytes(K.F32, K.OP_ADD, n)
+    assert L.kf_scan_shaped(K.OP_ADD, 0, 0, K.F32, 0, p, 1, q, 1, n, 1024, 4, ctypes.c_void_p(1 << 30), small,
+                            None) == K.KF_ENOSCRATCH
 
 
 def _err(kf):

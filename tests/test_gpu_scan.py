@@ -561,3 +561,56 @@ def test_misaligned_view_headline_size(kf, oracle, dev):
     ref = np.cumsum(x[1:], dtype=np.float64)
     assert ref[-1] < 2**24
     assert np.array_equal(got.astype(np.float64), ref)
+
+
+@pytest.mark.parametrize("dt", [np.int32, np.int64, np.uint8, np.float32, np.float64])
+def test_launch_shape_keywords_every_compiled_shape(kf, oracle, dev, dt):
+    # scan!(...; Nitem, workgroup) takes the nearest compiled tile shape;
+    # run each shape of this element type at sizes around its tile and over
+    # enough tiles to leave the all-resident lookback (floats: sparse 0/1
+    # values, exact in any grouping)
+    epv = 16 // np.dtype(dt).itemsize
+    probe = torch.from_numpy(np.zeros(1, dt)).to(dev)
+    shapes = sorted({kf.scan_shape(probe, "+", Nitem=epv * v, workgroup=b)
+                     for b in (512, 768, 1024) for v in (1, 2, 4, 8, 12, 16)})
+    want = {np.uint8: [(512, epv * v) for v in (1, 2, 4, 8, 12, 16)]}.get(
+        dt, [(768, epv * 8)] + [(1024, epv * v) for v in (1, 2, 4, 8)])
+    assert shapes == sorted(want)
+    rng = np.random.default_rng(5)
+    for threads, items in shapes:
+        tile = threads * items
+        for n in (1, tile - 1, tile + 1, 3 * tile + 5, 1200 * tile + 7):
+            x = (rng.random(n) < 1 / 16).astype(dt) if np.dtype(dt).kind == "f" else gen(rng, dt, n)
+            t = torch.from_numpy(x).to(dev)
+            for exclusive in (False, True):
+                y = kf.scan("+", t, exclusive=exclusive, Nitem=items, workgroup=threads)
+                assert np.array_equal(y.cpu().numpy(), oracle.scan(x, "+", exclusive=exclusive)), \
+                    (threads, items, n, exclusive)
+
+
+def test_launch_shape_keywords_scratch(kf, oracle, dev):
+    # get_allocation(Scan1D, f, op, src, workgroup, blocks) sizes for the
+    # shape and tile count; a default-sized tmp is refused by a call whose
+    # shape needs more tiles; the reference's get_allocation(..., blocks)
+    rng = np.random.default_rng(6)
+    n = 10**6
+    x = gen(rng, np.int32, n)
+    src = torch.from_numpy(x).to(dev)
+    dst = torch.empty_like(src)
+    small = kf.get_allocation(kf.Scan1D, kf.identity, "+", src)
+    with pytest.raises(kf.ArgumentError, match="needs"):
+        kf.scan_("+", dst, src, tmp=small, Nitem=4, workgroup=1024)
+    tiles = -(-n // (1024 * 4))
+    tmp = kf.get_allocation(kf.Scan1D, kf.identity, "+", src, 1024, tiles + 1)
+    assert tmp.nbytes >= 256 + 128 * (tiles + 1)
+    for _ in range(2):
+        kf.scan_("+", dst, src, tmp=tmp, Nitem=4, workgroup=1024)
+        assert np.array_equal(dst.cpu().numpy(), oracle.scan(x))
+    big = kf.get_allocation(kf.Scan1D, kf.identity, "+", src, 100_000)
+    assert big.nbytes >= 256 + 128 * 100_000
+    kf.scan_("+", dst, src, tmp=big, Nitem=4)
+    assert np.array_equal(dst.cpu().numpy(), oracle.scan(x))
+    with pytest.raises(kf.ArgumentError, match="Nitem"):
+        kf.scan_("+", dst, src, Nitem=0)
+    with pytest.raises(kf.ArgumentError, match="unknown keyword"):
+        kf.scan_("+", dst, src, Nitems=4)

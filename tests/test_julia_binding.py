@@ -82,7 +82,8 @@ def test_every_ccall_matches_kf_h():
         assert args == cargs, f"{name}: kf.h {cargs} vs binding {args}"
     # the hot path's entry points are all bound
     bound = {c[0] for c in calls}
-    for name in ("kf_scan", "kf_scan_scratch_bytes", "kf_scan_scratch_status", "kf_reduce", "kf_reduce_scratch_bytes",
+    for name in ("kf_scan_shaped", "kf_scan_shaped_scratch_bytes", "kf_scan_shape", "kf_scan_scratch_status",
+                 "kf_reduce", "kf_reduce_scratch_bytes",
                  "kf_reduce2", "kf_reduce3", "kf_reduce_dim", "kf_reduce_dim_x", "kf_reduce_dim_scratch_bytes",
                  "kf_reduce_dim_batched", "kf_reduce_dim_batched_scratch_bytes", "kf_post_map", "kf_copy", "kf_fill",
                  "kf_last_error"):
