@@ -8,9 +8,9 @@
 // design differs from the reference in these ways:
 //
 //  * Large tiles: 8 16-byte vectors per lane x 1024 threads = 128 KiB (768
-//    threads = 96 KiB for 4- and 8-byte types from 20 MiB on; 512 threads
+//    threads = 96 KiB for 4- and 8-byte types from 17 MiB on; 512 threads
 //    x 8/12/16 vectors for UInt8; 2 or 4 vectors per lane for arrays too
-//    small to make 240 such tiles), so 2^28 Float32 is 10923 tiles and the
+//    small to make 160 such tiles), so 2^28 Float32 is 10923 tiles and the
 //    per-tile lookback is amortised over a large streaming body. The tile
 //    stays in registers in "striped" order: lane l of wave w holds vector
 //    j*64 + l of the wave's contiguous chunk, so every load and store is a
@@ -78,7 +78,10 @@ constexpr int kScanBlock = 1024;       // large tiles (default)
 // numbered by workgroup id: 240 tiles rather than 120 gives Float32 2^21
 // 7.68 -> 6.80 us, 2*10^6 7.55 -> 7.04 us, 4*10^6 10.4 -> 8.8 us, 10^6 6.06
 // -> 6.16 us. Letting 10^6 drop to 16 KiB tiles to reach 240 cost 9 %,
-// hence the floor.
+// hence the floor. A later sweep with every shape forced in turn (the
+// launch-shape keywords) lowered the minimum to 160: Float32 3.5*10^6
+// 8.8 -> 8.1 us, Float64 1.6*10^6 10.2 -> 9.4 us (Float32 2.5*10^6 tied,
+// Int32 3*10^6 8.2 -> 8.6 us the one loss).
 // Threads per tile by element type (2^28 Float32 / Int32, 2^27 Float64,
 // 2^26 affine pairs, 2^30 UInt8 over 512, 768 and 1024): UInt8 (16
 // elements per vector, long in-tile work) gains most from co-resident
@@ -89,7 +92,7 @@ constexpr int kScanBlock = 1024;       // large tiles (default)
 // 335 us, Float64 2^27 324 vs 353 us.
 constexpr int kTiers = 4;
 constexpr int kTierV[kTiers] = {1, 2, 4, 8};
-constexpr int64_t kMinTiles = 240;
+constexpr int64_t kMinTiles = 160;
 // UInt8 tiles carry 4x the elements per byte of work: they need more tiles
 // (480) before a larger shape pays (10^7 9.7 us at 480, 10.7 at 240, 18.2
 // at 960).
@@ -103,18 +106,22 @@ template <class T> constexpr int kMinTier = sizeof(T) == 1 ? 0 : 1;
 // 10^9 343 -> 329 us at 12; 2^30 361 -> 341 us, 2^31 702 -> 657 us at 16,
 // where 12 gives 350 / 673 (20 and 24 vectors lose 8-10 %; at 32 the
 // compiler no longer keeps the tile in registers).
-// The 4- and 8-byte types take it from 20 MiB, where two co-resident 96 KiB
+// The 4- and 8-byte types take it from 17 MiB, where two co-resident 96 KiB
 // tiles per CU balance the last round of tiles better than one 128 KiB tile
 // (HIP graphs, us, 1024 x 8 -> 768 x 8): Float32 6*10^6 11.3 -> 9.9, 10^7
 // 16.4 -> 14.6, 10^8 124.3 -> 122.7; Float64 6*10^6 24.6 -> 17.9, 10^7
 // 35.6 -> 31.5, 2*10^7 64.5 -> 55.1, 5*10^7 142.0 -> 125.4; affine pairs
 // 5*10^6 21.5 -> 17.0, 5*10^7 141.8 -> 125.6. Worst case Float32 2*10^7
-// 29.7 -> 30.6; below 20 MiB (Float32 4*10^6) the 64 KiB tiles stay ahead.
-constexpr int64_t kWideBytes = 20LL << 20;
+// 29.7 -> 30.6. The forced-shape sweep moved the threshold from 20 down to
+// 17 MiB: at 18 MiB Float32 9.6 -> 9.5 us, Int32 9.9 -> 9.2, Float64 and
+// Int64 11.0 -> 10.9, affine pairs 10.6 -> 10.3 (Float32 5.2*10^6 10.4 ->
+// 9.7); at 16 MiB the 1024-thread tiles are still 2-7 % ahead.
+constexpr int64_t kWideBytes = 17LL << 20;
 constexpr int64_t kHugeBytes = 1LL << 30;
-// UInt8 takes the 12-vector shape from 256 MiB (3*10^8: 118 -> 116 us; at
-// 10^8 the 8-vector tiles stay ahead, 50.6 vs 53.3 us).
-constexpr int64_t kU8WideBytes = 1LL << 28;
+// UInt8 takes the 12-vector shape from 384 MiB (forced-shape sweep: 3*10^8
+// 106.5 us at 8 vectors vs 107.8 at 12, 3.5-4*10^8 tied, 4.5*10^8 153.7 vs
+// 152.3, 5*10^8 169.7 vs 167.3).
+constexpr int64_t kU8WideBytes = 384LL << 20;
 constexpr int kTierWide = kTiers;      // tier index of the wide shape
 constexpr int kTierHuge = kTiers + 1;  // UInt8 from kHugeBytes
 template <class T> constexpr bool has_wide_tier() {

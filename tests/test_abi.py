@@ -40,15 +40,15 @@ def test_version(kf):
 def test_scratch_queries(kf):
     L = kf._lib.lib()
     # one 128-byte descriptor line per tile + a 256-byte header; large arrays
-    # use 8 x 16-byte vectors per thread, 768 threads from 20 MiB on for
+    # use 8 x 16-byte vectors per thread, 768 threads from 17 MiB on for
     # 4- and 8-byte types (96 KiB tiles); the tile count covers
     # operands that start up to 15 bytes past a 16-byte boundary
     tiles = -(-(2**28 + 3) // (768 * 8 * 4))
     assert L.kf_scan_scratch_bytes(kf._lib.F32, kf._lib.OP_ADD, 2**28) == 256 + tiles * 128
     assert L.kf_scan_scratch_bytes(kf._lib.F32X2, kf._lib.OP_AFFINE, 2**26) == 256 + -(-(2**26 + 1) // (768 * 8 * 2)) * 128
     assert L.kf_scan_scratch_bytes(kf._lib.F32X2, kf._lib.OP_AFFINE, 2**25) == 256 + -(-(2**25 + 1) // (768 * 8 * 2)) * 128
-    # just below 20 MiB: 1024 threads x 4 vectors (64 KiB tiles)
-    n = (20 << 20) // 4 - 1
+    # just below 17 MiB: 1024 threads x 4 vectors (64 KiB tiles)
+    n = (17 << 20) // 4 - 1
     assert L.kf_scan_scratch_bytes(kf._lib.F32, kf._lib.OP_ADD, n) == 256 + -(-(n + 3) // (1024 * 4 * 4)) * 128
     assert L.kf_scan_scratch_bytes(kf._lib.U8, kf._lib.OP_ADD, 1) == 256 + 128
     assert L.kf_reduce_scratch_bytes(kf._lib.F64, 10) >= 256 + 4096 * 8

@@ -38,10 +38,10 @@ def test_uint8_scan_beyond_2pow31(kf, dev):
 
 
 def test_uint8_scan_wide_shape_switchover(kf, dev):
-    # UInt8 arrays switch to 512 x 12-vector tiles at 2^28 bytes and to
+    # UInt8 arrays switch to 512 x 12-vector tiles at 384 MiB and to
     # 512 x 16 at 2^30: both sides of each switch, inclusive and exclusive,
     # against the closed-form prefix of x[k] = k mod 256
-    for edge in (1 << 28, 1 << 30):
+    for edge in (384 << 20, 1 << 30):
         for n in (edge - 1, edge, edge + 1):
             x = torch.empty(n, dtype=torch.uint8, device=dev)
             for s in range(0, n, CHUNK):

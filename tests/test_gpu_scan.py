@@ -225,10 +225,10 @@ def test_affine_scan(kf, oracle, dev, n):
         assert_mixed(got, oracle.scan(ab, "affine", exclusive=exclusive), 1e-5, what=f"affine n={n} excl={exclusive}")
 
 
-@pytest.mark.parametrize("n", [(20 << 20) // 8 - 1, (20 << 20) // 8, 10**7 + 3])
+@pytest.mark.parametrize("n", [(17 << 20) // 8 - 1, (17 << 20) // 8, 10**7 + 3])
 def test_affine_scan_wide_tiles(kf, oracle, dev, n):
-    # the affine pairs (8 bytes) switch from 1024 x 4-vector tiles to
-    # 768 x 8-vector tiles at 20 MiB; 10^7 pairs give more tiles than the GPU
+    # the affine pairs (8 bytes) switch from 1024 x 8-vector tiles to
+    # 768 x 8-vector tiles at 17 MiB; 10^7 pairs give more tiles than the GPU
     # holds at once, so the windowed lookback runs as well
     rng = np.random.default_rng(n)
     ab = np.stack([rng.uniform(0.9, 1.0, n), rng.standard_normal(n)], 1).astype(np.float32)
@@ -307,9 +307,9 @@ def test_views_offsets_strides_inplace(kf, oracle, dev):
 @pytest.mark.parametrize("dt", [np.float32, np.float64, np.int32, np.int64, np.uint8])
 def test_tile_size_switchover(kf, oracle, dev, dt):
     # tiles are 1024 threads (512 for uint8; 768 x 8 vectors for 4- and
-    # 8-byte types from 20 MiB on; uint8's own 12- and 16-vector shapes from 256 MiB and
+    # 8-byte types from 17 MiB on; uint8's own 12- and 16-vector shapes from 384 MiB and
     # 1 GiB are checked in test_gpu_large.py) x V 16-byte vectors, V in
-    # (1, 2, 4, 8): the largest V that still makes >= 240 tiles (480 for
+    # (1, 2, 4, 8): the largest V that still makes >= 160 tiles (480 for
     # uint8), never below 2 except for uint8. The lookback polls 64 tiles
     # while every tile is resident, else 2, 4 or 8 by tile size (2 for
     # 128 KiB tiles from 4 generations on). Check both sides of every switch
@@ -317,13 +317,13 @@ def test_tile_size_switchover(kf, oracle, dev, dt):
     # exact in any order).
     epv = 16 // np.dtype(dt).itemsize
     block = {np.uint8: 512}.get(dt, 1024)
-    min_tiles = 480 if dt == np.uint8 else 240
+    min_tiles = 480 if dt == np.uint8 else 160
     rng = np.random.default_rng(23)
     edges = [min_tiles * block * v * epv for v in (2, 4, 8)] + [512 * block * 8 * epv]
     if dt != np.uint8:
         edges.append(4 * 512 * block * 8 * epv)        # window 2 from 4 generations of 128 KiB tiles
     if dt in (np.float32, np.float64, np.int32, np.int64):
-        edges.append((20 << 20) // np.dtype(dt).itemsize)   # 768-thread tiles from 20 MiB on
+        edges.append((17 << 20) // np.dtype(dt).itemsize)   # 768-thread tiles from 17 MiB on
     for e in edges:
         for n in (e - 1, e, e + 1):
             x = (rng.random(n) < 1 / 16).astype(dt) if np.dtype(dt).kind == "f" else gen(rng, dt, n)
