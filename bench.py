@@ -64,12 +64,15 @@ def time_calls(fn, reps, batches=5, with_min=False):
 
 
 def load_traffic():
-    """HBM bytes per scan launch measured with rocprofv3 --pmc (FETCH_SIZE +
-    WRITE_SIZE, scaled by the copy-kernel calibration), if recorded."""
-    p = os.path.join(REPO, "profiles", "traffic_scan_f32_2p28.json")
+    """HBM bytes per launch of the headline scan (row H1 of the per-config
+    rocprofv3 --pmc summary: FETCH_SIZE + WRITE_SIZE, scaled by the
+    copy-kernel calibration), if recorded."""
+    p = os.path.join(REPO, "profiles", "traffic_all_configs.json")
     if os.path.exists(p):
         with open(p) as fh:
-            return json.load(fh).get("hbm_bytes_per_launch")
+            h = json.load(fh)["configs"].get("H1")
+        if h:
+            return int(round((h["fetch_bytes"] + h["write_bytes"]) / h["dispatches_per_call"]))
     return None
 
 
@@ -386,6 +389,15 @@ def config_cases(kf, dev):
     def tmp_for(kind, src):
         return kf.get_allocation(kind, kf.identity, "+", src)
 
+    # the bench step's two calls (Float32 n=2^28), for their counters
+    xh = torch.rand(2**28, device=dev, generator=g)
+    yh = torch.empty_like(xh)
+    oh = torch.empty(1, device=dev)
+    th, trh = tmp_for(kf.Scan1D, xh), tmp_for(kf.MapReduce1D, xh)
+    yield "H1", "H1 scan F32 incl n=2^28 (bench step)", 8 * 2**28, lambda: kf.scan_("+", yh, xh, tmp=th), 20
+    yield "H2", "H2 mapreduce F32 n=2^28 (bench step)", 4 * 2**28, \
+        lambda: kf.mapreduce_(kf.identity, "+", oh, xh, tmp=trh), 20
+    del xh, yh
     x = torch.rand(10**6, device=dev, generator=g)
     y = torch.empty_like(x)
     t1 = tmp_for(kf.Scan1D, x)

@@ -239,7 +239,11 @@ __global__ __launch_bounds__(kRedBlock) void reduce_once_kernel(const T* src, in
 // Persistent single-launch reduction for arrays of kChunkMinVecs vectors
 // (256 MiB) or more: kFoldMax workgroups, workgroup b streaming the
 // contiguous chunk [b*chunk, (b+1)*chunk) of vectors with U loads in flight
-// per lane, then the fold. Measured on MI355X against one-shot level 0 +
+// per lane, then the fold. The host makes `chunk` a whole number of
+// U * kRedBlock-vector rounds, so only the last non-empty chunk ends in a
+// partial round, which is one guarded round with every load in flight (a
+// one-load-per-iteration remainder loop cost 13 serial memory latencies per
+// workgroup at 10^9 Float32: 630 vs 590 us). Measured on MI355X against one-shot level 0 +
 // folding level 1 (eager, us): Float32 2^26 41.0 vs 41.9-43.1, 2^28 154.0
 // vs 156.9, 2^30 606 vs 622; Float64 2^26 79.1 vs 80.9, 2^28 305 vs 318;
 // Int32 2^28 153.7 vs 156.7. At 200 MB (5*10^7 Float32, 1.5 loop
@@ -273,12 +277,20 @@ __global__ __launch_bounds__(kRedBlock) void reduce_chunk_kernel(const T* src, i
       for (int e = 0; e < EPV; ++e) a[e] = Op::combine(a[e], Map::apply(x[e]));
     }
   }
-  for (; i < b1; i += kRedBlock) {
-    const uint4 r = ld_stream(v + i);
-    T x[EPV];
-    __builtin_memcpy(x, &r, 16);
+  if (i < b1) {  // the partial last round: fewer than U vectors per lane
+    uint4 r[U];
 #pragma unroll
-    for (int e = 0; e < EPV; ++e) a[e] = Op::combine(a[e], Map::apply(x[e]));
+    for (int u = 0; u < U; ++u)
+      if (i + u * kRedBlock < b1) r[u] = ld_stream(v + i + u * kRedBlock);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (i + u * kRedBlock < b1) {
+        T x[EPV];
+        __builtin_memcpy(x, &r[u], 16);
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) a[e] = Op::combine(a[e], Map::apply(x[e]));
+      }
+    }
   }
   T acc = a[0];
 #pragma unroll
@@ -436,7 +448,8 @@ int launch_reduce(const void* src, int64_t n, int64_t stride, void* dst, void* s
   if (nvec >= kChunkMinVecs) {
     // kFoldMax persistent workgroups over contiguous chunks, folded in the
     // same launch
-    const int64_t chunk = (nvec + kFoldMax - 1) / kFoldMax;
+    constexpr int64_t kRound = (int64_t)kChunkUnroll * kRedBlock;
+    const int64_t chunk = ((nvec + kFoldMax - 1) / kFoldMax + kRound - 1) / kRound * kRound;
     hipLaunchKernelGGL((reduce_chunk_kernel<T, Op, Map, kChunkUnroll>), dim3(kFoldMax), dim3(kRedBlock), 0, stream,
                        (const T*)src, n, head, nvec, chunk, (T*)dst, (uint64_t*)scratch);
     return kf_check_launch("reduce_chunk_kernel");

@@ -436,10 +436,13 @@ def test_multilevel_full_reduce_exact(kf, oracle, dev, dt):
     # unaligned starts (exact integer results): one launch of one-shot
     # workgroups at 2 and 4 vectors per lane (2048 * 256 * 2 vectors), the
     # same just past 128 MiB (one-shot level 0 + folding level 1), and from
-    # 256 MiB the persistent chunked single launch
+    # 256 MiB the persistent chunked single launch: whole rounds only, and
+    # (2^24 + 5000 vectors) chunks rounded up to whole rounds, so one
+    # workgroup ends in a partial round and the last 682 get no vectors
     rng = np.random.default_rng(47)
     epv = 16 // np.dtype(dt).itemsize
-    for n in (2048 * 512 * epv - 1, 2048 * 512 * epv + 5, 2048 * 256 * 16 * epv + 5, 2**24 * epv + 3):
+    for n in (2048 * 512 * epv - 1, 2048 * 512 * epv + 5, 2048 * 256 * 16 * epv + 5, 2**24 * epv + 3,
+              (2**24 + 5000) * epv + 7):
         print(f"multilevel {np.dtype(dt).name} n={n}", flush=True)
         x = gen(rng, dt, n + 3)
         t = torch.from_numpy(x).to(dev)
