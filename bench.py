@@ -17,6 +17,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--all [--all-json PA
                  and the rows inside the JSON line as "all_configs")
   --all-json     also write those rows, with the ceilings, to PATH
   --sweep        the reference's 10^6..10^9 size sweep
+  --sweep-2d     the reference's matvec / vecmat shape sweep (n*p = 10^7..10^9)
   --timeline [large|mid]  only the per-tile phases of the scan (instrumented library)
   --pmc-run      only the marked dispatch sequence of every configuration,
                  for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs
@@ -129,6 +130,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--sweep", action="store_true",
                     help="the reference's scan/mapreduce size sweep (perfs/julia/benchmarks)")
+    ap.add_argument("--sweep-2d", action="store_true",
+                    help="the reference's matvec/vecmat shape sweep (perfs/julia/benchmarks)")
     ap.add_argument("--timeline", nargs="?", const="large", choices=("large", "mid"),
                     help="only the per-tile scan timeline (libkfhip_timeline.so): the large "
                          "scans (default) or the mid sizes of the reference's sweep")
@@ -249,6 +252,8 @@ def main():
         line["all_configs"] = bench_all(kf, dev, ceil, args.all_json)
     if args.sweep:
         line["sweep"] = bench_sweep(kf, dev, ceil)
+    if args.sweep_2d:
+        line["sweep_2d"] = bench_sweep_2d(kf, dev, ceil)
     print(json.dumps(line), flush=True)
 
 
@@ -376,6 +381,66 @@ def bench_sweep(kf, dev, ceil):
                     f"same-size {'copy' if what == 'scan' else 'read'} {same[what]*1e6:.1f} us "
                     f"({same[what]/sec*100:.0f}%)")
             del x, y, ts, tr, pscr
+    return rows
+
+
+def bench_sweep_2d(kf, dev, ceil):
+    """The reference's matvec / vecmat sweeps (perfs/julia/benchmarks/
+    matvec_perf_comparison.jl:77-88, vecmat_perf_comparison.jl:59-70): n x p
+    column-major matrices of n*p in {10^7, 10^8, 10^9} elements, n = 10^k
+    (k = 0..log10(total), 1..log10(total)-1 at 10^9), Float32, Float64 and
+    UInt8; matvec!(*, +, y, A, x) (y[i] = sum_j A[i,j] x[j]) and
+    vecmat!(*, +, y, x, A) (y[j] = sum_i x[i] A[i,j]). HIP-graph timed; GB/s
+    of algorithmic bytes (A, x and y once each), as a fraction of the read
+    ceiling and of a same-size read (the best read probe over A's bytes)."""
+    import ctypes
+    import operator
+    L, K = kf._lib.lib(), kf._lib
+    rows = []
+    g = torch.Generator(device=dev).manual_seed(20261201)
+    tmp = kf.KernelBuffer(kf.MapReduce2D, 64 << 20, dev)
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+    for total in (10**7, 10**8, 10**9):
+        top = round(np.log10(total))
+        ks = range(0, top + 1) if total <= 10**8 else range(1, top)
+        for dt in (torch.float32, torch.float64, torch.uint8):
+            es = torch.empty(0, dtype=dt).element_size()
+            flat = (torch.randint(0, 4, (total,), device=dev, generator=g, dtype=dt) if dt == torch.uint8
+                    else torch.rand(total, device=dev, generator=g, dtype=dt))
+            nb = total * es // 16 * 16
+            pscr = torch.empty(L.kf_bw_probe_scratch_bytes(nb), dtype=torch.uint8, device=dev)
+            same = None
+            for kind in (K.BW_READ, K.BW_READ_TILED):
+                def fn():
+                    K.check(L.kf_bw_probe(kind, ctypes.c_void_p(sink.data_ptr()), ctypes.c_void_p(flat.data_ptr()), nb,
+                                          ctypes.c_void_p(pscr.data_ptr()), pscr.numel(),
+                                          ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)), "kf_bw_probe")
+                t = _graph_time(fn, reps=20 if nb < 10**9 else 5)
+                same = t if same is None else min(same, t)
+            for k in ks:
+                n = 10**k
+                p = total // n
+                A = flat[:n * p].as_strided((n, p), (1, n))
+                xr = torch.ones(p, device=dev, dtype=dt)
+                xc = torch.ones(n, device=dev, dtype=dt)
+                yr = torch.empty(n, device=dev, dtype=dt)
+                yc = torch.empty(p, device=dev, dtype=dt)
+                for what, bytes_, fn in (
+                        ("matvec", es * (n * p + p + n), lambda: kf.matvec_(operator.mul, "+", yr, A, xr, tmp=tmp)),
+                        ("vecmat", es * (n * p + n + p), lambda: kf.vecmat_(operator.mul, "+", yc, xc, A, tmp=tmp))):
+                    _mark(kf, dev, True)
+                    sec = _graph_time(fn, reps=20 if total < 10**9 else 5)
+                    _mark(kf, dev, False)
+                    gb = bytes_ / sec / 1e9
+                    c = ceil["read_ceiling_gbps"]
+                    rows.append({"op": what, "total": total, "n": n, "p": p, "dtype": str(dt).replace("torch.", ""),
+                                 "us": round(sec * 1e6, 2), "gbps": round(gb, 1), "frac_ceiling": round(gb / c, 4),
+                                 "same_size_read_us": round(same * 1e6, 2), "frac_same_size": round(same / sec, 4)})
+                    log(f"  {what} {str(dt):14s} n={n:>10d} p={p:>10d} {sec*1e6:10.1f} us {gb:8.0f} GB/s "
+                        f"{gb/c*100:5.1f}% of the read ceiling, same-size read {same*1e6:.1f} us "
+                        f"({same/sec*100:.0f}%)")
+                del A, xr, xc, yr, yc
+            del flat, pscr
     return rows
 
 

@@ -39,6 +39,9 @@ extern "C" int kf_reduce_dim_x(kf_op op, kf_map2 f, kf_dtype dt, const void* A, 
   const size_t es = kf_dtype_size(dt);
   if ((uintptr_t)A % es || (uintptr_t)dst % es || (uintptr_t)x % es)
     return kf_set_error(KF_EINVAL, "kf_reduce_dim_x: pointers not aligned to the element type");
+  if (dim_is_1d(rows, cols, dim))  // a dot product of one row or column with x
+    return kf_reduce2(op, f, dt, A, dim == 2 ? col_stride : 1, x, x_stride, dim == 2 ? cols : rows, dst, scratch,
+                      scratch_bytes, stream);
   const DimVec dv = dim_vec(A, rows, col_stride, es, dim, 1, 0, true, x, x_stride);
   const DimPlan p = plan_dim(es, rows, cols, dim, dv.vec);
   if (dim_need(es, rows, cols, dim, 1, dv) > 0) {

@@ -24,6 +24,45 @@ __global__ __launch_bounds__(kRedBlock) void combine_split_kernel(const T* parti
   dst[i * ds] = x;
 }
 
+// Stage 2 for many splits of few rows: the S partial columns are cut into
+// kCombWaves consecutive ranges, one per wave; lane l of every wave owns row
+// blockIdx.x * 64 + l, so each load of a wave reads 64 consecutive partials,
+// with kCombUnroll loads in flight; the ranges are then combined in order.
+// (One workgroup of the narrow kernel folding 512 partial columns of 1000
+// rows took longer than the streaming pass it finished.)
+constexpr int kCombWaves = 16;
+constexpr int kCombUnroll = 8;
+template <class T, class Op>
+__global__ __launch_bounds__(kCombWaves * kWave) void combine_cols_kernel(const T* partials, int S, int64_t m,
+                                                                          T* dst, int64_t ds, int64_t dst_bstride) {
+  __shared__ T s_part[kCombWaves][kWave];
+  const int lane = lane_id(), wave = threadIdx.x / kWave;
+  const int64_t i = (int64_t)blockIdx.x * kWave + lane;
+  partials += (int64_t)blockIdx.y * S * m;
+  const int per = (S + kCombWaves - 1) / kCombWaves;
+  const int s0 = wave * per, s1 = kmin(S, s0 + per);
+  T acc = Op::template identity<T>();
+  if (i < m) {
+    int s = s0;
+    for (; s + kCombUnroll <= s1; s += kCombUnroll) {
+      T x[kCombUnroll];
+#pragma unroll
+      for (int u = 0; u < kCombUnroll; ++u) x[u] = partials[(int64_t)(s + u) * m + i];
+#pragma unroll
+      for (int u = 0; u < kCombUnroll; ++u) acc = Op::combine(acc, x[u]);
+    }
+    for (; s < s1; ++s) acc = Op::combine(acc, partials[(int64_t)s * m + i]);
+  }
+  s_part[wave][lane] = acc;
+  __syncthreads();
+  if (wave == 0 && i < m) {
+    T x = s_part[0][lane];
+#pragma unroll
+    for (int w = 1; w < kCombWaves; ++w) x = Op::combine(x, s_part[w][lane]);
+    dst[(int64_t)blockIdx.y * dst_bstride + i * ds] = x;
+  }
+}
+
 // ---------------------------------------------------------------------------
 // dim = 1: one wave per column (a column of a column-major matrix is
 // contiguous), optionally split into S row segments when there are too few
@@ -547,6 +586,12 @@ inline DimPlan plan_dim(size_t es, int64_t rows, int64_t cols, int dim, bool vec
   return p;
 }
 
+// A single row reduced along dim 2, or a single column along dim 1: the
+// entry points hand these to the 1-D reductions (kf_reduce, kf_reduce2),
+// which stream them with every workgroup reading contiguous memory (one row
+// of a 1 x 10^8 Float32 matrix: 2.2 TB/s through the narrow dim-2 kernel).
+inline bool dim_is_1d(int64_t rows, int64_t cols, int dim) { return dim == 2 ? rows == 1 : cols == 1; }
+
 inline bool dim_vec_ok(const void* A, int64_t cs, size_t es) {
   return ((uintptr_t)A % 16 == 0) && ((cs * (int64_t)es) % 16 == 0);
 }
@@ -634,6 +679,11 @@ void launch_narrow(bool unit_vec, dim3 grid, const T* A, int64_t rows, int64_t c
                        cs, out, ods, seg, a_bstride, out_bstride, x, xs);
 }
 
+// combine_cols_kernel from kCombMinSplits partial columns of more than
+// kCombMinUnits row units (fewer rows leave most of its lanes idle, where
+// the narrow kernel's phases use them)
+constexpr int kCombMinSplits = 64;
+constexpr int kCombMinUnits = 16;
 // Second stage of a split dims reduction: nz batches of an m x S partial
 // matrix (column s at s*m, batch z at z*S*m; the scratch is 256-byte
 // aligned) reduced along dim 2 into dst[i*ds + z*dst_bstride].
@@ -641,7 +691,10 @@ template <class T, class Op>
 void launch_combine(const T* part, int S, int64_t m, T* dst, int64_t ds, int64_t dst_bstride, unsigned nz,
                     hipStream_t stream) {
   const int64_t nu = row_units(sizeof(T), m, true);
-  if (nu <= kDimBlock)
+  if (nu <= kDimBlock && nu > kCombMinUnits && S >= kCombMinSplits)
+    hipLaunchKernelGGL((combine_cols_kernel<T, Op>), dim3((unsigned)((m + kWave - 1) / kWave), nz),
+                       dim3(kCombWaves * kWave), 0, stream, part, S, m, dst, ds, dst_bstride);
+  else if (nu <= kDimBlock)
     launch_narrow<T, Op, Unary<MapIdentity>>(nu != m, dim3(1, 1, nz), part, m, S, m, dst, ds, S, (int64_t)S * m,
                                              dst_bstride, nullptr, 0, stream);
   else

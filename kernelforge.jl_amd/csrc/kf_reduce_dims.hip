@@ -8,7 +8,10 @@ using namespace kf;
 extern "C" size_t kf_reduce_dim_scratch_bytes(kf_dtype dt, int64_t rows, int64_t cols, int dim) {
   const size_t es = kf_dtype_size(dt);
   if (es == 0 || rows <= 0 || cols <= 0 || (dim != 1 && dim != 2)) return 256;
-  return dim_query(es, rows, cols, dim, 1);  // the plan depends on alignment: every case
+  const size_t b = dim_query(es, rows, cols, dim, 1);  // the plan depends on alignment: every case
+  // one row reduced along dim 2, or one column along dim 1, is a 1-D reduction
+  if (dim_is_1d(rows, cols, dim)) return kmax(b, kf_reduce_scratch_bytes(dt, dim == 2 ? cols : rows));
+  return b;
 }
 
 extern "C" int kf_reduce_dim(kf_op op, kf_map f, kf_dtype dt, const void* A, int64_t rows, int64_t cols,
@@ -29,6 +32,9 @@ extern "C" int kf_reduce_dim(kf_op op, kf_map f, kf_dtype dt, const void* A, int
   const size_t es = kf_dtype_size(dt);
   if ((uintptr_t)A % es || (uintptr_t)dst % es)
     return kf_set_error(KF_EINVAL, "kf_reduce_dim: A/dst not aligned to the element type");
+  if (dim_is_1d(rows, cols, dim))  // the 1-D kernels stream it as one vector (strided for one row)
+    return kf_reduce(op, f, dt, A, dim == 2 ? cols : rows, dim == 2 ? col_stride : 1, dst, scratch, scratch_bytes,
+                     stream);
   const size_t need = kf_reduce_dim_scratch_bytes(dt, rows, cols, dim);
   const DimVec dv = dim_vec(A, rows, col_stride, es, dim, 1, 0, false, nullptr, 0);
   const DimPlan p = plan_dim(es, rows, cols, dim, dv.vec);

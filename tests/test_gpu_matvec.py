@@ -12,7 +12,9 @@ pytestmark = pytest.mark.gpu
 
 SHAPES = [(1, 1), (3, 3), (101, 101), (512, 512), (1000, 1000), (1024, 10), (4096, 32), (65536, 16),
           (3, 10_000), (32, 50_000), (4, 1000), (63, 1000), (2048, 1000), (32768, 50),
-          (8, 300_000), (12, 100_000), (300_000, 3), (100, 20_000)]
+          (8, 300_000), (12, 100_000), (300_000, 3), (100, 20_000),
+          # one row (matvec) / one column (vecmat): the 1-D dot-product route
+          (1, 3), (1, 100_003), (1, 2**20 + 5), (5, 1), (200_001, 1)]
 
 
 def mk(rng, dt, shape):
@@ -99,3 +101,27 @@ def test_get_allocation_kinds_reference_order(kf, oracle, dev):
     ref = int((x.cpu().numpy().astype(np.int64) * y.cpu().numpy()).sum())
     for _ in range(3):
         assert kf.mapreduce(operator.mul, "+", (x, y), tmp=t2) == ref
+
+
+@pytest.mark.parametrize("dt", [np.int32, np.uint8, np.float64])
+def test_single_row_or_column_dims_route(kf, oracle, dev, dt):
+    # mapreduce(f, op, A; dims) over one row (dims=2) or one column (dims=1)
+    # is handed to the 1-D reduction: contiguous, strided (column stride of a
+    # view) and element-offset operands, against numpy (integers exact)
+    rng = np.random.default_rng(79)
+    for n in (1, 7, 4099, 1_000_003):
+        for off in (0, 1):
+            flat = mk(rng, dt, 2 * n + 2)
+            t = torch.from_numpy(flat).to(dev)
+            for dims, shape, strides, take in ((2, (1, n), (1, 1), flat[off:off + n]),
+                                               (2, (1, n), (1, 2), flat[off:off + 2 * n:2]),
+                                               (1, (n, 1), (1, n), flat[off:off + n])):
+                A = t[off:].as_strided(shape, strides)
+                for op, npf in (("+", np.sum), (max, np.max)):
+                    got = kf.mapreduce(kf.identity, op, A, dims=dims).cpu().numpy().reshape(-1)
+                    if np.dtype(dt).kind == "f":
+                        ref = npf(take.astype(np.float64))
+                        assert abs(got[0] - ref) <= 1e-12 * max(1.0, np.abs(take).sum()), (n, off, dims, op)
+                    else:
+                        ref = npf(take.astype(np.int64)) if op == "+" else npf(take)
+                        assert int(got[0]) == int(np.array(ref).astype(dt)), (n, off, dims, op)
