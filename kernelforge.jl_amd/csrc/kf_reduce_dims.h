@@ -284,6 +284,111 @@ __global__ __launch_bounds__(kDimBlock) void reduce_cols_seg_kernel(const T* A, 
 }
 
 // ---------------------------------------------------------------------------
+// dim = 1, short columns of a contiguous matrix (column stride = rows, 16-byte
+// aligned): workgroups stage blocks of whole columns, at most kFlatBlockBytes
+// each, through LDS with 16-byte loads (every load of a block in flight),
+// then reduce each column from LDS with L lanes per column (lane j combines
+// rows j, j + L, ...; then a shuffle tree). Blocks hold a multiple of 16
+// bytes except the matrix's last, whose ragged end is loaded per element.
+// Persistent workgroups walk the blocks. With a vector operand x (vecmat),
+// x sits in LDS for the whole launch. Replaces L lanes per column reading
+// global memory (reduce_cols_seg_kernel), whose short per-lane loops left
+// few loads in flight and, for rows not a multiple of the vector width, ran
+// on element loads.
+// ---------------------------------------------------------------------------
+constexpr int kFlatVecs = 4;                                   // 16-byte vectors per thread per block
+constexpr int kFlatBlockBytes = kDimBlock * kFlatVecs * 16;   // 16 KiB
+constexpr int kFlatMaxColBytes = 2048;                         // longest column this path takes
+constexpr int kFlatMaxBlocks = 4096;                           // persistent grid cap
+constexpr int kFlatRowsPerLane = 16;
+template <class T, class Op, class F, int L>
+__global__ __launch_bounds__(kDimBlock) void reduce_cols_flat_kernel(const T* A, int64_t rows, int64_t cols,
+                                                                     int64_t cpb, T* out, int64_t out_stride,
+                                                                     const T* xv, int64_t xs) {
+  __shared__ uint4 s_blk[kDimBlock * kFlatVecs];
+  __shared__ T s_x[F::kHasX ? kFlatMaxColBytes / sizeof(T) : 1];
+  const T* sb = reinterpret_cast<const T*>(s_blk);
+  const T id = Op::template identity<T>();
+  const int tid = threadIdx.x;
+  if constexpr (F::kHasX)
+    for (int64_t i = tid; i < rows; i += kDimBlock) s_x[i] = xv[i * xs];
+  constexpr int G = kDimBlock / L;
+  const int g = tid / L, j = tid % L;
+  const int64_t nblk = (cols + cpb - 1) / cpb;
+  for (int64_t b = blockIdx.x; b < nblk; b += gridDim.x) {
+    const int64_t c0 = b * cpb;
+    const int64_t nc = kmin<int64_t>(cpb, cols - c0);
+    const int64_t nel = nc * rows;
+    const int64_t nvec = nel * (int64_t)sizeof(T) / 16;  // whole vectors of the block
+    const uint4* src = reinterpret_cast<const uint4*>(A + c0 * rows);
+    uint4 r[kFlatVecs];
+#pragma unroll
+    for (int u = 0; u < kFlatVecs; ++u)
+      if (u * kDimBlock + tid < nvec) r[u] = ld_stream(src + u * kDimBlock + tid);
+#pragma unroll
+    for (int u = 0; u < kFlatVecs; ++u)
+      if (u * kDimBlock + tid < nvec) s_blk[u * kDimBlock + tid] = r[u];
+    // the ragged end of the matrix's last block, per element
+    const int64_t e0 = nvec * 16 / (int64_t)sizeof(T);
+    if (e0 + tid < nel) const_cast<T*>(sb)[e0 + tid] = A[c0 * rows + e0 + tid];
+    __syncthreads();
+    for (int64_t c = g; c < nc; c += G) {
+      const T* col = sb + c * rows;
+      T acc = id;
+      for (int64_t i = j; i < rows; i += L) acc = Op::combine(acc, F::apply(col[i], F::kHasX ? s_x[i] : col[i]));
+      acc = group_reduce<Op, L>(acc);
+      if (j == 0) out[(c0 + c) * out_stride] = acc;
+    }
+    __syncthreads();  // the next block overwrites the LDS
+  }
+}
+
+// Columns per block for reduce_cols_flat_kernel: as many as fit in
+// kFlatBlockBytes, a multiple of the count that keeps block starts 16-byte
+// aligned; 0 if not even that many fit.
+inline int64_t flat_cols_per_block(size_t es, int64_t rows) {
+  const int64_t cb = rows * (int64_t)es;
+  int64_t g = 16;
+  while (cb % g) g >>= 1;
+  const int64_t ca = 16 / g;
+  return kFlatBlockBytes / cb / ca * ca;
+}
+
+// The flat path applies to a single 16-byte aligned contiguous matrix with
+// columns of at most kFlatMaxColBytes.
+inline bool use_flat_cols(const void* A, int64_t rows, int64_t cs, size_t es, int64_t batch) {
+  return batch == 1 && cs == rows && (uintptr_t)A % 16 == 0 && rows * (int64_t)es <= kFlatMaxColBytes &&
+         flat_cols_per_block(es, rows) > 0;
+}
+
+template <class T, class Op, class F>
+int launch_flat_cols(const T* A, int64_t rows, int64_t cols, T* dst, int64_t ds, const T* x, int64_t xs,
+                     hipStream_t stream) {
+  const int64_t cpb = flat_cols_per_block(sizeof(T), rows);
+  const int64_t nblk = (cols + cpb - 1) / cpb;
+  const dim3 grid((unsigned)kmin<int64_t>(nblk, kFlatMaxBlocks));
+  // about kFlatRowsPerLane rows per lane; UInt8 takes at least 2 lanes per
+  // column (one lane per column reads LDS bytes at the column stride, with
+  // bank conflicts: 10 x 10^7 UInt8 vecmat 44.9 us at 1 lane, 37.6 at 2)
+  int L = sizeof(T) == 1 && rows >= 4 ? 2 : 1;
+  while (L < kWave && (int64_t)L * kFlatRowsPerLane < rows) L <<= 1;
+#define KF_FLAT(LL)                                                                                            \
+  hipLaunchKernelGGL((reduce_cols_flat_kernel<T, Op, F, LL>), grid, dim3(kDimBlock), 0, stream, A, rows, cols, cpb, \
+                     dst, ds, x, xs)
+  switch (L) {
+    case 1: KF_FLAT(1); break;
+    case 2: KF_FLAT(2); break;
+    case 4: KF_FLAT(4); break;
+    case 8: KF_FLAT(8); break;
+    case 16: KF_FLAT(16); break;
+    case 32: KF_FLAT(32); break;
+    default: KF_FLAT(64); break;
+  }
+#undef KF_FLAT
+  return kf_check_launch("reduce_cols_flat_kernel");
+}
+
+// ---------------------------------------------------------------------------
 // dim = 2: a workgroup owns a strip of 256*kRowVecs*EPV rows (4-32 KiB of
 // each column; thread t holds vectors t, t+256, ... of the strip) and a range
 // of columns, which it walks kColUnroll at a time, so every load is part of a
@@ -759,6 +864,8 @@ int launch_reduce_dim(const void* A, int64_t rows, int64_t cols, int64_t cs, int
     }
   }
   if (dim == 1) {
+    if (use_flat_cols(A, rows, cs, sizeof(T), batch))
+      return launch_flat_cols<T, Op, F>((const T*)A, rows, cols, (T*)dst, ds, (const T*)x, xs, stream);
     if (p.seg_lanes) {
       const dim3 grid((unsigned)p.groups);
 #define KF_SEG(V, L)                                                                                          \

@@ -125,3 +125,26 @@ def test_single_row_or_column_dims_route(kf, oracle, dev, dt):
                     else:
                         ref = npf(take.astype(np.int64)) if op == "+" else npf(take)
                         assert int(got[0]) == int(np.array(ref).astype(dt)), (n, off, dims, op)
+
+
+@pytest.mark.parametrize("dt", [np.uint8, np.int32, np.int64])
+def test_short_contiguous_columns_flat_path(kf, oracle, dev, dt):
+    # dims=1 over contiguous matrices with columns of at most 2 KiB: blocks of
+    # whole columns staged through LDS (column counts that leave a ragged
+    # last block, rows that are and are not a multiple of the vector width,
+    # every lanes-per-column choice), vecmat and plain mapreduce, exact
+    rng = np.random.default_rng(83)
+    es = np.dtype(dt).itemsize
+    for rows in (1, 2, 3, 5, 10, 16, 17, 63, 100, 127, 2048 // es, 2048 // es + 1):
+        for cols in (1, 7, 4099, 100_003 // max(1, rows // 8)):
+            buf = mk(rng, dt, rows * cols)
+            A = torch.from_numpy(buf).to(dev).as_strided((rows, cols), (1, rows))
+            x = mk(rng, dt, rows)
+            got = kf.vecmat(operator.mul, "+", torch.from_numpy(x).to(dev), A).cpu().numpy()
+            ref = oracle.reduce_dim_x(buf, rows, cols, rows, x, 1, "+", "mul")
+            assert np.array_equal(got, ref), (rows, cols, "vecmat")
+            M = buf.reshape(cols, rows)
+            for op, npf in (("+", np.sum), (max, np.max)):
+                got = kf.mapreduce(kf.identity, op, A, dims=1).cpu().numpy().reshape(-1)
+                ref = (M.astype(np.int64).sum(axis=1).astype(dt) if op == "+" else M.max(axis=1))
+                assert np.array_equal(got, ref), (rows, cols, op)
