@@ -343,6 +343,82 @@ __global__ __launch_bounds__(kDimBlock) void reduce_cols_flat_kernel(const T* A,
   }
 }
 
+// dim = 2 counterpart for short contiguous columns: the same blocks of whole
+// columns through LDS; thread t owns row t % rows (rows t, t + 256, ... when
+// rows > 256) and column phase t / rows of every block, accumulating over
+// all blocks it visits; at the end the phases of each row are combined in
+// order and each workgroup writes one partial per row (or the result when
+// it is alone). With a vector operand x (matvec), each block's slice of x
+// is staged in LDS beside it.
+template <class T, class Op, class F, int R>
+__global__ __launch_bounds__(kDimBlock) void reduce_rows_flat_kernel(const T* A, int64_t rows, int64_t cols,
+                                                                     int64_t cpb, T* out, int64_t out_stride,
+                                                                     const T* xv, int64_t xs) {
+  __shared__ uint4 s_blk[kDimBlock * kFlatVecs];
+  __shared__ T s_x[F::kHasX ? kFlatBlockBytes / 2 / sizeof(T) : 1];
+  T* sb = reinterpret_cast<T*>(s_blk);
+  const T id = Op::template identity<T>();
+  const int tid = threadIdx.x;
+  const int P = rows <= kDimBlock ? kDimBlock / (int)rows : 1;  // column phases
+  const int ph = rows <= kDimBlock ? tid / (int)rows : 0;
+  const int i0 = rows <= kDimBlock ? tid % (int)rows : tid;
+  const bool active = ph < P;
+  T acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = id;
+  const int64_t nblk = (cols + cpb - 1) / cpb;
+  for (int64_t b = blockIdx.x; b < nblk; b += gridDim.x) {
+    const int64_t c0 = b * cpb;
+    const int64_t nc = kmin<int64_t>(cpb, cols - c0);
+    const int64_t nel = nc * rows;
+    const int64_t nvec = nel * (int64_t)sizeof(T) / 16;
+    const uint4* src = reinterpret_cast<const uint4*>(A + c0 * rows);
+    uint4 v[kFlatVecs];
+#pragma unroll
+    for (int u = 0; u < kFlatVecs; ++u)
+      if (u * kDimBlock + tid < nvec) v[u] = ld_stream(src + u * kDimBlock + tid);
+    if constexpr (F::kHasX)
+      for (int64_t c = tid; c < nc; c += kDimBlock) s_x[c] = xv[(c0 + c) * xs];
+#pragma unroll
+    for (int u = 0; u < kFlatVecs; ++u)
+      if (u * kDimBlock + tid < nvec) s_blk[u * kDimBlock + tid] = v[u];
+    const int64_t e0 = nvec * 16 / (int64_t)sizeof(T);
+    if (e0 + tid < nel) sb[e0 + tid] = A[c0 * rows + e0 + tid];
+    __syncthreads();
+    if (active) {
+      for (int64_t c = ph; c < nc; c += P) {
+        const T w = F::kHasX ? s_x[c] : id;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const int64_t i = i0 + (int64_t)r * kDimBlock;
+          if (i < rows) acc[r] = Op::combine(acc[r], F::apply(sb[c * rows + i], w));
+        }
+      }
+    }
+    __syncthreads();  // the next block (or the phase combine) overwrites the LDS
+  }
+  // rows <= 256: combine the phases of row tid in phase order; else every
+  // thread holds whole rows
+#pragma unroll
+  for (int r = 0; r < R; ++r) sb[r * kDimBlock + tid] = acc[r];
+  __syncthreads();
+  T* o = gridDim.x == 1 ? out : out + (int64_t)blockIdx.x * rows;
+  const int64_t os = gridDim.x == 1 ? out_stride : 1;
+  if (rows <= kDimBlock) {
+    if (tid < rows) {
+      T a = sb[tid];
+      for (int q = 1; q < P; ++q) a = Op::combine(a, sb[q * rows + tid]);
+      o[tid * os] = a;
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t i = tid + (int64_t)r * kDimBlock;
+      if (i < rows) o[i * os] = sb[r * kDimBlock + tid];
+    }
+  }
+}
+
 // Columns per block for reduce_cols_flat_kernel: as many as fit in
 // kFlatBlockBytes, a multiple of the count that keeps block starts 16-byte
 // aligned; 0 if not even that many fit.
@@ -360,6 +436,22 @@ inline bool use_flat_cols(const void* A, int64_t rows, int64_t cs, size_t es, in
   return batch == 1 && cs == rows && (uintptr_t)A % 16 == 0 && rows * (int64_t)es <= kFlatMaxColBytes &&
          flat_cols_per_block(es, rows) > 0;
 }
+
+constexpr int kFlatRowsMinSplit = 64;  // workgroups the dims=2 flat path needs from the plan
+// The dims=2 flat path pays for the 8-byte types, and for the 4-byte types
+// whose rows are not a multiple of the vector width (the narrow kernel's
+// element path): n x 10^9/n matvec, n = 10, Float32 1052 -> 851 us, Float64
+// 1666 -> 1354; n = 100 Float64 1567 -> 1322, but Float32 (16-byte row units
+// in the narrow kernel) 706 -> 762, and UInt8, one LDS byte per element, lost
+// 10-40 % at every size.
+template <class T> inline bool use_flat_rows(const void* A, int64_t rows, int64_t cs, int64_t batch) {
+  constexpr int64_t ev = 16 / (int64_t)sizeof(T);
+  return sizeof(T) >= 4 && (sizeof(T) == 8 || rows % ev != 0) && use_flat_cols(A, rows, cs, sizeof(T), batch);
+}
+
+template <class T, class Op, class F>
+int launch_flat_rows(const T* A, int64_t rows, int64_t cols, int S, T* scratch, T* dst, int64_t ds, const T* x,
+                     int64_t xs, hipStream_t stream);
 
 template <class T, class Op, class F>
 int launch_flat_cols(const T* A, int64_t rows, int64_t cols, T* dst, int64_t ds, const T* x, int64_t xs,
@@ -824,12 +916,40 @@ void launch_combine(const T* part, int S, int64_t m, T* dst, int64_t ds, int64_t
                        dim3(kRedBlock), 0, stream, part, S, m, dst, ds, dst_bstride);
 }
 
+// S persistent workgroups write S partial rows-vectors into the scratch,
+// combined by launch_combine (S = 1: straight into dst).
+template <class T, class Op, class F>
+int launch_flat_rows(const T* A, int64_t rows, int64_t cols, int S, T* scratch, T* dst, int64_t ds, const T* x,
+                     int64_t xs, hipStream_t stream) {
+  const int64_t cpb = flat_cols_per_block(sizeof(T), rows);
+  T* out = S > 1 ? scratch : dst;
+  const int R = (int)((rows + kDimBlock - 1) / kDimBlock);
+#define KF_FLATR(RR)                                                                                           \
+  hipLaunchKernelGGL((reduce_rows_flat_kernel<T, Op, F, RR>), dim3((unsigned)S), dim3(kDimBlock), 0, stream, A, rows, \
+                     cols, cpb, out, ds, x, xs)
+  if (R <= 1) KF_FLATR(1);
+  else if (R <= 2) KF_FLATR(2);
+  else if (R <= 4) KF_FLATR(4);
+  else KF_FLATR(8);
+#undef KF_FLATR
+  if (S > 1) launch_combine<T, Op>(scratch, S, rows, dst, ds, 0, 1, stream);
+  return kf_check_launch("reduce_rows_flat_kernel");
+}
+
 template <class T, class Op, class F>
 int launch_reduce_dim(const void* A, int64_t rows, int64_t cols, int64_t cs, int dim, void* dst,
                       int64_t ds, void* scratch, hipStream_t stream, int64_t batch = 1, int64_t a_bstride = 0,
                       const void* x = nullptr, int64_t xs = 0, int64_t dst_bstride = -1, bool may_peel = true) {
   if (dst_bstride < 0) dst_bstride = rows * ds;
   const DimVec dv = dim_vec(A, rows, cs, sizeof(T), dim, batch, a_bstride, F::kHasX, x, xs);
+  if (dim == 2 && !dv.head && !dv.tail && use_flat_rows<T>(A, rows, cs, batch)) {
+    // short contiguous columns: the LDS-staged flat kernel, with as many
+    // workgroups (and partial rows-vectors) as the plan's column splits
+    const DimPlan pf = plan_dim(sizeof(T), rows, cols, 2, dv.vec, batch);
+    if (pf.split >= kFlatRowsMinSplit)
+      return launch_flat_rows<T, Op, F>((const T*)A, rows, cols, pf.split, (T*)scratch, (T*)dst, ds, (const T*)x, xs,
+                                        stream);
+  }
   if (may_peel && (dv.head || dv.tail)) {
     // element-path launches for the head and tail rows around the vector
     // launch; stream order lets all of them use the same scratch

@@ -148,3 +148,26 @@ def test_short_contiguous_columns_flat_path(kf, oracle, dev, dt):
                 got = kf.mapreduce(kf.identity, op, A, dims=1).cpu().numpy().reshape(-1)
                 ref = (M.astype(np.int64).sum(axis=1).astype(dt) if op == "+" else M.max(axis=1))
                 assert np.array_equal(got, ref), (rows, cols, op)
+
+
+@pytest.mark.parametrize("dt", [np.int32, np.int64])
+def test_short_contiguous_columns_flat_rows_path(kf, oracle, dev, dt):
+    # dims=2 over contiguous matrices with columns of at most 2 KiB (8-byte
+    # types, and 4-byte types whose rows are not a multiple of 4): blocks of
+    # whole columns through LDS, row phases, partial rows-vectors per
+    # workgroup and the split combine; matvec and plain mapreduce, exact
+    rng = np.random.default_rng(89)
+    es = np.dtype(dt).itemsize
+    for rows in (2, 3, 5, 10, 63, 255, 257, 2048 // es - 1, 2048 // es):
+        for cols in (1000, 40_003, 1_000_003 // rows):
+            buf = mk(rng, dt, rows * cols)
+            A = torch.from_numpy(buf).to(dev).as_strided((rows, cols), (1, rows))
+            x = mk(rng, dt, cols)
+            got = kf.matvec(operator.mul, "+", A, torch.from_numpy(x).to(dev)).cpu().numpy()
+            ref = oracle.reduce_dim_x(buf, rows, cols, rows, x, 2, "+", "mul")
+            assert np.array_equal(got, ref), (rows, cols, "matvec")
+            M = buf.reshape(cols, rows)
+            for op in ("+", max):
+                got = kf.mapreduce(kf.identity, op, A, dims=2).cpu().numpy().reshape(-1)
+                ref = (M.astype(np.int64).sum(axis=0).astype(dt) if op == "+" else M.max(axis=0))
+                assert np.array_equal(got, ref), (rows, cols, op)
