@@ -76,6 +76,32 @@ template <class Map> struct Unary {
   template <class T> __device__ static T apply(T a, T) { return Map::apply(a); }
 };
 
+// UInt8 sums through v_dot4_u32_u8: for op + with f = identity, abs2 or x*y
+// (the reference's UInt8 benchmarks), four bytes fold into a 32-bit
+// accumulator per instruction; the low byte of the 32-bit sum is the UInt8
+// (mod 256) result, exactly as a byte-by-byte wrapping sum.
+template <class T, class Op, class F> struct Dot4 {
+  static constexpr int kind = -1;  // not applicable
+};
+template <> struct Dot4<uint8_t, OpAdd, Unary<MapIdentity>> {
+  static constexpr int kind = 0;  // sum of bytes: dot with 0x01010101
+};
+template <> struct Dot4<uint8_t, OpAdd, Unary<MapAbs2>> {
+  static constexpr int kind = 1;  // sum of squares: dot with itself
+};
+template <> struct Dot4<uint8_t, OpAdd, Map2Mul> {
+  static constexpr int kind = 2;  // dot product with the operand
+};
+template <int K> __device__ inline uint32_t dot4_word(uint32_t acc, uint32_t a, uint32_t x) {
+  return __builtin_amdgcn_udot4(a, K == 0 ? 0x01010101u : K == 1 ? a : x, acc, false);
+}
+template <int K> __device__ inline uint32_t dot4_vec(uint32_t acc, uint4 a, uint4 x) {
+  acc = dot4_word<K>(acc, a.x, x.x);
+  acc = dot4_word<K>(acc, a.y, x.y);
+  acc = dot4_word<K>(acc, a.z, x.z);
+  return dot4_word<K>(acc, a.w, x.w);
+}
+
 constexpr int kDimBlock = 256;
 constexpr int kDimWaves = kDimBlock / kWave;
 constexpr int kDimUnroll = 4;
@@ -119,6 +145,27 @@ __global__ __launch_bounds__(kDimBlock) void reduce_cols_kernel(
     const int64_t nv = r1 > r0 ? (r1 - r0) / EPV : 0;
     const uint4* v = reinterpret_cast<const uint4*>(c + r0);
     const uint4* vx = reinterpret_cast<const uint4*>(xv + r0);  // used only with an operand (16-B aligned, xs = 1)
+    if constexpr (Dot4<T, Op, F>::kind >= 0) {
+      constexpr int K = Dot4<T, Op, F>::kind;
+      uint32_t d[kDimUnroll] = {};
+      int64_t i = lane;
+      for (; i + (kDimUnroll - 1) * kWave < nv; i += kDimUnroll * kWave) {
+        uint4 r[kDimUnroll], rx[kDimUnroll];
+#pragma unroll
+        for (int u = 0; u < kDimUnroll; ++u) {
+          r[u] = ld_stream(v + i + u * kWave);
+          if constexpr (F::kHasX) rx[u] = vx[i + u * kWave];
+        }
+#pragma unroll
+        for (int u = 0; u < kDimUnroll; ++u) d[u] = dot4_vec<K>(d[u], r[u], F::kHasX ? rx[u] : r[u]);
+      }
+      for (; i < nv; i += kWave) {
+        const uint4 r = ld_stream(v + i);
+        d[0] = dot4_vec<K>(d[0], r, F::kHasX ? vx[i] : r);
+      }
+      static_assert(kDimUnroll == 4, "the four dot4 accumulators");
+      acc = Op::combine(acc, (T)(d[0] + d[1] + d[2] + d[3]));
+    } else {
     T a[kDimUnroll][EPV];
 #pragma unroll
     for (int u = 0; u < kDimUnroll; ++u)
@@ -156,6 +203,7 @@ __global__ __launch_bounds__(kDimBlock) void reduce_cols_kernel(
     for (int u = 0; u < kDimUnroll; ++u)
 #pragma unroll
       for (int e = 0; e < EPV; ++e) acc = Op::combine(acc, a[u][e]);
+    }
     const int64_t t = r0 + nv * EPV + lane;
     if (t < r1) acc = Op::combine(acc, F::apply(c[t], F::kHasX ? xv[t] : c[t]));
   } else {
@@ -301,12 +349,13 @@ constexpr int kFlatBlockBytes = kDimBlock * kFlatVecs * 16;   // 16 KiB
 constexpr int kFlatMaxColBytes = 2048;                         // longest column this path takes
 constexpr int kFlatMaxBlocks = 4096;                           // persistent grid cap
 constexpr int kFlatRowsPerLane = 16;
+constexpr int kFlatWordsPerLane = 8;  // UInt8 dot4 columns
 template <class T, class Op, class F, int L>
 __global__ __launch_bounds__(kDimBlock) void reduce_cols_flat_kernel(const T* A, int64_t rows, int64_t cols,
                                                                      int64_t cpb, T* out, int64_t out_stride,
                                                                      const T* xv, int64_t xs) {
   __shared__ uint4 s_blk[kDimBlock * kFlatVecs];
-  __shared__ T s_x[F::kHasX ? kFlatMaxColBytes / sizeof(T) : 1];
+  __shared__ __align__(16) T s_x[F::kHasX ? kFlatMaxColBytes / sizeof(T) : 4];
   const T* sb = reinterpret_cast<const T*>(s_blk);
   const T id = Op::template identity<T>();
   const int tid = threadIdx.x;
@@ -335,7 +384,20 @@ __global__ __launch_bounds__(kDimBlock) void reduce_cols_flat_kernel(const T* A,
     for (int64_t c = g; c < nc; c += G) {
       const T* col = sb + c * rows;
       T acc = id;
-      for (int64_t i = j; i < rows; i += L) acc = Op::combine(acc, F::apply(col[i], F::kHasX ? s_x[i] : col[i]));
+      if constexpr (Dot4<T, Op, F>::kind >= 0) {
+        if (rows % 4 == 0) {  // dword-aligned columns: four rows per dot4
+          const uint32_t* cw = reinterpret_cast<const uint32_t*>(col);
+          const uint32_t* xw = reinterpret_cast<const uint32_t*>(s_x);
+          uint32_t d = 0;
+          for (int64_t q = j; q < rows / 4; q += L)
+            d = dot4_word<Dot4<T, Op, F>::kind>(d, cw[q], F::kHasX ? xw[q] : cw[q]);
+          acc = (T)d;
+        } else {
+          for (int64_t i = j; i < rows; i += L) acc = Op::combine(acc, F::apply(col[i], F::kHasX ? s_x[i] : col[i]));
+        }
+      } else {
+        for (int64_t i = j; i < rows; i += L) acc = Op::combine(acc, F::apply(col[i], F::kHasX ? s_x[i] : col[i]));
+      }
       acc = group_reduce<Op, L>(acc);
       if (j == 0) out[(c0 + c) * out_stride] = acc;
     }
@@ -463,7 +525,11 @@ int launch_flat_cols(const T* A, int64_t rows, int64_t cols, T* dst, int64_t ds,
   // column (one lane per column reads LDS bytes at the column stride, with
   // bank conflicts: 10 x 10^7 UInt8 vecmat 44.9 us at 1 lane, 37.6 at 2)
   int L = sizeof(T) == 1 && rows >= 4 ? 2 : 1;
-  while (L < kWave && (int64_t)L * kFlatRowsPerLane < rows) L <<= 1;
+  // UInt8 dot4 columns: rows counted in 4-row words
+  const int64_t units = Dot4<T, Op, F>::kind >= 0 && rows % 4 == 0 ? rows / 4 : rows;
+  const int per = units != rows ? kFlatWordsPerLane : kFlatRowsPerLane;
+  if (units != rows) L = 1;
+  while (L < kWave && (int64_t)L * per < units) L <<= 1;
 #define KF_FLAT(LL)                                                                                            \
   hipLaunchKernelGGL((reduce_cols_flat_kernel<T, Op, F, LL>), grid, dim3(kDimBlock), 0, stream, A, rows, cols, cpb, \
                      dst, ds, x, xs)
