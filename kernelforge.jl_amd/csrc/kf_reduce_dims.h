@@ -102,6 +102,38 @@ template <int K> __device__ inline uint32_t dot4_vec(uint32_t acc, uint4 a, uint
   return dot4_word<K>(acc, a.w, x.w);
 }
 
+// The same UInt8 sums by rows (dims=2, every byte of a vector its own row):
+// the even and odd bytes of each 32-bit word accumulate apart in packed
+// 16-bit lanes (v_pk_mad_u16: two rows per instruction); the low byte of
+// each 16-bit lane is the UInt8 (mod 256) result.
+typedef unsigned short kf_us2 __attribute__((ext_vector_type(2)));
+template <int K> __device__ inline void pk16_word(uint32_t& ae, uint32_t& ao, uint32_t a, uint32_t w16) {
+  const kf_us2 e = __builtin_bit_cast(kf_us2, a & 0x00ff00ffu);
+  const kf_us2 o = __builtin_bit_cast(kf_us2, (a >> 8) & 0x00ff00ffu);
+  kf_us2 E = __builtin_bit_cast(kf_us2, ae), O = __builtin_bit_cast(kf_us2, ao);
+  if constexpr (K == 0) {
+    E += e;
+    O += o;
+  } else if constexpr (K == 1) {
+    E += e * e;
+    O += o * o;
+  } else {
+    const kf_us2 w = __builtin_bit_cast(kf_us2, w16);
+    E += e * w;
+    O += o * w;
+  }
+  ae = __builtin_bit_cast(uint32_t, E);
+  ao = __builtin_bit_cast(uint32_t, O);
+}
+template <int K> __device__ inline void pk16_vec(uint32_t (&ae)[4], uint32_t (&ao)[4], uint4 a, uint32_t w16) {
+  pk16_word<K>(ae[0], ao[0], a.x, w16);
+  pk16_word<K>(ae[1], ao[1], a.y, w16);
+  pk16_word<K>(ae[2], ao[2], a.z, w16);
+  pk16_word<K>(ae[3], ao[3], a.w, w16);
+}
+// the four result bytes of one word: rows 0 and 2 from the even lanes, 1 and 3 from the odd
+__device__ inline uint32_t pk16_bytes(uint32_t ae, uint32_t ao) { return (ae & 0x00ff00ffu) | ((ao & 0x00ff00ffu) << 8); }
+
 constexpr int kDimBlock = 256;
 constexpr int kDimWaves = kDimBlock / kWave;
 constexpr int kDimUnroll = 4;
@@ -405,6 +437,80 @@ __global__ __launch_bounds__(kDimBlock) void reduce_cols_flat_kernel(const T* A,
   }
 }
 
+// UInt8 + by rows on dword-aligned columns (rows % 4 == 0) of the flat
+// path: thread t owns 32-bit word t % W of every column (rows 4w..4w+3, W =
+// rows / 4; words t, t + 256 when W > 256) and column phase t / W, and keeps
+// packed 16-bit accumulators (pk16_word); phases are added in order, then
+// turned into bytes.
+template <int K, bool X>
+__device__ inline void flat_rows_u8_words(const uint8_t* A, int64_t rows, int64_t cols, int64_t cpb, uint8_t* out,
+                                          int64_t out_stride, const uint8_t* xv, int64_t xs, uint4* s_blk,
+                                          uint8_t* s_x) {
+  constexpr int RW = 2;  // words per thread: rows <= kFlatMaxColBytes = 2048
+  const int tid = threadIdx.x;
+  const int W = (int)(rows / 4);
+  const int P = W <= kDimBlock ? kDimBlock / W : 1;
+  const int ph = W <= kDimBlock ? tid / W : 0;
+  const int w0 = W <= kDimBlock ? tid % W : tid;
+  const bool active = ph < P;
+  const uint32_t* sw = reinterpret_cast<const uint32_t*>(s_blk);
+  uint8_t* sb = reinterpret_cast<uint8_t*>(s_blk);
+  uint32_t ae[RW] = {}, ao[RW] = {};
+  const int64_t nblk = (cols + cpb - 1) / cpb;
+  for (int64_t b = blockIdx.x; b < nblk; b += gridDim.x) {
+    const int64_t c0 = b * cpb;
+    const int64_t nc = kmin<int64_t>(cpb, cols - c0);
+    const int64_t nel = nc * rows;
+    const int64_t nvec = nel / 16;
+    const uint4* src = reinterpret_cast<const uint4*>(A + c0 * rows);
+    uint4 v[kFlatVecs];
+#pragma unroll
+    for (int u = 0; u < kFlatVecs; ++u)
+      if (u * kDimBlock + tid < nvec) v[u] = ld_stream(src + u * kDimBlock + tid);
+    if constexpr (X)
+      for (int64_t c = tid; c < nc; c += kDimBlock) s_x[c] = xv[(c0 + c) * xs];
+#pragma unroll
+    for (int u = 0; u < kFlatVecs; ++u)
+      if (u * kDimBlock + tid < nvec) s_blk[u * kDimBlock + tid] = v[u];
+    const int64_t e0 = nvec * 16;
+    if (e0 + tid < nel) sb[e0 + tid] = A[c0 * rows + e0 + tid];
+    __syncthreads();
+    if (active) {
+      for (int64_t c = ph; c < nc; c += P) {
+        const uint32_t w16 = X ? 0x00010001u * (uint32_t)s_x[c] : 0u;
+#pragma unroll
+        for (int r = 0; r < RW; ++r) {
+          const int wi = w0 + r * kDimBlock;
+          if (wi < W) pk16_word<K>(ae[r], ao[r], sw[c * W + wi], w16);
+        }
+      }
+    }
+    __syncthreads();
+  }
+  // phases of word w: add the packed lanes in phase order, then to bytes
+  uint32_t* sp = reinterpret_cast<uint32_t*>(s_blk);
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    sp[(r * kDimBlock + tid) * 2] = ae[r];
+    sp[(r * kDimBlock + tid) * 2 + 1] = ao[r];
+  }
+  __syncthreads();
+  uint8_t* o = gridDim.x == 1 ? out : out + (int64_t)blockIdx.x * rows;
+  const int64_t os = gridDim.x == 1 ? out_stride : 1;
+  for (int wi = tid; wi < W; wi += kDimBlock) {
+    kf_us2 E = {0, 0}, O = {0, 0};
+    // word wi lives at thread q*W + wi of phase q (W <= 256), or at thread wi - r*256 of slot r
+    for (int q = 0; q < P; ++q) {
+      const int slot = W <= kDimBlock ? q * W + wi : wi;  // r * kDimBlock + thread
+      E += __builtin_bit_cast(kf_us2, sp[slot * 2]);
+      O += __builtin_bit_cast(kf_us2, sp[slot * 2 + 1]);
+    }
+    const uint32_t bytes = pk16_bytes(__builtin_bit_cast(uint32_t, E), __builtin_bit_cast(uint32_t, O));
+#pragma unroll
+    for (int k = 0; k < 4; ++k) o[(int64_t)(4 * wi + k) * os] = (uint8_t)(bytes >> (8 * k));
+  }
+}
+
 // dim = 2 counterpart for short contiguous columns: the same blocks of whole
 // columns through LDS; thread t owns row t % rows (rows t, t + 256, ... when
 // rows > 256) and column phase t / rows of every block, accumulating over
@@ -421,6 +527,12 @@ __global__ __launch_bounds__(kDimBlock) void reduce_rows_flat_kernel(const T* A,
   T* sb = reinterpret_cast<T*>(s_blk);
   const T id = Op::template identity<T>();
   const int tid = threadIdx.x;
+  if constexpr (Dot4<T, Op, F>::kind >= 0) {
+    if (rows % 4 == 0) {
+      flat_rows_u8_words<Dot4<T, Op, F>::kind, F::kHasX>(A, rows, cols, cpb, out, out_stride, xv, xs, s_blk, s_x);
+      return;
+    }
+  }
   const int P = rows <= kDimBlock ? kDimBlock / (int)rows : 1;  // column phases
   const int ph = rows <= kDimBlock ? tid / (int)rows : 0;
   const int i0 = rows <= kDimBlock ? tid % (int)rows : tid;
@@ -499,16 +611,36 @@ inline bool use_flat_cols(const void* A, int64_t rows, int64_t cs, size_t es, in
          flat_cols_per_block(es, rows) > 0;
 }
 
-constexpr int kFlatRowsMinSplit = 64;  // workgroups the dims=2 flat path needs from the plan
+constexpr int kFlatRowsMinSplit = 64;  // column splits of the plan that send dims=2 to the flat path
+constexpr int kFlatRowsMaxBlocks = 2048;
+constexpr int kFlatRowsMinBlocks = 256;
+constexpr int64_t kFlatRowsWgBytes = 64 << 10;
+// Workgroups of the dims=2 flat path (one partial rows-vector each): one per
+// kFlatRowsWgBytes of the matrix within [kFlatRowsMinBlocks,
+// kFlatRowsMaxBlocks], at most one per block of columns; the launch takes
+// the larger of this and the plan's column splits (1000 x 10^6 UInt8: 625
+// us at the plan's 512 workgroups, 205 at 2048; 10 x 10^6 Float32: 14.3 us
+// at the plan's 1220, 18.5 at 610 and 16.3 at 2048).
+inline int64_t flat_rows_grid(size_t es, int64_t rows, int64_t cols) {
+  const int64_t cpb = flat_cols_per_block(es, rows);
+  const int64_t want = kmin<int64_t>(kFlatRowsMaxBlocks,
+                                     kmax<int64_t>(kFlatRowsMinBlocks, rows * cols * (int64_t)es / kFlatRowsWgBytes));
+  return kmin<int64_t>((cols + cpb - 1) / cpb, want);
+}
 // The dims=2 flat path pays for the 8-byte types, and for the 4-byte types
 // whose rows are not a multiple of the vector width (the narrow kernel's
 // element path): n x 10^9/n matvec, n = 10, Float32 1052 -> 851 us, Float64
 // 1666 -> 1354; n = 100 Float64 1567 -> 1322, but Float32 (16-byte row units
 // in the narrow kernel) 706 -> 762, and UInt8, one LDS byte per element, lost
 // 10-40 % at every size.
-template <class T> inline bool use_flat_rows(const void* A, int64_t rows, int64_t cs, int64_t batch) {
+// UInt8 + (identity, abs2, x*y) over rows that are a multiple of 4 takes it
+// with packed 16-bit accumulators over 32-bit words (flat_rows_u8_words).
+template <class T, class Op, class F>
+inline bool use_flat_rows(const void* A, int64_t rows, int64_t cs, int64_t batch) {
   constexpr int64_t ev = 16 / (int64_t)sizeof(T);
-  return sizeof(T) >= 4 && (sizeof(T) == 8 || rows % ev != 0) && use_flat_cols(A, rows, cs, sizeof(T), batch);
+  const bool words = Dot4<T, Op, F>::kind >= 0 && rows % 4 == 0;
+  return (words || (sizeof(T) >= 4 && (sizeof(T) == 8 || rows % ev != 0))) &&
+         use_flat_cols(A, rows, cs, sizeof(T), batch);
 }
 
 template <class T, class Op, class F>
@@ -574,7 +706,40 @@ __global__ __launch_bounds__(kDimBlock) void reduce_rows_kernel(
   for (int u = 0; u < kRowVecs; ++u)
 #pragma unroll
     for (int e = 0; e < EPV; ++e) a[u][e] = id;
-  if constexpr (VEC) {
+  if constexpr (VEC && Dot4<T, Op, F>::kind >= 0) {
+    // UInt8 +: packed 16-bit accumulators (whole strips only, as below)
+    constexpr int K = Dot4<T, Op, F>::kind;
+    uint32_t ae[kRowVecs][4] = {}, ao[kRowVecs][4] = {};
+    const T* p = A + strip;
+    int64_t c = c0;
+    for (; c + kColUnroll <= c1; c += kColUnroll) {
+      uint4 r[kColUnroll][kRowVecs];
+#pragma unroll
+      for (int q = 0; q < kColUnroll; ++q)
+#pragma unroll
+        for (int u = 0; u < kRowVecs; ++u)
+          r[q][u] = ld_stream(reinterpret_cast<const uint4*>(p + (c + q) * col_stride) + u * kDimBlock + tid);
+#pragma unroll
+      for (int q = 0; q < kColUnroll; ++q) {
+        const uint32_t w16 = F::kHasX ? 0x00010001u * (uint32_t)xv[(c + q) * xs] : 0u;
+#pragma unroll
+        for (int u = 0; u < kRowVecs; ++u) pk16_vec<K>(ae[u], ao[u], r[q][u], w16);
+      }
+    }
+    for (; c < c1; ++c) {
+      const uint32_t w16 = F::kHasX ? 0x00010001u * (uint32_t)xv[c * xs] : 0u;
+#pragma unroll
+      for (int u = 0; u < kRowVecs; ++u)
+        pk16_vec<K>(ae[u], ao[u], ld_stream(reinterpret_cast<const uint4*>(p + c * col_stride) + u * kDimBlock + tid),
+                    w16);
+    }
+#pragma unroll
+    for (int u = 0; u < kRowVecs; ++u) {
+      const uint32_t wd[4] = {pk16_bytes(ae[u][0], ao[u][0]), pk16_bytes(ae[u][1], ao[u][1]),
+                              pk16_bytes(ae[u][2], ao[u][2]), pk16_bytes(ae[u][3], ao[u][3])};
+      __builtin_memcpy(a[u], wd, sizeof(wd));
+    }
+  } else if constexpr (VEC) {
   {  // vector launches cover whole strips only (the host splits off the rest)
     const T* p = A + strip;
     int64_t c = c0;
@@ -940,6 +1105,8 @@ inline size_t dim_query(size_t es, int64_t rows, int64_t cols, int dim, int64_t 
   if (dim == 2) {
     const int64_t ev = (int64_t)(16 / es);
     if (rows % ev == 0) b = kmax(b, dim2_vec_need(es, rows, cols, batch));
+    if (batch == 1 && rows * (int64_t)es <= kFlatMaxColBytes && flat_cols_per_block(es, rows) > 0)
+      b = kmax(b, round256((size_t)flat_rows_grid(es, rows, cols) * (size_t)rows * es));  // the flat path's partials
     for (int64_t h = 0; h < ev && h < rows; ++h) {
       const int64_t t = (rows - h) % ev;  // the tail a head of h rows leaves
       if (rows - h - t > 0 && (h > 0 || t > 0)) b = kmax(b, dim_need(es, rows, cols, 2, batch, {true, h, t}));
@@ -1008,13 +1175,16 @@ int launch_reduce_dim(const void* A, int64_t rows, int64_t cols, int64_t cs, int
                       const void* x = nullptr, int64_t xs = 0, int64_t dst_bstride = -1, bool may_peel = true) {
   if (dst_bstride < 0) dst_bstride = rows * ds;
   const DimVec dv = dim_vec(A, rows, cs, sizeof(T), dim, batch, a_bstride, F::kHasX, x, xs);
-  if (dim == 2 && !dv.head && !dv.tail && use_flat_rows<T>(A, rows, cs, batch)) {
+  if (dim == 2 && !dv.head && !dv.tail && use_flat_rows<T, Op, F>(A, rows, cs, batch)) {
     // short contiguous columns: the LDS-staged flat kernel, with as many
     // workgroups (and partial rows-vectors) as the plan's column splits
     const DimPlan pf = plan_dim(sizeof(T), rows, cols, 2, dv.vec, batch);
+    // workgroups: the plan's column splits or the flat grid, whichever is
+    // larger (the scratch query covers both partial sets)
     if (pf.split >= kFlatRowsMinSplit)
-      return launch_flat_rows<T, Op, F>((const T*)A, rows, cols, pf.split, (T*)scratch, (T*)dst, ds, (const T*)x, xs,
-                                        stream);
+      return launch_flat_rows<T, Op, F>((const T*)A, rows, cols,
+                                        (int)kmax<int64_t>(pf.split, flat_rows_grid(sizeof(T), rows, cols)),
+                                        (T*)scratch, (T*)dst, ds, (const T*)x, xs, stream);
   }
   if (may_peel && (dv.head || dv.tail)) {
     // element-path launches for the head and tail rows around the vector

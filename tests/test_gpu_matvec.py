@@ -150,7 +150,7 @@ def test_short_contiguous_columns_flat_path(kf, oracle, dev, dt):
                 assert np.array_equal(got, ref), (rows, cols, op)
 
 
-@pytest.mark.parametrize("dt", [np.int32, np.int64])
+@pytest.mark.parametrize("dt", [np.int32, np.int64, np.uint8])
 def test_short_contiguous_columns_flat_rows_path(kf, oracle, dev, dt):
     # dims=2 over contiguous matrices with columns of at most 2 KiB (8-byte
     # types, and 4-byte types whose rows are not a multiple of 4): blocks of
@@ -158,7 +158,10 @@ def test_short_contiguous_columns_flat_rows_path(kf, oracle, dev, dt):
     # workgroup and the split combine; matvec and plain mapreduce, exact
     rng = np.random.default_rng(89)
     es = np.dtype(dt).itemsize
-    for rows in (2, 3, 5, 10, 63, 255, 257, 2048 // es - 1, 2048 // es):
+    rows_set = (2, 3, 5, 10, 63, 255, 257, 2048 // es - 1, 2048 // es)
+    if dt == np.uint8:  # + over 32-bit words (packed 16-bit sums) when rows % 4 == 0
+        rows_set = (4, 8, 12, 100, 252, 1000, 1020, 1028, 2044, 2048, 10)
+    for rows in rows_set:
         for cols in (1000, 40_003, 1_000_003 // rows):
             buf = mk(rng, dt, rows * cols)
             A = torch.from_numpy(buf).to(dev).as_strided((rows, cols), (1, rows))
@@ -171,3 +174,6 @@ def test_short_contiguous_columns_flat_rows_path(kf, oracle, dev, dt):
                 got = kf.mapreduce(kf.identity, op, A, dims=2).cpu().numpy().reshape(-1)
                 ref = (M.astype(np.int64).sum(axis=0).astype(dt) if op == "+" else M.max(axis=0))
                 assert np.array_equal(got, ref), (rows, cols, op)
+            got = kf.mapreduce(kf.abs2, "+", A, dims=2).cpu().numpy().reshape(-1)
+            ref = (M.astype(np.int64) ** 2).sum(axis=0).astype(dt)
+            assert np.array_equal(got, ref), (rows, cols, "abs2")
