@@ -36,6 +36,57 @@ template <class T, class Op> __device__ inline T block_reduce(T x, T* s_wave) {
 
 // Two-operand element maps: reduce2 (dot product, squared distance and the
 // asymmetric maps) and the matvec / vecmat operand map.
+// v_dot4_u32_u8 folds: K 0 = sum of the four bytes, 1 = sum of their
+// squares, 2 = dot product with the operand's four bytes. The low byte of a
+// 32-bit sum of UInt8 terms is their mod-256 (Julia UInt8) sum.
+template <int K> __device__ inline uint32_t dot4_word(uint32_t acc, uint32_t a, uint32_t x) {
+  return __builtin_amdgcn_udot4(a, K == 0 ? 0x01010101u : K == 1 ? a : x, acc, false);
+}
+template <int K> __device__ inline uint32_t dot4_vec(uint32_t acc, uint4 a, uint4 x) {
+  acc = dot4_word<K>(acc, a.x, x.x);
+  acc = dot4_word<K>(acc, a.y, x.y);
+  acc = dot4_word<K>(acc, a.z, x.z);
+  return dot4_word<K>(acc, a.w, x.w);
+}
+
+// Per-lane fold of 16-byte vectors of T for the 1-D reductions: one
+// accumulator per element slot, combined in slot order at the end; UInt8 +
+// over identity or abs2 keeps one 32-bit dot4 sum instead (four bytes per
+// instruction rather than sixteen byte operations per vector).
+template <class T, class Op, class Map> struct VecFold {
+  static constexpr int EPV = 16 / (int)sizeof(T);
+  static constexpr int K = !__is_same(T, uint8_t) || !__is_same(Op, OpAdd) ? -1
+                           : __is_same(Map, MapIdentity)                  ? 0
+                           : __is_same(Map, MapAbs2)                      ? 1
+                                                                          : -1;
+  T a[K >= 0 ? 1 : EPV];
+  uint32_t d = 0;
+  __device__ VecFold() {
+#pragma unroll
+    for (int e = 0; e < (K >= 0 ? 1 : EPV); ++e) a[e] = Op::template identity<T>();
+  }
+  __device__ void add(uint4 r) {
+    if constexpr (K >= 0) {
+      d = dot4_vec<K>(d, r, r);
+    } else {
+      T x[EPV];
+      __builtin_memcpy(x, &r, 16);
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) a[e] = Op::combine(a[e], Map::apply(x[e]));
+    }
+  }
+  __device__ T total() const {
+    if constexpr (K >= 0) {
+      return (T)d;
+    } else {
+      T acc = a[0];
+#pragma unroll
+      for (int e = 1; e < EPV; ++e) acc = Op::combine(acc, a[e]);
+      return acc;
+    }
+  }
+};
+
 struct Map2Mul {
   static constexpr bool kHasX = true;
   template <class T> __device__ static T apply(T a, T b) { return a * b; }

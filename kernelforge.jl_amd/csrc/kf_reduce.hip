@@ -201,7 +201,6 @@ __global__ __launch_bounds__(kRedBlock) void reduce_once_kernel(const T* src, in
                                                                 int64_t nvec, T* out, uint64_t* fold_hdr) {
   constexpr int EPV = 16 / (int)sizeof(T);
   __shared__ T s_wave[kRedWaves];
-  const T id = Op::template identity<T>();
   const int tid = threadIdx.x;
   const uint4* v = reinterpret_cast<const uint4*>(src + head);
   const int64_t base = (int64_t)blockIdx.x * (kRedBlock * U) + tid;
@@ -209,20 +208,11 @@ __global__ __launch_bounds__(kRedBlock) void reduce_once_kernel(const T* src, in
 #pragma unroll
   for (int u = 0; u < U; ++u)
     if (base + u * kRedBlock < nvec) r[u] = ld_stream(v + base + u * kRedBlock);
-  T a[EPV];
-#pragma unroll
-  for (int e = 0; e < EPV; ++e) a[e] = id;
+  VecFold<T, Op, Map> f;
 #pragma unroll
   for (int u = 0; u < U; ++u)
-    if (base + u * kRedBlock < nvec) {
-      T x[EPV];
-      __builtin_memcpy(x, &r[u], 16);
-#pragma unroll
-      for (int e = 0; e < EPV; ++e) a[e] = Op::combine(a[e], Map::apply(x[e]));
-    }
-  T acc = a[0];
-#pragma unroll
-  for (int e = 1; e < EPV; ++e) acc = Op::combine(acc, a[e]);
+    if (base + u * kRedBlock < nvec) f.add(r[u]);
+  T acc = f.total();
   if (blockIdx.x == 0) {
     const int64_t tail0 = head + nvec * EPV;
     if (tid < head) acc = Op::combine(acc, Map::apply(src[tid]));
@@ -256,26 +246,18 @@ __global__ __launch_bounds__(kRedBlock) void reduce_chunk_kernel(const T* src, i
                                                                  int64_t chunk, T* out, uint64_t* fold_hdr) {
   constexpr int EPV = 16 / (int)sizeof(T);
   __shared__ T s_wave[kRedWaves];
-  const T id = Op::template identity<T>();
   const int tid = threadIdx.x;
   const uint4* v = reinterpret_cast<const uint4*>(src + head);
   const int64_t b0 = (int64_t)blockIdx.x * chunk;
   const int64_t b1 = kmin<int64_t>(nvec, b0 + chunk);
-  T a[EPV];
-#pragma unroll
-  for (int e = 0; e < EPV; ++e) a[e] = id;
+  VecFold<T, Op, Map> f;
   int64_t i = b0 + tid;
   for (; i + (int64_t)(U - 1) * kRedBlock < b1; i += (int64_t)U * kRedBlock) {
     uint4 r[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) r[u] = ld_stream(v + i + u * kRedBlock);
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      T x[EPV];
-      __builtin_memcpy(x, &r[u], 16);
-#pragma unroll
-      for (int e = 0; e < EPV; ++e) a[e] = Op::combine(a[e], Map::apply(x[e]));
-    }
+    for (int u = 0; u < U; ++u) f.add(r[u]);
   }
   if (i < b1) {  // the partial last round: fewer than U vectors per lane
     uint4 r[U];
@@ -283,18 +265,10 @@ __global__ __launch_bounds__(kRedBlock) void reduce_chunk_kernel(const T* src, i
     for (int u = 0; u < U; ++u)
       if (i + u * kRedBlock < b1) r[u] = ld_stream(v + i + u * kRedBlock);
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if (i + u * kRedBlock < b1) {
-        T x[EPV];
-        __builtin_memcpy(x, &r[u], 16);
-#pragma unroll
-        for (int e = 0; e < EPV; ++e) a[e] = Op::combine(a[e], Map::apply(x[e]));
-      }
-    }
+    for (int u = 0; u < U; ++u)
+      if (i + u * kRedBlock < b1) f.add(r[u]);
   }
-  T acc = a[0];
-#pragma unroll
-  for (int e = 1; e < EPV; ++e) acc = Op::combine(acc, a[e]);
+  T acc = f.total();
   if (blockIdx.x == 0) {
     const int64_t tail0 = head + nvec * EPV;
     if (tid < head) acc = Op::combine(acc, Map::apply(src[tid]));

@@ -92,15 +92,6 @@ template <> struct Dot4<uint8_t, OpAdd, Unary<MapAbs2>> {
 template <> struct Dot4<uint8_t, OpAdd, Map2Mul> {
   static constexpr int kind = 2;  // dot product with the operand
 };
-template <int K> __device__ inline uint32_t dot4_word(uint32_t acc, uint32_t a, uint32_t x) {
-  return __builtin_amdgcn_udot4(a, K == 0 ? 0x01010101u : K == 1 ? a : x, acc, false);
-}
-template <int K> __device__ inline uint32_t dot4_vec(uint32_t acc, uint4 a, uint4 x) {
-  acc = dot4_word<K>(acc, a.x, x.x);
-  acc = dot4_word<K>(acc, a.y, x.y);
-  acc = dot4_word<K>(acc, a.z, x.z);
-  return dot4_word<K>(acc, a.w, x.w);
-}
 
 // The same UInt8 sums by rows (dims=2, every byte of a vector its own row):
 // the even and odd bytes of each 32-bit word accumulate apart in packed
