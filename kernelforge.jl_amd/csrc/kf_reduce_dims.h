@@ -630,7 +630,8 @@ template <class T, class Op, class F>
 inline bool use_flat_rows(const void* A, int64_t rows, int64_t cs, int64_t batch) {
   constexpr int64_t ev = 16 / (int64_t)sizeof(T);
   const bool words = Dot4<T, Op, F>::kind >= 0 && rows % 4 == 0;
-  return (words || (sizeof(T) >= 4 && (sizeof(T) == 8 || rows % ev != 0))) &&
+  // (rows >= 2: each block's slice of x must fit the kernel's LDS for it)
+  return rows >= 2 && (words || (sizeof(T) >= 4 && (sizeof(T) == 8 || rows % ev != 0))) &&
          use_flat_cols(A, rows, cs, sizeof(T), batch);
 }
 
