@@ -278,6 +278,76 @@ __global__ __launch_bounds__(kRedBlock) void reduce_chunk_kernel(const T* src, i
   fold_partial<T, Op>(part, out, fold_hdr, s_wave);
 }
 
+// Strided views with short strides (stride * sizeof(T) <= kStrideVecBytes,
+// e.g. x[1:2:end]): every 128-byte line of the view's span holds elements of
+// the view, so HBM reads the whole span either way. Stream the span with
+// 16-byte loads instead of element loads, combining only the elements at
+// span offsets that are multiples of the stride. kFoldMax persistent
+// workgroups over contiguous chunks (whole rounds but the last), folded in
+// the same launch; workgroup 0 folds in the head (up to the first 128-byte
+// line) and the tail of the span. The vector holding span offset q keeps the
+// elements e with (q + e) % stride == 0: a bit pattern of period `stride`,
+// shifted by the vector's residue, which each lane advances by a constant
+// per vector instead of dividing.
+constexpr int kStrideVecBytes = 32;
+constexpr int kStrideUnroll = 8;
+template <class T, class Op, class Map>
+__global__ __launch_bounds__(kRedBlock) void reduce_stride_kernel(const T* src, int64_t span, int stride,
+                                                                  int64_t head, int64_t nvec, int64_t chunk, T* out,
+                                                                  uint64_t* fold_hdr) {
+  constexpr int EPV = 16 / (int)sizeof(T);
+  constexpr int U = kStrideUnroll;
+  __shared__ T s_wave[kRedWaves];
+  const T id = Op::template identity<T>();
+  const int tid = threadIdx.x;
+  const uint4* v = reinterpret_cast<const uint4*>(src + head);
+  const int64_t b0 = (int64_t)blockIdx.x * chunk;
+  const int64_t b1 = kmin<int64_t>(nvec, b0 + chunk);
+  // bits e = 0, stride, 2*stride, ... below EPV
+  uint32_t pat = 0;
+  for (int e = 0; e < EPV; e += stride) pat |= 1u << e;
+  // residue of the span offset of this lane's vectors, and its steps
+  int rr = (int)((head + (b0 + tid) * (int64_t)EPV) % stride);
+  const int step_u = (int)(((int64_t)kRedBlock * EPV) % stride);
+  const int step_round = (int)(((int64_t)U * kRedBlock * EPV) % stride);
+  T a[EPV];
+#pragma unroll
+  for (int e = 0; e < EPV; ++e) a[e] = id;
+  for (int64_t i = b0 + tid; i < b1; i += (int64_t)U * kRedBlock) {
+    uint4 r[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (i + u * kRedBlock < b1) r[u] = ld_stream(v + i + u * kRedBlock);
+    int q = rr;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (i + u * kRedBlock < b1) {
+        const uint32_t m = pat << (q == 0 ? 0 : stride - q);
+        T x[EPV];
+        __builtin_memcpy(x, &r[u], 16);
+#pragma unroll
+        for (int e = 0; e < EPV; ++e)
+          if ((m >> e) & 1u) a[e] = Op::combine(a[e], Map::apply(x[e]));
+      }
+      q += step_u;
+      if (q >= stride) q -= stride;
+    }
+    rr += step_round;
+    if (rr >= stride) rr -= stride;
+  }
+  T acc = a[0];
+#pragma unroll
+  for (int e = 1; e < EPV; ++e) acc = Op::combine(acc, a[e]);
+  if (blockIdx.x == 0) {
+    // head: span offsets [0, head); tail: [head + nvec * EPV, span)
+    if (tid < head && tid % stride == 0) acc = Op::combine(acc, Map::apply(src[tid]));
+    const int64_t t = head + nvec * EPV + tid;
+    if (t < span && t % stride == 0) acc = Op::combine(acc, Map::apply(src[t]));
+  }
+  const T part = block_reduce<T, Op>(acc, s_wave);
+  fold_partial<T, Op>(part, out, fold_hdr, s_wave);
+}
+
 // Full reduction, stage 2: one 1024-thread workgroup combines `count`
 // partials; each thread issues all of its (at most kRedMaxBlocks/1024) loads
 // before combining, so the stage costs about one memory latency.
@@ -400,6 +470,24 @@ int launch_reduce(const void* src, int64_t n, int64_t stride, void* dst, void* s
                   hipStream_t stream) {
   constexpr int EPV = 16 / (int)sizeof(T);
   uint8_t* work = (uint8_t*)red_work(scratch);
+  if (stride != 1 && n > 1 && stride * (int64_t)sizeof(T) <= kStrideVecBytes) {
+    const int64_t span = (n - 1) * stride + 1;
+    const int64_t head = kmin<int64_t>(span, (int64_t)(((kHeadAlign - ((uintptr_t)src & (kHeadAlign - 1))) &
+                                                        (kHeadAlign - 1)) / sizeof(T)));
+    const int64_t nvec = (span - head) / EPV;
+    constexpr int64_t kRound = (int64_t)kStrideUnroll * kRedBlock;
+    const int64_t grid = kmax<int64_t>(1, kmin<int64_t>(kFoldMax, (nvec + kRound - 1) / kRound));
+    const int64_t chunk = ((nvec + grid - 1) / grid + kRound - 1) / kRound * kRound;
+    if (grid == 1) {
+      // one workgroup: its partial is the result (no fold)
+      hipLaunchKernelGGL((reduce_kernel<T, Op, Map>), dim3(1), dim3(kRedBlock), 0, stream, (const T*)src, n, stride,
+                         (T*)dst, 0);
+      return kf_check_launch("reduce_kernel");
+    }
+    hipLaunchKernelGGL((reduce_stride_kernel<T, Op, Map>), dim3((unsigned)grid), dim3(kRedBlock), 0, stream,
+                       (const T*)src, span, (int)stride, head, nvec, chunk, (T*)dst, (uint64_t*)scratch);
+    return kf_check_launch("reduce_stride_kernel");
+  }
   if (stride != 1) {
     const int grid = reduce_grid<T>(n);
     T* out = grid == 1 ? (T*)dst : (T*)work;

@@ -122,6 +122,33 @@ def test_views_and_strides(kf, oracle, dev):
         assert kf.mapreduce(kf.abs2, "+", src[sl], g=np.sqrt) == pytest.approx(np.sqrt((v * v).sum()), rel=1e-12)
 
 
+@pytest.mark.parametrize("dt", [np.int32, np.uint8, np.int64, np.float32])
+def test_short_stride_views_vector_path(kf, oracle, dev, dt):
+    # strided 1-D views whose stride spans at most 32 bytes stream the whole
+    # span with 16-byte loads and combine the elements at multiples of the
+    # stride: every stride up to that, start offsets that put the 128-byte
+    # head at every phase, lengths from a single element to several
+    # persistent rounds, + (integers exact) and max
+    rng = np.random.default_rng(97)
+    es = np.dtype(dt).itemsize
+    for stride in range(2, 32 // es + 1):
+        for n in (1, 2, 3, 40, 1000, 65_537, 3_000_001 // stride):
+            for off in (0, 1, 5):
+                flat = (rng.integers(0, 256, n * stride + off + 1).astype(dt) if dt != np.float32 else
+                        (rng.random(n * stride + off + 1) < 0.25).astype(dt))
+                t = torch.from_numpy(flat).to(dev)
+                v = flat[off:off + (n - 1) * stride + 1:stride]
+                assert v.shape[0] == n
+                got = kf.mapreduce(kf.identity, "+", t[off:off + (n - 1) * stride + 1:stride])
+                ref = v.astype(np.int64).sum()
+                if dt == np.float32:
+                    assert got == float(ref), (stride, n, off)  # sparse 0/1: exact in any order
+                else:
+                    assert int(got) == int(np.array(ref).astype(dt)), (stride, n, off)
+                assert kf.mapreduce(kf.identity, max, t[off:off + (n - 1) * stride + 1:stride]) == v.max(), \
+                    (stride, n, off)
+
+
 def test_full_reduce_of_2d_and_3d(kf, dev):
     # reference test/tests/mapreduce/mapreduce_test.jl:9-28
     rng = np.random.default_rng(41)
