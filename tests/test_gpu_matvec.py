@@ -177,3 +177,44 @@ def test_short_contiguous_columns_flat_rows_path(kf, oracle, dev, dt):
             got = kf.mapreduce(kf.abs2, "+", A, dims=2).cpu().numpy().reshape(-1)
             ref = (M.astype(np.int64) ** 2).sum(axis=0).astype(dt)
             assert np.array_equal(got, ref), (rows, cols, "abs2")
+
+
+@pytest.mark.parametrize("dt", [np.int32, np.uint8, np.int64])
+def test_flat_paths_with_strided_x_and_dst(kf, oracle, dev, dt):
+    # the LDS-staged dims kernels with an every-other-element x and an
+    # every-third-element destination (vecmat!: dims=1; matvec!: dims=2)
+    rng = np.random.default_rng(101)
+    for rows, cols in ((4, 50_003), (10, 30_001), (100, 4_001), (256, 2_003)):
+        buf = mk(rng, dt, rows * cols)
+        A = torch.from_numpy(buf).to(dev).as_strided((rows, cols), (1, rows))
+        for dim, m, k in ((1, cols, rows), (2, rows, cols)):
+            xb = mk(rng, dt, 2 * k)
+            x = torch.from_numpy(xb).to(dev)[::2]
+            dbuf = torch.zeros(3 * m, dtype=A.dtype, device=dev)
+            d = dbuf[::3]
+            if dim == 1:
+                kf.vecmat_(operator.mul, "+", d, x, A)
+            else:
+                kf.matvec_(operator.mul, "+", d, A, x)
+            ref = oracle.reduce_dim_x(buf, rows, cols, rows, np.ascontiguousarray(xb[::2]), dim, "+", "mul")
+            assert np.array_equal(d.cpu().numpy(), ref), (rows, cols, dim)
+            assert not dbuf.cpu().numpy()[1::3].any() and not dbuf.cpu().numpy()[2::3].any()
+
+
+@pytest.mark.parametrize("dt", [np.int32, np.float64])
+def test_batched_middle_dims_many_splits(kf, dev, dt):
+    # mapreducedims over the middle dim of a Julia pre x mid x post array with
+    # few rows and long reduced dims: the batched narrow kernel splits the
+    # reduced columns and the many-wave combine folds every batch entry
+    rng = np.random.default_rng(103)
+    for pre, mid, post in ((40, 20_000, 3), (70, 9_001, 5), (20, 30_000, 2)):
+        a = mk(rng, dt, (post, mid, pre))  # numpy C order == Julia pre x mid x post
+        x = torch.from_numpy(a).to(dev).permute(2, 1, 0)
+        got = kf.mapreduce(kf.identity, "+", x, dims=2).cpu().numpy()
+        ref = a.astype(np.float64 if dt == np.float64 else np.int64).sum(axis=1)  # post x pre
+        ref = np.ascontiguousarray(ref.T)[:, None, :]
+        if dt == np.float64:
+            assert np.allclose(got.reshape(pre, 1, post), ref, rtol=1e-12, atol=1e-9), (pre, mid, post)
+        else:
+            assert np.array_equal(got.reshape(pre, 1, post).astype(np.int64), ref.astype(dt).astype(np.int64)), \
+                (pre, mid, post)
