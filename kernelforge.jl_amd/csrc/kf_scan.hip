@@ -24,7 +24,9 @@
 //    the descriptor of tile (t - 64 + j) for the last `win` lanes, so
 //    lane order is tile order and a DPP scan combines the window in the
 //    order a non-commutative op needs (lookback_all, for fully resident
-//    grids, gives each lane a contiguous chunk of predecessors instead).
+//    grids, gives each lane a contiguous chunk of predecessors instead, and
+//    for up to 2 * BLOCK + 1 resident tiles every wave of the workgroup
+//    reads a share, the waves' folds combined through LDS).
 //  * Each tile descriptor owns a 128-byte line (kDescWords words): tiles are
 //    published from different XCDs, and packing several descriptors per line
 //    made those writers and the pollers contend for one line (measured: 5.0
@@ -165,8 +167,27 @@ constexpr uint32_t kFlagPollMask = 1023;   // a waiting lookback re-reads the gi
 // 8 lost 5 % at 10^7 Float32.
 constexpr int kAllChunk = 4;
 template <class T> constexpr bool kLookAllFor = sizeof(T) <= 4;
-inline int look_window(int64_t ntiles, int64_t resident, int64_t tile_bytes, bool look_all) {
-  if (ntiles <= resident) return look_all && ntiles <= (int64_t)kWave * kAllChunk + 1 ? 0 : kWave;
+// Grids of up to BLOCK * kBlockChunk + 1 tiles, all resident, let every
+// wave of the workgroup read a share of the predecessors (window code -1):
+// one poll round where lookback_all does not apply (more than 257 tiles,
+// or 8-byte types, which keep its registers out of their kernels).
+// Measured with HIP graphs, us, 64-tile window -> whole workgroup: UInt8
+// 3*10^6 7.2 -> 6.5, 5*10^6 8.5 -> 7.5, 10^7 9.9 -> 9.0; Float64 10^6 8.9 ->
+// 8.1, 1.6*10^6 10.1 -> 9.4; affine pairs 10^6 9.0 -> 8.2; Float32 2*10^6
+// 7.3 -> 7.0. Only for tiles of at most 2 vectors per lane (4 for the
+// 8-byte types): 4-vector UInt8 tiles lost 7 % (2*10^7 13.2 -> 14.1 us,
+// 3*10^7 16.0 -> 17.1), their longer loads overlapping more of the
+// workgroup-wide polling.
+constexpr int kBlockChunk = 2;
+template <class T, int BLOCK, int VPL>
+constexpr bool kLookBlockFor = sizeof(T) <= 8 && VPL <= (sizeof(T) == 8 ? 4 : 2);
+inline int look_window(int64_t ntiles, int64_t resident, int64_t tile_bytes, bool look_all, bool look_block,
+                       int block) {
+  if (ntiles <= resident) {
+    if (look_all && ntiles <= (int64_t)kWave * kAllChunk + 1) return 0;
+    if (look_block && ntiles <= (int64_t)block * kBlockChunk + 1) return -1;
+    return kWave;
+  }
   if (tile_bytes >= (128 << 10) && ntiles > 4 * resident) return 2;
   if (tile_bytes <= (64 << 10)) return 8;
   return 4;
@@ -290,20 +311,22 @@ __device__ inline T lookback(const uint64_t* desc, int64_t tile, uint32_t epoch3
   }
 }
 
-// Lookback when every tile of the grid is resident at once: lane L reads
-// the descriptors of its contiguous chunk [L*c, L*c + c) of all `tile`
-// predecessors (c <= CH) with every load in flight together, folds them in
-// tile order (restarting at a PREFIX), and an ordered wave reduction from
-// the newest lane holding a PREFIX gives the exclusive prefix; a lane
-// whose chunk still holds an unpublished descriptor re-reads it.
+// Lookback when every tile of the grid is resident at once, by P readers
+// (one wave: P = 64; the whole workgroup: P = BLOCK): reader `idx` reads the
+// descriptors of its contiguous chunk [idx*c, idx*c + c) of all `tile`
+// predecessors (c <= CH) with every load in flight together and folds them
+// in tile order (restarting at a PREFIX); a reader whose chunk still holds
+// an unpublished descriptor re-reads it. Returns, for the calling wave, the
+// ordered fold from its newest lane holding a PREFIX (from lane 0 if none
+// does) in `out`, and whether any of its lanes holds one.
 template <class T, class Op, int CH>
-__device__ inline T lookback_all(const uint64_t* desc, int64_t tile, uint32_t epoch30, uint32_t limit,
-                                 bool& gave_up) {
+__device__ inline bool lookback_all_wave(const uint64_t* desc, int64_t tile, uint32_t epoch30, uint32_t limit,
+                                         bool& gave_up, int64_t idx, int64_t P, T& out) {
   constexpr int W = ScanShape<T>::W;
   const int lane = lane_id();
   const T id = Op::template identity<T>();
-  const int64_t c = (tile + kWave - 1) / kWave;
-  const int64_t t0 = (int64_t)lane * c;
+  const int64_t c = (tile + P - 1) / P;
+  const int64_t t0 = idx * c;
   const int cnt = (int)kmax<int64_t>(0, kmin<int64_t>(c, tile - t0));
   T val = id;
   bool has_prefix = false;
@@ -354,7 +377,17 @@ __device__ inline T lookback_all(const uint64_t* desc, int64_t tile, uint32_t ep
   }
   const uint64_t pm = __builtin_amdgcn_ballot_w64(has_prefix);
   const int m = pm ? 63 - __builtin_clzll(pm) : 0;
-  return wave_reduce<Op>(lane >= m ? val : id);
+  out = wave_reduce<Op>(lane >= m ? val : id);
+  return pm != 0;
+}
+
+// One wave's lookback_all: the exclusive prefix of `tile`.
+template <class T, class Op, int CH>
+__device__ inline T lookback_all(const uint64_t* desc, int64_t tile, uint32_t epoch30, uint32_t limit,
+                                 bool& gave_up) {
+  T out;
+  lookback_all_wave<T, Op, CH>(desc, tile, epoch30, limit, gave_up, lane_id(), kWave, out);
+  return out;
 }
 
 // Byte-wise a + b (mod 256 in every byte) of four packed bytes.
@@ -457,6 +490,8 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
   constexpr int kScanWaves = BLOCK / kWave;
   __shared__ T wave_agg[kScanWaves];
   __shared__ T wave_pre[kScanWaves];
+  __shared__ T s_look_val[kLookBlockFor<T, BLOCK, VPL> ? kScanWaves : 1];
+  __shared__ int s_look_pre[kLookBlockFor<T, BLOCK, VPL> ? kScanWaves : 1];
   __shared__ uint64_t s_ticket;
   __shared__ int s_stop;
   constexpr bool kLdsRows = kLdsRowsFor<Op, V>;
@@ -575,6 +610,12 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
   // ---- publish, look back, publish the inclusive prefix (wave 0) ----------
   // Lane w of wave 0 holds wave w's aggregate; a DPP scan over those lanes
   // gives the tile aggregate and every wave's exclusive prefix in the tile.
+  // With win < 0 every wave of the workgroup reads a share of the
+  // predecessors (lookback_all_wave) and wave 0 combines the waves' folds.
+  const bool look_block = kLookBlockFor<T, BLOCK, VPL> && win < 0;
+  T wexcl = id, agg = id, excl = id;
+  bool gave_up = false;
+  const bool pub = tile != withhold;
   if (wave == 0) {
     if constexpr (kStashForLookback<T, BLOCK>) {
       // park wave 0's tile in LDS so the lookback's registers do not add to
@@ -588,22 +629,40 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
     }
     const T wagg = lane < kScanWaves ? wave_agg[lane] : id;
     const T wincl = wave_inclusive_scan<Op>(wagg);
-    const T wexcl = wave_shift_right<Op>(wincl);
-    const T agg = read_lane(wincl, kScanWaves - 1);
-    T excl = id;
-    bool gave_up = false;
-    const bool pub = tile != withhold;
-    if (tile == 0) {
-      if (lane == 0 && pub) publish(desc, tile, (epoch30 << 2) | kStatePrefix, agg);
-    } else {
-      if (lane == 0 && pub) publish(desc, tile, (epoch30 << 2) | kStatePartial, agg);
+    wexcl = wave_shift_right<Op>(wincl);
+    agg = read_lane(wincl, kScanWaves - 1);
+    if (lane == 0 && pub) publish(desc, tile, (epoch30 << 2) | (tile == 0 ? kStatePrefix : kStatePartial), agg);
+  }
+  if constexpr (kLookBlockFor<T, BLOCK, VPL>) {
+    if (look_block) {
+      if (tile > 0) {
+        T wv;
+        const bool wp = lookback_all_wave<T, Op, kBlockChunk>(desc, tile, epoch30, limit, gave_up, tid, BLOCK, wv);
+        if (lane == 0) {
+          s_look_val[wave] = wv;
+          s_look_pre[wave] = (wp ? 1 : 0) | (gave_up ? 2 : 0);
+        }
+      }
+      __syncthreads();
+      if (wave == 0 && tile > 0) {
+        const int f = lane < kScanWaves ? s_look_pre[lane] : 0;
+        gave_up = __builtin_amdgcn_ballot_w64((f & 2) != 0) != 0;
+        const uint64_t pm = __builtin_amdgcn_ballot_w64((f & 1) != 0);
+        const int m = pm ? 63 - __builtin_clzll(pm) : 0;
+        excl = wave_reduce<Op>(lane >= m && lane < kScanWaves ? s_look_val[lane] : id);
+      }
+    }
+  }
+  if (wave == 0) {
+    if (tile > 0 && !look_block) {
       if constexpr (kLookAllFor<T>)
         excl = win == 0 ? lookback_all<T, Op, kAllChunk>(desc, tile, epoch30, limit, gave_up)
                         : lookback<T, Op>(desc, tile, epoch30, win, limit, gave_up);
       else
         excl = lookback<T, Op>(desc, tile, epoch30, win, limit, gave_up);
-      if (lane == 0 && pub && !gave_up) publish(desc, tile, (epoch30 << 2) | kStatePrefix, Op::combine(excl, agg));
     }
+    if (tile > 0 && lane == 0 && pub && !gave_up)
+      publish(desc, tile, (epoch30 << 2) | kStatePrefix, Op::combine(excl, agg));
     // next call's epoch, once every tile has read this one (the last tile's
     // completed lookback implies it); not after a give-up, which leaves the
     // buffer to the status query or a reset
@@ -781,12 +840,14 @@ void launch_scan_tier(const void* src, int64_t ss, void* dst, int64_t ds, int64_
   if (mode & 1) {
     constexpr auto kernel = scan_kernel<T, Op, Map, true, B, V>;
     hipLaunchKernelGGL(kernel, dim3((unsigned)ntiles), dim3(B), 0, stream, (const T*)src, ss, (T*)dst, ds, n,
-                       ntiles, (uint64_t*)scratch, vec, off, look_window(ntiles, resident_tiles<kernel>(B), (int64_t)B * V * kVecBytes<T>, kLookAllFor<T>), post,
+                       ntiles, (uint64_t*)scratch, vec, off, look_window(ntiles, resident_tiles<kernel>(B), (int64_t)B * V * kVecBytes<T>, kLookAllFor<T>,
+                                   kLookBlockFor<T, B, V>, B), post,
                        g_spin_limit, g_withhold);
   } else {
     constexpr auto kernel = scan_kernel<T, Op, Map, false, B, V>;
     hipLaunchKernelGGL(kernel, dim3((unsigned)ntiles), dim3(B), 0, stream, (const T*)src, ss, (T*)dst, ds, n,
-                       ntiles, (uint64_t*)scratch, vec, off, look_window(ntiles, resident_tiles<kernel>(B), (int64_t)B * V * kVecBytes<T>, kLookAllFor<T>), post,
+                       ntiles, (uint64_t*)scratch, vec, off, look_window(ntiles, resident_tiles<kernel>(B), (int64_t)B * V * kVecBytes<T>, kLookAllFor<T>,
+                                   kLookBlockFor<T, B, V>, B), post,
                        g_spin_limit, g_withhold);
   }
 }

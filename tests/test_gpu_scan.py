@@ -487,7 +487,9 @@ def test_post_map_g_in_the_store(kf, oracle, dev, exclusive):
 
 
 # ---- the lookback's give-up path, forced from the host -----------------------
-@pytest.mark.parametrize("n", [300_000, 3_000_000])  # all tiles resident / windowed lookback
+# one wave reads all predecessors / every wave of the workgroup reads a share /
+# more tiles than the GPU holds at once (64-tile windows)
+@pytest.mark.parametrize("n", [300_000, 3_000_000, 30_000_000])
 def test_lookback_giveup_is_raised_by_the_kernel(kf, oracle, dev, n):
     # kf_debug_scan_giveup makes tile 3 never publish and gives every
     # lookback a budget of 4096 polls: the tile after it gives up, raises the
@@ -525,6 +527,33 @@ def test_lookback_giveup_is_raised_by_the_kernel(kf, oracle, dev, n):
         assert L.kf_debug_scan_giveup(-1, 0) == 0
     kf.scan_("+", dst, src, tmp=tmp, check=True)
     assert np.array_equal(dst.cpu().numpy(), oracle.scan(x, "+"))
+
+
+# ---- grids of 258..2049 resident tiles: the workgroup-wide lookback -----------
+@pytest.mark.parametrize("dt,n", [(np.uint8, 3_000_007), (np.uint8, 10**7), (np.int32, 2_500_001),
+                                  (np.int64, 10**6 + 3), (np.int64, 1_600_000), (np.float64, 2 * 10**6)])
+def test_workgroup_wide_lookback(kf, oracle, dev, dt, n):
+    rng = np.random.default_rng(n)
+    x = gen(rng, dt, n)
+    src = torch.from_numpy(x).to(dev)
+    for excl in (False, True):
+        got = kf.scan("+", src, exclusive=excl).cpu().numpy()
+        ref = oracle.scan(x, "+", exclusive=excl)
+        if dt == np.float64:
+            assert np.allclose(got, ref, rtol=1e-12, atol=1e-9), (n, excl)
+        else:
+            assert np.array_equal(got, ref), (dt, n, excl)
+
+
+@pytest.mark.parametrize("n", [10**6, 1_500_001])
+def test_affine_workgroup_wide_lookback(kf, oracle, dev, n):
+    # the affine pairs are not commutative: the waves' shares of the
+    # predecessors must be combined in tile order
+    rng = np.random.default_rng(n)
+    ab = np.stack([rng.uniform(0.9, 1.0, n), rng.standard_normal(n)], 1).astype(np.float32)
+    for exclusive in (False, True):
+        got = kf.scan(kf.affine, torch.from_numpy(ab).to(dev), exclusive=exclusive).cpu().numpy()
+        assert_mixed(got, oracle.scan(ab, "affine", exclusive=exclusive), 1e-5, what=f"affine n={n} excl={exclusive}")
 
 
 # ---- source and destination misaligned differently ---------------------------
