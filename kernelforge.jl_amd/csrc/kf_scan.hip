@@ -216,6 +216,13 @@ __device__ inline uint4x2 ld_vec(const uint4x2* p) {
   return uint4x2{ld_stream_u(q), ld_stream_u(q + 1)};
 }
 __device__ inline void st_vec(uint4* p, uint4 v) { st_stream(p, v); }
+// Cached (temporal) accesses of a whole unit, for the blocked layout, where
+// one instruction touches every V-th unit and the lane's next instruction
+// the units between: the line must stay in the cache in between.
+__device__ inline uint4x2 ld_unit_cached(const uint4x2* p) { return *p; }
+__device__ inline uint4 ld_unit_cached(const uint4* p) { return *p; }
+__device__ inline void st_unit_cached(uint4x2* p, uint4x2 v) { *p = v; }
+__device__ inline void st_unit_cached(uint4* p, uint4 v) { *p = v; }
 __device__ inline void st_vec(uint4x2* p, uint4x2 v) {
   uint4* q = reinterpret_cast<uint4*>(p);
   st_stream(q, v.lo);
@@ -413,7 +420,11 @@ template <class T> __device__ inline T post_apply(int post, T v) {
   if constexpr (__is_same(T, f32x2) || is_quat<T>) {
     return v;
   } else if constexpr (__is_same(T, float)) {
-    return post == KF_POST_SQRT ? __builtin_sqrtf(v) : v * v;
+    // v_sqrt_f32 (within 1 ulp) rather than the correctly rounded
+    // expansion: the scanned values themselves carry reassociation error
+    // far above 1 ulp, and the expansion's VALU work in the store phase
+    // cost 12 % of a 2^28 scan
+    return post == KF_POST_SQRT ? __builtin_amdgcn_sqrtf(v) : v * v;
   } else if constexpr (__is_same(T, double)) {
     return post == KF_POST_SQRT ? __builtin_sqrt(v) : v * v;
   } else {
@@ -472,6 +483,24 @@ __device__ inline T wave_row_prefixes(const T (&t)[V], T* a, int lane) {
 // per-row DPP scans are already one fused instruction per step.
 constexpr int kRowsViaLds = 4;
 template <class Op, int V> constexpr bool kLdsRowsFor = __is_same(Op, OpAffine) && V >= kRowsViaLds;
+// Elements of 16 bytes or more (one element per lane unit: the
+// quaternions) take a blocked layout instead of the striped one: lane l
+// holds units l*V .. l*V + V-1 of its wave's chunk, scans them serially in
+// registers, and one wave scan over the lane totals follows. Striped, every
+// 64-element row needed its own 6-step wave scan (6 of the 16-product
+// combines per element); blocked, about 2 to 3.5. The loads of one
+// instruction then stride V units and the V instructions of a lane cover
+// its contiguous chunk, so these accesses go through the cache (temporal
+// loads and stores) and every line is still read from HBM once. Measured
+// (HIP graphs, 2^26 quaternions): QuaternionF32 897 -> 608 us, Float64
+// 1916 -> 1874 us (nontemporal accesses in this layout: 1580 / 2335 us).
+// Both stay bound by their combine chains at one or two workgroups per CU
+// (QuaternionF32 at 8 units per lane, one workgroup per CU: 675 us;
+// Float64 quaternions at 512 threads: 2343 us).
+template <class T> constexpr bool kBlockedFor = ScanShape<T>::EPV == 1;
+template <class T, int V> __device__ inline int unit_slot(int j, int lane) {
+  return kBlockedFor<T> ? lane * V + j : j * kWave + lane;
+}
 
 template <class T, class Op, class Map, bool EXCL, int BLOCK, int VPL>
 __global__ __launch_bounds__(BLOCK) void scan_kernel(
@@ -533,7 +562,8 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
   if (full) {
     const Vec* g = reinterpret_cast<const Vec*>(srcv + wbase);
 #pragma unroll
-    for (int j = 0; j < V; ++j) r[j] = ld_vec(g + j * kWave + lane);
+    for (int j = 0; j < V; ++j)
+      r[j] = kBlockedFor<T> ? ld_unit_cached(g + unit_slot<T, V>(j, lane)) : ld_vec(g + unit_slot<T, V>(j, lane));
     if constexpr (!__is_same(Map, MapIdentity)) {
 #pragma unroll
       for (int j = 0; j < V; ++j) {
@@ -554,13 +584,14 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
     bool inside[V];
 #pragma unroll
     for (int j = 0; j < V; ++j) {
-      const int64_t e0 = wbase + (int64_t)(j * kWave + lane) * EPV - off;  // real index of element 0
+      const int64_t e0 = wbase + (int64_t)unit_slot<T, V>(j, lane) * EPV - off;  // real index of element 0
       inside[j] = vec && e0 >= 0 && e0 + EPV <= n;
-      if (inside[j]) r[j] = ld_vec(g + j * kWave + lane);
+      if (inside[j])
+        r[j] = kBlockedFor<T> ? ld_unit_cached(g + unit_slot<T, V>(j, lane)) : ld_vec(g + unit_slot<T, V>(j, lane));
     }
 #pragma unroll
     for (int j = 0; j < V; ++j) {
-      const int64_t e0 = wbase + (int64_t)(j * kWave + lane) * EPV - off;
+      const int64_t e0 = wbase + (int64_t)unit_slot<T, V>(j, lane) * EPV - off;
       T x[EPV];
       if (inside[j]) {
         __builtin_memcpy(x, &r[j], sizeof(Vec));
@@ -580,24 +611,41 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
 
   // ---- in-lane and wave scans; rowpre[j] = everything in the wave before
   // vector j's lane (earlier rows and earlier lanes of row j) --------------
-  // (with kLdsRows the prefixes stay in s_rows until the store phase)
+  // (with kLdsRows the prefixes stay in s_rows until the store phase;
+  // blocked: r[j] becomes the lane's inclusive scan and rowpre[0] the
+  // lane's exclusive prefix in the wave)
   T carry = id;
-  T rowpre[V];
+  T rowpre[kBlockedFor<T> ? 1 : V];
   T tot[V];
+  if constexpr (kBlockedFor<T>) {
+    T run;
+    __builtin_memcpy(&run, &r[0], sizeof(T));
 #pragma unroll
-  for (int j = 0; j < V; ++j) {
-    T x[EPV];
-    __builtin_memcpy(x, &r[j], sizeof(Vec));
+    for (int j = 1; j < V; ++j) {
+      T x;
+      __builtin_memcpy(&x, &r[j], sizeof(T));
+      run = Op::combine(run, x);
+      __builtin_memcpy(&r[j], &run, sizeof(T));
+    }
+    const T incl = wave_inclusive_scan<Op>(run);
+    rowpre[0] = wave_shift_right<Op>(incl);
+    carry = read_lane(incl, kWave - 1);
+  } else {
 #pragma unroll
-    for (int k = 1; k < EPV; ++k) x[k] = Op::combine(x[k - 1], x[k]);
-    __builtin_memcpy(&r[j], x, sizeof(Vec));
-    pin_packed<T>(r[j]);
-    if constexpr (kLdsRows) {
-      tot[j] = x[EPV - 1];
-    } else {
-      const T incl = wave_inclusive_scan<Op>(x[EPV - 1]);
-      rowpre[j] = Op::combine(carry, wave_shift_right<Op>(incl));
-      carry = Op::combine(carry, read_lane(incl, kWave - 1));
+    for (int j = 0; j < V; ++j) {
+      T x[EPV];
+      __builtin_memcpy(x, &r[j], sizeof(Vec));
+#pragma unroll
+      for (int k = 1; k < EPV; ++k) x[k] = Op::combine(x[k - 1], x[k]);
+      __builtin_memcpy(&r[j], x, sizeof(Vec));
+      pin_packed<T>(r[j]);
+      if constexpr (kLdsRows) {
+        tot[j] = x[EPV - 1];
+      } else {
+        const T incl = wave_inclusive_scan<Op>(x[EPV - 1]);
+        rowpre[j] = Op::combine(carry, wave_shift_right<Op>(incl));
+        carry = Op::combine(carry, read_lane(incl, kWave - 1));
+      }
     }
   }
   if constexpr (kLdsRows) carry = wave_row_prefixes<T, Op, V>(tot, s_rows[wave], lane);
@@ -707,25 +755,44 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
     }
     T x[EPV], o[EPV];
     __builtin_memcpy(x, &r[j], sizeof(Vec));
-    const T p = Op::combine(prefix, rowpre[j]);
-    if constexpr (EXCL) {
-      o[0] = p;
-#pragma unroll
-      for (int k = 1; k < EPV; ++k) o[k] = Op::combine(p, x[k - 1]);
-      if (j == 0 && tile == 0 && tid == 0) o[off] = exclusive_first<T, Op>();  // element 0
+    if constexpr (kBlockedFor<T>) {
+      // r[j] holds the lane's inclusive scan up to unit j
+      const T p = Op::combine(prefix, rowpre[0]);
+      if constexpr (EXCL) {
+        if (j == 0) {
+          o[0] = (tile == 0 && tid == 0) ? exclusive_first<T, Op>() : p;  // element 0
+        } else {
+          T prev;
+          __builtin_memcpy(&prev, &r[j - 1], sizeof(T));
+          o[0] = Op::combine(p, prev);
+        }
+      } else {
+        o[0] = Op::combine(p, x[0]);
+      }
     } else {
+      const T p = Op::combine(prefix, rowpre[j]);
+      if constexpr (EXCL) {
+        o[0] = p;
 #pragma unroll
-      for (int k = 0; k < EPV; ++k) o[k] = Op::combine(p, x[k]);
+        for (int k = 1; k < EPV; ++k) o[k] = Op::combine(p, x[k - 1]);
+        if (j == 0 && tile == 0 && tid == 0) o[off] = exclusive_first<T, Op>();  // element 0
+      } else {
+#pragma unroll
+        for (int k = 0; k < EPV; ++k) o[k] = Op::combine(p, x[k]);
+      }
     }
     if (post != KF_POST_IDENTITY) {  // the reference's g, applied at the store only
 #pragma unroll
       for (int k = 0; k < EPV; ++k) o[k] = post_apply(post, o[k]);
     }
-    const int64_t e0 = wbase + (int64_t)(j * kWave + lane) * EPV - off;  // real index of element 0
+    const int64_t e0 = wbase + (int64_t)unit_slot<T, V>(j, lane) * EPV - off;  // real index of element 0
     if (full || (vec && e0 >= 0 && e0 + EPV <= n)) {
       Vec w;
       __builtin_memcpy(&w, o, sizeof(Vec));
-      st_vec(reinterpret_cast<Vec*>(dstv + wbase) + j * kWave + lane, w);
+      if constexpr (kBlockedFor<T>)
+        st_unit_cached(reinterpret_cast<Vec*>(dstv + wbase) + unit_slot<T, V>(j, lane), w);
+      else
+        st_vec(reinterpret_cast<Vec*>(dstv + wbase) + unit_slot<T, V>(j, lane), w);
     } else {
 #pragma unroll
       for (int k = 0; k < EPV; ++k) {

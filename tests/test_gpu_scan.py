@@ -167,6 +167,27 @@ def test_quaternion_scan_q8_exact(kf, oracle, dev, dt):
     assert np.array_equal(kf.scan("*", t).cpu().numpy().astype(np.float64), oracle.scan(q[::3], "*"))
 
 
+@pytest.mark.parametrize("dt", [np.float32, np.float64])
+def test_quaternion_scan_every_compiled_shape(kf, oracle, dev, dt):
+    # the quaternion tiles (lane l holding units l*V .. l*V + V-1 of its
+    # wave's chunk) at every compiled shape, around one tile and over more
+    # tiles than the GPU holds at once; exact on the group {+-1, +-i, +-j, +-k}
+    import operator
+    probe = torch.from_numpy(q8_sequence(np.random.default_rng(0), 1, dt)).to(dev)
+    shapes = sorted({kf.scan_shape(probe, "*", Nitem=v, workgroup=1024) for v in (1, 2, 4, 8)})
+    assert shapes == ([(1024, 1), (1024, 2), (1024, 4)] if dt == np.float32 else [(1024, 1), (1024, 2)])
+    rng = np.random.default_rng(47)
+    for threads, items in shapes:
+        tile = threads * items
+        for n in (tile - 1, tile + 1, 3 * tile + 5, 700 * tile + 7):
+            q = q8_sequence(rng, n, dt)
+            t = torch.from_numpy(q).to(dev)
+            for exclusive in (False, True):
+                got = kf.scan(operator.mul, t, exclusive=exclusive, Nitem=items, workgroup=threads).cpu().numpy()
+                assert np.array_equal(got.astype(np.float64), oracle.scan(q, "*", exclusive=exclusive)), \
+                    (threads, items, n, exclusive)
+
+
 @pytest.mark.parametrize("dt,n", [(np.float64, 10**6), (np.float32, 10**4)])
 def test_quaternion_scan_reference_case(kf, oracle, dev, dt, n):
     # reference test/tests/scan/scan_test.jl:22-33: scan!(identity, *, dst,
