@@ -218,3 +218,40 @@ def test_batched_middle_dims_many_splits(kf, dev, dt):
         else:
             assert np.array_equal(got.reshape(pre, 1, post).astype(np.int64), ref.astype(dt).astype(np.int64)), \
                 (pre, mid, post)
+
+
+@pytest.mark.parametrize("dt", [np.uint8, np.int32, np.float32, np.float64])
+def test_few_long_columns(kf, dev, dt):
+    # 2..16 long columns along dims=1: every workgroup reads all columns of
+    # its row range and the operand x once (one or many row ranges; rows off
+    # the 16-byte vector length leave a tail; a strided destination)
+    rng = np.random.default_rng(107)
+    for rows, cols in ((600, 16), (777_777, 2), (100_003, 7), (2**20 + 3, 16), (50_001, 9), (4_000_000, 10)):
+        if np.dtype(dt).kind == "f":
+            a = rng.random((cols, rows)).astype(dt)
+            xv = rng.random(rows).astype(dt)
+        else:
+            a = rng.integers(0, 256 if dt == np.uint8 else 100, (cols, rows)).astype(dt)
+            xv = rng.integers(0, 256 if dt == np.uint8 else 100, rows).astype(dt)
+        A = torch.from_numpy(a).to(dev).T                      # rows x cols, column-major
+        x = torch.from_numpy(xv).to(dev)
+        a64 = a.astype(np.float64 if np.dtype(dt).kind == "f" else np.int64)
+        x64 = xv.astype(a64.dtype)
+        dbuf = torch.zeros(3 * cols, dtype=A.dtype, device=dev)
+        d = dbuf.as_strided((1, cols), (3 * cols, 3))
+        kf.mapreduce_(kf.identity, "+", d, A, dims=1)
+        got_sum = dbuf[::3].cpu().numpy()
+        got_max = kf.mapreduce(kf.identity, max, A, dims=1).cpu().numpy().reshape(-1)
+        got_vm = kf.vecmat(operator.mul, "+", x, A).cpu().numpy()
+        ref_sum, ref_vm = a64.sum(axis=1), (a64 * x64[None, :]).sum(axis=1)
+        assert np.array_equal(got_max, a.max(axis=1)), (rows, cols)
+        if np.dtype(dt).kind == "f":
+            tol = 1e-5 if dt == np.float32 else 1e-12
+            assert np.allclose(got_sum, ref_sum, rtol=tol), (rows, cols)
+            assert np.allclose(got_vm, ref_vm, rtol=tol), (rows, cols)
+        else:
+            m = 256 if dt == np.uint8 else 2**32
+            wrap = lambda v: (v % m).astype(np.uint64 if dt == np.uint8 else np.int64)
+            assert np.array_equal(wrap(got_sum.astype(np.int64)), wrap(ref_sum)), (rows, cols)
+            assert np.array_equal(wrap(got_vm.astype(np.int64)), wrap(ref_vm)), (rows, cols)
+        assert not dbuf.cpu().numpy()[1::3].any()
