@@ -140,6 +140,7 @@ constexpr int kDim2FewStrips = 64;
 // column) that still gives kDim2Blocks workgroups; columns in flight per
 // thread for each strip width.
 constexpr int kDim2MaxRowVecs = 8;
+constexpr int kDim2MaxRowVecsU8 = 2;
 constexpr int kColUnrollRv1 = 16;
 constexpr int kColUnrollRv2 = 8;
 constexpr int kColUnrollRv4 = 4;
@@ -892,6 +893,72 @@ __global__ __launch_bounds__(kDimBlock) void reduce_rows_kernel(
 }
 
 
+// dim = 2 over few columns (2..kFewMaxCols, rows a multiple of the vector
+// width, 16-byte aligned columns) of matrices up to kFewMaxBytes: thread i
+// reads vector i of every column in one batch of loads and stores one
+// output vector, grid-stride over the rows. The strip kernel above carries
+// at most kColUnroll columns of loads per pass and takes the remainder one
+// column at a time (10 columns at 8 vectors per thread: 4, 4, 1, 1).
+// Measured (HIP graphs, us, strip kernel -> this): matvec 10^6 x 10 Float32
+// 11.5 -> 9.6, Float64 21.2 -> 15.8, UInt8 10.9 -> 8.0; 10^7 x 10 Float32
+// 85.8 -> 80.7, Float64 156 -> 146, UInt8 31.1 -> 25.4. Larger matrices
+// stream better through the strips, whose threads read 1-2 KiB runs per
+// column (10^8 x 10 Float32 771 us there, 893 here), and UInt8 x*y keeps its
+// 16 packed operands in VGPRs (129, 3 waves per SIMD): up to 32 MiB only.
+constexpr int kFewMaxCols = 16;
+constexpr int kFewBlocks = 4096;
+constexpr int64_t kFewMaxBytes = 512LL << 20;
+constexpr int64_t kFewMaxBytesU8X = 32LL << 20;
+template <class T, class Op, class F>
+__global__ __launch_bounds__(kDimBlock) void reduce_rows_few_kernel(
+    const T* A, int64_t rows, int cols, int64_t col_stride, T* out, int64_t out_stride, const T* xv, int64_t xs) {
+  constexpr int EPV = 16 / (int)sizeof(T);
+  constexpr int C = kFewMaxCols;
+  constexpr int K = Dot4<T, Op, F>::kind;
+  const T id = Op::template identity<T>();
+  T w[C];
+#pragma unroll
+  for (int c = 0; c < C; ++c) w[c] = F::kHasX && c < cols ? xv[c * xs] : id;
+  const int64_t nv = rows / EPV;
+  for (int64_t i = (int64_t)blockIdx.x * kDimBlock + threadIdx.x; i < nv; i += (int64_t)gridDim.x * kDimBlock) {
+    uint4 r[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c)
+      if (c < cols) r[c] = ld_stream(reinterpret_cast<const uint4*>(A + c * col_stride) + i);
+    T a[EPV];
+    if constexpr (K >= 0) {
+      // UInt8 +: packed 16-bit accumulators, two rows per instruction
+      uint32_t ae[4] = {}, ao[4] = {};
+#pragma unroll
+      for (int c = 0; c < C; ++c)
+        if (c < cols) pk16_vec<K>(ae, ao, r[c], F::kHasX ? 0x00010001u * (uint32_t)w[c] : 0u);
+      const uint32_t wd[4] = {pk16_bytes(ae[0], ao[0]), pk16_bytes(ae[1], ao[1]), pk16_bytes(ae[2], ao[2]),
+                              pk16_bytes(ae[3], ao[3])};
+      __builtin_memcpy(a, wd, sizeof(wd));
+    } else {
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) a[e] = id;
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+        if (c >= cols) continue;
+        T x[EPV];
+        __builtin_memcpy(x, &r[c], 16);
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) a[e] = Op::combine(a[e], F::apply(x[e], w[c]));
+      }
+    }
+    T* o = out + i * EPV * out_stride;
+    if (out_stride == 1 && (uintptr_t)o % 16 == 0) {
+      uint4 v;
+      __builtin_memcpy(&v, a, sizeof(v));
+      *reinterpret_cast<uint4*>(o) = v;
+    } else {
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) o[e * out_stride] = a[e];
+    }
+  }
+}
+
 // dim = 2, narrow matrices (at most kDimBlock row units: 16-byte vectors
 // when VEC, i.e. rows % EPV == 0 and aligned columns, else elements): the
 // workgroup is split into P = kDimBlock / units column phases; thread
@@ -1075,6 +1142,15 @@ inline DimPlan plan_dim(size_t es, int64_t rows, int64_t cols, int dim, bool vec
           break;
         }
       }
+    }
+    if (vec) {
+      // UInt8: at most 2 vectors per thread (10^7 x 100 matvec 199 -> 180
+      // us, 1000 x 10^6 at 8 and 4 vectors 242 / 230 against 174); few
+      // columns (larger than reduce_rows_few_kernel takes): one vector per
+      // thread, more strips in flight (10^8 x 10 Float32 826 -> 771 us,
+      // Float64 1676 -> 1544)
+      if (es == 1) rv = kmin(rv, kDim2MaxRowVecsU8);
+      if (cols <= kFewMaxCols) rv = es == 1 ? kmin(rv, 2) : 1;
     }
     p.row_vecs = rv;
     const int cu = vec ? col_unroll_for(rv) : kColUnrollDefault;
@@ -1269,6 +1345,15 @@ int launch_reduce_dim(const void* A, int64_t rows, int64_t cols, int64_t cs, int
     return rc;
   }
   const bool vec = dv.vec;
+  if (dim == 2 && vec && batch <= 1 && cols <= kFewMaxCols && rows % (int64_t)(16 / sizeof(T)) == 0 &&
+      row_units(sizeof(T), rows, true) > kDimBlock &&
+      rows * cols * (int64_t)sizeof(T) <= (Dot4<T, Op, F>::kind == 2 ? kFewMaxBytesU8X : kFewMaxBytes)) {
+    const int64_t nv = rows / (int64_t)(16 / sizeof(T));
+    const unsigned grid = (unsigned)kmin<int64_t>((nv + kDimBlock - 1) / kDimBlock, kFewBlocks);
+    hipLaunchKernelGGL((reduce_rows_few_kernel<T, Op, F>), dim3(grid), dim3(kDimBlock), 0, stream, (const T*)A,
+                       rows, (int)cols, cs, (T*)dst, ds, (const T*)x, xs);
+    return kf_check_launch("reduce_rows_few_kernel");
+  }
   const DimPlan p = plan_dim(sizeof(T), rows, cols, dim, vec, batch);
   if (dim == 2 && vec && !p.narrow) {
     // the vector kernel takes whole strips only; the rest is launched under

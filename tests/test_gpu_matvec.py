@@ -255,3 +255,40 @@ def test_few_long_columns(kf, dev, dt):
             assert np.array_equal(wrap(got_sum.astype(np.int64)), wrap(ref_sum)), (rows, cols)
             assert np.array_equal(wrap(got_vm.astype(np.int64)), wrap(ref_vm)), (rows, cols)
         assert not dbuf.cpu().numpy()[1::3].any()
+
+
+@pytest.mark.parametrize("dt", [np.uint8, np.int32, np.float32, np.float64])
+def test_few_columns_dims2(kf, dev, dt):
+    # 2..16 columns along dims=2 (matvec and mapreducedims): one batch of
+    # loads over every column per output vector; rows off the vector width
+    # (peeled head/tail rows), a strided destination, UInt8 packed sums
+    rng = np.random.default_rng(109)
+    for rows, cols in ((4096, 16), (1_000_000, 10), (300_003, 3), (2**20, 2), (77_777, 7)):
+        if np.dtype(dt).kind == "f":
+            a = rng.random((cols, rows)).astype(dt)
+            xv = rng.random(cols).astype(dt)
+        else:
+            a = rng.integers(0, 256 if dt == np.uint8 else 100, (cols, rows)).astype(dt)
+            xv = rng.integers(0, 256 if dt == np.uint8 else 100, cols).astype(dt)
+        A = torch.from_numpy(a).to(dev).T                      # rows x cols, column-major
+        x = torch.from_numpy(xv).to(dev)
+        a64 = a.astype(np.float64 if np.dtype(dt).kind == "f" else np.int64)
+        x64 = xv.astype(a64.dtype)
+        dbuf = torch.zeros(2 * rows, dtype=A.dtype, device=dev)
+        d = dbuf.as_strided((rows, 1), (2, 2 * rows))
+        kf.mapreduce_(kf.identity, "+", d, A, dims=2)
+        got_sum = dbuf[::2].cpu().numpy()
+        got_sq = kf.mapreduce(kf.abs2, "+", A, dims=2).cpu().numpy().reshape(-1)
+        got_max = kf.mapreduce(kf.identity, max, A, dims=2).cpu().numpy().reshape(-1)
+        got_mv = kf.matvec(operator.mul, "+", A, x).cpu().numpy()
+        ref_sum, ref_sq, ref_mv = a64.sum(axis=0), (a64 * a64).sum(axis=0), (a64 * x64[:, None]).sum(axis=0)
+        assert np.array_equal(got_max, a.max(axis=0)), (rows, cols)
+        if np.dtype(dt).kind == "f":
+            tol = 1e-5 if dt == np.float32 else 1e-12
+            for g_, r_ in ((got_sum, ref_sum), (got_sq, ref_sq), (got_mv, ref_mv)):
+                assert np.allclose(g_, r_, rtol=tol), (rows, cols)
+        else:
+            m = 256 if dt == np.uint8 else 2**32
+            for g_, r_ in ((got_sum, ref_sum), (got_sq, ref_sq), (got_mv, ref_mv)):
+                assert np.array_equal(g_.astype(np.int64) % m, r_ % m), (rows, cols)
+        assert not dbuf.cpu().numpy()[1::2].any()
