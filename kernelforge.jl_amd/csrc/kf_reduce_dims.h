@@ -263,6 +263,11 @@ __global__ __launch_bounds__(kDimBlock) void reduce_cols_kernel(
 // accumulator per column and lane; waves combine through LDS into
 // partials[s*cols + c] (or dst when one workgroup covers the rows).
 constexpr int kMultiMaxCols = 16;
+constexpr int kMultiBlocks = 2048;
+// below this the wave per column stays ahead (10^6 x 10 vecmat Float32 11.9
+// against 12.9 us, Float64 21.4 / 23.2, UInt8 7.0 / 8.5; 10^7 x 10 UInt8
+// 26.7 against 24.6)
+constexpr int64_t kMultiMinBytes = 80LL << 20;
 template <class T, class Op, class F>
 __global__ __launch_bounds__(kDimBlock) void reduce_cols_multi_kernel(
     const T* A, int64_t rows, int cols, int64_t col_stride, T* out, int64_t out_stride, int64_t seg, const T* xv) {
@@ -463,6 +468,9 @@ constexpr int kFlatMaxColBytes = 2048;                         // longest column
 // -> 843 us, Float64 1924 -> 1812 us, 100 x 10^7 Float32 720 -> 664 us; 8K
 // to 64K workgroups in between)
 constexpr int kFlatMaxBlocks = 1 << 24;
+// UInt8 blocks are grid-strided over 16K workgroups: 1000 x 10^6 vecmat 241
+// us at one block each, 188 at 16K, 181 at 4K; 100 x 10^7 183 / 164 / 175
+constexpr int kFlatMaxBlocksU8 = 16384;
 constexpr int kFlatRowsPerLane = 16;
 constexpr int kFlatWordsPerLane = 8;  // UInt8 dot4 columns
 template <class T, class Op, class F, int L>
@@ -736,7 +744,7 @@ int launch_flat_cols(const T* A, int64_t rows, int64_t cols, T* dst, int64_t ds,
                      hipStream_t stream) {
   const int64_t cpb = flat_cols_per_block(sizeof(T), rows);
   const int64_t nblk = (cols + cpb - 1) / cpb;
-  const dim3 grid((unsigned)kmin<int64_t>(nblk, kFlatMaxBlocks));
+  const dim3 grid((unsigned)kmin<int64_t>(nblk, sizeof(T) == 1 ? kFlatMaxBlocksU8 : kFlatMaxBlocks));
   // about kFlatRowsPerLane rows per lane; UInt8 takes at least 2 lanes per
   // column (one lane per column reads LDS bytes at the column stride, with
   // bank conflicts: 10 x 10^7 UInt8 vecmat 44.9 us at 1 lane, 37.6 at 2)
@@ -1074,6 +1082,7 @@ struct DimPlan {
   int seg_lanes;   // dim 1: lanes per column of reduce_cols_seg_kernel (0: one wave per column)
   bool narrow;     // dim 2: reduce_rows_narrow_kernel
   bool unit_vec;   // seg / narrow kernels: 16-byte units (rows % EPV == 0, aligned columns)
+  int multi_split; // dim 1, at most kMultiMaxCols columns: workgroups of reduce_cols_multi_kernel
   size_t partial_bytes;
 };
 
@@ -1127,6 +1136,12 @@ inline DimPlan plan_dim(size_t es, int64_t rows, int64_t cols, int dim, bool vec
         S = kmin<int64_t>(S, narrow2 ? kDimMaxSplitNarrow : kDimMaxSplit);
       }
       p.split = (int)S;
+      if (vec && cols <= kMultiMaxCols && rows * cols * (int64_t)es >= kMultiMinBytes) {
+        // one vector per thread up to kMultiBlocks workgroups (10^6 x 10
+        // Float32 vecmat: 14.6 us at the wave-per-column split's 244)
+        const int64_t nv = rows / epv;
+        p.multi_split = (int)kmax<int64_t>(1, kmin<int64_t>(kMultiBlocks, (nv + kDimBlock - 1) / kDimBlock));
+      }
     }
   } else if (row_units(es, rows, vec) <= kDimBlock) {
     // Narrow: one strip covers every row; column ranges fill the GPU.
@@ -1186,7 +1201,8 @@ inline DimPlan plan_dim(size_t es, int64_t rows, int64_t cols, int dim, bool vec
     }
     p.split = (int)S;
   }
-  if (p.split > 1) p.partial_bytes = round256((size_t)p.split * (size_t)(dim == 1 ? cols : rows) * es * (size_t)nb);
+  const int64_t parts = kmax<int64_t>(p.split, p.multi_split);
+  if (parts > 1) p.partial_bytes = round256((size_t)parts * (size_t)(dim == 1 ? cols : rows) * es * (size_t)nb);
   return p;
 }
 
@@ -1424,10 +1440,13 @@ int launch_reduce_dim(const void* A, int64_t rows, int64_t cols, int64_t cs, int
     int64_t seg = (rows + p.split - 1) / p.split;
     seg = (seg + EPV - 1) / EPV * EPV;
     if constexpr (F::kHasX) {
-      if (vec && cols <= kMultiMaxCols) {
-        hipLaunchKernelGGL((reduce_cols_multi_kernel<T, Op, F>), dim3((unsigned)p.split), dim3(kDimBlock), 0, stream,
-                           (const T*)A, rows, (int)cols, cs, out, ds, seg, (const T*)x);
-        if (p.split > 1) launch_combine<T, Op>((const T*)scratch, p.split, cols, (T*)dst, ds, 0, 1, stream);
+      if (p.multi_split > 0) {
+        const int S = p.multi_split;
+        int64_t mseg = (rows + S - 1) / S;
+        mseg = (mseg + EPV - 1) / EPV * EPV;
+        hipLaunchKernelGGL((reduce_cols_multi_kernel<T, Op, F>), dim3((unsigned)S), dim3(kDimBlock), 0, stream,
+                           (const T*)A, rows, (int)cols, cs, S > 1 ? (T*)scratch : (T*)dst, ds, mseg, (const T*)x);
+        if (S > 1) launch_combine<T, Op>((const T*)scratch, S, cols, (T*)dst, ds, 0, 1, stream);
         return kf_check_launch("reduce_cols_multi_kernel");
       }
     }

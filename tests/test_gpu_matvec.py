@@ -226,7 +226,9 @@ def test_few_long_columns(kf, dev, dt):
     # its row range and the operand x once (one or many row ranges; rows off
     # the 16-byte vector length leave a tail; a strided destination)
     rng = np.random.default_rng(107)
-    for rows, cols in ((600, 16), (777_777, 2), (100_003, 7), (2**20 + 3, 16), (50_001, 9), (4_000_000, 10)):
+    # (matrices from 80 MiB take the one-workgroup-for-all-columns kernel)
+    extra = [(10_000_003, 10)] if dt == np.uint8 else []
+    for rows, cols in [(600, 16), (777_777, 2), (100_003, 7), (2**20 + 3, 16), (50_001, 9), (4_000_000, 10)] + extra:
         if np.dtype(dt).kind == "f":
             a = rng.random((cols, rows)).astype(dt)
             xv = rng.random(rows).astype(dt)
