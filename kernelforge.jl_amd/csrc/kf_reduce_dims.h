@@ -468,9 +468,10 @@ constexpr int kFlatMaxColBytes = 2048;                         // longest column
 // -> 843 us, Float64 1924 -> 1812 us, 100 x 10^7 Float32 720 -> 664 us; 8K
 // to 64K workgroups in between)
 constexpr int kFlatMaxBlocks = 1 << 24;
-// UInt8 blocks are grid-strided over 16K workgroups: 1000 x 10^6 vecmat 241
-// us at one block each, 188 at 16K, 181 at 4K; 100 x 10^7 183 / 164 / 175
-constexpr int kFlatMaxBlocksU8 = 16384;
+// UInt8 blocks are grid-strided over 16K workgroups, 4K from 256 rows:
+// 1000 x 10^6 vecmat 241 us at one block each, 188 at 16K, 181 at 4K;
+// 1000 x 10^5 25.3 / 22.7 at 16K / 4K; 100 x 10^7 183 / 164 / 175
+constexpr int kFlatMaxBlocksU8 = 16384, kFlatMaxBlocksU8Long = 4096;
 constexpr int kFlatRowsPerLane = 16;
 constexpr int kFlatWordsPerLane = 8;  // UInt8 dot4 columns
 template <class T, class Op, class F, int L>
@@ -744,7 +745,8 @@ int launch_flat_cols(const T* A, int64_t rows, int64_t cols, T* dst, int64_t ds,
                      hipStream_t stream) {
   const int64_t cpb = flat_cols_per_block(sizeof(T), rows);
   const int64_t nblk = (cols + cpb - 1) / cpb;
-  const dim3 grid((unsigned)kmin<int64_t>(nblk, sizeof(T) == 1 ? kFlatMaxBlocksU8 : kFlatMaxBlocks));
+  const int64_t cap = sizeof(T) != 1 ? kFlatMaxBlocks : rows >= 256 ? kFlatMaxBlocksU8Long : kFlatMaxBlocksU8;
+  const dim3 grid((unsigned)kmin<int64_t>(nblk, cap));
   // about kFlatRowsPerLane rows per lane; UInt8 takes at least 2 lanes per
   // column (one lane per column reads LDS bytes at the column stride, with
   // bank conflicts: 10 x 10^7 UInt8 vecmat 44.9 us at 1 lane, 37.6 at 2)
@@ -934,6 +936,9 @@ __global__ __launch_bounds__(kDimBlock) void reduce_rows_kernel(
 constexpr int kFewMaxCols = 16;
 constexpr int kFewBlocks = 4096;
 constexpr int64_t kFewMaxBytes = 512LL << 20;
+// a single column (a scaled copy) streams better through the strips beyond
+// 128 MiB (10^8 x 1 Float32 169 against 146 us; 10^7 x 1 17.5 against 21.1)
+constexpr int64_t kFewMaxBytesOne = 128LL << 20;
 constexpr int64_t kFewMaxBytesU8X = 32LL << 20;
 template <class T, class Op, class F>
 __global__ __launch_bounds__(kDimBlock) void reduce_rows_few_kernel(
@@ -1388,7 +1393,8 @@ int launch_reduce_dim(const void* A, int64_t rows, int64_t cols, int64_t cs, int
   const bool vec = dv.vec;
   if (dim == 2 && vec && batch <= 1 && cols <= kFewMaxCols && rows % (int64_t)(16 / sizeof(T)) == 0 &&
       row_units(sizeof(T), rows, true) > kDimBlock &&
-      rows * cols * (int64_t)sizeof(T) <= (Dot4<T, Op, F>::kind == 2 ? kFewMaxBytesU8X : kFewMaxBytes)) {
+      rows * cols * (int64_t)sizeof(T) <=
+          (Dot4<T, Op, F>::kind == 2 ? kFewMaxBytesU8X : cols == 1 ? kFewMaxBytesOne : kFewMaxBytes)) {
     const int64_t nv = rows / (int64_t)(16 / sizeof(T));
     const unsigned grid = (unsigned)kmin<int64_t>((nv + kDimBlock - 1) / kDimBlock, kFewBlocks);
     hipLaunchKernelGGL((reduce_rows_few_kernel<T, Op, F>), dim3(grid), dim3(kDimBlock), 0, stream, (const T*)A,
