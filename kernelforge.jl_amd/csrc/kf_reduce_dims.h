@@ -479,12 +479,32 @@ __global__ __launch_bounds__(kDimBlock) void reduce_cols_flat_kernel(const T* A,
                                                                      int64_t cpb, T* out, int64_t out_stride,
                                                                      const T* xv, int64_t xs) {
   __shared__ uint4 s_blk[kDimBlock * kFlatVecs];
+  // UInt8 dot4 columns off the word boundary (rows % 4 != 0) also keep x
+  // pre-shifted for each byte offset sh of a column: word k of copy sh holds
+  // x[4k - sh .. 4k - sh + 3] (zero outside x)
+  constexpr bool kShiftX = F::kHasX && Dot4<T, Op, F>::kind >= 0;
+  constexpr int kXWords = kFlatMaxColBytes / 4 + 1;
   __shared__ __align__(16) T s_x[F::kHasX ? kFlatMaxColBytes / sizeof(T) : 4];
+  __shared__ uint32_t s_xsh[kShiftX ? 4 : 1][kShiftX ? kXWords : 1];
   const T* sb = reinterpret_cast<const T*>(s_blk);
   const T id = Op::template identity<T>();
   const int tid = threadIdx.x;
   if constexpr (F::kHasX)
     for (int64_t i = tid; i < rows; i += kDimBlock) s_x[i] = xv[i * xs];
+  if constexpr (kShiftX) {
+    if (rows % 4 != 0) {
+      const int nw = (int)(rows + 3) / 4 + 1;
+      for (int k = tid; k < 4 * nw; k += kDimBlock) {
+        const int sh = k / nw, kw = k % nw;
+        uint32_t v = 0;
+        for (int b = 0; b < 4; ++b) {
+          const int64_t r = 4 * (int64_t)kw - sh + b;
+          if (r >= 0 && r < rows) v |= (uint32_t)(uint8_t)xv[r * xs] << (8 * b);
+        }
+        s_xsh[sh][kw] = v;
+      }
+    }
+  }
   constexpr int G = kDimBlock / L;
   const int g = tid / L, j = tid % L;
   const int64_t nblk = (cols + cpb - 1) / cpb;
@@ -509,16 +529,30 @@ __global__ __launch_bounds__(kDimBlock) void reduce_cols_flat_kernel(const T* A,
       const T* col = sb + c * rows;
       T acc = id;
       if constexpr (Dot4<T, Op, F>::kind >= 0) {
+        constexpr int K = Dot4<T, Op, F>::kind;
+        const uint32_t* xw = reinterpret_cast<const uint32_t*>(s_x);
+        uint32_t d = 0;
         if (rows % 4 == 0) {  // dword-aligned columns: four rows per dot4
           const uint32_t* cw = reinterpret_cast<const uint32_t*>(col);
-          const uint32_t* xw = reinterpret_cast<const uint32_t*>(s_x);
-          uint32_t d = 0;
-          for (int64_t q = j; q < rows / 4; q += L)
-            d = dot4_word<Dot4<T, Op, F>::kind>(d, cw[q], F::kHasX ? xw[q] : cw[q]);
-          acc = (T)d;
+          for (int64_t q = j; q < rows / 4; q += L) d = dot4_word<K>(d, cw[q], F::kHasX ? xw[q] : cw[q]);
         } else {
-          for (int64_t i = j; i < rows; i += L) acc = Op::combine(acc, F::apply(col[i], F::kHasX ? s_x[i] : col[i]));
+          // the aligned words over the column's bytes [b0, b0 + rows), bytes
+          // outside it masked off; x realigned to the column's byte offset
+          const int64_t b0 = c * rows;
+          const int sh = (int)(b0 & 3);
+          const uint32_t* bw = reinterpret_cast<const uint32_t*>(s_blk);
+          const int64_t w0 = b0 >> 2, w1 = (b0 + rows - 1) >> 2;
+          for (int64_t w = w0 + j; w <= w1; w += L) {
+            const int64_t lo = kmax<int64_t>(b0, 4 * w) - 4 * w, hi = kmin<int64_t>(b0 + rows, 4 * w + 4) - 4 * w;
+            const uint32_t m = (0xffffffffu << (8 * lo)) & (0xffffffffu >> (8 * (4 - hi)));
+            const uint32_t a = bw[w] & m;
+            // rows 4w - b0 .. 4w - b0 + 3 of x: word w - w0 of the copy for sh
+            uint32_t xa = 0;
+            if constexpr (kShiftX) xa = s_xsh[sh][w - w0];
+            d = dot4_word<K>(d, a, F::kHasX ? xa : a);
+          }
         }
+        acc = (T)d;
       } else {
         for (int64_t i = j; i < rows; i += L) acc = Op::combine(acc, F::apply(col[i], F::kHasX ? s_x[i] : col[i]));
       }
@@ -752,7 +786,7 @@ int launch_flat_cols(const T* A, int64_t rows, int64_t cols, T* dst, int64_t ds,
   // bank conflicts: 10 x 10^7 UInt8 vecmat 44.9 us at 1 lane, 37.6 at 2)
   int L = sizeof(T) == 1 && rows >= 4 ? 2 : 1;
   // UInt8 dot4 columns: rows counted in 4-row words
-  const int64_t units = Dot4<T, Op, F>::kind >= 0 && rows % 4 == 0 ? rows / 4 : rows;
+  const int64_t units = Dot4<T, Op, F>::kind >= 0 ? (rows + 3) / 4 + (rows % 4 != 0) : rows;
   const int per = units != rows ? kFlatWordsPerLane : kFlatRowsPerLane;
   if (units != rows) L = 1;
   while (L < kWave && (int64_t)L * per < units) L <<= 1;

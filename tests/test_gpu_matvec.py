@@ -135,7 +135,7 @@ def test_short_contiguous_columns_flat_path(kf, oracle, dev, dt):
     # every lanes-per-column choice), vecmat and plain mapreduce, exact
     rng = np.random.default_rng(83)
     es = np.dtype(dt).itemsize
-    for rows in (1, 2, 3, 5, 10, 16, 17, 63, 100, 127, 2048 // es, 2048 // es + 1):
+    for rows in (1, 2, 3, 5, 10, 16, 17, 63, 100, 127, 2048 // es - 1, 2048 // es, 2048 // es + 1):
         for cols in (1, 7, 4099, 100_003 // max(1, rows // 8)):
             buf = mk(rng, dt, rows * cols)
             A = torch.from_numpy(buf).to(dev).as_strided((rows, cols), (1, rows))
@@ -148,6 +148,10 @@ def test_short_contiguous_columns_flat_path(kf, oracle, dev, dt):
                 got = kf.mapreduce(kf.identity, op, A, dims=1).cpu().numpy().reshape(-1)
                 ref = (M.astype(np.int64).sum(axis=1).astype(dt) if op == "+" else M.max(axis=1))
                 assert np.array_equal(got, ref), (rows, cols, op)
+            # sum of squares (UInt8: dot4 of each column's bytes with themselves)
+            got = kf.mapreduce(kf.abs2, "+", A, dims=1).cpu().numpy().reshape(-1)
+            M64 = M.astype(np.int64)
+            assert np.array_equal(got, (M64 * M64).sum(axis=1).astype(dt)), (rows, cols, "abs2")
 
 
 @pytest.mark.parametrize("dt", [np.int32, np.int64, np.uint8])
