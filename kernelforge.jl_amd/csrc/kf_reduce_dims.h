@@ -563,6 +563,21 @@ __global__ __launch_bounds__(kDimBlock) void reduce_cols_flat_kernel(const T* A,
   }
 }
 
+// A block's slice x[c0 .. c0 + nc) of a UInt8 operand into LDS: 32-bit
+// loads when x is contiguous and the slice word-aligned (one byte per lane
+// and load doubled the memory instructions of a 10-row matvec).
+__device__ inline void stage_x_u8(uint8_t* s_x, const uint8_t* xv, int64_t xs, int64_t c0, int64_t nc) {
+  const int tid = threadIdx.x;
+  if (xs == 1 && ((uintptr_t)(xv + c0) & 3) == 0) {
+    const int64_t nw = nc / 4;
+    const uint32_t* xw = reinterpret_cast<const uint32_t*>(xv + c0);
+    for (int64_t w = tid; w < nw; w += kDimBlock) reinterpret_cast<uint32_t*>(s_x)[w] = xw[w];
+    for (int64_t c = 4 * nw + tid; c < nc; c += kDimBlock) s_x[c] = xv[c0 + c];
+  } else {
+    for (int64_t c = tid; c < nc; c += kDimBlock) s_x[c] = xv[(c0 + c) * xs];
+  }
+}
+
 // UInt8 + by rows on dword-aligned columns (rows % 4 == 0) of the flat
 // path: thread t owns 32-bit word t % W of every column (rows 4w..4w+3, W =
 // rows / 4; words t, t + 256 when W > 256) and column phase t / W, and keeps
@@ -593,8 +608,7 @@ __device__ inline void flat_rows_u8_words(const uint8_t* A, int64_t rows, int64_
 #pragma unroll
     for (int u = 0; u < kFlatVecs; ++u)
       if (u * kDimBlock + tid < nvec) v[u] = ld_stream(src + u * kDimBlock + tid);
-    if constexpr (X)
-      for (int64_t c = tid; c < nc; c += kDimBlock) s_x[c] = xv[(c0 + c) * xs];
+    if constexpr (X) stage_x_u8(s_x, xv, xs, c0, nc);
 #pragma unroll
     for (int u = 0; u < kFlatVecs; ++u)
       if (u * kDimBlock + tid < nvec) s_blk[u * kDimBlock + tid] = v[u];
@@ -637,6 +651,109 @@ __device__ inline void flat_rows_u8_words(const uint8_t* A, int64_t rows, int64_
   }
 }
 
+// UInt8 + by rows on columns off the word boundary (rows % 4 != 0) of the
+// flat path: the block's bytes repeat their row pattern every P =
+// lcm(rows, 4) / 4 words, so thread t owns word phase k = t % P (words k,
+// k + P, ... of every block; the rows of its 4 byte lanes are fixed) and
+// keeps packed 16-bit sums per byte lane (pk16); with x each byte takes its
+// own column's value. At the end the threads add their byte-lane sums into
+// per-row LDS totals. Needs P <= kDimBlock.
+constexpr int64_t flat_period_words(int64_t rows) { return (rows % 2 == 0 ? rows / 2 : rows); }
+// From 5 to 128 rows and matrices of 96 MiB (256 MiB with x); elsewhere
+// the narrow kernel's element loads keep up (2 x 10^8 sum 43 against 45
+// us, 254 x 10^6 49 against 53; matvec 10 x 10^7 38 against 42). Measured
+// (us, narrow kernel -> this): 10 x 10^8 sum 223 -> 170, sum of squares 227
+// -> 163, matvec 380 -> 328; 7 x 10^8 sum 156 -> 120; 101 x 9*10^6 sum 235
+// -> 163, matvec 405 -> 320.
+template <bool X> constexpr bool flat_period_ok(int64_t rows, int64_t cols) {
+  return rows % 4 != 0 && rows >= 5 && rows <= 128 && rows * cols >= (X ? 256LL << 20 : 96LL << 20);
+}
+template <int K, bool X>
+__device__ inline void flat_rows_u8_period(const uint8_t* A, int64_t rows, int64_t cols, int64_t cpb, uint8_t* out,
+                                           int64_t out_stride, const uint8_t* xv, int64_t xs, uint4* s_blk,
+                                           uint8_t* s_x) {
+  __shared__ uint32_t s_row[kFlatMaxColBytes];
+  const int tid = threadIdx.x;
+  const int P = (int)flat_period_words(rows);
+  const int G = kDimBlock / P;           // threads per phase
+  const int k = tid % P, g = tid / P;
+  const bool active = g < G;
+  const int cpp = (int)(4 * (int64_t)P / rows);  // columns per period
+  const uint32_t* sw = reinterpret_cast<const uint32_t*>(s_blk);
+  uint8_t* sb = reinterpret_cast<uint8_t*>(s_blk);
+  int cb0[4];  // column of byte lane b in word k of a block
+  bool nx[4];  // byte lane b in the word's second column
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    cb0[b] = (int)((4 * (int64_t)k + b) / rows);
+    nx[b] = cb0[b] != cb0[0];
+  }
+  uint32_t ae = 0, ao = 0;
+  for (int64_t i = tid; i < rows; i += kDimBlock) s_row[i] = 0;
+  __syncthreads();
+  const int64_t nblk = (cols + cpb - 1) / cpb;
+  for (int64_t bk = blockIdx.x; bk < nblk; bk += gridDim.x) {
+    const int64_t c0 = bk * cpb;
+    const int64_t nc = kmin<int64_t>(cpb, cols - c0);
+    const int64_t nel = nc * rows;
+    const int64_t nvec = nel / 16;
+    const uint4* src = reinterpret_cast<const uint4*>(A + c0 * rows);
+    uint4 v[kFlatVecs];
+#pragma unroll
+    for (int u = 0; u < kFlatVecs; ++u)
+      if (u * kDimBlock + tid < nvec) v[u] = ld_stream(src + u * kDimBlock + tid);
+    if constexpr (X) stage_x_u8(s_x, xv, xs, c0, nc);
+#pragma unroll
+    for (int u = 0; u < kFlatVecs; ++u)
+      if (u * kDimBlock + tid < nvec) s_blk[u * kDimBlock + tid] = v[u];
+    const int64_t e0 = nvec * 16;
+    if (e0 + tid < nel) sb[e0 + tid] = A[c0 * rows + e0 + tid];
+    __syncthreads();
+    if (active) {
+      const int64_t nw = (nel + 3) / 4;
+      int64_t s = g;  // period index of word k + P*s
+      for (int64_t w = k + (int64_t)P * g; w < nw; w += (int64_t)P * G, s += G) {
+        uint32_t a = sw[w];
+        if (4 * w + 4 > nel) a &= 0xffffffffu >> (8 * (4 * w + 4 - nel));  // bytes past the block's end
+        uint32_t w16e = 0, w16o = 0;
+        if constexpr (X) {
+          // an aligned word of rows >= 2 spans at most two columns, c and c + 1
+          const int64_t c = cb0[0] + s * cpp;
+          const uint32_t x0 = s_x[c], x1 = s_x[kmin<int64_t>(c + 1, nc - 1)];
+          w16e = x0 | ((nx[2] ? x1 : x0) << 16);
+          w16o = (nx[1] ? x1 : x0) | ((nx[3] ? x1 : x0) << 16);
+        }
+        const kf_us2 e = __builtin_bit_cast(kf_us2, a & 0x00ff00ffu);
+        const kf_us2 o = __builtin_bit_cast(kf_us2, (a >> 8) & 0x00ff00ffu);
+        kf_us2 E = __builtin_bit_cast(kf_us2, ae), O = __builtin_bit_cast(kf_us2, ao);
+        if constexpr (K == 0) {
+          E += e;
+          O += o;
+        } else if constexpr (K == 1) {
+          E += e * e;
+          O += o * o;
+        } else {
+          E += e * __builtin_bit_cast(kf_us2, w16e);
+          O += o * __builtin_bit_cast(kf_us2, w16o);
+        }
+        ae = __builtin_bit_cast(uint32_t, E);
+        ao = __builtin_bit_cast(uint32_t, O);
+      }
+    }
+    __syncthreads();
+  }
+  if (active) {
+    atomicAdd(&s_row[(4 * k + 0) % rows], ae & 0xffffu);
+    atomicAdd(&s_row[(4 * k + 1) % rows], ao & 0xffffu);
+    atomicAdd(&s_row[(4 * k + 2) % rows], ae >> 16);
+    atomicAdd(&s_row[(4 * k + 3) % rows], ao >> 16);
+  }
+  __syncthreads();
+  uint8_t* o = gridDim.x == 1 ? out : out + (int64_t)blockIdx.x * rows;
+  const int64_t os = gridDim.x == 1 ? out_stride : 1;
+  for (int64_t i = tid; i < rows; i += kDimBlock) o[i * os] = (uint8_t)s_row[i];
+}
+
 // dim = 2 counterpart for short contiguous columns: the same blocks of whole
 // columns through LDS; thread t owns row t % rows (rows t, t + 256, ... when
 // rows > 256) and column phase t / rows of every block, accumulating over
@@ -649,13 +766,17 @@ __global__ __launch_bounds__(kDimBlock) void reduce_rows_flat_kernel(const T* A,
                                                                      int64_t cpb, T* out, int64_t out_stride,
                                                                      const T* xv, int64_t xs) {
   __shared__ uint4 s_blk[kDimBlock * kFlatVecs];
-  __shared__ T s_x[F::kHasX ? kFlatBlockBytes / 2 / sizeof(T) : 1];
+  __shared__ __align__(16) T s_x[F::kHasX ? kFlatBlockBytes / 2 / sizeof(T) : 1];
   T* sb = reinterpret_cast<T*>(s_blk);
   const T id = Op::template identity<T>();
   const int tid = threadIdx.x;
   if constexpr (Dot4<T, Op, F>::kind >= 0) {
     if (rows % 4 == 0) {
       flat_rows_u8_words<Dot4<T, Op, F>::kind, F::kHasX>(A, rows, cols, cpb, out, out_stride, xv, xs, s_blk, s_x);
+      return;
+    }
+    if (flat_period_ok<F::kHasX>(rows, cols)) {
+      flat_rows_u8_period<Dot4<T, Op, F>::kind, F::kHasX>(A, rows, cols, cpb, out, out_stride, xv, xs, s_blk, s_x);
       return;
     }
   }
@@ -762,9 +883,9 @@ inline int64_t flat_rows_grid(size_t es, int64_t rows, int64_t cols) {
 // UInt8 + (identity, abs2, x*y) over rows that are a multiple of 4 takes it
 // with packed 16-bit accumulators over 32-bit words (flat_rows_u8_words).
 template <class T, class Op, class F>
-inline bool use_flat_rows(const void* A, int64_t rows, int64_t cs, int64_t batch) {
+inline bool use_flat_rows(const void* A, int64_t rows, int64_t cols, int64_t cs, int64_t batch) {
   constexpr int64_t ev = 16 / (int64_t)sizeof(T);
-  const bool words = Dot4<T, Op, F>::kind >= 0 && rows % 4 == 0;
+  const bool words = Dot4<T, Op, F>::kind >= 0 && (rows % 4 == 0 || flat_period_ok<F::kHasX>(rows, cols));
   // (rows >= 2: each block's slice of x must fit the kernel's LDS for it)
   return rows >= 2 && (words || (sizeof(T) >= 4 && (sizeof(T) == 8 || rows % ev != 0))) &&
          use_flat_cols(A, rows, cs, sizeof(T), batch);
@@ -1396,7 +1517,7 @@ int launch_reduce_dim(const void* A, int64_t rows, int64_t cols, int64_t cs, int
                       const void* x = nullptr, int64_t xs = 0, int64_t dst_bstride = -1, bool may_peel = true) {
   if (dst_bstride < 0) dst_bstride = rows * ds;
   const DimVec dv = dim_vec(A, rows, cs, sizeof(T), dim, batch, a_bstride, F::kHasX, x, xs);
-  if (dim == 2 && !dv.head && !dv.tail && use_flat_rows<T, Op, F>(A, rows, cs, batch)) {
+  if (dim == 2 && !dv.head && !dv.tail && use_flat_rows<T, Op, F>(A, rows, cols, cs, batch)) {
     // short contiguous columns: the LDS-staged flat kernel, with as many
     // workgroups (and partial rows-vectors) as the plan's column splits
     const DimPlan pf = plan_dim(sizeof(T), rows, cols, 2, dv.vec, batch);

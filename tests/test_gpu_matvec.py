@@ -163,8 +163,9 @@ def test_short_contiguous_columns_flat_rows_path(kf, oracle, dev, dt):
     rng = np.random.default_rng(89)
     es = np.dtype(dt).itemsize
     rows_set = (2, 3, 5, 10, 63, 255, 257, 2048 // es - 1, 2048 // es)
-    if dt == np.uint8:  # + over 32-bit words (packed 16-bit sums) when rows % 4 == 0
-        rows_set = (4, 8, 12, 100, 252, 1000, 1020, 1028, 2044, 2048, 10)
+    if dt == np.uint8:  # + over 32-bit words (packed 16-bit sums) when rows % 4 == 0, else over
+        # the words of the rows' period (lcm(rows, 4) bytes; up to 255 odd / 510 even rows)
+        rows_set = (4, 8, 12, 100, 252, 1000, 1020, 1028, 2044, 2048, 10, 2, 3, 5, 7, 14, 255, 257, 510)
     for rows in rows_set:
         for cols in (1000, 40_003, 1_000_003 // rows):
             buf = mk(rng, dt, rows * cols)
@@ -298,3 +299,31 @@ def test_few_columns_dims2(kf, dev, dt):
             for g_, r_ in ((got_sum, ref_sum), (got_sq, ref_sq), (got_mv, ref_mv)):
                 assert np.array_equal(g_.astype(np.int64) % m, r_ % m), (rows, cols)
         assert not dbuf.cpu().numpy()[1::2].any()
+
+
+@pytest.mark.parametrize("rows", [7, 10])
+def test_u8_rows_off_the_word_large(kf, dev, rows):
+    # UInt8 dims=2 over short columns off the word boundary, large enough for
+    # the flat path's period kernel (sums from 96 MiB, matvec from 256 MiB):
+    # each word phase keeps packed 16-bit sums for fixed rows, exact mod 256
+    rng = np.random.default_rng(113 + rows)
+    for cols, with_x in ((105_000_000 // rows, False), (281_000_000 // rows, True)):
+        a = rng.integers(0, 256, (cols, rows), dtype=np.uint8)   # Julia rows x cols, column-major
+        A = torch.from_numpy(a).to(dev).T
+        if with_x:
+            xv = rng.integers(0, 256, cols, dtype=np.uint8)
+            got = kf.matvec(operator.mul, "+", A, torch.from_numpy(xv).to(dev)).cpu().numpy()
+            ref = np.zeros(rows, np.int64)
+            for c0 in range(0, cols, 1 << 24):  # products mod 2^16 in chunks
+                blk = a[c0:c0 + (1 << 24)].astype(np.uint16) * xv[c0:c0 + (1 << 24), None].astype(np.uint16)
+                ref += blk.sum(axis=0, dtype=np.int64)
+            assert np.array_equal(got.astype(np.int64), ref % 256), (rows, cols, "matvec")
+        else:
+            got = kf.mapreduce(kf.identity, "+", A, dims=2).cpu().numpy().reshape(-1)
+            assert np.array_equal(got.astype(np.int64), a.sum(axis=0, dtype=np.int64) % 256), (rows, cols, "+")
+            got = kf.mapreduce(kf.abs2, "+", A, dims=2).cpu().numpy().reshape(-1)
+            sq = np.zeros(rows, np.int64)
+            for c0 in range(0, cols, 1 << 24):
+                b = a[c0:c0 + (1 << 24)].astype(np.uint16)
+                sq += (b * b).sum(axis=0, dtype=np.int64)
+            assert np.array_equal(got.astype(np.int64), sq % 256), (rows, cols, "abs2")
