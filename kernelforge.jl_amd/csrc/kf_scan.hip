@@ -523,6 +523,7 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
   __shared__ int s_look_pre[kLookBlockFor<T, BLOCK, VPL> ? kScanWaves : 1];
   __shared__ uint64_t s_ticket;
   __shared__ int s_stop;
+  __shared__ int s_hdr_stop;  // the header's give-up flag (s_stop: this call's)
   constexpr bool kLdsRows = kLdsRowsFor<Op, V>;
   using Vec = VecT<T>;
   __shared__ Vec s_stash[kStashForLookback<T, BLOCK> ? V : 1][kWave];
@@ -534,18 +535,20 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
   const int wave = tid / kWave;
   const T id = Op::template identity<T>();
 
-  if (tid == 0) {
-    s_ticket = ((scratch[0] >> 32) << 32) | (uint64_t)blockIdx.x;  // {epoch, tile}
-    s_stop = ld_agent(scratch + 1) != 0;  // an earlier give-up: every call is a no-op until cleared
-  }
-  __syncthreads();
-  if (s_stop) return;
 #ifdef KF_TIMELINE
   const uint64_t tl_start = __builtin_amdgcn_s_memrealtime();
 #endif
-  const uint64_t tk = s_ticket;
-  const int64_t tile = (int64_t)(uint32_t)tk;
-  const uint32_t epoch30 = (uint32_t)(tk >> 32) & 0x3fffffffu;
+  // Thread 0 reads the header (epoch, give-up flag) without waiting for it:
+  // the tile's loads and in-register scan do not depend on either, so the
+  // round trip overlaps them and both reach the workgroup through LDS at
+  // the barrier after the block scan (10^7 UInt8: the read had delayed
+  // every tile's first load by one memory latency).
+  uint64_t hdr_epoch = 0, hdr_stop = 0;
+  if (tid == 0) {
+    hdr_epoch = scratch[0];
+    hdr_stop = ld_agent(scratch + 1);  // an earlier give-up: every call is a no-op until cleared
+  }
+  const int64_t tile = blockIdx.x;
   uint64_t* desc = scratch + kScanHeaderBytes / sizeof(uint64_t);
 
   const int64_t wbase = tile * S::TILE + (int64_t)wave * S::WAVE_ELEMS;  // this wave's virtual chunk
@@ -650,7 +653,14 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
   }
   if constexpr (kLdsRows) carry = wave_row_prefixes<T, Op, V>(tot, s_rows[wave], lane);
   if (lane == 0) wave_agg[wave] = carry;
+  if (tid == 0) {
+    s_ticket = ((hdr_epoch >> 32) << 32) | (uint64_t)blockIdx.x;  // {epoch, tile}
+    s_hdr_stop = hdr_stop != 0;
+  }
   __syncthreads();
+  if (s_hdr_stop) return;  // no store and no publication yet
+  const uint64_t tk = s_ticket;
+  const uint32_t epoch30 = (uint32_t)(tk >> 32) & 0x3fffffffu;
 #ifdef KF_TIMELINE
   const uint64_t tl_scanned = __builtin_amdgcn_s_memrealtime();
 #endif
