@@ -118,21 +118,24 @@ constexpr int kOnceVecs = kRedBlock * kOnceUnroll;
 // (8 per thread, all in flight together) until every word carries the
 // tag, then combines them in slot order with its own partial last, so
 // the result does not depend on timing. It stores the result and the tag
-// as the new epoch. The tag is epoch + 1, read with a plain load at kernel
-// start: the previous call's last workgroup wrote it before that kernel
+// as the new epoch. The tag is epoch + 1, read by thread 0 with a plain
+// load at kernel start, before the workgroup's data loads (`hdr0`), so its
+// round trip overlaps them: the previous call's last workgroup wrote it before that kernel
 // ended, and within a call every reader loads it before publishing,
 // which the waiter's completion depends on. Slots of older calls never
 // match. Only one workgroup ever waits, so progress needs no co-residency;
 // a bounded spin (only a corrupted or concurrently shared buffer can
 // exhaust it) keeps a bad buffer from hanging the GPU.
 constexpr uint32_t kFoldSpinLimit = 1u << 22;
-template <class T, class Op> __device__ inline void fold_partial(T part, T* out, uint64_t* hdr, T* s_wave) {
+__device__ inline uint32_t fold_epoch(const uint64_t* hdr) { return threadIdx.x == 0 ? (uint32_t)hdr[0] : 0u; }
+template <class T, class Op>
+__device__ inline void fold_partial(T part, T* out, uint64_t* hdr, T* s_wave, uint32_t hdr0) {
   constexpr int W = Words<T>::W;
   constexpr int PER = kFoldMax / kRedBlock;
   __shared__ uint32_t s_tag;
   const int tid = threadIdx.x;
   if (tid == 0) {
-    const uint32_t t = (uint32_t)hdr[0] + 1u;
+    const uint32_t t = hdr0 + 1u;
     s_tag = t == 0 ? 1u : t;
   }
   __syncthreads();
@@ -202,6 +205,7 @@ __global__ __launch_bounds__(kRedBlock) void reduce_once_kernel(const T* src, in
   constexpr int EPV = 16 / (int)sizeof(T);
   __shared__ T s_wave[kRedWaves];
   const int tid = threadIdx.x;
+  const uint32_t hdr0 = FOLD ? fold_epoch(fold_hdr) : 0u;  // fold tag, read ahead of the data
   const uint4* v = reinterpret_cast<const uint4*>(src + head);
   const int64_t base = (int64_t)blockIdx.x * (kRedBlock * U) + tid;
   uint4 r[U];
@@ -222,7 +226,7 @@ __global__ __launch_bounds__(kRedBlock) void reduce_once_kernel(const T* src, in
   if constexpr (!FOLD) {
     if (tid == 0) out[blockIdx.x] = part;  // a partial, or the result when gridDim.x == 1
   } else {
-    fold_partial<T, Op>(part, out, fold_hdr, s_wave);  // out is the result
+    fold_partial<T, Op>(part, out, fold_hdr, s_wave, hdr0);  // out is the result
   }
 }
 
@@ -247,6 +251,7 @@ __global__ __launch_bounds__(kRedBlock) void reduce_chunk_kernel(const T* src, i
   constexpr int EPV = 16 / (int)sizeof(T);
   __shared__ T s_wave[kRedWaves];
   const int tid = threadIdx.x;
+  const uint32_t hdr0 = fold_epoch(fold_hdr);  // fold tag, read ahead of the data
   const uint4* v = reinterpret_cast<const uint4*>(src + head);
   const int64_t b0 = (int64_t)blockIdx.x * chunk;
   const int64_t b1 = kmin<int64_t>(nvec, b0 + chunk);
@@ -275,7 +280,7 @@ __global__ __launch_bounds__(kRedBlock) void reduce_chunk_kernel(const T* src, i
     if (tail0 + tid < n) acc = Op::combine(acc, Map::apply(src[tail0 + tid]));
   }
   const T part = block_reduce<T, Op>(acc, s_wave);
-  fold_partial<T, Op>(part, out, fold_hdr, s_wave);
+  fold_partial<T, Op>(part, out, fold_hdr, s_wave, hdr0);
 }
 
 // Strided views with short strides (stride * sizeof(T) <= kStrideVecBytes,
@@ -300,6 +305,7 @@ __global__ __launch_bounds__(kRedBlock) void reduce_stride_kernel(const T* src, 
   __shared__ T s_wave[kRedWaves];
   const T id = Op::template identity<T>();
   const int tid = threadIdx.x;
+  const uint32_t hdr0 = fold_epoch(fold_hdr);  // fold tag, read ahead of the data
   const uint4* v = reinterpret_cast<const uint4*>(src + head);
   const int64_t b0 = (int64_t)blockIdx.x * chunk;
   const int64_t b1 = kmin<int64_t>(nvec, b0 + chunk);
@@ -345,7 +351,7 @@ __global__ __launch_bounds__(kRedBlock) void reduce_stride_kernel(const T* src, 
     if (t < span && t % stride == 0) acc = Op::combine(acc, Map::apply(src[t]));
   }
   const T part = block_reduce<T, Op>(acc, s_wave);
-  fold_partial<T, Op>(part, out, fold_hdr, s_wave);
+  fold_partial<T, Op>(part, out, fold_hdr, s_wave, hdr0);
 }
 
 // Full reduction, stage 2: one 1024-thread workgroup combines `count`
@@ -574,6 +580,7 @@ __global__ __launch_bounds__(kRedBlock) void reducek_once_kernel(Operands<T, K> 
   __shared__ T s_wave[kRedWaves];
   const T id = Op::template identity<T>();
   const int tid = threadIdx.x;
+  const uint32_t hdr0 = FOLD ? fold_epoch(fold_hdr) : 0u;  // fold tag, read ahead of the data
   const int64_t nvec = n / EPV;
   const int64_t base = (int64_t)blockIdx.x * kOnceVecs + tid;
   uint4 r[kOnceUnroll][K];
@@ -613,7 +620,7 @@ __global__ __launch_bounds__(kRedBlock) void reducek_once_kernel(Operands<T, K> 
   if constexpr (!FOLD) {
     if (tid == 0) out[blockIdx.x] = part;
   } else {
-    fold_partial<T, Op>(part, out, fold_hdr, s_wave);  // out is the result
+    fold_partial<T, Op>(part, out, fold_hdr, s_wave, hdr0);  // out is the result
   }
 }
 
