@@ -675,14 +675,18 @@ constexpr int64_t flat_period_words(int64_t rows) { return (rows % 2 == 0 ? rows
 // (us, narrow kernel -> this): 10 x 10^8 sum 223 -> 170, sum of squares 227
 // -> 163, matvec 380 -> 328; 7 x 10^8 sum 156 -> 120; 101 x 9*10^6 sum 235
 // -> 163, matvec 405 -> 320.
+constexpr int kPeriodMaxRows = 128;
 template <bool X> constexpr bool flat_period_ok(int64_t rows, int64_t cols) {
-  return rows % 4 != 0 && rows >= 5 && rows <= 128 && rows * cols >= (X ? 256LL << 20 : 96LL << 20);
+  return rows % 4 != 0 && rows >= 5 && rows <= kPeriodMaxRows && rows * cols >= (X ? 256LL << 20 : 96LL << 20);
 }
 template <int K, bool X>
 __device__ inline void flat_rows_u8_period(const uint8_t* A, int64_t rows, int64_t cols, int64_t cpb, uint8_t* out,
                                            int64_t out_stride, const uint8_t* xv, int64_t xs, uint4* s_blk,
                                            uint8_t* s_x) {
-  __shared__ uint32_t s_row[kFlatMaxColBytes];
+  // (a static LDS array here counts against every reduce_rows_flat_kernel
+  // instance, the words path included: 8 KiB of it had cost the 100- and
+  // 1000-row UInt8 matvecs a workgroup per CU)
+  __shared__ uint32_t s_row[kPeriodMaxRows];
   const int tid = threadIdx.x;
   const int P = (int)flat_period_words(rows);
   const int G = kDimBlock / P;           // threads per phase
@@ -1496,6 +1500,11 @@ void launch_combine(const T* part, int S, int64_t m, T* dst, int64_t ds, int64_t
 
 // S persistent workgroups write S partial rows-vectors into the scratch,
 // combined by launch_combine (S = 1: straight into dst).
+// UInt8 takes at most 6 workgroups per CU (HIP graphs, us, at 3 / 4 / 5 /
+// 6 / 8 per CU): 100 x 10^7 sum 219 / 183 / 163 / 158 / 178, 1000 x 10^6
+// sum 213 / 176 / 158 / 163 / 180, 128 x 7812500 sum 215 / 177 / 158 / 157
+// / 175; matvec 100 x 10^7 254 / 215 / 193 / 197 / 196.
+constexpr int kFlatRowsU8PerCu = 6;
 template <class T, class Op, class F>
 int launch_flat_rows(const T* A, int64_t rows, int64_t cols, int S, T* scratch, T* dst, int64_t ds, const T* x,
                      int64_t xs, hipStream_t stream) {
@@ -1509,6 +1518,7 @@ int launch_flat_rows(const T* A, int64_t rows, int64_t cols, int S, T* scratch, 
   do {                                                                                                        \
     constexpr auto kernel = reduce_rows_flat_kernel<T, Op, F, RR>;                                            \
     S = (int)kmin<int64_t>(S, resident_blocks<kernel>(kDimBlock));                                            \
+    if (sizeof(T) == 1) S = (int)kmin<int64_t>(S, kFlatRowsU8PerCu * kf_device_cu_count());                \
     hipLaunchKernelGGL(kernel, dim3((unsigned)S), dim3(kDimBlock), 0, stream, A, rows, cols, cpb,             \
                        S > 1 ? scratch : dst, ds, x, xs);                                                     \
   } while (0)
