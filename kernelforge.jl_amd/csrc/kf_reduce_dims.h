@@ -1531,11 +1531,77 @@ int launch_flat_rows(const T* A, int64_t rows, int64_t cols, int S, T* scratch, 
   return kf_check_launch("reduce_rows_flat_kernel");
 }
 
+// A reduction over a dimension of length 1 (dims=1 over one row, dims=2
+// over one column): every output is f of one element, out[k*os] =
+// f(A[k*as], x[0]), a streaming map (16-byte loads and stores when both
+// sides are contiguous and aligned). Through the flat dims=1 kernel one
+// 1-byte column per lane had taken 1 x 10^8 UInt8 vecmat to 136 us.
+constexpr int kMapOneBlocks = 8192;  // element path: grid-stride
+// vector path: one-shot workgroups of kMapOneVecs vectors per lane (HIP
+// graphs, us, 1, 2, 4 vectors: Float64 10^8 x 1 matvec 245 / 263 / 268,
+// 1 x 10^8 vecmat 243 / 266 / 266; Float32 122 / 129 / 132)
+constexpr int kMapOneVecs = 1;
+template <class T, class F>
+__global__ __launch_bounds__(kDimBlock) void map_one_kernel(const T* A, int64_t n, int64_t as, T* out, int64_t os,
+                                                            const T* xv, int vec) {
+  constexpr int EPV = 16 / (int)sizeof(T);
+  constexpr int U = kMapOneVecs;
+  const T x0 = F::kHasX ? xv[0] : T();
+  const int tid = threadIdx.x;
+  if (vec) {
+    // workgroup b maps vectors [b*U*256, (b+1)*U*256), its loads in flight
+    // before any store; workgroup 0 also maps the tail elements
+    const int64_t nv = n / EPV;
+    const uint4* src = reinterpret_cast<const uint4*>(A);
+    uint4* dst = reinterpret_cast<uint4*>(out);
+    const int64_t base = (int64_t)blockIdx.x * (U * kDimBlock) + tid;
+    uint4 r[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (base + u * kDimBlock < nv) r[u] = ld_stream(src + base + u * kDimBlock);
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (base + u * kDimBlock < nv) {
+        T a[EPV];
+        __builtin_memcpy(a, &r[u], 16);
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) a[e] = F::apply(a[e], F::kHasX ? x0 : a[e]);
+        uint4 w;
+        __builtin_memcpy(&w, a, 16);
+        st_stream(dst + base + u * kDimBlock, w);
+      }
+    if (blockIdx.x == 0)
+      for (int64_t k = nv * EPV + tid; k < n; k += kDimBlock) out[k] = F::apply(A[k], F::kHasX ? x0 : A[k]);
+    return;
+  }
+  const int64_t step = (int64_t)gridDim.x * kDimBlock;
+  for (int64_t k = (int64_t)blockIdx.x * kDimBlock + tid; k < n; k += step) {
+    const T a = A[k * as];
+    out[k * os] = F::apply(a, F::kHasX ? x0 : a);
+  }
+}
+
+template <class T, class F>
+int launch_map_one(const T* A, int64_t n, int64_t as, T* out, int64_t os, const T* x, hipStream_t stream) {
+  const int vec = as == 1 && os == 1 && (uintptr_t)A % 16 == 0 && (uintptr_t)out % 16 == 0;
+  const int64_t per = vec ? (int64_t)kDimBlock * kMapOneVecs * (16 / (int64_t)sizeof(T)) : kDimBlock;
+  int64_t grid = (n + per - 1) / per;
+  if (!vec) grid = kmin<int64_t>(grid, kMapOneBlocks);
+  if (grid > (int64_t)(0xffffffffu / kDimBlock))  // threads of one launch: fewer than 2^32
+    return kf_set_error(KF_EINVAL, "map_one_kernel: %lld elements exceed one launch", (long long)n);
+  hipLaunchKernelGGL((map_one_kernel<T, F>), dim3((unsigned)kmax<int64_t>(grid, 1)), dim3(kDimBlock), 0, stream, A,
+                     n, as, out, os, x, vec);
+  return kf_check_launch("map_one_kernel");
+}
+
 template <class T, class Op, class F>
 int launch_reduce_dim(const void* A, int64_t rows, int64_t cols, int64_t cs, int dim, void* dst,
                       int64_t ds, void* scratch, hipStream_t stream, int64_t batch = 1, int64_t a_bstride = 0,
                       const void* x = nullptr, int64_t xs = 0, int64_t dst_bstride = -1, bool may_peel = true) {
   if (dst_bstride < 0) dst_bstride = rows * ds;
+  if (batch <= 1 && (dim == 1 ? rows == 1 && cols > 1 : cols == 1 && rows > 1))
+    return dim == 1 ? launch_map_one<T, F>((const T*)A, cols, cs, (T*)dst, ds, (const T*)x, stream)
+                    : launch_map_one<T, F>((const T*)A, rows, 1, (T*)dst, ds, (const T*)x, stream);
   const DimVec dv = dim_vec(A, rows, cs, sizeof(T), dim, batch, a_bstride, F::kHasX, x, xs);
   if (dim == 2 && !dv.head && !dv.tail && use_flat_rows<T, Op, F>(A, rows, cols, cs, batch)) {
     // short contiguous columns: the LDS-staged flat kernel, with as many

@@ -327,3 +327,27 @@ def test_u8_rows_off_the_word_large(kf, dev, rows):
                 b = a[c0:c0 + (1 << 24)].astype(np.uint16)
                 sq += (b * b).sum(axis=0, dtype=np.int64)
             assert np.array_equal(got.astype(np.int64), sq % 256), (rows, cols, "abs2")
+
+
+@pytest.mark.parametrize("dt", [np.uint8, np.int32, np.float32, np.float64])
+def test_length_one_dimension_is_a_map(kf, dev, dt):
+    # dims=1 over a single row / dims=2 over a single column: every output is
+    # f of one element (no combine), with and without a vector operand, for
+    # aligned, element-offset (off the 16-byte vector) and strided views;
+    # one IEEE operation per output, so floats are exact too
+    rng = np.random.default_rng(83)
+    for n in (2, 17, 4099, 1_000_003):
+        for off in (0, 1):
+            flat = mk(rng, dt, 2 * n + 2)
+            t = torch.from_numpy(flat).to(dev)
+            for dims, shape, strides, take in ((1, (1, n), (1, 1), flat[off:off + n]),
+                                               (1, (1, n), (1, 2), flat[off:off + 2 * n:2]),
+                                               (2, (n, 1), (1, n), flat[off:off + n])):
+                A = t[off:].as_strided(shape, strides)
+                got = kf.mapreduce(kf.abs2, "+", A, dims=dims).cpu().numpy().reshape(-1)
+                assert np.array_equal(got, (take * take).astype(dt)), (n, off, dims, strides)
+                x = mk(rng, dt, 1)
+                tx = torch.from_numpy(x).to(dev)
+                got = (kf.vecmat(operator.mul, "+", tx, A) if dims == 1 else
+                       kf.matvec(operator.mul, "+", A, tx)).cpu().numpy().reshape(-1)
+                assert np.array_equal(got, (take * x[0]).astype(dt)), (n, off, dims, strides)
