@@ -564,7 +564,23 @@ __global__ __launch_bounds__(kDimBlock) void reduce_cols_flat_kernel(const T* A,
           if (++i == rows) i = 0;
         }
       } else {
-        for (int64_t i = j; i < rows; i += L) acc = Op::combine(acc, F::apply(col[i], F::kHasX ? s_x[i] : col[i]));
+        // lane j of the column's group takes rows j, j + L, ...; when the
+        // column stride is a multiple of 64 bytes (every column starting in
+        // the same few LDS banks) it starts at a column-dependent one of
+        // them and wraps around (32 x 3*10^7 Float32 at 2 lanes: 917 -> 626
+        // us; at other strides the rotation only scattered the x reads: 100
+        // x 10^7 Float32 vecmat 643 -> 732)
+        if ((rows * (int64_t)sizeof(T)) % 64 == 0) {
+          const int cnt = (int)((rows - j + L - 1) / L);
+          int64_t i = cnt > 0 ? j + (int64_t)L * ((int)c % cnt) : j;
+          for (int t = 0; t < cnt; ++t) {
+            acc = Op::combine(acc, F::apply(col[i], F::kHasX ? s_x[i] : col[i]));
+            i += L;
+            if (i >= rows) i = j;
+          }
+        } else {
+          for (int64_t i = j; i < rows; i += L) acc = Op::combine(acc, F::apply(col[i], F::kHasX ? s_x[i] : col[i]));
+        }
       }
       acc = group_reduce<Op, L>(acc);
       if (j == 0) out[(c0 + c) * out_stride] = acc;
