@@ -462,6 +462,9 @@ template <auto KERNEL> int64_t resident_blocks(int block) {
 constexpr int kFlatVecs = 4;                                   // 16-byte vectors per thread per block
 constexpr int kFlatBlockBytes = kDimBlock * kFlatVecs * 16;   // 16 KiB
 constexpr int kFlatMaxColBytes = 2048;                         // longest column this path takes
+// dims=1 takes columns of up to 4 KiB of 4- and 8-byte types (a wave per
+// 4000-byte Float32 column left 10^3 x 10^6 vecmat at 767 us)
+constexpr int kFlatMaxColBytesWide = 4096;
 // one block of columns per workgroup (grid-stride beyond this cap): the
 // dispatcher then balances the blocks, where a persistent grid of 4096
 // workgroups left its last ones running alone (10 x 10^8 dims=1 Float32 934
@@ -484,7 +487,7 @@ __global__ __launch_bounds__(kDimBlock) void reduce_cols_flat_kernel(const T* A,
   // x[4k - sh .. 4k - sh + 3] (zero outside x)
   constexpr bool kShiftX = F::kHasX && Dot4<T, Op, F>::kind >= 0;
   constexpr int kXWords = kFlatMaxColBytes / 4 + 1;
-  __shared__ __align__(16) T s_x[F::kHasX ? kFlatMaxColBytes / sizeof(T) : 4];
+  __shared__ __align__(16) T s_x[F::kHasX ? (sizeof(T) >= 4 ? kFlatMaxColBytesWide : kFlatMaxColBytes) / sizeof(T) : 4];
   __shared__ uint32_t s_xsh[kShiftX ? 4 : 1][kShiftX ? kXWords : 1];
   const T* sb = reinterpret_cast<const T*>(s_blk);
   const T id = Op::template identity<T>();
@@ -886,6 +889,21 @@ inline int64_t flat_cols_per_block(size_t es, int64_t rows) {
 inline bool use_flat_cols(const void* A, int64_t rows, int64_t cs, size_t es, int64_t batch) {
   return batch == 1 && cs == rows && (uintptr_t)A % 16 == 0 && rows * (int64_t)es <= kFlatMaxColBytes &&
          flat_cols_per_block(es, rows) > 0;
+}
+
+// Columns of 2-4 KiB go flat only when a block's columns take one pass of
+// the workgroup's lanes (columns x lanes per column <= 256): HIP graphs, us,
+// wave per column -> flat: Float32 10^3 x 10^6 768 -> 697, 1023 rows 783 ->
+// 698; Float64 500 x 10^6 781 -> 646, 511 rows 1200 -> 664, 300 rows 424 ->
+// 404; but Float32 600 / 700 rows (two passes) 427 -> 466 / 460 -> 534.
+inline bool use_flat_cols_dim1(const void* A, int64_t rows, int64_t cs, size_t es, int64_t batch) {
+  if (use_flat_cols(A, rows, cs, es, batch)) return true;
+  if (es < 4 || batch != 1 || cs != rows || (uintptr_t)A % 16 != 0 || rows * (int64_t)es > kFlatMaxColBytesWide)
+    return false;
+  int64_t L = 1;  // lanes per column, as launch_flat_cols picks them
+  while (L < kWave && L * kFlatRowsPerLane < rows) L <<= 1;
+  const int64_t cpb = flat_cols_per_block(es, rows);
+  return cpb > 0 && cpb * L <= kDimBlock;
 }
 
 constexpr int kFlatRowsMinSplit = 64;  // column splits of the plan that send dims=2 to the flat path
@@ -1690,7 +1708,7 @@ int launch_reduce_dim(const void* A, int64_t rows, int64_t cols, int64_t cs, int
     }
   }
   if (dim == 1) {
-    if (use_flat_cols(A, rows, cs, sizeof(T), batch))
+    if (use_flat_cols_dim1(A, rows, cs, sizeof(T), batch))
       return launch_flat_cols<T, Op, F>((const T*)A, rows, cols, (T*)dst, ds, (const T*)x, xs, stream);
     if (p.seg_lanes) {
       const dim3 grid((unsigned)p.groups);

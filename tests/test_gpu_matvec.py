@@ -351,3 +351,34 @@ def test_length_one_dimension_is_a_map(kf, dev, dt):
                 got = (kf.vecmat(operator.mul, "+", tx, A) if dims == 1 else
                        kf.matvec(operator.mul, "+", A, tx)).cpu().numpy().reshape(-1)
                 assert np.array_equal(got, (take * x[0]).astype(dt)), (n, off, dims, strides)
+
+
+@pytest.mark.parametrize("dt", [np.int32, np.int64, np.float64])
+def test_flat_path_columns_up_to_4k(kf, oracle, dev, dt):
+    # dims=1 over contiguous columns of 2-4 KiB of 4- and 8-byte types: the
+    # flat path when a block's columns take one pass of the workgroup's lanes
+    # (Int32 1000 / 1023 rows, Int64 300 / 500 / 511 rows), the wave per
+    # column otherwise (Int32 600 / 700 rows); ragged last blocks; integers
+    # exact, Float64 within 1e-12 of the column's sum of |f|
+    rng = np.random.default_rng(89)
+    es = np.dtype(dt).itemsize
+    for rows in ((600, 700, 1000, 1023, 1024) if es == 4 else (300, 500, 511, 512)):
+        for cols in (1, 5, 4099):
+            buf = mk(rng, dt, rows * cols)
+            A = torch.from_numpy(buf).to(dev).as_strided((rows, cols), (1, rows))
+            x = mk(rng, dt, rows)
+            got = kf.vecmat(operator.mul, "+", torch.from_numpy(x).to(dev), A).cpu().numpy()
+            ref = oracle.reduce_dim_x(buf, rows, cols, rows, x, 1, "+", "mul")
+            M = buf.reshape(cols, rows).astype(np.float64)
+            if np.dtype(dt).kind == "f":
+                bound = np.abs(M * x.astype(np.float64)[None, :]).sum(axis=1) * 1e-12
+                assert np.all(np.abs(got - ref) <= bound), (rows, cols, "vecmat")
+                got = kf.mapreduce(kf.identity, "+", A, dims=1).cpu().numpy().reshape(-1)
+                assert np.all(np.abs(got - M.sum(axis=1)) <= np.abs(M).sum(axis=1) * 1e-12), (rows, cols)
+            else:
+                assert np.array_equal(got, ref), (rows, cols, "vecmat")
+                Mi = buf.reshape(cols, rows)
+                for op, npf in (("+", np.sum), (max, np.max)):
+                    got = kf.mapreduce(kf.identity, op, A, dims=1).cpu().numpy().reshape(-1)
+                    ref = Mi.astype(np.int64).sum(axis=1).astype(dt) if op == "+" else Mi.max(axis=1)
+                    assert np.array_equal(got, ref), (rows, cols, op)
