@@ -930,13 +930,21 @@ inline int64_t flat_rows_grid(size_t es, int64_t rows, int64_t cols) {
 // 10-40 % at every size.
 // UInt8 + (identity, abs2, x*y) over rows that are a multiple of 4 takes it
 // with packed 16-bit accumulators over 32-bit words (flat_rows_u8_words).
+// 8-byte types take it for columns of up to 4 KiB (HIP graphs, us, narrow
+// kernel -> flat: Float64 matvec 300 x 10^6 604 -> 380, 500 x 10^6 791 -> 665,
+// 511 x 10^6 947 -> 666, 400 x 10^5 90 -> 70)
+inline int64_t flat_rows_max_bytes(size_t es) { return es == 8 ? kFlatMaxColBytesWide : kFlatMaxColBytes; }
+inline bool flat_rows_shape_ok(const void* A, int64_t rows, int64_t cs, size_t es, int64_t batch) {
+  return batch == 1 && cs == rows && (uintptr_t)A % 16 == 0 && rows * (int64_t)es <= flat_rows_max_bytes(es) &&
+         flat_cols_per_block(es, rows) > 0;
+}
 template <class T, class Op, class F>
 inline bool use_flat_rows(const void* A, int64_t rows, int64_t cols, int64_t cs, int64_t batch) {
   constexpr int64_t ev = 16 / (int64_t)sizeof(T);
   const bool words = Dot4<T, Op, F>::kind >= 0 && (rows % 4 == 0 || flat_period_ok<F::kHasX>(rows, cols));
   // (rows >= 2: each block's slice of x must fit the kernel's LDS for it)
   return rows >= 2 && (words || (sizeof(T) >= 4 && (sizeof(T) == 8 || rows % ev != 0))) &&
-         use_flat_cols(A, rows, cs, sizeof(T), batch);
+         flat_rows_shape_ok(A, rows, cs, sizeof(T), batch);
 }
 
 template <class T, class Op, class F>
@@ -1504,7 +1512,7 @@ inline size_t dim_query(size_t es, int64_t rows, int64_t cols, int dim, int64_t 
   if (dim == 2) {
     const int64_t ev = (int64_t)(16 / es);
     if (rows % ev == 0) b = kmax(b, dim2_vec_need(es, rows, cols, batch));
-    if (batch == 1 && rows * (int64_t)es <= kFlatMaxColBytes && flat_cols_per_block(es, rows) > 0)
+    if (flat_rows_shape_ok(nullptr, rows, rows, es, batch))
       b = kmax(b, round256((size_t)flat_rows_grid(es, rows, cols) * (size_t)rows * es));  // the flat path's partials
     for (int64_t h = 0; h < ev && h < rows; ++h) {
       const int64_t t = (rows - h) % ev;  // the tail a head of h rows leaves
