@@ -930,10 +930,12 @@ inline int64_t flat_rows_grid(size_t es, int64_t rows, int64_t cols) {
 // 10-40 % at every size.
 // UInt8 + (identity, abs2, x*y) over rows that are a multiple of 4 takes it
 // with packed 16-bit accumulators over 32-bit words (flat_rows_u8_words).
-// 8-byte types take it for columns of up to 4 KiB (HIP graphs, us, narrow
-// kernel -> flat: Float64 matvec 300 x 10^6 604 -> 380, 500 x 10^6 791 -> 665,
-// 511 x 10^6 947 -> 666, 400 x 10^5 90 -> 70)
-inline int64_t flat_rows_max_bytes(size_t es) { return es == 8 ? kFlatMaxColBytesWide : kFlatMaxColBytes; }
+// 4- and 8-byte types take it for columns of 2-4 KiB too, whatever their
+// row count (HIP graphs, us, narrow kernel -> flat: Float64 matvec 300 x 10^6
+// 604 -> 380, 500 x 10^6 791 -> 665, 511 x 10^6 947 -> 666, 400 x 10^5 90 ->
+// 70; Float32 600 x 10^6 492 -> 378, 1000 x 10^6 720 -> 655, 513 x 10^6 611
+// -> 351, 800 x 10^5 72.5 -> 62.8)
+inline int64_t flat_rows_max_bytes(size_t es) { return es >= 4 ? kFlatMaxColBytesWide : kFlatMaxColBytes; }
 inline bool flat_rows_shape_ok(const void* A, int64_t rows, int64_t cs, size_t es, int64_t batch) {
   return batch == 1 && cs == rows && (uintptr_t)A % 16 == 0 && rows * (int64_t)es <= flat_rows_max_bytes(es) &&
          flat_cols_per_block(es, rows) > 0;
@@ -943,7 +945,8 @@ inline bool use_flat_rows(const void* A, int64_t rows, int64_t cols, int64_t cs,
   constexpr int64_t ev = 16 / (int64_t)sizeof(T);
   const bool words = Dot4<T, Op, F>::kind >= 0 && (rows % 4 == 0 || flat_period_ok<F::kHasX>(rows, cols));
   // (rows >= 2: each block's slice of x must fit the kernel's LDS for it)
-  return rows >= 2 && (words || (sizeof(T) >= 4 && (sizeof(T) == 8 || rows % ev != 0))) &&
+  return rows >= 2 &&
+         (words || (sizeof(T) >= 4 && (sizeof(T) == 8 || rows % ev != 0 || rows * (int64_t)sizeof(T) > kFlatMaxColBytes))) &&
          flat_rows_shape_ok(A, rows, cs, sizeof(T), batch);
 }
 
