@@ -930,12 +930,15 @@ inline int64_t flat_rows_grid(size_t es, int64_t rows, int64_t cols) {
 // 10-40 % at every size.
 // UInt8 + (identity, abs2, x*y) over rows that are a multiple of 4 takes it
 // with packed 16-bit accumulators over 32-bit words (flat_rows_u8_words).
-// 4- and 8-byte types take it for columns of 2-4 KiB too, whatever their
-// row count (HIP graphs, us, narrow kernel -> flat: Float64 matvec 300 x 10^6
-// 604 -> 380, 500 x 10^6 791 -> 665, 511 x 10^6 947 -> 666, 400 x 10^5 90 ->
-// 70; Float32 600 x 10^6 492 -> 378, 1000 x 10^6 720 -> 655, 513 x 10^6 611
-// -> 351, 800 x 10^5 72.5 -> 62.8)
-inline int64_t flat_rows_max_bytes(size_t es) { return es >= 4 ? kFlatMaxColBytesWide : kFlatMaxColBytes; }
+// 4- and 8-byte types take it for columns of 2-8 KiB too, whatever their
+// row count (HIP graphs, us, narrow or strip kernels -> flat: Float64 matvec
+// 300 x 10^6 604 -> 380, 500 x 10^6 791 -> 665, 511 x 10^6 947 -> 666, 700 x
+// 5*10^5 581 -> 429, 1000 x 10^6 1526 -> 1276, 1000 x 10^5 195 -> 148;
+// Float32 600 x 10^6 492 -> 378, 1000 x 10^6 720 -> 655, 513 x 10^6 611 ->
+// 351, 1200 x 10^6 839 -> 745, 1500 x 5*10^5 613 -> 487, 2000 x 5*10^5 712
+// -> 641; the one loss seen, Float64 1023 x 5*10^5, 692 -> 711)
+constexpr int64_t kFlatRowsMaxColBytes = 8192;  // two columns per 16 KiB block, 8 rows per thread
+inline int64_t flat_rows_max_bytes(size_t es) { return es >= 4 ? kFlatRowsMaxColBytes : kFlatMaxColBytes; }
 inline bool flat_rows_shape_ok(const void* A, int64_t rows, int64_t cs, size_t es, int64_t batch) {
   return batch == 1 && cs == rows && (uintptr_t)A % 16 == 0 && rows * (int64_t)es <= flat_rows_max_bytes(es) &&
          flat_cols_per_block(es, rows) > 0;

@@ -164,7 +164,7 @@ def test_short_contiguous_columns_flat_rows_path(kf, oracle, dev, dt):
     es = np.dtype(dt).itemsize
     rows_set = (2, 3, 5, 10, 63, 255, 257, 2048 // es - 1, 2048 // es)
     if es >= 4:  # 4- and 8-byte types up to 4 KiB columns
-        rows_set += (300, 511, 512) if es == 8 else (513, 600, 1000, 1023, 1024)
+        rows_set += (300, 511, 512, 700, 1000, 1023, 1024) if es == 8 else (513, 600, 1000, 1023, 1024, 1500, 2048)
     if dt == np.uint8:  # + over 32-bit words (packed 16-bit sums) when rows % 4 == 0, else over
         # the words of the rows' period (lcm(rows, 4) bytes; up to 255 odd / 510 even rows)
         rows_set = (4, 8, 12, 100, 252, 1000, 1020, 1028, 2044, 2048, 10, 2, 3, 5, 7, 14, 255, 257, 510)
