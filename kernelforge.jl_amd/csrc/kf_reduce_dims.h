@@ -1432,11 +1432,26 @@ inline DimPlan plan_dim(size_t es, int64_t rows, int64_t cols, int dim, bool vec
     // 10^4 Float32 98.9 -> 77.5 us at 10 strips), else until kDim2Blocks
     // (65536 x 4096, 64 strips: 159 us at S = 4, 172 at S = 16)
     const int64_t want = p.groups * nb < kDim2FewStrips ? kDim2SplitBlocks : kDim2Blocks;
-    if (p.groups * nb < want) {
-      S = (want + p.groups * nb - 1) / (p.groups * nb);
-      S = kmin<int64_t>(S, kmax<int64_t>(cols / (2 * cu), 1));
-      S = kmin<int64_t>(S, 256);
-    }
+    const int64_t g = p.groups * nb;
+    const int64_t smax = kmin<int64_t>(256, kmax<int64_t>(cols / (2 * cu), 1));
+    if (g < want) S = kmin<int64_t>((want + g - 1) / g, smax);
+    // whole rounds of workgroups over the CUs: the fewest splits from S up
+    // whose grid is within 7 % of a multiple of the CU count (HIP graphs,
+    // us, matvec: 10^5 x 10^4 Float32, 97 strips, 741 at S = 3 (291
+    // workgroups, 35 CUs with two) -> 587 at S = 5, Float64 1305 -> 1262;
+    // 3*10^5 x 3000 Float32, 292 strips, 689 at S = 1 -> 581; 10^4 x 10^5
+    // Float64 1308 -> 1220; 10^5 x 10^3 Float32 90 -> 75; UInt8 10^5 x 10^4
+    // 206 -> 194)
+    const auto over = [&](int64_t t) {
+      const int64_t w = g * t;
+      return (w + kDim2Blocks - 1) / kDim2Blocks * kDim2Blocks * 100 > w * 107;
+    };
+    if (over(S))
+      for (int64_t t = S + 1; t <= kmin<int64_t>(8 * S, smax); ++t)
+        if (!over(t)) {
+          S = t;
+          break;
+        }
     p.split = (int)S;
   }
   const int64_t parts = kmax<int64_t>(p.split, p.multi_split);
