@@ -973,13 +973,10 @@ inline int64_t flat_cols_per_block_out(size_t es, int64_t rows, int64_t ds) {
   while (q % ca) q <<= 1;
   return cpb >= q ? cpb / q * q : cpb;
 }
+constexpr int64_t kFlatMinPassBytes = 8192;
 template <class T, class Op, class F>
 int launch_flat_cols(const T* A, int64_t rows, int64_t cols, T* dst, int64_t ds, const T* x, int64_t xs,
                      hipStream_t stream) {
-  const int64_t cpb = flat_cols_per_block_out(sizeof(T), rows, ds);
-  const int64_t nblk = (cols + cpb - 1) / cpb;
-  const int64_t cap = sizeof(T) != 1 ? kFlatMaxBlocks : rows >= 256 ? kFlatMaxBlocksU8Long : kFlatMaxBlocksU8;
-  const dim3 grid((unsigned)kmin<int64_t>(nblk, cap));
   // about kFlatRowsPerLane rows per lane; UInt8 takes at least 2 lanes per
   // column (one lane per column reads LDS bytes at the column stride, with
   // bank conflicts: 10 x 10^7 UInt8 vecmat 44.9 us at 1 lane, 37.6 at 2)
@@ -989,6 +986,17 @@ int launch_flat_cols(const T* A, int64_t rows, int64_t cols, T* dst, int64_t ds,
   const int per = units != rows ? kFlatWordsPerLane : kFlatRowsPerLane;
   if (units != rows) L = 1;
   while (L < kWave && (int64_t)L * per < units) L <<= 1;
+  int64_t cpb = flat_cols_per_block_out(sizeof(T), rows, ds);
+  // 4-byte columns: a block takes one pass of the lanes when that still
+  // leaves at least 8 KiB per block (HIP graphs, us, sums over 10^9
+  // Float32: 8 rows 818 -> 727, 10 rows 824 -> 763, 12 rows 798 -> 731, 24
+  // rows 681 -> 656; 4 rows, 4 KiB blocks, 831 -> 970 is left as it was;
+  // Float64 4 rows 828 -> 841, the one 8-byte case it would change)
+  if (sizeof(T) == 4 && cpb * L > kDimBlock && (int64_t)(kDimBlock / L) * rows * (int64_t)sizeof(T) >= kFlatMinPassBytes)
+    cpb = kDimBlock / L;
+  const int64_t nblk = (cols + cpb - 1) / cpb;
+  const int64_t cap = sizeof(T) != 1 ? kFlatMaxBlocks : rows >= 256 ? kFlatMaxBlocksU8Long : kFlatMaxBlocksU8;
+  const dim3 grid((unsigned)kmin<int64_t>(nblk, cap));
 #define KF_FLAT(LL)                                                                                            \
   hipLaunchKernelGGL((reduce_cols_flat_kernel<T, Op, F, LL>), grid, dim3(kDimBlock), 0, stream, A, rows, cols, cpb, \
                      dst, ds, x, xs)
