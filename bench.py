@@ -239,6 +239,7 @@ def main():
                      "avg_launch_us": round(scan_s * 1e6, 2), "algorithmic_bytes_per_launch": 8 * N},
         "kernels": {
             "scan_gbps": round(scan_gbps, 1), "scan_frac_of_copy_ceiling": round(scan_gbps / copy_ceiling, 4),
+            "scan_frac_of_rw_bound": round(scan_gbps / ceil["rw_bound_gbps"], 4),
             "mapreduce_gbps": round(red_gbps, 1), "mapreduce_frac_of_read_ceiling": round(red_gbps / read_ceiling, 4),
             "mapreduce_frac_of_peak": round(red_gbps / PEAK_HBM_GBPS, 4), "mapreduce_avg_launch_us": round(red_s * 1e6, 2),
             "scan_gbps_best_batch": round(8 * N / scan_min / 1e9, 1),
@@ -249,7 +250,7 @@ def main():
         "wall_s_timed": round(wall, 4),
     }
     if args.all:
-        line["all_configs"] = bench_all(kf, dev, ceil, args.all_json)
+        line["all_configs"] = bench_all(kf, dev, ceil, args.all_json, cpu=not args.no_cpu)
     if args.sweep:
         line["sweep"] = bench_sweep(kf, dev, ceil)
     if args.sweep_2d:
@@ -301,9 +302,19 @@ def measure_ceilings(kf, dev, src):
     assert torch.equal(cbuf, src), "copy probe mismatch"
     for name, kind in (("read_kernel_gbps", K.BW_READ), ("read_tiled_gbps", K.BW_READ_TILED)):
         out[name] = nbytes / time_calls(probe(kind, sink), 20) / 1e9
+    # write-only: kf_fill of the same 1 GiB (16-byte stores, nothing read)
+    val = ctypes.create_string_buffer(b"\0" * 4, 4)
+
+    def fill():
+        K.check(L.kf_fill(ctypes.c_void_p(cbuf.data_ptr()), cbuf.numel(), ctypes.cast(val, ctypes.c_void_p), 4,
+                          ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)), "kf_fill")
+    out["write_kernel_gbps"] = nbytes / time_calls(fill, 20) / 1e9
     out["copy_ceiling_gbps"] = max(out[k] for k in ("copy_kernel_gbps", "copy_tiled_gbps", "copy_ordered_gbps",
                                                     "hipMemcpyDtoD_gbps"))
     out["read_ceiling_gbps"] = max(out["read_kernel_gbps"], out["read_tiled_gbps"])
+    # a copy cannot beat reading its bytes at the best read rate and writing
+    # them at the write rate one after the other: bytes/R_read + bytes/R_write
+    out["rw_bound_gbps"] = 2.0 / (1.0 / out["read_ceiling_gbps"] + 1.0 / out["write_kernel_gbps"])
     del cbuf, scratch
     return out
 
@@ -444,10 +455,40 @@ def bench_sweep_2d(kf, dev, ceil):
     return rows
 
 
+_HOST = {}
+_HOST_USED = set()
+
+
+def _host(t, out=False):
+    """Host (numpy) copy of a device tensor's storage span, cached by
+    tensor, or an uninitialised host array of its size for outputs."""
+    key = (t.data_ptr(), t.numel(), t.dtype, out)
+    _HOST_USED.add(key)
+    if key not in _HOST:
+        if out:
+            _HOST[key] = np.empty(tuple(t.shape), dtype=t.cpu()[:0].numpy().dtype)
+        else:
+            _HOST[key] = t.contiguous().cpu().numpy()
+    return _HOST[key]
+
+
+def _cpu_prep(make):
+    """The CPU baseline of one configuration: prep() copies its inputs
+    (the same seeded data the GPU row used) to the host and returns
+    run(threads), one call of the oracle's restatement of the reference's
+    CPU path (Base.accumulate! / Base.mapreduce, or their chunked
+    Threads.@threads variant)."""
+    def prep():
+        from oracle import oracle
+        return make(oracle, _host)
+    return prep
+
+
 def config_cases(kf, dev):
-    """(key, name, algorithmic bytes, fn, reps) for every BASELINE.json
-    configuration (C1-C5) and the extra rows (X1-X8); each case's inputs are
-    alive until the next case is requested."""
+    """(key, name, algorithmic bytes, fn, reps, elements, cpu prep or None)
+    for every BASELINE.json configuration (C1-C5) and the extra rows
+    (X1-X9); each case's inputs are alive until the next case is
+    requested."""
     import operator
     g = torch.Generator(device=dev).manual_seed(20261201)
 
@@ -459,66 +500,79 @@ def config_cases(kf, dev):
     yh = torch.empty_like(xh)
     oh = torch.empty(1, device=dev)
     th, trh = tmp_for(kf.Scan1D, xh), tmp_for(kf.MapReduce1D, xh)
-    yield "H1", "H1 scan F32 incl n=2^28 (bench step)", 8 * 2**28, lambda: kf.scan_("+", yh, xh, tmp=th), 20
+    yield "H1", "H1 scan F32 incl n=2^28 (bench step)", 8 * 2**28, lambda: kf.scan_("+", yh, xh, tmp=th), 20, \
+        2**28, _cpu_prep(lambda o, h: (lambda t: o.baseline_scan_add_f32(h(xh), h(yh, True), t)))
     yield "H2", "H2 mapreduce F32 n=2^28 (bench step)", 4 * 2**28, \
-        lambda: kf.mapreduce_(kf.identity, "+", oh, xh, tmp=trh), 20
+        lambda: kf.mapreduce_(kf.identity, "+", oh, xh, tmp=trh), 20, \
+        2**28, _cpu_prep(lambda o, h: (lambda t: o.baseline_sum_f32(h(xh), t)))
     del xh, yh
     x = torch.rand(10**6, device=dev, generator=g)
     y = torch.empty_like(x)
     t1 = tmp_for(kf.Scan1D, x)
-    yield "C1", "C1 scan F32 incl n=1e6", 8e6, lambda: kf.scan_("+", y, x, tmp=t1), 20
+    yield "C1", "C1 scan F32 incl n=1e6", 8e6, lambda: kf.scan_("+", y, x, tmp=t1), 20, \
+        10**6, _cpu_prep(lambda o, h: (lambda t: o.baseline_scan_add_f32(h(x), h(y, True), t)))
     del x, y
     xi = torch.randint(0, 16, (2**28,), device=dev, generator=g, dtype=torch.int32)
     yi = torch.empty_like(xi)
     t2 = tmp_for(kf.Scan1D, xi)
-    yield "C2i", "C2 scan Int32 incl n=2^28", 8 * 2**28, lambda: kf.scan_("+", yi, xi, tmp=t2), 20
-    yield "C2e", "C2 scan Int32 excl n=2^28", 8 * 2**28, lambda: kf.scan_("+", yi, xi, exclusive=True, tmp=t2), 20
+    yield "C2i", "C2 scan Int32 incl n=2^28", 8 * 2**28, lambda: kf.scan_("+", yi, xi, tmp=t2), 20, \
+        2**28, _cpu_prep(lambda o, h: (lambda t: o.baseline_scan_add_i32(h(xi), h(yi, True), False, t)))
+    yield "C2e", "C2 scan Int32 excl n=2^28", 8 * 2**28, lambda: kf.scan_("+", yi, xi, exclusive=True, tmp=t2), 20, \
+        2**28, _cpu_prep(lambda o, h: (lambda t: o.baseline_scan_add_i32(h(xi), h(yi, True), True, t)))
     o = torch.empty(1, device=dev, dtype=torch.int32)
     xr = torch.randint(-2**31, 2**31 - 1, (2**28,), device=dev, generator=g, dtype=torch.int32)
     t3 = tmp_for(kf.MapReduce1D, xr)
-    yield "C3c", "C3c mapreduce max Int32 n=2^28", 4 * 2**28, lambda: kf.mapreduce_(kf.identity, max, o, xr, tmp=t3), 20
+    yield "C3c", "C3c mapreduce max Int32 n=2^28", 4 * 2**28, lambda: kf.mapreduce_(kf.identity, max, o, xr, tmp=t3), 20, \
+        2**28, _cpu_prep(lambda o_, h: (lambda t: o_.baseline_max_i32(h(xr), t)))
     del xi, yi, xr
     xf = torch.randn(2**30, device=dev, generator=g)
     of = torch.empty(1, device=dev)
     t3f = tmp_for(kf.MapReduce1D, xf)
-    yield "C3a", "C3a mapreduce abs2,+ F32 n=2^30", 4 * 2**30, lambda: kf.mapreduce_(kf.abs2, "+", of, xf, tmp=t3f), 10
+    yield "C3a", "C3a mapreduce abs2,+ F32 n=2^30", 4 * 2**30, lambda: kf.mapreduce_(kf.abs2, "+", of, xf, tmp=t3f), 10, \
+        2**30, _cpu_prep(lambda o, h: (lambda t: o.baseline_sum_abs2(h(xf), t)))
     del xf
     xd = torch.randn(2**28, device=dev, generator=g, dtype=torch.float64)
     od = torch.empty(1, device=dev, dtype=torch.float64)
     t3d = tmp_for(kf.MapReduce1D, xd)
-    yield "C3b", "C3b mapreduce abs2,+ F64 n=2^28", 8 * 2**28, lambda: kf.mapreduce_(kf.abs2, "+", od, xd, tmp=t3d), 20
+    yield "C3b", "C3b mapreduce abs2,+ F64 n=2^28", 8 * 2**28, lambda: kf.mapreduce_(kf.abs2, "+", od, xd, tmp=t3d), 20, \
+        2**28, _cpu_prep(lambda o, h: (lambda t: o.baseline_sum_abs2(h(xd), t)))
     del xd
     ab = torch.empty(2**26, 2, device=dev)
     ab[:, 0].uniform_(0.9, 1.0, generator=g)
     ab[:, 1].normal_(generator=g)
     yab = torch.empty_like(ab)
     t4 = kf.get_allocation(kf.Scan1D, kf.identity, kf.affine, ab)
-    yield "C4", "C4 affine scan n=2^26", 16 * 2**26, lambda: kf.scan_(kf.affine, yab, ab, tmp=t4), 20
+    yield "C4", "C4 affine scan n=2^26", 16 * 2**26, lambda: kf.scan_(kf.affine, yab, ab, tmp=t4), 20, \
+        2**26, _cpu_prep(lambda o, h: (lambda t: o.baseline_scan_affine_f32(h(ab), h(yab, True), t)))
     del ab, yab
     t = torch.rand(2**28, device=dev, generator=g) * 2 - 1
     A1 = t.as_strided((4096, 65536), (1, 4096))
     t5 = kf.KernelBuffer(kf.MapReduce2D, 64 << 20, dev)  # >= every dims plan below
     d1 = torch.empty(65536, device=dev)
     yield "C5a", "C5a dims=1 4096x65536", 4 * 2**28 + 4 * 65536, \
-        lambda: kf.mapreduce_(kf.identity, "+", d1, A1, dims=1, tmp=t5), 20
+        lambda: kf.mapreduce_(kf.identity, "+", d1, A1, dims=1, tmp=t5), 20, \
+        2**28, _cpu_prep(lambda o, h: (lambda th: o.baseline_sum_dims_f32(h(t), 4096, 65536, 4096, 1, h(d1, True), th)))
     A2 = t.as_strided((65536, 4096), (1, 65536))
     d2 = torch.empty(65536, device=dev)
     yield "C5b", "C5b dims=2 65536x4096", 4 * 2**28 + 4 * 65536, \
-        lambda: kf.mapreduce_(kf.identity, "+", d2, A2, dims=2, tmp=t5), 20
+        lambda: kf.mapreduce_(kf.identity, "+", d2, A2, dims=2, tmp=t5), 20, \
+        2**28, _cpu_prep(lambda o, h: (lambda th: o.baseline_sum_dims_f32(h(t), 65536, 4096, 65536, 2, h(d2, True), th)))
     V1 = A1[:, ::2]
     d1v = torch.empty(32768, device=dev)
     yield "C5c", "C5c dims=1 view 4096x(65536/2)", 4 * 2**27 + 4 * 32768, \
-        lambda: kf.mapreduce_(kf.identity, "+", d1v, V1, dims=1, tmp=t5), 20
+        lambda: kf.mapreduce_(kf.identity, "+", d1v, V1, dims=1, tmp=t5), 20, \
+        2**27, _cpu_prep(lambda o, h: (lambda th: o.baseline_sum_dims_f32(h(t), 4096, 32768, 8192, 1, h(d1v, True), th)))
     V2 = A2[:, ::2]
     yield "C5d", "C5d dims=2 view 65536x(4096/2)", 4 * 2**27 + 4 * 65536, \
-        lambda: kf.mapreduce_(kf.identity, "+", d2, V2, dims=2, tmp=t5), 20
+        lambda: kf.mapreduce_(kf.identity, "+", d2, V2, dims=2, tmp=t5), 20, \
+        2**27, _cpu_prep(lambda o, h: (lambda th: o.baseline_sum_dims_f32(h(t), 65536, 2048, 131072, 2, h(d2, True), th)))
     # beyond the BASELINE configs: vector operands and layouts off the vector path
     xv = torch.rand(4096, device=dev, generator=g)
     yield "X1", "X1 matvec 65536x4096 F32", 4 * 2**28 + 8 * 65536 + 4 * 4096, \
-        lambda: kf.matvec_(operator.mul, "+", d2, A2, xv, tmp=t5), 20
+        lambda: kf.matvec_(operator.mul, "+", d2, A2, xv, tmp=t5), 20, 2**28, None
     xr = torch.rand(4096, device=dev, generator=g)
     yield "X2", "X2 vecmat 4096x65536 F32", 4 * 2**28 + 8 * 65536, \
-        lambda: kf.vecmat_(operator.mul, "+", d1, xr, A1, tmp=t5), 20
+        lambda: kf.vecmat_(operator.mul, "+", d1, xr, A1, tmp=t5), 20, 2**28, None
     del t, A1, A2, V1, V2
     xs = torch.rand(2**28, device=dev, generator=g)
     ys = torch.empty_like(xs)
@@ -526,36 +580,76 @@ def config_cases(kf, dev):
     of1 = torch.empty(1, device=dev)
     t3s = tmp_for(kf.MapReduce1D, xs)
     yield "X3", "X3 scan F32 unaligned view x[1:] n=2^28-1", 8 * (2**28 - 1), \
-        lambda: kf.scan_("+", ys[1:], xs[1:], tmp=ts), 20
+        lambda: kf.scan_("+", ys[1:], xs[1:], tmp=ts), 20, 2**28 - 1, None
     yield "X8", "X8 scan F32 x[1:] -> aligned dst n=2^28-1", 8 * (2**28 - 1), \
-        lambda: kf.scan_("+", ys[:-1], xs[1:], tmp=ts), 20
+        lambda: kf.scan_("+", ys[:-1], xs[1:], tmp=ts), 20, 2**28 - 1, None
     yield "X4", "X4 mapreduce F32 unaligned view x[1:]", 4 * (2**28 - 1), \
-        lambda: kf.mapreduce_(kf.identity, "+", of1, xs[1:], tmp=t3s), 20
+        lambda: kf.mapreduce_(kf.identity, "+", of1, xs[1:], tmp=t3s), 20, 2**28 - 1, None
     del xs, ys
     xd = torch.rand(2**27, device=dev, generator=g, dtype=torch.float64)
     yd = torch.empty_like(xd)
     td = tmp_for(kf.Scan1D, xd)
-    yield "X5", "X5 scan F64 incl n=2^27", 16 * 2**27, lambda: kf.scan_("+", yd, xd, tmp=td), 20
+    yield "X5", "X5 scan F64 incl n=2^27", 16 * 2**27, lambda: kf.scan_("+", yd, xd, tmp=td), 20, 2**27, None
     del xd, yd
     xb = torch.randint(0, 255, (2**30,), device=dev, generator=g, dtype=torch.uint8)
     yb = torch.empty_like(xb)
     tb = tmp_for(kf.Scan1D, xb)
-    yield "X6", "X6 scan UInt8 incl n=2^30", 2 * 2**30, lambda: kf.scan_("+", yb, xb, tmp=tb), 20
+    yield "X6", "X6 scan UInt8 incl n=2^30", 2 * 2**30, lambda: kf.scan_("+", yb, xb, tmp=tb), 20, 2**30, None
     del xb, yb
     for n, label in ((10**5, "10^5"), (2**21, "2^21"), (2**23, "2^23")):
         xs = torch.rand(n, device=dev, generator=g)
         ys = torch.empty_like(xs)
         ts = tmp_for(kf.Scan1D, xs)
-        yield f"X7-{label}", f"X7 scan F32 incl n={label}", 8 * n, lambda: kf.scan_("+", ys, xs, tmp=ts), 20
+        yield f"X7-{label}", f"X7 scan F32 incl n={label}", 8 * n, lambda: kf.scan_("+", ys, xs, tmp=ts), 20, n, None
+    # the reference's non-commutative test case (test/tests/scan/scan_test.jl:22-33):
+    # QuaternionF64 at its n = 10^6 and QuaternionF32 at 2^26, Hamilton products
+    for n, dt, label in ((10**6, torch.float64, "QuaternionF64 n=10^6"), (2**26, torch.float32, "QuaternionF32 n=2^26")):
+        q = torch.randn(n, 4, device=dev, generator=g, dtype=dt)
+        q = q / q.norm(dim=1, keepdim=True)
+        yq = torch.empty_like(q)
+        tq = kf.get_allocation(kf.Scan1D, kf.identity, "*", q)
+        yield f"X9-{label.split()[0]}", f"X9 scan {label}", 2 * q.numel() * q.element_size(), \
+            lambda: kf.scan_("*", yq, q, tmp=tq), 20, n, None
+        del q, yq
 
 
-def bench_all(kf, dev, ceil, json_path=None):
+def _cpu_seconds(run, budget_s):
+    """Seconds per call of run(): one untimed call (page faults of the
+    output), then calls until budget_s has passed (at least one)."""
+    run()
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        run()
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or reps >= 200:
+            return el / reps, reps
+
+
+def cpu_row(cpu_prep, bytes_, elems, threads, budget_s=1.0):
+    """The reference's CPU path for one configuration on this host, on the
+    GPU row's own data: `threads` OpenMP threads (chunked) and one thread
+    (sequential), each timed over about budget_s of calls."""
+    _HOST_USED.clear()
+    run = cpu_prep()
+    tm, nm = _cpu_seconds(lambda: run(threads), budget_s)
+    t1, n1 = _cpu_seconds(lambda: run(1), budget_s)
+    for k in [k for k in _HOST if k not in _HOST_USED]:  # keep only this case's host copies
+        del _HOST[k]
+    return {"kind": "port", "threads": threads, "gbps": round(bytes_ / tm / 1e9, 3),
+            "gelems_per_s": round(elems / tm / 1e9, 4), "ms": round(tm * 1e3, 3), "calls": nm,
+            "single_thread_gbps": round(bytes_ / t1 / 1e9, 3), "single_thread_gelems_per_s": round(elems / t1 / 1e9, 4),
+            "single_thread_ms": round(t1 * 1e3, 3), "single_thread_calls": n1}
+
+
+def bench_all(kf, dev, ceil, json_path=None, cpu=True):
     """Every configuration of config_cases: GB/s, % of peak, % of the ceiling
     of its kind (scans: the copy ceiling; reductions: the read ceiling), and
     the HBM traffic ratio recorded by rocprofv3 --pmc when profiles/ holds it."""
     rows = []
     traffic = load_config_traffic()
-    for key, name, bytes_, fn, reps in config_cases(kf, dev):
+    threads = max(1, min(16, os.cpu_count() or 1))
+    for key, name, bytes_, fn, reps, elems, cpu_prep in config_cases(kf, dev):
         # captured in a HIP graph so that host launch overhead does not hide
         # the kernel time of the small configurations
         _mark(kf, dev, True)
@@ -574,11 +668,20 @@ def bench_all(kf, dev, ceil, json_path=None):
         kind = "copy" if " scan " in f" {name} " else "read"
         c = ceil[f"{kind}_ceiling_gbps"]
         row = {"config": name, "us": round(s * 1e6, 2), "gbps": round(gb, 1),
+               "gelems_per_s": round(elems / s / 1e9, 3),
                "frac_peak": round(gb / PEAK_HBM_GBPS, 4), "ceiling": kind, "frac_ceiling": round(gb / c, 4),
                "hbm_traffic_ratio": traffic.get(key)}
+        if kind == "copy":
+            row["frac_rw_bound"] = round(gb / ceil["rw_bound_gbps"], 4)
+        if cpu and cpu_prep is not None:
+            row["cpu"] = cpu_row(cpu_prep, bytes_, elems, threads)
         rows.append(row)
-        log(f"  {name:48s} {s*1e6:10.1f} us {gb:8.0f} GB/s  {gb/c*100:5.1f}% of {kind} ceiling"
-            + (f"  traffic {row['hbm_traffic_ratio']:.4f}x" if row["hbm_traffic_ratio"] else ""))
+        log(f"  {name:48s} {s*1e6:10.1f} us {gb:8.0f} GB/s {elems / s / 1e9:8.2f} Gelem/s "
+            f"{gb/c*100:5.1f}% of {kind} ceiling"
+            + (f"  traffic {row['hbm_traffic_ratio']:.4f}x" if row["hbm_traffic_ratio"] else "")
+            + (f"  | CPU {row['cpu']['threads']} thr {row['cpu']['gbps']:.1f} GB/s, 1 thr "
+               f"{row['cpu']['single_thread_gbps']:.1f} GB/s" if "cpu" in row else ""))
+    _HOST.clear()
     if json_path:
         os.makedirs(os.path.dirname(os.path.abspath(json_path)), exist_ok=True)
         with open(json_path, "w") as fh:
@@ -700,7 +803,7 @@ def pmc_run(kf, dev):
     end()
     torch.cuda.synchronize()
     del a, b
-    for key, name, bytes_, fn, reps in config_cases(kf, dev):
+    for key, name, bytes_, fn, reps, *_ in config_cases(kf, dev):
         fn()  # outside the counted segment: first-call setup
         torch.cuda.synchronize()
         begin()

@@ -19,7 +19,9 @@
  *
  * Return codes: KF_OK, KF_EINVAL (bad enum, shape, stride or alignment),
  * KF_ENOSCRATCH (scratch missing or too small), KF_EHIP (a HIP error; the
- * text is in kf_last_error()). n == 0 is a successful no-op.
+ * text is in kf_last_error()), KF_EGIVEUP (an earlier call's kernel gave
+ * up waiting on its scratch buffer: see kf_async_status; the call that
+ * returns it queued nothing). n == 0 is a successful no-op.
  *
  * Semantics follow Julia Base, as the reference's tests require
  * (reference test/tests/scan/scan_test.jl:1-125 compares against
@@ -41,7 +43,8 @@ typedef enum {
   KF_OK = 0,
   KF_EINVAL = 1,
   KF_ENOSCRATCH = 2,
-  KF_EHIP = 3
+  KF_EHIP = 3,
+  KF_EGIVEUP = 4
 } kf_status;
 
 /* Binary operator `op` of scan!/mapreduce. KF_OP_AFFINE is the
@@ -109,6 +112,27 @@ const char* kf_last_error(void);
  * node, so it is safe inside captured graphs). */
 int kf_scratch_reset(void* scratch, size_t bytes, void* stream);
 
+/* Give-up reports (no counterpart in the reference, whose kernels spin
+ * without bound). The scan's lookback and the reduction's fold wait on
+ * other workgroups through the scratch buffer; only out-of-order dispatch,
+ * a corrupted buffer or overlapping calls on one buffer can keep them
+ * waiting, and then they stop after a poll budget instead of hanging the
+ * GPU. A kernel that stops stores nothing as a result and raises a flag in
+ * its scratch header (kf_scan_scratch_status / kf_reduce_scratch_status)
+ * and in a pinned, host-mapped report word of the library. The report
+ * surfaces without any synchronisation: the next compute entry point
+ * (kf_scan*, kf_reduce*) called after the failed kernel has finished
+ * returns KF_EGIVEUP without queuing anything and clears the report, and
+ * kf_async_status reads and clears it (after a stream synchronisation it
+ * covers every kernel queued before it). Like the asynchronous errors of
+ * HIP itself, the report belongs to the process, not to one buffer or
+ * stream. The report word is allocated (pinned host memory, 256 bytes,
+ * once per process) by kf_init or by the first call of any compute entry
+ * point except kf_reduce_noalloc, which never allocates: call kf_init at
+ * set-up to have its give-ups reported too. */
+int kf_init(void);
+int kf_async_status(int* gave_up);
+
 /* ---------------------------------------------------------------- scan ----
  * dst[i] = g(f(src[0]) op ... op f(src[i]))           (exclusive = 0)
  * dst[0] = g(identity(op)); dst[i] = g(incl[i-1])      (exclusive = 1)
@@ -175,11 +199,6 @@ int kf_scan_shaped(kf_op op, kf_map f, kf_post g, kf_dtype dt, int exclusive,
  * valid again; kf_scratch_reset (a zero fill) also clears it. */
 int kf_scan_scratch_status(void* scratch, void* stream, int* gave_up);
 
-/* Test hook: on the calling host thread, later kf_scan calls leave tile
- * `tile` unpublished and give up after `spin_limit` polls, so that the
- * give-up path runs with every kernel exiting normally; tile < 0 restores
- * normal operation. */
-int kf_debug_scan_giveup(int64_t tile, uint32_t spin_limit);
 
 /* -------------------------------------------------------------- reduce ----
  * dst[0] = f(src[0]) op f(src[stride]) op ... (n terms), written on device.
@@ -195,6 +214,14 @@ size_t kf_reduce_scratch_bytes(kf_dtype dt, int64_t n);
 int kf_reduce(kf_op op, kf_map f, kf_dtype dt,
               const void* src, int64_t n, int64_t stride,
               void* dst, void* scratch, size_t scratch_bytes, void* stream);
+
+/* After a fold give-up (see kf_async_status) dst is left untouched and the
+ * buffer is already valid for the next call (the fold's epoch skips past
+ * every slot of the failed call). kf_reduce_scratch_status synchronises
+ * `stream`, sets *gave_up = 1 if a call on this reduction scratch buffer
+ * gave up since the last query, and clears that flag. No counterpart in the
+ * reference (whose finisher, mapreduce1d_kernel.jl:58-92, spins unbounded). */
+int kf_reduce_scratch_status(void* scratch, void* stream, int* gave_up);
 
 /* ------------------------------------------------------------- reduce2 ----
  * dst[0] = f(x[0], y[0]) op ... op f(x[n-1], y[n-1]) (element strides xs, ys).

@@ -38,6 +38,7 @@ shapes are fixed for gfx950. Calls are asynchronous on torch's current stream ex
 import contextlib
 import ctypes
 import operator
+import weakref
 
 import torch
 
@@ -47,7 +48,7 @@ __all__ = [
     "ArgumentError", "KernelBuffer", "AffineOp", "affine", "identity", "abs2", "sqdiff", "wsq", "expdiff", "prod3",
     "scan_shape",
     "scan", "scan_", "mapreduce", "mapreduce_", "get_allocation", "vcopy_", "setvalue_", "scan_status",
-    "maximum", "maximum_", "minimum", "mapreduce1d", "mapreduce1d_", "mapreduce2d", "mapreduce2d_",
+    "check_async", "maximum", "maximum_", "minimum", "mapreduce1d", "mapreduce1d_", "mapreduce2d", "mapreduce2d_",
     "mapreducedims", "mapreducedims_",
     "Scan1D", "MapReduce1D", "MapReduce2D", "MatVec", "VecMat", "matvec", "matvec_", "vecmat", "vecmat_",
 ]
@@ -236,6 +237,8 @@ class KernelBuffer:
         off = (-raw.data_ptr()) % 256
         self._raw = raw
         self.arr = raw[off:off + self.nbytes]
+        if kind == Scan1D:
+            _scan_buffers.add(self)
 
     @property
     def ptr(self):
@@ -246,6 +249,39 @@ class KernelBuffer:
 
 
 _default_tmp = {}
+# every live Scan1D buffer, re-validated when the library reports a give-up
+_scan_buffers = weakref.WeakSet()
+
+
+def _revalidate_scan_buffers():
+    """Clear the sticky give-up flag of every live Scan1D buffer (each query
+    synchronises its device's current stream); returns a sentence for the
+    error message saying which scans are affected."""
+    hit = 0
+    for buf in list(_scan_buffers):
+        flag = ctypes.c_int(0)
+        with _on(buf.arr.device):
+            rc = _L.lib().kf_scan_scratch_status(buf.ptr, _raw_stream(buf.arr.device), ctypes.byref(flag))
+        if rc == _L.KF_OK and flag.value:
+            hit += 1
+    if hit:
+        return (f"{hit} scan scratch buffer(s) had given up: the scans on them since then stored nothing; "
+                "they are valid again")
+    return "(a reduction fold gave up: its destination was left untouched; its buffer is valid again)"
+
+
+def check_async():
+    """Raise KernelForgeError if a kernel queued earlier gave up waiting on
+    its scratch buffer (kf_async_status), after re-validating every scan
+    buffer. Non-blocking: it covers the kernels that have finished, so call
+    it after a synchronisation to cover all of them. No counterpart in the
+    reference, whose waits are unbounded."""
+    flag = ctypes.c_int(0)
+    _L.check(_L.lib().kf_async_status(ctypes.byref(flag)), "check_async")
+    if flag.value:
+        raise _L.KernelForgeError(
+            "a scan lookback or reduction fold gave up waiting on its scratch buffer; its results are invalid. "
+            + _revalidate_scan_buffers())
 
 
 def _scratch(kind, need, device, tmp, stream=None):
@@ -341,9 +377,10 @@ def scan_(*args, exclusive=False, tmp=None, g=None, check=False, **tuning):
     dst[i] = f(src[1]) op ... op f(src[i]) (inclusive, the reference's only
     mode), or the exclusive variant dst[1] = identity(op),
     dst[i] = inclusive[i-1]. In place (dst is src) is allowed.
-    check=True synchronises after the launch and raises KernelForgeError if
-    the lookback gave up (see scan_status), which a successful launch does
-    not rule out. Nitem / workgroup select the nearest compiled tile shape
+    A lookback that gives up (see scan_status) is never silent: the next
+    call into the library after that kernel has finished raises
+    KernelForgeError, and so do check_async() and the full mapreduce's
+    read-back; check=True synchronises after the launch and raises at once. Nitem / workgroup select the nearest compiled tile shape
     (scan_shape); a tmp for such a call comes from
     get_allocation(Scan1D, f, op, src, workgroup, blocks) or is sized for
     the shape (ArgumentError if it is too small)."""
@@ -370,9 +407,11 @@ def scan_(*args, exclusive=False, tmp=None, g=None, check=False, **tuning):
                               _stream_ptr(src))
     _L.check(rc, "scan!")  # g is applied by the kernel as each value is stored
     if check and scan_status(buf):
+        # this give-up is raised here, so its pending report is consumed
+        _L.check(_L.lib().kf_async_status(ctypes.byref(ctypes.c_int(0))), "scan!")
         raise _L.KernelForgeError(
             "scan!: a tile's lookback gave up waiting for its predecessor; the results are invalid "
-            "(the scratch buffer has been re-validated)")
+            "(the scratch buffer has been re-validated) " + _revalidate_scan_buffers())
     return dst
 
 
@@ -380,7 +419,8 @@ def scan_status(tmp):
     """True if a scan! on the Scan1D buffer `tmp` gave up waiting for a
     predecessor tile since the last query (its results are then invalid:
     only out-of-order workgroup dispatch, a corrupted buffer or overlapping
-    calls can cause it; until the query, later scans on `tmp` do nothing).
+    calls can cause it; until the query, later scans on `tmp` store
+    nothing, and each of them is reported by the next library call).
     Clears the flag and re-validates the buffer; synchronises the current
     stream. No counterpart in the reference."""
     if not isinstance(tmp, KernelBuffer) or tmp.kind != Scan1D:
@@ -537,7 +577,9 @@ def _reduce_dim_into(fc, opc, dst, dst_stride, src, rows, cols, cs, dim, tmp, ba
 
 
 def _to_scalar(t):
-    return t.item()
+    v = t.item()  # synchronises: every kernel queued so far has finished
+    check_async()
+    return v
 
 
 def mapreduce(f, op, src, dims=None, g=None, tmp=None, **tuning):

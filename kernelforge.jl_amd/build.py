@@ -17,7 +17,7 @@ OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libkfhip.so")
 # instrumented scan (per-tile timestamps, KF_TIMELINE) for bench.py --timeline
 TIMELINE_LIB = os.path.join(HERE, "libkfhip_timeline.so")
-TIMELINE_SOURCES = ["kf_api.hip", "kf_scan.hip"]
+TIMELINE_SOURCES = ["kf_api.hip", "kf_scan.hip", "kf_reduce.hip"]
 DRIVER = os.path.join(HERE, "kf_driver")
 SOURCES = ["kf_api.hip", "kf_scan.hip", "kf_reduce.hip", "kf_reduce_dims.hip", "kf_matvec.hip", "kf_copy.hip"]
 

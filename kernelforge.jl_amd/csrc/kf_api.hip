@@ -1,4 +1,6 @@
 // Error reporting, validation and device queries shared by the entry points.
+#include <atomic>
+#include <mutex>
 #include <stdarg.h>
 #include <stdio.h>
 
@@ -69,6 +71,59 @@ int kf_device_cu_count() {
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
   if (dev < kMaxDevices) g_cu_count[dev] = cus;
   return cus;
+}
+
+// The give-up report word: pinned, host-mapped and coherent, so a kernel's
+// system-scope store is visible to a plain host read once it lands. One per
+// process, shared by every device (pinned host memory is portable).
+namespace {
+std::mutex g_mbox_mu;
+std::atomic<uint32_t*> g_mbox{nullptr};
+bool g_mbox_failed = false;
+}  // namespace
+
+uint32_t* kf_mailbox_peek() { return g_mbox.load(std::memory_order_acquire); }
+
+uint32_t* kf_mailbox() {
+  uint32_t* p = g_mbox.load(std::memory_order_acquire);
+  if (p) return p;
+  std::lock_guard<std::mutex> lock(g_mbox_mu);
+  p = g_mbox.load(std::memory_order_relaxed);
+  if (p || g_mbox_failed) return p;
+  void* q = nullptr;
+  if (hipHostMalloc(&q, 256, hipHostMallocPortable | hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess ||
+      !q) {
+    (void)hipGetLastError();
+    g_mbox_failed = true;
+    return nullptr;
+  }
+  *(volatile uint32_t*)q = 0;
+  p = (uint32_t*)q;
+  g_mbox.store(p, std::memory_order_release);
+  return p;
+}
+
+int kf_take_giveup(const char* who) {
+  uint32_t* p = kf_mailbox_peek();
+  if (!p || __atomic_load_n(p, __ATOMIC_ACQUIRE) == 0) return KF_OK;
+  if (__atomic_exchange_n(p, 0u, __ATOMIC_ACQ_REL) == 0) return KF_OK;
+  return kf_set_error(KF_EGIVEUP,
+                      "%s: not run: a kernel queued by an earlier call gave up waiting on its scratch buffer, so "
+                      "that call's results are invalid (a scan buffer stays inert until kf_scan_scratch_status "
+                      "clears it)",
+                      who);
+}
+
+extern "C" int kf_init(void) {
+  if (!kf_mailbox()) return kf_set_error(KF_EHIP, "kf_init: could not allocate the pinned give-up report word");
+  return KF_OK;
+}
+
+extern "C" int kf_async_status(int* gave_up) {
+  if (!gave_up) return kf_set_error(KF_EINVAL, "kf_async_status: null pointer");
+  uint32_t* p = kf_mailbox_peek();
+  *gave_up = p && __atomic_exchange_n(p, 0u, __ATOMIC_ACQ_REL) != 0;
+  return KF_OK;
 }
 
 extern "C" int kf_version(void) { return KF_VERSION; }

@@ -226,6 +226,14 @@ __device__ inline void st_agent(uint64_t* p, uint64_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Give-up report: a kernel that stopped waiting on its scratch buffer (a
+// scan lookback or a reduction fold past its poll budget) stores 1 into the
+// library's host-mapped report word, which every later entry point reads
+// on the host without synchronising (kf_async_status). Null: no report.
+__device__ inline void report_giveup(uint32_t* mbox) {
+  if (mbox) __hip_atomic_store(mbox, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 // 16-byte streaming accesses.
 typedef uint32_t v4u32 __attribute__((ext_vector_type(4)));
 __device__ inline uint4 ld_stream(const uint4* p) {
@@ -258,3 +266,10 @@ int kf_check_launch(const char* what);
 size_t kf_dtype_size(kf_dtype dt);
 int kf_validate_op(kf_op op, kf_map f, kf_dtype dt, int allow_affine);
 int kf_device_cu_count();
+// Host-mapped give-up report word (allocated on first use; null if that
+// failed). kf_mailbox_peek never allocates (for kf_reduce_noalloc).
+uint32_t* kf_mailbox();
+uint32_t* kf_mailbox_peek();
+// KF_EGIVEUP (and clears the report) if a kernel queued by an earlier call
+// has given up since the last report; KF_OK otherwise. Non-blocking.
+int kf_take_giveup(const char* who);

@@ -13,6 +13,8 @@
 // per thread, 5.2 TB/s for grid-stride copies and 4.8-5.5 TB/s for
 // hipMemcpyDtoD.
 #include <atomic>
+#include <chrono>
+#include <unistd.h>
 
 #include "kf_common.h"
 
@@ -118,8 +120,24 @@ __global__ __launch_bounds__(256) void read_probe_kernel(const uint4* src, int64
 using namespace kf;
 
 namespace {
+// Flag values of the ordered copy: a per-process nonce (time and pid) in the
+// high 32 bits and a call counter in the low ones, so that flags left in a
+// reused scratch buffer by an earlier call or an earlier process never
+// match the current call's value (a match would let a tile skip its wait and
+// turn the probe into an unordered copy).
 std::atomic<uint64_t> g_probe_epoch{0};
+uint64_t probe_epoch() {
+  static const uint64_t nonce = [] {
+    const uint64_t t = (uint64_t)std::chrono::steady_clock::now().time_since_epoch().count();
+    uint64_t h = t ^ ((uint64_t)getpid() << 17) ^ 0x9e3779b97f4a7c15ull;
+    h ^= h >> 31;
+    h *= 0xbf58476d1ce4e5b9ull;
+    h ^= h >> 29;
+    return (h & 0xffffffff00000000ull) | 0x100000000ull;  // never 0 in the high half
+  }();
+  return nonce | ((g_probe_epoch.fetch_add(1) + 1) & 0xffffffffull);
 }
+}  // namespace
 
 extern "C" size_t kf_bw_probe_scratch_bytes(size_t bytes) {
   return 256 + (bytes / 16 + 255) / 256 * kProbeFlagWords * sizeof(uint64_t);
@@ -150,7 +168,7 @@ extern "C" int kf_bw_probe(int kind, void* dst, const void* src, size_t bytes, v
         return kf_set_error(KF_ENOSCRATCH, "kf_bw_probe: the ordered copy needs %zu bytes of scratch",
                             kf_bw_probe_scratch_bytes(bytes));
       if (tiles > 0x7fffffffLL) return kf_set_error(KF_EINVAL, "kf_bw_probe: buffer exceeds the grid limit");
-      const uint64_t epoch = g_probe_epoch.fetch_add(1) + 1;
+      const uint64_t epoch = probe_epoch();
       hipLaunchKernelGGL(copy_ordered_kernel, dim3((unsigned)tiles), dim3(256), 0, s, d, p, nvec,
                          (uint64_t*)((uint8_t*)scratch + 256), epoch);
       return kf_check_launch("copy_ordered_kernel");

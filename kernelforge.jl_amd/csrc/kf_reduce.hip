@@ -27,6 +27,28 @@
 #include "kf_reduce.h"
 
 namespace kf {
+#ifdef KF_TIMELINE
+// Instrumented build only: every workgroup of a folding one-launch
+// reduction records, by thread 0, three 100 MHz realtime stamps (start,
+// its loads folded into its partial, slot published or fold done), its XCD
+// and its HW_ID word at g_red_timeline + workgroup * kRedTimelineWords.
+__device__ uint64_t* g_red_timeline = nullptr;
+constexpr int kRedTimelineWords = 6;
+__device__ inline void red_timeline(uint64_t t0, uint64_t t1) {
+  if (threadIdx.x == 0 && g_red_timeline) {
+    uint64_t* w = g_red_timeline + (int64_t)blockIdx.x * kRedTimelineWords;
+    w[0] = t0;
+    w[1] = t1;
+    w[2] = __builtin_amdgcn_s_memrealtime();
+    w[3] = __builtin_amdgcn_s_getreg((3 << 11) | 20);  // HW_REG_XCC_ID[3:0]
+    w[4] = __builtin_amdgcn_s_getreg((31 << 11) | 4);  // HW_REG_HW_ID
+    w[5] = gridDim.x;
+  }
+}
+#define KF_RED_STAMP(v) const uint64_t v = __builtin_amdgcn_s_memrealtime()
+#else
+#define KF_RED_STAMP(v)
+#endif
 // ---------------------------------------------------------------------------
 // Full reduction, stage 1: grid-stride over 16-byte vectors. An unaligned
 // head and the ragged tail are folded in by workgroup 0, so any
@@ -125,11 +147,29 @@ constexpr int kOnceVecs = kRedBlock * kOnceUnroll;
 // which the waiter's completion depends on. Slots of older calls never
 // match. Only one workgroup ever waits, so progress needs no co-residency;
 // a bounded spin (only a corrupted or concurrently shared buffer can
-// exhaust it) keeps a bad buffer from hanging the GPU.
+// exhaust it) keeps a bad buffer from hanging the GPU, and its exhaustion
+// is reported, never passed off as a result (see the give-up branch).
 constexpr uint32_t kFoldSpinLimit = 1u << 22;
+// The fold's give-up controls: the host-mapped report word, the waiter's
+// poll budget and, in the instrumented library only, a workgroup that
+// withholds its slot (kf_debug_reduce_giveup) so that the give-up path can
+// be tested with every kernel exiting normally.
+struct FoldCtl {
+  uint32_t* mbox;
+  uint32_t limit;
+  int withhold;
+};
+#ifdef KF_TIMELINE
+thread_local int g_fold_withhold = -1;
+thread_local uint32_t g_fold_limit = kFoldSpinLimit;
+#else
+constexpr int g_fold_withhold = -1;
+constexpr uint32_t g_fold_limit = kFoldSpinLimit;
+#endif
+inline FoldCtl fold_ctl() { return FoldCtl{kf_mailbox_peek(), g_fold_limit, g_fold_withhold}; }
 __device__ inline uint32_t fold_epoch(const uint64_t* hdr) { return threadIdx.x == 0 ? (uint32_t)hdr[0] : 0u; }
 template <class T, class Op>
-__device__ inline void fold_partial(T part, T* out, uint64_t* hdr, T* s_wave, uint32_t hdr0) {
+__device__ inline void fold_partial(T part, T* out, uint64_t* hdr, T* s_wave, uint32_t hdr0, FoldCtl ctl) {
   constexpr int W = Words<T>::W;
   constexpr int PER = kFoldMax / kRedBlock;
   __shared__ uint32_t s_tag;
@@ -143,7 +183,7 @@ __device__ inline void fold_partial(T part, T* out, uint64_t* hdr, T* s_wave, ui
   uint64_t* slots = hdr + 256 / sizeof(uint64_t);
   const int last = (int)gridDim.x - 1;
   if ((int)blockIdx.x != last) {
-    if (tid == 0) {
+    if (tid == 0 && (int)blockIdx.x != ctl.withhold) {
       const Words<T> w = to_words(part);
 #pragma unroll
       for (int i = 0; i < W; ++i) st_agent(slots + 2 * blockIdx.x + i, ((uint64_t)tag << 32) | w.w[i]);
@@ -159,7 +199,8 @@ __device__ inline void fold_partial(T part, T* out, uint64_t* hdr, T* s_wave, ui
     v[k] = id;
     done[k] = k * kRedBlock + tid >= last;
   }
-  for (uint32_t polls = 0; polls < kFoldSpinLimit; ++polls) {
+  bool complete = false;
+  for (uint32_t polls = 0; polls < ctl.limit; ++polls) {
     uint64_t d[PER][W];
 #pragma unroll
     for (int k = 0; k < PER; ++k)
@@ -185,8 +226,23 @@ __device__ inline void fold_partial(T part, T* out, uint64_t* hdr, T* s_wave, ui
           all = false;
         }
       }
-    if (__syncthreads_and(all)) break;
+    if (__syncthreads_and(all)) {
+      complete = true;
+      break;
+    }
     __builtin_amdgcn_s_sleep(1);
+  }
+  if (!complete) {
+    // Gave up: out[0] keeps its old value. The flag (header word 1) stays
+    // set for kf_reduce_scratch_status, the report word tells the host,
+    // and the epoch skips one value so that no slot this call's workgroups
+    // published (or publish late) reads as current in the next call.
+    if (tid == 0) {
+      hdr[1] = 1;
+      hdr[0] = tag + 1u;
+      report_giveup(ctl.mbox);
+    }
+    return;
   }
   T acc = v[0];
 #pragma unroll
@@ -201,10 +257,11 @@ __device__ inline void fold_partial(T part, T* out, uint64_t* hdr, T* s_wave, ui
 
 template <class T, class Op, class Map, bool FOLD = false, int U = kOnceUnroll>
 __global__ __launch_bounds__(kRedBlock) void reduce_once_kernel(const T* src, int64_t n, int64_t head,
-                                                                int64_t nvec, T* out, uint64_t* fold_hdr) {
+                                                                int64_t nvec, T* out, uint64_t* fold_hdr, FoldCtl ctl) {
   constexpr int EPV = 16 / (int)sizeof(T);
   __shared__ T s_wave[kRedWaves];
   const int tid = threadIdx.x;
+  KF_RED_STAMP(tl_start);
   const uint32_t hdr0 = FOLD ? fold_epoch(fold_hdr) : 0u;  // fold tag, read ahead of the data
   const uint4* v = reinterpret_cast<const uint4*>(src + head);
   const int64_t base = (int64_t)blockIdx.x * (kRedBlock * U) + tid;
@@ -217,6 +274,7 @@ __global__ __launch_bounds__(kRedBlock) void reduce_once_kernel(const T* src, in
   for (int u = 0; u < U; ++u)
     if (base + u * kRedBlock < nvec) f.add(r[u]);
   T acc = f.total();
+  KF_RED_STAMP(tl_loaded);
   if (blockIdx.x == 0) {
     const int64_t tail0 = head + nvec * EPV;
     if (tid < head) acc = Op::combine(acc, Map::apply(src[tid]));
@@ -226,7 +284,10 @@ __global__ __launch_bounds__(kRedBlock) void reduce_once_kernel(const T* src, in
   if constexpr (!FOLD) {
     if (tid == 0) out[blockIdx.x] = part;  // a partial, or the result when gridDim.x == 1
   } else {
-    fold_partial<T, Op>(part, out, fold_hdr, s_wave, hdr0);  // out is the result
+    fold_partial<T, Op>(part, out, fold_hdr, s_wave, hdr0, ctl);  // out is the result
+#ifdef KF_TIMELINE
+    red_timeline(tl_start, tl_loaded);
+#endif
   }
 }
 
@@ -247,10 +308,11 @@ constexpr int64_t kChunkMinVecs = (int64_t)1 << 24;
 constexpr int kChunkUnroll = 16;
 template <class T, class Op, class Map, int U>
 __global__ __launch_bounds__(kRedBlock) void reduce_chunk_kernel(const T* src, int64_t n, int64_t head, int64_t nvec,
-                                                                 int64_t chunk, T* out, uint64_t* fold_hdr) {
+                                                                 int64_t chunk, T* out, uint64_t* fold_hdr, FoldCtl ctl) {
   constexpr int EPV = 16 / (int)sizeof(T);
   __shared__ T s_wave[kRedWaves];
   const int tid = threadIdx.x;
+  KF_RED_STAMP(tl_start);
   const uint32_t hdr0 = fold_epoch(fold_hdr);  // fold tag, read ahead of the data
   const uint4* v = reinterpret_cast<const uint4*>(src + head);
   const int64_t b0 = (int64_t)blockIdx.x * chunk;
@@ -274,13 +336,17 @@ __global__ __launch_bounds__(kRedBlock) void reduce_chunk_kernel(const T* src, i
       if (i + u * kRedBlock < b1) f.add(r[u]);
   }
   T acc = f.total();
+  KF_RED_STAMP(tl_loaded);
   if (blockIdx.x == 0) {
     const int64_t tail0 = head + nvec * EPV;
     if (tid < head) acc = Op::combine(acc, Map::apply(src[tid]));
     if (tail0 + tid < n) acc = Op::combine(acc, Map::apply(src[tail0 + tid]));
   }
   const T part = block_reduce<T, Op>(acc, s_wave);
-  fold_partial<T, Op>(part, out, fold_hdr, s_wave, hdr0);
+  fold_partial<T, Op>(part, out, fold_hdr, s_wave, hdr0, ctl);
+#ifdef KF_TIMELINE
+  red_timeline(tl_start, tl_loaded);
+#endif
 }
 
 // Strided views with short strides (stride * sizeof(T) <= kStrideVecBytes,
@@ -299,7 +365,7 @@ constexpr int kStrideUnroll = 8;
 template <class T, class Op, class Map>
 __global__ __launch_bounds__(kRedBlock) void reduce_stride_kernel(const T* src, int64_t span, int stride,
                                                                   int64_t head, int64_t nvec, int64_t chunk, T* out,
-                                                                  uint64_t* fold_hdr) {
+                                                                  uint64_t* fold_hdr, FoldCtl ctl) {
   constexpr int EPV = 16 / (int)sizeof(T);
   constexpr int U = kStrideUnroll;
   __shared__ T s_wave[kRedWaves];
@@ -351,7 +417,7 @@ __global__ __launch_bounds__(kRedBlock) void reduce_stride_kernel(const T* src, 
     if (t < span && t % stride == 0) acc = Op::combine(acc, Map::apply(src[t]));
   }
   const T part = block_reduce<T, Op>(acc, s_wave);
-  fold_partial<T, Op>(part, out, fold_hdr, s_wave, hdr0);
+  fold_partial<T, Op>(part, out, fold_hdr, s_wave, hdr0, ctl);
 }
 
 // Full reduction, stage 2: one 1024-thread workgroup combines `count`
@@ -457,16 +523,16 @@ void launch_once(int u, unsigned grid, const T* src, int64_t n, int64_t head, in
                  hipStream_t stream) {
   if (u == 16)
     hipLaunchKernelGGL((reduce_once_kernel<T, Op, Map, FOLD, 16>), dim3(grid), dim3(kRedBlock), 0, stream, src, n, head,
-                       nvec, out, hdr);
+                       nvec, out, hdr, fold_ctl());
   else if (u == 8)
     hipLaunchKernelGGL((reduce_once_kernel<T, Op, Map, FOLD, 8>), dim3(grid), dim3(kRedBlock), 0, stream, src, n, head,
-                       nvec, out, hdr);
+                       nvec, out, hdr, fold_ctl());
   else if (u == 4)
     hipLaunchKernelGGL((reduce_once_kernel<T, Op, Map, FOLD, 4>), dim3(grid), dim3(kRedBlock), 0, stream, src, n, head,
-                       nvec, out, hdr);
+                       nvec, out, hdr, fold_ctl());
   else
     hipLaunchKernelGGL((reduce_once_kernel<T, Op, Map, FOLD, kOnceUnroll>), dim3(grid), dim3(kRedBlock), 0, stream, src,
-                       n, head, nvec, out, hdr);
+                       n, head, nvec, out, hdr, fold_ctl());
 }
 
 constexpr uintptr_t kHeadAlign = 128;  // head elements, up to 127 (< kRedBlock)
@@ -491,7 +557,7 @@ int launch_reduce(const void* src, int64_t n, int64_t stride, void* dst, void* s
       return kf_check_launch("reduce_kernel");
     }
     hipLaunchKernelGGL((reduce_stride_kernel<T, Op, Map>), dim3((unsigned)grid), dim3(kRedBlock), 0, stream,
-                       (const T*)src, span, (int)stride, head, nvec, chunk, (T*)dst, (uint64_t*)scratch);
+                       (const T*)src, span, (int)stride, head, nvec, chunk, (T*)dst, (uint64_t*)scratch, fold_ctl());
     return kf_check_launch("reduce_stride_kernel");
   }
   if (stride != 1) {
@@ -519,7 +585,7 @@ int launch_reduce(const void* src, int64_t n, int64_t stride, void* dst, void* s
     constexpr int64_t kRound = (int64_t)kChunkUnroll * kRedBlock;
     const int64_t chunk = ((nvec + kFoldMax - 1) / kFoldMax + kRound - 1) / kRound * kRound;
     hipLaunchKernelGGL((reduce_chunk_kernel<T, Op, Map, kChunkUnroll>), dim3(kFoldMax), dim3(kRedBlock), 0, stream,
-                       (const T*)src, n, head, nvec, chunk, (T*)dst, (uint64_t*)scratch);
+                       (const T*)src, n, head, nvec, chunk, (T*)dst, (uint64_t*)scratch, fold_ctl());
     return kf_check_launch("reduce_chunk_kernel");
   }
   size_t abytes = 0;
@@ -575,7 +641,7 @@ template <class M, class T, int K> __device__ inline T apply_k(const T (&v)[K]) 
 // reduce_once_kernel, each loading the same 16-byte vectors of all K arrays.
 template <class T, class Op, class M, int K, bool FOLD = false>
 __global__ __launch_bounds__(kRedBlock) void reducek_once_kernel(Operands<T, K> a, int64_t n, T* out,
-                                                                 uint64_t* fold_hdr) {
+                                                                 uint64_t* fold_hdr, FoldCtl ctl) {
   constexpr int EPV = 16 / (int)sizeof(T);
   __shared__ T s_wave[kRedWaves];
   const T id = Op::template identity<T>();
@@ -620,7 +686,7 @@ __global__ __launch_bounds__(kRedBlock) void reducek_once_kernel(Operands<T, K> 
   if constexpr (!FOLD) {
     if (tid == 0) out[blockIdx.x] = part;
   } else {
-    fold_partial<T, Op>(part, out, fold_hdr, s_wave, hdr0);  // out is the result
+    fold_partial<T, Op>(part, out, fold_hdr, s_wave, hdr0, ctl);  // out is the result
   }
 }
 
@@ -658,7 +724,7 @@ int launch_reducek(const Operands<T, K>& a, int64_t n, void* dst, void* scratch_
   const OnceLevels L = once_levels(n / EPV, EPV, /*adaptive=*/false);
   if (L.nlev == 1 && L.count[0] > 1) {
     hipLaunchKernelGGL((reducek_once_kernel<T, Op, M, K, true>), dim3((unsigned)L.count[0]), dim3(kRedBlock), 0,
-                       stream, a, n, (T*)dst, (uint64_t*)scratch_base);
+                       stream, a, n, (T*)dst, (uint64_t*)scratch_base, fold_ctl());
     return kf_check_launch("reducek_once_kernel");
   }
   size_t abytes = 0;
@@ -666,7 +732,7 @@ int launch_reducek(const Operands<T, K>& a, int64_t n, void* dst, void* scratch_
   T* buf[2] = {(T*)scratch, (T*)((uint8_t*)scratch + abytes)};
   const int last = L.nlev - 1;
   hipLaunchKernelGGL((reducek_once_kernel<T, Op, M, K>), dim3((unsigned)L.count[0]), dim3(kRedBlock), 0, stream,
-                     a, n, last == 0 ? (T*)dst : buf[0], (uint64_t*)nullptr);
+                     a, n, last == 0 ? (T*)dst : buf[0], (uint64_t*)nullptr, fold_ctl());
   for (int i = 1; i <= last; ++i) {
     const int64_t m = L.count[i - 1];
     const unsigned grid = (unsigned)L.count[i];
@@ -734,6 +800,8 @@ extern "C" int kf_reduce(kf_op op, kf_map f, kf_dtype dt, const void* src, int64
                          void* dst, void* scratch, size_t scratch_bytes, void* stream) {
   int rc = kf_validate_op(op, f, dt, /*allow_affine=*/0);
   if (rc) return rc;
+  kf_mailbox();
+  if ((rc = kf_take_giveup("kf_reduce"))) return rc;
   if (n < 0) return kf_set_error(KF_EINVAL, "kf_reduce: n = %lld < 0", (long long)n);
   if (n == 0) return KF_OK;
   if (!src || !dst) return kf_set_error(KF_EINVAL, "kf_reduce: null src or dst");
@@ -775,6 +843,8 @@ extern "C" int kf_reduce2(kf_op op, kf_map2 f, kf_dtype dt, const void* x, int64
                           int64_t y_stride, int64_t n, void* dst, void* scratch, size_t scratch_bytes, void* stream) {
   int rc = kf_validate_op(op, KF_MAP_IDENTITY, dt, /*allow_affine=*/0);
   if (rc) return rc;
+  kf_mailbox();
+  if ((rc = kf_take_giveup("kf_reduce2"))) return rc;
   if (f != KF_MAP2_MUL && f != KF_MAP2_SQDIFF && f != KF_MAP2_WSQ && f != KF_MAP2_EXPDIFF)
     return kf_set_error(KF_EINVAL, "kf_reduce2: unknown map %d", (int)f);
   if (f == KF_MAP2_EXPDIFF && dt != KF_F32 && dt != KF_F64)
@@ -819,6 +889,8 @@ extern "C" int kf_reduce3(kf_op op, kf_map3 f, kf_dtype dt, const void* x, int64
                           size_t scratch_bytes, void* stream) {
   int rc = kf_validate_op(op, KF_MAP_IDENTITY, dt, /*allow_affine=*/0);
   if (rc) return rc;
+  kf_mailbox();
+  if ((rc = kf_take_giveup("kf_reduce3"))) return rc;
   if (f != KF_MAP3_MUL) return kf_set_error(KF_EINVAL, "kf_reduce3: unknown map %d", (int)f);
   if (n < 0) return kf_set_error(KF_EINVAL, "kf_reduce3: n = %lld < 0", (long long)n);
   if (n == 0) return KF_OK;
@@ -887,6 +959,44 @@ extern "C" int kf_scratch_reset(void* scratch, size_t bytes, void* stream) {
   return kf_check_launch("fill_zero_kernel");
 }
 
+namespace kf {
+__global__ void clear_fold_flag_kernel(uint64_t* hdr) { hdr[1] = 0; }
+}  // namespace kf
+
+extern "C" int kf_reduce_scratch_status(void* scratch, void* stream, int* gave_up) {
+  if (!scratch || !gave_up) return kf_set_error(KF_EINVAL, "kf_reduce_scratch_status: null pointer");
+  hipStream_t s = (hipStream_t)stream;
+  uint64_t w = 0;
+  if (hipMemcpyAsync(&w, (uint64_t*)scratch + 1, sizeof w, hipMemcpyDeviceToHost, s) != hipSuccess ||
+      hipStreamSynchronize(s) != hipSuccess)
+    return kf_check_launch("kf_reduce_scratch_status");
+  *gave_up = w != 0;
+  // the epoch already moved past the failed call's slots; only the flag is
+  // cleared (a kernel, not a memset node: the call may sit in a graph)
+  if (w != 0) hipLaunchKernelGGL(clear_fold_flag_kernel, dim3(1), dim3(1), 0, s, (uint64_t*)scratch);
+  return kf_check_launch("clear_fold_flag_kernel");
+}
+
+#ifdef KF_TIMELINE
+extern "C" int kf_debug_reduce_timeline(void* buf) {
+  if (hipMemcpyToSymbol(HIP_SYMBOL(g_red_timeline), &buf, sizeof(buf)) != hipSuccess)
+    return kf_check_launch("kf_debug_reduce_timeline");
+  return KF_OK;
+}
+
+extern "C" int kf_debug_reduce_giveup(int workgroup, uint32_t spin_limit) {
+  if (workgroup < 0) {
+    g_fold_withhold = -1;
+    g_fold_limit = kFoldSpinLimit;
+    return KF_OK;
+  }
+  if (spin_limit == 0) return kf_set_error(KF_EINVAL, "kf_debug_reduce_giveup: spin_limit must be > 0");
+  g_fold_withhold = workgroup;
+  g_fold_limit = spin_limit;
+  return KF_OK;
+}
+#endif
+
 // ---------------------------------------------------------------------------
 // Allocation-free full reduction: kf_reduce with its scratch in a static
 // device array instead of a caller buffer.
@@ -930,6 +1040,7 @@ extern "C" int kf_reduce_noalloc(kf_op op, kf_map f, kf_dtype dt, const void* sr
                                  void* dst, void* stream) {
   int rc = kf_validate_op(op, f, dt, /*allow_affine=*/0);
   if (rc) return rc;
+  if ((rc = kf_take_giveup("kf_reduce_noalloc"))) return rc;
   if (n < 0) return kf_set_error(KF_EINVAL, "kf_reduce_noalloc: n = %lld < 0", (long long)n);
   if (n == 0) return KF_OK;
   if (!src || !dst) return kf_set_error(KF_EINVAL, "kf_reduce_noalloc: null src or dst");

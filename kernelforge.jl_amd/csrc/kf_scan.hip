@@ -505,7 +505,8 @@ template <class T, int V> __device__ inline int unit_slot(int j, int lane) {
 template <class T, class Op, class Map, bool EXCL, int BLOCK, int VPL>
 __global__ __launch_bounds__(BLOCK) void scan_kernel(
     const T* src, int64_t src_stride, T* dst, int64_t dst_stride, int64_t n,
-    int64_t ntiles, uint64_t* scratch, int vec, int off, int win, int post, uint32_t limit, int64_t withhold) {
+    int64_t ntiles, uint64_t* scratch, int vec, int off, int win, int post, uint32_t limit, int64_t withhold,
+    uint32_t* mbox) {
   // Tiles cover the virtual range [0, n + off): element i sits at virtual
   // position i + off, where `off` is dst's misalignment in elements, so
   // every interior tile stores whole 16-byte vectors at aligned addresses
@@ -513,7 +514,8 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
   // same way, and unaligned loads otherwise). Virtual positions before
   // `off` and after the end hold the identity and are never stored.
   // `limit` is the lookback's poll budget; `withhold` >= 0 makes that tile
-  // publish nothing (a test hook that forces the give-up path).
+  // publish nothing (a test hook that forces the give-up path). `mbox` is
+  // the host-mapped give-up report word (report_giveup).
   using S = ScanShape<T, BLOCK, VPL>;
   constexpr int V = S::V, EPV = S::EPV;
   constexpr int kScanWaves = BLOCK / kWave;
@@ -658,7 +660,12 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
     s_hdr_stop = hdr_stop != 0;
   }
   __syncthreads();
-  if (s_hdr_stop) return;  // no store and no publication yet
+  if (s_hdr_stop) {
+    // no store and no publication: reported, so that the skipped call
+    // surfaces at the caller's next entry point instead of passing silently
+    if (tid == 0 && tile == 0) report_giveup(mbox);
+    return;
+  }
   const uint64_t tk = s_ticket;
   const uint32_t epoch30 = (uint32_t)(tk >> 32) & 0x3fffffffu;
 #ifdef KF_TIMELINE
@@ -726,6 +733,7 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
     // buffer to the status query or a reset
     if (lane == 0 && tile == ntiles - 1 && !gave_up) st_agent(scratch, ((tk >> 32) + 1) << 32);
     if (lane == 0) s_stop = gave_up;
+    if (lane == 0 && gave_up) report_giveup(mbox);
     if (lane < kScanWaves) wave_pre[lane] = lane == 0 ? excl : Op::combine(excl, wexcl);
     if constexpr (kStashForLookback<T, BLOCK>) {
       asm volatile("" ::: "memory");
@@ -904,10 +912,16 @@ template <auto KERNEL> int64_t resident_tiles(int block) {
 
 // `mode` below carries the exclusive flag in bit 0 and the post-map g
 // (kf_post) in the bits above.
-// Test hook (kf_debug_scan_giveup): on this host thread, scans withhold the
-// publication of one tile and give up after a short poll budget.
+#ifdef KF_TIMELINE
+// Test hook (kf_debug_scan_giveup, instrumented library only): on this host
+// thread, scans withhold the publication of one tile and give up after a
+// short poll budget.
 thread_local int64_t g_withhold = -1;
 thread_local uint32_t g_spin_limit = kSpinLimit;
+#else
+constexpr int64_t g_withhold = -1;
+constexpr uint32_t g_spin_limit = kSpinLimit;
+#endif
 
 template <class T, class Op, class Map, int TIER>
 void launch_scan_tier(const void* src, int64_t ss, void* dst, int64_t ds, int64_t n, int mode, int64_t ntiles,
@@ -919,13 +933,13 @@ void launch_scan_tier(const void* src, int64_t ss, void* dst, int64_t ds, int64_
     hipLaunchKernelGGL(kernel, dim3((unsigned)ntiles), dim3(B), 0, stream, (const T*)src, ss, (T*)dst, ds, n,
                        ntiles, (uint64_t*)scratch, vec, off, look_window(ntiles, resident_tiles<kernel>(B), (int64_t)B * V * kVecBytes<T>, kLookAllFor<T>,
                                    kLookBlockFor<T, B, V>, B), post,
-                       g_spin_limit, g_withhold);
+                       g_spin_limit, g_withhold, kf_mailbox());
   } else {
     constexpr auto kernel = scan_kernel<T, Op, Map, false, B, V>;
     hipLaunchKernelGGL(kernel, dim3((unsigned)ntiles), dim3(B), 0, stream, (const T*)src, ss, (T*)dst, ds, n,
                        ntiles, (uint64_t*)scratch, vec, off, look_window(ntiles, resident_tiles<kernel>(B), (int64_t)B * V * kVecBytes<T>, kLookAllFor<T>,
                                    kLookBlockFor<T, B, V>, B), post,
-                       g_spin_limit, g_withhold);
+                       g_spin_limit, g_withhold, kf_mailbox());
   }
 }
 
@@ -1035,6 +1049,7 @@ extern "C" int kf_scan_scratch_status(void* scratch, void* stream, int* gave_up)
   return kf_check_launch("reepoch_kernel");
 }
 
+#ifdef KF_TIMELINE
 extern "C" int kf_debug_scan_giveup(int64_t tile, uint32_t spin_limit) {
   if (tile < 0) {
     g_withhold = -1;
@@ -1046,6 +1061,7 @@ extern "C" int kf_debug_scan_giveup(int64_t tile, uint32_t spin_limit) {
   g_spin_limit = spin_limit;
   return KF_OK;
 }
+#endif
 
 extern "C" size_t kf_scan_shaped_scratch_bytes(kf_dtype dt, kf_op op, int64_t n, int workgroup, int nitem) {
   (void)op;
@@ -1079,6 +1095,7 @@ extern "C" int kf_scan_shaped(kf_op op, kf_map f, kf_post g, kf_dtype dt, int ex
                               int nitem, void* scratch, size_t scratch_bytes, void* stream) {
   int rc = kf_validate_op(op, f, dt, /*allow_affine=*/1);
   if (rc) return rc;
+  if ((rc = kf_take_giveup("kf_scan"))) return rc;
   if (g != KF_POST_IDENTITY && g != KF_POST_SQRT && g != KF_POST_ABS2)
     return kf_set_error(KF_EINVAL, "kf_scan: unknown post-map g = %d", (int)g);
   if (g != KF_POST_IDENTITY && (dt == KF_F32X2 || dt == KF_Q32 || dt == KF_Q64))

@@ -17,7 +17,8 @@
 # abs2; a full reduction returned to the host takes any g.
 #
 # Errors follow the reference: ArgumentError for bad arguments (library codes
-# KF_EINVAL / KF_ENOSCRATCH), ErrorException for HIP failures (KF_EHIP).
+# KF_EINVAL / KF_ENOSCRATCH), ErrorException for HIP failures (KF_EHIP) and
+# for a give-up of an earlier kernel (KF_EGIVEUP, see `check_async`).
 module KernelForgeHIP
 
 using AMDGPU
@@ -57,8 +58,11 @@ struct KernelBuffer{Arrays<:NamedTuple}
     arrays::Arrays
 end
 
-_buffer(family::Symbol, nbytes::Integer) =
-    KernelBuffer(NamedTuple{(family,)}((AMDGPU.zeros(UInt8, max(Int(nbytes), 256)),)))
+function _buffer(family::Symbol, nbytes::Integer)
+    v = AMDGPU.zeros(UInt8, max(Int(nbytes), 256))
+    family === :scan && (SCAN_BUFFERS[v] = nothing)
+    return KernelBuffer(NamedTuple{(family,)}((v,)))
+end
 
 function _scratch(tmp::KernelBuffer, family::Symbol, need::Integer)
     haskey(tmp.arrays, family) ||
@@ -150,11 +154,39 @@ function dtcode(::Type{T}) where {T}
     throw(ArgumentError("unsupported element type $T"))
 end
 
+# Every live scan scratch vector, so that a give-up report can re-validate
+# them all (their sticky flags would otherwise keep later scans inert).
+const SCAN_BUFFERS = WeakKeyDict{ROCVector{UInt8},Nothing}()
+
 function _check(rc::Cint, what)
     rc == 0 && return nothing
     msg = unsafe_string(ccall((:kf_last_error, libkf), Cstring, ()))
     rc in (Cint(1), Cint(2)) && throw(ArgumentError("$what: $msg"))
+    rc == Cint(4) && error("$what: $msg $(_revalidate_scan_buffers())")
     error("$what: $msg")
+end
+
+function _revalidate_scan_buffers()
+    hit = count(_scan_status, collect(keys(SCAN_BUFFERS)))
+    hit > 0 && return "$hit scan scratch buffer(s) had given up: the scans on them since then stored " *
+                      "nothing; they are valid again"
+    return "(a reduction fold gave up: its destination was left untouched; its buffer is valid again)"
+end
+
+"""
+    check_async()
+
+Throw if a kernel queued earlier gave up waiting on its scratch buffer
+(`kf_async_status`), after re-validating every scan buffer. Non-blocking: it
+covers the kernels that have finished, so call it after a synchronisation
+to cover them all. No counterpart in the reference, whose waits are unbounded.
+"""
+function check_async()
+    flag = Ref{Cint}(0)
+    _check(ccall((:kf_async_status, libkf), Cint, (Ptr{Cint},), flag), "check_async")
+    flag[] != 0 && error("a scan lookback or reduction fold gave up waiting on its scratch buffer; " *
+                         "its results are invalid. $(_revalidate_scan_buffers())")
+    return nothing
 end
 
 _stream() = AMDGPU.stream().stream                        # hipStream_t of the task-local stream
@@ -262,8 +294,10 @@ end
 
 `dst[i] = g(f(src[1]) op ... op f(src[i]))` (reference src/scan/scan.jl:251-284).
 `exclusive=true` gives `dst[1] = g(identity of op)`, `dst[i] = g(inclusive[i-1])`
-(no reference counterpart). `check=true` synchronises and throws if a tile's
-lookback gave up (see `scan_status`). `Nitem` (elements per thread) and
+(no reference counterpart). A lookback that gives up (see `scan_status`) is
+reported by the library's next call after that kernel has finished (an
+error), by `check_async` and by the full `mapreduce`'s read-back;
+`check=true` synchronises and throws at once. `Nitem` (elements per thread) and
 `workgroup` (threads per workgroup) select the nearest compiled tile shape
 (`scan_shape`); `family` and `arch` are accepted for compatibility.
 """
@@ -290,9 +324,12 @@ function scan!(f::F, op::O, dst::AbstractArray, src::AbstractArray; g::G=identit
                devptr(src), _linear(src, "scan!"), devptr(dst), _linear(dst, "scan!"), n, wg, ni,
                devptr(buf), length(buf), _stream())
     _check(rc, "scan!")
-    check && _scan_status(buf) &&
+    if check && _scan_status(buf)
+        # raised here, so the pending report is consumed
+        _check(ccall((:kf_async_status, libkf), Cint, (Ptr{Cint},), Ref{Cint}(0)), "scan!")
         error("scan!: a tile's lookback gave up waiting for its predecessor; the results are invalid " *
-              "(the scratch buffer has been re-validated)")
+              "(the scratch buffer has been re-validated) $(_revalidate_scan_buffers())")
+    end
     return dst
 end
 
@@ -305,11 +342,13 @@ function scan(op::O, src::AbstractArray; kwargs...) where {O<:Function}
     return scan(identity, op, src; kwargs...)
 end
 
-function scan(f::F, op::O, src::AbstractArray; kwargs...) where {F<:Function,O<:Function}
-    dst = similar(src)
-    return scan!(f, op, dst, src; kwargs...)
+function scan(f::F, op::O, src::AbstractArray; g::G=identity, kwargs...) where {F<:Function,O<:Function,G<:Function}
+    # a vector of length(src) with eltype promote_op(g, promote_op(f, T)), as
+    # the reference allocates it (src/scan/scan.jl:226-244), for any shape of src
+    H = Base.promote_op(g, Base.promote_op(f, eltype(src)))
+    dst = similar(src, H, length(src))
+    return scan!(f, op, dst, src; g, kwargs...)
 end
-
 function _scan_status(buf::ROCVector{UInt8})
     flag = Ref{Cint}(0)
     rc = ccall((:kf_scan_scratch_status, libkf), Cint, (Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cint}),
@@ -417,7 +456,9 @@ function mapreduce1d(f::F, op::O, srcs::NTuple{U,AbstractArray}; g::G=identity, 
     dst = ROCVector{eltype(srcs[1])}(undef, 1)
     if to_cpu
         mapreduce1d!(f, op, dst, srcs; tmp)
-        return g(Array(dst)[1])           # the read-back synchronises; any g on the host
+        v = Array(dst)[1]                 # the read-back synchronises; any g on the host
+        check_async()
+        return g(v)
     end
     return mapreduce1d!(f, op, dst, srcs; g, tmp)
 end

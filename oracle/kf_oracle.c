@@ -405,6 +405,174 @@ float kfb_sum_f32_par(const float* x, int64_t n, int threads) {
   return (float)total;
 }
 
+/* ---- CPU baseline of every BASELINE configuration -----------------------
+ * Each function runs on `threads` host threads (<= 1: the sequential left
+ * fold Base.accumulate! / Base.mapreduce computes; > 1: the chunked
+ * Threads.@threads variant: per-chunk folds, then for scans an ordered
+ * combine of the chunk totals and a second pass that re-scans each chunk
+ * from its prefix). Element arithmetic throughout (Int32 wraps, Float32 and
+ * Float64 stay in their width); sums keep 8 independent partials per
+ * thread, as Base's vectorised blocks do. Compiled at -O3 so that the
+ * independent partials vectorise. */
+#pragma GCC push_options
+#pragma GCC optimize("O3")
+
+static int clamp_threads(int threads) { return threads < 1 ? 1 : threads > 1024 ? 1024 : threads; }
+
+/* Base.accumulate!(+, dst, src) on Int32 (wrap-around); exclusive shifts
+ * by one with 0 first. */
+static void scan_i32_range(const int32_t* x, int32_t* y, int64_t lo, int64_t hi, uint32_t acc, int exclusive) {
+  if (exclusive)
+    for (int64_t i = lo; i < hi; ++i) {
+      y[i] = (int32_t)acc;
+      acc += (uint32_t)x[i];
+    }
+  else
+    for (int64_t i = lo; i < hi; ++i) {
+      acc += (uint32_t)x[i];
+      y[i] = (int32_t)acc;
+    }
+}
+
+void kfb_scan_add_i32(const int32_t* x, int32_t* y, int64_t n, int exclusive, int threads) {
+  threads = clamp_threads(threads);
+  if (threads == 1) {
+    scan_i32_range(x, y, 0, n, 0u, exclusive);
+    return;
+  }
+  uint32_t totals[1024];
+  const int64_t chunk = (n + threads - 1) / threads;
+#pragma omp parallel num_threads(threads)
+  {
+    const int t = omp_get_thread_num();
+    const int64_t lo = t * chunk < n ? t * chunk : n, hi = lo + chunk < n ? lo + chunk : n;
+    uint32_t s = 0;
+    for (int64_t i = lo; i < hi; ++i) s += (uint32_t)x[i];
+    totals[t] = s;
+#pragma omp barrier
+    uint32_t off = 0;
+    for (int k = 0; k < t; ++k) off += totals[k];
+    scan_i32_range(x, y, lo, hi, off, exclusive);
+  }
+}
+
+/* The affine recurrence's scan on interleaved Float32 pairs: (A, B) <-
+ * (a*A, a*B + b), inclusive, in Float32. */
+static void affine_range(const float* ab, float* out, int64_t lo, int64_t hi, float A, float B) {
+  for (int64_t i = lo; i < hi; ++i) {
+    const float a = ab[2 * i], b = ab[2 * i + 1];
+    A = a * A;
+    B = a * B + b;
+    out[2 * i] = A;
+    out[2 * i + 1] = B;
+  }
+}
+
+void kfb_scan_affine_f32(const float* ab, float* out, int64_t n, int threads) {
+  threads = clamp_threads(threads);
+  if (threads == 1 || n < 2) {
+    if (n > 0) {
+      out[0] = ab[0];
+      out[1] = ab[1];
+      affine_range(ab, out, 1, n, ab[0], ab[1]);
+    }
+    return;
+  }
+  float tA[1024], tB[1024];
+  const int64_t chunk = (n + threads - 1) / threads;
+#pragma omp parallel num_threads(threads)
+  {
+    const int t = omp_get_thread_num();
+    const int64_t lo = t * chunk < n ? t * chunk : n, hi = lo + chunk < n ? lo + chunk : n;
+    float A = 1.0f, B = 0.0f;  /* the chunk's composition, older first */
+    for (int64_t i = lo; i < hi; ++i) {
+      const float a = ab[2 * i], b = ab[2 * i + 1];
+      A = a * A;
+      B = a * B + b;
+    }
+    tA[t] = A;
+    tB[t] = B;
+#pragma omp barrier
+    float pA = 1.0f, pB = 0.0f;
+    for (int k = 0; k < t; ++k) {
+      pA = tA[k] * pA;
+      pB = tA[k] * pB + tB[k];
+    }
+    affine_range(ab, out, lo, hi, pA, pB);
+  }
+}
+
+#define KFB_FOLD8(T, NAME, INIT, STEP, JOIN)                                        \
+  static T NAME##_seq(const T* x, int64_t n) {                                      \
+    T s[8];                                                                         \
+    for (int k = 0; k < 8; ++k) s[k] = INIT;                                        \
+    int64_t i = 0;                                                                  \
+    for (; i + 8 <= n; i += 8)                                                      \
+      for (int k = 0; k < 8; ++k) s[k] = STEP(s[k], x[i + k]);                      \
+    for (; i < n; ++i) s[0] = STEP(s[0], x[i]);                                     \
+    T r = s[0];                                                                     \
+    for (int k = 1; k < 8; ++k) r = JOIN(r, s[k]);                                  \
+    return r;                                                                       \
+  }                                                                                 \
+  T NAME(const T* x, int64_t n, int threads) {                                      \
+    threads = clamp_threads(threads);                                               \
+    if (threads == 1) return NAME##_seq(x, n);                                      \
+    T part[1024];                                                                   \
+    const int64_t chunk = (n + threads - 1) / threads;                              \
+    _Pragma("omp parallel num_threads(threads)") {                                  \
+      const int t = omp_get_thread_num();                                           \
+      const int64_t lo = t * chunk < n ? t * chunk : n;                             \
+      const int64_t hi = lo + chunk < n ? lo + chunk : n;                           \
+      part[t] = NAME##_seq(x + lo, hi - lo);                                        \
+    }                                                                               \
+    T r = part[0];                                                                  \
+    for (int k = 1; k < threads; ++k) r = JOIN(r, part[k]);                         \
+    return r;                                                                       \
+  }
+
+#define KFB_ADD(a, b) ((a) + (b))
+#define KFB_ADDSQ(a, v) ((a) + (v) * (v))
+#define KFB_MAX(a, b) ((a) > (b) ? (a) : (b))
+/* Base.mapreduce(abs2, +, x) on Float32 / Float64 and maximum(x) on Int32 */
+KFB_FOLD8(float, kfb_sum_abs2_f32, 0.0f, KFB_ADDSQ, KFB_ADD)
+KFB_FOLD8(double, kfb_sum_abs2_f64, 0.0, KFB_ADDSQ, KFB_ADD)
+KFB_FOLD8(int32_t, kfb_max_i32, INT32_MIN, KFB_MAX, KFB_MAX)
+
+/* Base.mapreduce(identity, +, A; dims) on a column-major Float32 matrix
+ * A[i, j] = A[i + j*cs]: dims=1 sums each column (columns split across
+ * threads), dims=2 adds the columns into the row sums (rows split across
+ * threads, each thread walking every column over its rows). */
+void kfb_sum_dims_f32(const float* A, int64_t rows, int64_t cols, int64_t cs, int dim, float* out, int threads) {
+  threads = clamp_threads(threads);
+  if (dim == 1) {
+#pragma omp parallel for num_threads(threads) schedule(static)
+    for (int64_t j = 0; j < cols; ++j) {
+      const float* c = A + j * cs;
+      float s[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+      int64_t i = 0;
+      for (; i + 8 <= rows; i += 8)
+        for (int k = 0; k < 8; ++k) s[k] += c[i + k];
+      for (; i < rows; ++i) s[0] += c[i];
+      float r = s[0];
+      for (int k = 1; k < 8; ++k) r += s[k];
+      out[j] = r;
+    }
+    return;
+  }
+  const int64_t chunk = (rows + threads - 1) / threads;
+#pragma omp parallel num_threads(threads)
+  {
+    const int t = omp_get_thread_num();
+    const int64_t lo = t * chunk < rows ? t * chunk : rows, hi = lo + chunk < rows ? lo + chunk : rows;
+    for (int64_t i = lo; i < hi; ++i) out[i] = A[i];
+    for (int64_t j = 1; j < cols; ++j) {
+      const float* c = A + j * cs;
+      for (int64_t i = lo; i < hi; ++i) out[i] += c[i];
+    }
+  }
+}
+#pragma GCC pop_options
+
 int kfo_omp_max_threads(void) {
 #ifdef _OPENMP
   return omp_get_max_threads();

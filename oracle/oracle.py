@@ -62,6 +62,15 @@ def lib():
         L.kfb_sum_f32_par.argtypes = [P, I64, I]
         L.kfb_sum_f32_par.restype = ctypes.c_float
         L.kfo_omp_max_threads.restype = I
+        L.kfb_scan_add_i32.argtypes = [P, P, I64, I, I]
+        L.kfb_scan_affine_f32.argtypes = [P, P, I64, I]
+        L.kfb_sum_abs2_f32.argtypes = [P, I64, I]
+        L.kfb_sum_abs2_f32.restype = ctypes.c_float
+        L.kfb_sum_abs2_f64.argtypes = [P, I64, I]
+        L.kfb_sum_abs2_f64.restype = D
+        L.kfb_max_i32.argtypes = [P, I64, I]
+        L.kfb_max_i32.restype = ctypes.c_int32
+        L.kfb_sum_dims_f32.argtypes = [P, I64, I64, I64, I, P, I]
         _lib = L
     return _lib
 
@@ -184,6 +193,32 @@ def baseline_sum_f32(x, threads=1):
     if threads <= 1:
         return L.kfb_sum_f32_seq(_p(x), x.shape[0])
     return L.kfb_sum_f32_par(_p(x), x.shape[0], threads)
+
+
+def baseline_scan_add_i32(x, y, exclusive=False, threads=1):
+    lib().kfb_scan_add_i32(_p(x), _p(y), x.shape[0], int(bool(exclusive)), threads)
+
+
+def baseline_scan_affine_f32(ab, out, threads=1):
+    """ab, out: (n, 2) float32 C-contiguous."""
+    lib().kfb_scan_affine_f32(_p(ab), _p(out), ab.shape[0], threads)
+
+
+def baseline_sum_abs2(x, threads=1):
+    L = lib()
+    if x.dtype == np.float32:
+        return L.kfb_sum_abs2_f32(_p(x), x.shape[0], threads)
+    return L.kfb_sum_abs2_f64(_p(x), x.shape[0], threads)
+
+
+def baseline_max_i32(x, threads=1):
+    return lib().kfb_max_i32(_p(x), x.shape[0], threads)
+
+
+def baseline_sum_dims_f32(buf, rows, cols, col_stride, dim, out, threads=1):
+    """buf: the flat Float32 storage of a column-major rows x cols matrix with
+    column stride col_stride; out: cols (dim=1) or rows (dim=2) values."""
+    lib().kfb_sum_dims_f32(_p(buf), rows, cols, col_stride, dim, _p(out), threads)
 
 
 def omp_max_threads():

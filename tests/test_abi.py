@@ -9,8 +9,8 @@ import pytest
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
-def declared_symbols():
-    text = open(os.path.join(REPO, "include", "kf.h")).read()
+def declared_symbols(header="kf.h"):
+    text = open(os.path.join(REPO, "include", header)).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return sorted(set(re.findall(r"\b(kf_[a-z0-9_]+)\s*\(", text)))
 
@@ -21,7 +21,7 @@ def test_header_declares_the_expected_surface():
         "kf_reduce_scratch_bytes", "kf_reduce", "kf_reduce_dim_scratch_bytes", "kf_reduce_dim", "kf_copy",
         "kf_reduce2_scratch_bytes", "kf_reduce2", "kf_reduce_dim_batched_scratch_bytes", "kf_reduce_dim_batched", "kf_post_map", "kf_reduce_dim_x",
         "kf_fill", "kf_scan_scratch_status", "kf_reduce3_scratch_bytes", "kf_reduce3",
-        "kf_reduce_noalloc", "kf_debug_scan_giveup",
+        "kf_reduce_noalloc", "kf_init", "kf_async_status", "kf_reduce_scratch_status",
         "kf_bw_probe_scratch_bytes", "kf_bw_probe",
         "kf_scan_shaped_scratch_bytes", "kf_scan_shape", "kf_scan_shaped"])
 
@@ -31,6 +31,29 @@ def test_library_exports_every_declared_symbol(kf):
     for name in declared_symbols():
         assert hasattr(L, name), name
         assert name in kf._lib.SIGNATURES, name
+
+
+def test_test_hooks_live_only_in_the_instrumented_library(kf):
+    # the production library exports no kf_debug_* symbol; the instrumented
+    # one exports every symbol include/kf_debug.h declares
+    L = kf._lib.lib()
+    debug = declared_symbols("kf_debug.h")
+    assert debug == sorted(kf._lib.DEBUG_SIGNATURES)
+    for name in debug:
+        assert not hasattr(L, name), name
+    D = kf._lib.debug_lib()
+    for name in debug + list(kf._lib.DEBUG_LIB_EXPORTS):
+        assert hasattr(D, name), name
+
+
+def test_async_status_is_clear_without_a_gpu(kf):
+    # no kernel has run, so nothing can have given up (the report word is
+    # not even allocated yet); the query neither blocks nor needs a device
+    flag = ctypes.c_int(7)
+    assert kf._lib.lib().kf_async_status(ctypes.byref(flag)) == kf._lib.KF_OK
+    assert flag.value == 0
+    assert kf._lib.lib().kf_async_status(None) == kf._lib.KF_EINVAL
+    kf.check_async()
 
 
 def test_version(kf):
@@ -165,6 +188,7 @@ def test_invalid_arguments_rejected_without_gpu(kf):
     assert L.kf_copy(p, p, 0, None) == K.KF_OK
     flag = ctypes.c_int(0)
     assert L.kf_scan_scratch_status(None, None, ctypes.byref(flag)) == K.KF_EINVAL
+    assert L.kf_reduce_scratch_status(None, None, ctypes.byref(flag)) == K.KF_EINVAL
     # fill: count 0 is a no-op; bad count, missing value, value size 0 or > 64
     v = ctypes.create_string_buffer(b"\x01" * 65, 65)
     assert L.kf_fill(p, 0, v, 4, None) == K.KF_OK

@@ -303,7 +303,9 @@ def test_few_columns_dims2(kf, dev, dt):
         assert not dbuf.cpu().numpy()[1::2].any()
 
 
-@pytest.mark.parametrize("rows", [7, 10])
+# 126 and 127 rows: the longest periods (63 and 127 words per period; at 127
+# each workgroup sees only two column phases)
+@pytest.mark.parametrize("rows", [7, 10, 126, 127])
 def test_u8_rows_off_the_word_large(kf, dev, rows):
     # UInt8 dims=2 over short columns off the word boundary, large enough for
     # the flat path's period kernel (sums from 96 MiB, matvec from 256 MiB):

@@ -507,49 +507,6 @@ def test_post_map_g_in_the_store(kf, oracle, dev, exclusive):
         kf.scan("+", torch.ones(10, dtype=torch.int32, device=dev), g="sqrt")
 
 
-# ---- the lookback's give-up path, forced from the host -----------------------
-# one wave reads all predecessors / every wave of the workgroup reads a share /
-# more tiles than the GPU holds at once (64-tile windows)
-@pytest.mark.parametrize("n", [300_000, 3_000_000, 30_000_000])
-def test_lookback_giveup_is_raised_by_the_kernel(kf, oracle, dev, n):
-    # kf_debug_scan_giveup makes tile 3 never publish and gives every
-    # lookback a budget of 4096 polls: the tile after it gives up, raises the
-    # flag, every waiting tile stops, and all kernels exit normally
-    L = kf._lib.lib()
-    rng = np.random.default_rng(41)
-    x = rng.integers(0, 16, n).astype(np.int32)
-    src = torch.from_numpy(x).to(dev)
-    dst = torch.empty_like(src)
-    tmp = kf.get_allocation(kf.Scan1D, kf.identity, "+", src)
-    print(f"give-up test n={n}", flush=True)
-    assert L.kf_debug_scan_giveup(3, 4096) == 0
-    try:
-        kf.scan_("+", dst, src, tmp=tmp)
-        torch.cuda.synchronize()
-    finally:
-        assert L.kf_debug_scan_giveup(-1, 0) == 0
-    # sticky: before the status query, a scan on that buffer stores nothing
-    sentinel = torch.full_like(src, -7)
-    kf.scan_("+", sentinel, src, tmp=tmp)
-    torch.cuda.synchronize()
-    assert bool((sentinel == -7).all())
-    assert kf.scan_status(tmp) is True
-    assert kf.scan_status(tmp) is False
-    # the query re-validated the buffer: the next scans are exact again
-    for excl in (False, True):
-        kf.scan_("+", dst, src, tmp=tmp, exclusive=excl)
-        assert np.array_equal(dst.cpu().numpy(), oracle.scan(x, "+", exclusive=excl))
-    # check=True surfaces a give-up as an exception
-    assert L.kf_debug_scan_giveup(3, 4096) == 0
-    try:
-        with pytest.raises(kf._lib.KernelForgeError):
-            kf.scan_("+", dst, src, tmp=tmp, check=True)
-    finally:
-        assert L.kf_debug_scan_giveup(-1, 0) == 0
-    kf.scan_("+", dst, src, tmp=tmp, check=True)
-    assert np.array_equal(dst.cpu().numpy(), oracle.scan(x, "+"))
-
-
 # ---- grids of 258..2049 resident tiles: the workgroup-wide lookback -----------
 @pytest.mark.parametrize("dt,n", [(np.uint8, 3_000_007), (np.uint8, 10**7), (np.int32, 2_500_001),
                                   (np.int64, 10**6 + 3), (np.int64, 1_600_000), (np.float64, 2 * 10**6)])

@@ -117,7 +117,7 @@ SIGNATURES = [
     ("scan!(f, op, dst, src; g, tmp, Nitem, workgroup, family, arch)",
      r"function scan!\(f::F, op::O, dst::AbstractArray, src::AbstractArray; g::G=identity, tmp=nothing,\s*Nitem=nothing, workgroup=nothing, family=nothing, arch=nothing"),
     ("scan(op, src; kw...)", r"function scan\(op::O, src::AbstractArray; kwargs\.\.\.\)"),
-    ("scan(f, op, src; kw...)", r"function scan\(f::F, op::O, src::AbstractArray; kwargs\.\.\.\)"),
+    ("scan(f, op, src; kw...)", r"function scan\(f::F, op::O, src::AbstractArray; g::G=identity, kwargs\.\.\.\)"),
     ("mapreduce(f, op, src; dims, g, kwargs...)",
      r"function mapreduce\(f::F, op::O, src::AbstractArray\{T\}; dims=nothing, g::G=identity,\s*kwargs\.\.\.\)"),
     ("mapreduce(f, op, srcs::NTuple; dims, g)", r"function mapreduce\(f::F, op::O, srcs::NTuple\{U,AbstractArray\}; dims=nothing"),
@@ -180,3 +180,24 @@ def test_blocks_are_balanced():
         openers += s.startswith("abstract type") + s.startswith("if ")
         ends += len(re.findall(r"\bend\b", s))
     assert openers == ends > 50
+
+
+def test_allocating_scan_returns_a_vector_of_the_promoted_eltype():
+    # reference src/scan/scan.jl:226-244: dst = similar(src, H, length(src))
+    # with H = promote_op(g, promote_op(f, T)), whatever the shape of src
+    text = open(JL).read()
+    m = re.search(r"function scan\(f::F, op::O, src::AbstractArray;(.*?)\nend", text, re.S)
+    assert m, "allocating scan(f, op, src) not found"
+    body = m.group(1)
+    assert "Base.promote_op(g, Base.promote_op(f, eltype(src)))" in body
+    assert "similar(src, H, length(src))" in body
+    assert "scan!(f, op, dst, src; g, kwargs...)" in body
+
+
+def test_give_up_reports_reach_the_julia_caller():
+    # KF_EGIVEUP (4) raises, and the full mapreduce checks the report after
+    # its synchronising read-back
+    text = open(JL).read()
+    assert "rc == Cint(4) && error(" in text
+    m = re.search(r"v = Array\(dst\)\[1\].*?\n\s*check_async\(\)", text, re.S)
+    assert m, "mapreduce1d does not call check_async after the read-back"

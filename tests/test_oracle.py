@@ -308,6 +308,53 @@ def test_cpu_baseline_agrees(oracle):
     assert abs(oracle.baseline_sum_f32(x, 4) - s) <= 1e-4 * s
 
 
+@pytest.mark.parametrize("threads", [1, 3, 16])
+@pytest.mark.parametrize("n", [5, 100_003])
+def test_cpu_baselines_of_every_config(oracle, threads, n):
+    # the timed CPU paths of C2-C5 against numpy (ragged chunks, and fewer
+    # elements than threads at n = 5)
+    rng = np.random.default_rng(n + threads)
+    xi = rng.integers(-2**31, 2**31 - 1, n).astype(np.int32)
+    for excl in (False, True):
+        y = np.empty_like(xi)
+        oracle.baseline_scan_add_i32(xi, y, excl, threads)
+        incl = np.cumsum(xi, dtype=np.int32)  # numpy's int32 cumsum wraps like Julia's Int32 +
+        ref = np.concatenate([[0], incl[:-1]]).astype(np.int32) if excl else incl
+        assert np.array_equal(y, ref), (excl, threads)
+    assert oracle.baseline_max_i32(xi, threads) == int(xi.max())
+    xf = rng.standard_normal(n).astype(np.float32)
+    assert abs(oracle.baseline_sum_abs2(xf, threads) - float((xf.astype(np.float64) ** 2).sum())) <= 1e-5 * n
+    xd = rng.standard_normal(n)
+    assert abs(oracle.baseline_sum_abs2(xd, threads) - float((xd ** 2).sum())) <= 1e-12 * n
+    # affine: a constant a = 1/2 and b = 1 give x_t = 2 - 2^(1-t) (closed
+    # form), and random pairs agree with the Float64 checker
+    ab = np.tile(np.array([[0.5, 1.0]], np.float32), (n, 1))
+    out = np.empty_like(ab)
+    oracle.baseline_scan_affine_f32(ab, out, threads)
+    t = np.arange(1, n + 1)
+    np.testing.assert_allclose(out[:, 1], 2.0 - 2.0 ** (1.0 - t), rtol=1e-6)
+    np.testing.assert_allclose(out[:, 0], 0.5 ** np.minimum(t, 200), rtol=1e-6, atol=1e-37)
+    ab = np.stack([rng.uniform(0.9, 1.0, n), rng.standard_normal(n)], 1).astype(np.float32)
+    oracle.baseline_scan_affine_f32(ab, out, threads)
+    ref = oracle.scan(ab, "affine")
+    assert np.all(np.abs(out - ref) <= 1e-4 * np.maximum(np.abs(ref), 1))
+
+
+@pytest.mark.parametrize("threads", [1, 4])
+def test_cpu_baseline_dims_matches_numpy(oracle, threads):
+    rng = np.random.default_rng(threads)
+    rows, cols = 37, 53
+    M = rng.uniform(-1, 1, (rows, 2 * cols)).astype(np.float32)
+    buf = M.reshape(-1, order="F")
+    for cs, view in ((rows, M[:, :cols]), (2 * rows, M[:, ::2])):
+        # the plain matrix (col stride = rows) and every second column
+        b = buf if cs == 2 * rows else M[:, :cols].reshape(-1, order="F")
+        for dim, ref in ((1, view.astype(np.float64).sum(0)), (2, view.astype(np.float64).sum(1))):
+            out = np.empty(cols if dim == 1 else rows, np.float32)
+            oracle.baseline_sum_dims_f32(b, rows, cols, cs, dim, out, threads)
+            np.testing.assert_allclose(out, ref, rtol=1e-4, atol=1e-5)
+
+
 def test_reduce2_matches_numpy_and_closed_forms(oracle):
     rng = np.random.default_rng(6)
     x = rng.standard_normal(10_000)
