@@ -18,7 +18,8 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--all [--all-json PA
   --all-json     also write those rows, with the ceilings, to PATH
   --sweep        the reference's 10^6..10^9 size sweep
   --sweep-2d     the reference's matvec / vecmat shape sweep (n*p = 10^7..10^9)
-  --timeline [large|mid]  only the per-tile phases of the scan (instrumented library)
+  --timeline [large|mid|reduce]  only the per-tile phases of the scan, or the
+                 per-workgroup phases of the full reduction (instrumented library)
   --pmc-run      only the marked dispatch sequence of every configuration,
                  for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs
   --pmc-summary  FETCH_DIR WRITE_DIR CASES_LOG OUT_JSON: per-configuration
@@ -132,7 +133,7 @@ def main():
                     help="the reference's scan/mapreduce size sweep (perfs/julia/benchmarks)")
     ap.add_argument("--sweep-2d", action="store_true",
                     help="the reference's matvec/vecmat shape sweep (perfs/julia/benchmarks)")
-    ap.add_argument("--timeline", nargs="?", const="large", choices=("large", "mid"),
+    ap.add_argument("--timeline", nargs="?", const="large", choices=("large", "mid", "reduce"),
                     help="only the per-tile scan timeline (libkfhip_timeline.so): the large "
                          "scans (default) or the mid sizes of the reference's sweep")
     ap.add_argument("--pmc-run", action="store_true",
@@ -159,6 +160,9 @@ def main():
     torch.cuda.set_device(dev)
     if args.pmc_run:
         pmc_run(kf, dev)
+        return
+    if args.timeline == "reduce":
+        print(json.dumps({"reduce_timeline": reduce_timeline(dev)}), flush=True)
         return
     if args.timeline:
         cases = TIMELINE_CASES if args.timeline == "large" else MID_TIMELINE_CASES
@@ -730,6 +734,10 @@ def scan_timeline(dev, cases=TIMELINE_CASES):
         elif dt == 4:
             x = torch.randint(0, 256, (n,), device=dev, generator=g, dtype=torch.uint8)
             op, es = 0, 1
+        elif dt in (6, 7):  # QuaternionF32 / QuaternionF64 (unit quaternions), Hamilton product
+            x = torch.randn(n, 4, device=dev, generator=g, dtype=torch.float32 if dt == 6 else torch.float64)
+            x /= x.norm(dim=1, keepdim=True)
+            op, es = 4, 4 * x.element_size()
         else:
             x = torch.rand(n, device=dev, generator=g, dtype=torch.float64 if dt == 1 else torch.float32)
             op, es = 0, x.element_size()
@@ -760,17 +768,87 @@ def scan_timeline(dev, cases=TIMELINE_CASES):
         full = ev[np.argmax(active >= 0.95 * active.max()), 0]
         last = st.max()
         tile_bytes = 2 * es * n / len(a)
-        steady = ((en >= full) & (en <= last)).sum() * tile_bytes / (last - full) / 1e3
+        # no steady window when every tile is resident at once (one generation)
+        steady = ((en >= full) & (en <= last)).sum() * tile_bytes / (last - full) / 1e3 if last > full else None
         row = {"case": label, "us": round(t * 1e6, 1), "gbps": round(2 * es * n / t / 1e9), "tiles": len(a),
                "peak_resident": int(active.max()), "span_us": round(float(en.max()), 1),
                "tile_life_us": round(float(np.median(en - st)), 2), "load_scan_us": round(float(np.median(sc - st)), 2),
                "lookback_us": round(float(np.median(pf - sc)), 2), "store_issue_us": round(float(np.median(en - pf)), 2),
-               "ramp_us": round(float(full), 2), "steady_gbps": round(float(steady)),
+               "ramp_us": round(float(full), 2), "steady_gbps": None if steady is None else round(float(steady)),
                "drain_us": round(float(en.max() - last), 1),
                "tiles_per_xcd": np.bincount(a[:, 4].astype(int) & 15, minlength=8)[:8].tolist()}
         rows.append(row)
         log(json.dumps(row))
         del x, y, scr, buf
+    return rows
+
+
+REDUCE_TIMELINE_CASES = (("Float32 n=10^6", 0, 10**6), ("Float32 n=10^7", 0, 10**7), ("Float32 n=10^8", 0, 10**8),
+                         ("Float64 n=10^7", 1, 10**7), ("UInt8 n=10^7", 4, 10**7), ("UInt8 n=10^8", 4, 10**8))
+
+
+def reduce_timeline(dev, cases=REDUCE_TIMELINE_CASES):
+    """Per-workgroup phases of the one-launch full reduction (mapreduce of
+    identity, +) from the instrumented library: each workgroup's thread 0
+    stamps the 100 MHz realtime counter at its start, once its loads are
+    folded into its partial and once its slot is published (the last
+    workgroup: once the fold is done). Per case: time per call (HIP graph of
+    uninstrumented calls of the same library), grid, span, the spread of
+    workgroup starts, median load phase, and the last workgroup's own
+    phases: start, loads, wait for the slots, and the fold's completion
+    after the last slot was published."""
+    import ctypes
+    import __graft_entry__
+    kf = __graft_entry__.load_package()
+    D, K = kf._lib.debug_lib(), kf._lib
+    g = torch.Generator(device=dev).manual_seed(20261201)
+    rows = []
+    for label, dt, n in cases:
+        if dt == 4:
+            x = torch.randint(0, 256, (n,), device=dev, generator=g, dtype=torch.uint8)
+        else:
+            x = torch.rand(n, device=dev, generator=g, dtype=torch.float64 if dt == 1 else torch.float32)
+        out = torch.empty(1, dtype=x.dtype, device=dev)
+        sb = D.kf_reduce_scratch_bytes(dt, n)
+        scr = torch.zeros(sb, dtype=torch.uint8, device=dev)
+
+        def call():
+            rc = D.kf_reduce(K.OP_ADD, K.MAP_IDENTITY, dt, ctypes.c_void_p(x.data_ptr()), n, 1,
+                             ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(scr.data_ptr()), sb,
+                             ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+            assert rc == 0, D.kf_last_error()
+        t = _graph_time(call)
+        L, sink, nb = K.lib(), torch.zeros(4, dtype=torch.int32, device=dev), x.numel() * x.element_size()
+
+        def probe(kind):
+            return lambda: K.check(L.kf_bw_probe(kind, ctypes.c_void_p(sink.data_ptr()), ctypes.c_void_p(x.data_ptr()),
+                                                 nb, None, 0, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)),
+                                   "kf_bw_probe")
+        t_read = min(_graph_time(probe(K.BW_READ)), _graph_time(probe(K.BW_READ_TILED)))
+        wmax = 1 << 16
+        buf = torch.zeros(wmax * 6, dtype=torch.int64, device=dev)
+        D.kf_debug_reduce_timeline(ctypes.c_void_p(buf.data_ptr()))
+        for _ in range(3):  # the last of three back-to-back calls, as in the graph
+            call()
+        torch.cuda.synchronize()
+        D.kf_debug_reduce_timeline(None)
+        a = buf.cpu().numpy().reshape(-1, 6)
+        grid = int(a[:, 5].max())
+        a = a[:grid]
+        t0 = a[:, 0].min()
+        st, ld, en = ((a[:, k] - t0) * 0.01 for k in range(3))  # microseconds
+        last_pub = float(en[:-1].max()) if grid > 1 else float(ld[-1])
+        row = {"case": label, "us": round(t * 1e6, 2), "gbps": round(x.numel() * x.element_size() / t / 1e9),
+               "read_probe_us": round(t_read * 1e6, 2), "frac_of_read_probe": round(t_read / t, 3),
+               "grid": grid, "span_us": round(float(en.max()), 2), "start_spread_us": round(float(st.max()), 2),
+               "load_us_median": round(float(np.median(ld - st)), 2), "load_us_max": round(float((ld - st).max()), 2),
+               "last_wg_start_us": round(float(st[-1]), 2), "last_wg_loaded_us": round(float(ld[-1]), 2),
+               "last_slot_published_us": round(last_pub, 2), "fold_done_us": round(float(en[-1]), 2),
+               "fold_after_last_slot_us": round(float(en[-1]) - last_pub, 2),
+               "wgs_per_xcd": np.bincount(a[:, 3].astype(int) & 15, minlength=8)[:8].tolist()}
+        rows.append(row)
+        log(json.dumps(row))
+        del x, scr, buf
     return rows
 
 

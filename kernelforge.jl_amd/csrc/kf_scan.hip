@@ -127,17 +127,31 @@ constexpr int64_t kU8WideBytes = 384LL << 20;
 constexpr int kTierWide = kTiers;      // tier index of the wide shape
 constexpr int kTierHuge = kTiers + 1;  // UInt8 from kHugeBytes
 template <class T> constexpr bool has_wide_tier() {
-  return sizeof(T) == 4 || sizeof(T) == 8 || sizeof(T) == 1;
+  return sizeof(T) == 4 || sizeof(T) == 8 || sizeof(T) == 1 || is_quat<T>;
 }
+// Quaternions take a wide shape of longer lane chunks: QuaternionF32 768
+// threads x 8 units (96 KiB) from kQ32WideBytes, QuaternionF64 512 x 4
+// units (64 KiB, as its 1024 x 2 default) from kWideBytes. More units per
+// lane spread the wave scan's six combines and the prefix combine over more
+// elements (about 2.9 Hamilton products per element at 8 units, 3.75 at 4),
+// and the shorter QuaternionF64 workgroups fit more tiles per CU. Measured
+// on MI355X (HIP graphs, us, default -> wide): QuaternionF32 2^26 588.7 ->
+// 549.3, 2^24 157.7 -> 150.6 (4*10^6: 43.9 -> 45.0, hence the threshold);
+// QuaternionF64 10^6 37.8 -> 36.7, 2^22 123.6 -> 103.6, 2^24 471.9 -> 401.4.
+// (QuaternionF32 at 512 x 8: 639.8 us at 2^26; at 256 x 8: 683.0.)
+constexpr int64_t kQ32WideBytes = 128LL << 20;
+constexpr int kWideBlockQ32 = 768, kWideVQ32 = 8, kWideBlockQ64 = 512, kWideVQ64 = 4;
 template <class T> constexpr bool has_huge_tier() { return sizeof(T) == 1; }
 // (Float32 and the 8-byte types measured 0.5-10 % slower at 512 x 12 or 16.)
 constexpr int kWideBlockF32 = 768, kWideVF32 = 8, kWideBlock8 = 768, kWideV8 = 8;
 template <class T> constexpr int scan_block(int tier) {
+  if (is_quat<T> && tier == kTierWide) return sizeof(T) == 16 ? kWideBlockQ32 : kWideBlockQ64;
   if (sizeof(T) == 1) return 512;
   if (tier != kTierWide) return kScanBlock;
   return sizeof(T) == 4 ? kWideBlockF32 : kWideBlock8;
 }
 template <class T> constexpr int tier_v(int tier) {
+  if (is_quat<T> && tier == kTierWide) return sizeof(T) == 16 ? kWideVQ32 : kWideVQ64;
   if (tier == kTierHuge) return 16;
   if (tier != kTierWide) return kTierV[tier];
   return sizeof(T) == 1 ? 12 : sizeof(T) == 4 ? kWideVF32 : kWideV8;
@@ -842,7 +856,9 @@ template <class T> constexpr int max_tier() { return sizeof(T) > 16 ? 1 : sizeof
 template <class T> int scan_tier(int64_t n) {
   const int64_t bytes = n * (int64_t)sizeof(T);
   if (has_huge_tier<T>() && bytes >= kHugeBytes) return kTierHuge;
-  if (has_wide_tier<T>() && bytes >= (sizeof(T) == 1 ? kU8WideBytes : kWideBytes)) return kTierWide;
+  if (has_wide_tier<T>() &&
+      bytes >= (sizeof(T) == 1 ? kU8WideBytes : sizeof(T) == 16 ? kQ32WideBytes : kWideBytes))
+    return kTierWide;
   int t = max_tier<T>();
   while (t > kMinTier<T> && bytes < min_tiles<T>() * (int64_t)scan_block<T>(t) * kTierV[t] * kVecBytes<T>) --t;
   return t;
