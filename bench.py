@@ -700,7 +700,7 @@ TIMELINE_CASES = (("C4 affine n=2^26", 5, 2**26), ("affine n=2^27", 5, 2**27), (
                   ("Float64 n=2^26", 1, 2**26), ("Float64 n=2^27", 1, 2**27), ("Float32 n=2^28", 0, 2**28))
 # Mid sizes: UInt8 and Float32 at equal bytes, from one generation of
 # resident tiles to many.
-MID_TIMELINE_CASES = (("UInt8 n=10^7", 4, 10**7), ("UInt8 n=10^8", 4, 10**8), ("UInt8 n=3*10^8", 4, 3 * 10**8),
+MID_TIMELINE_CASES = (("Float32 n=10^6 (C1)", 0, 10**6), ("UInt8 n=10^7", 4, 10**7), ("UInt8 n=10^8", 4, 10**8), ("UInt8 n=3*10^8", 4, 3 * 10**8),
                       ("UInt8 n=2^30", 4, 2**30), ("Float32 n=2.5*10^6", 0, 25 * 10**5),
                       ("Float32 n=2.5*10^7", 0, 25 * 10**6), ("Float32 n=10^8", 0, 10**8),
                       ("Float64 n=10^7", 1, 10**7))

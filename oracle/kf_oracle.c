@@ -334,6 +334,10 @@ void kfo_reduce_dim_i(const void* A, int dt, int64_t rows, int64_t cols, int64_t
 }
 
 /* ------------------------------------------------------- CPU baseline ---- */
+/* Compiled at -O3 so that the independent partial sums vectorise, as Base's
+ * @simd blocks do. */
+#pragma GCC push_options
+#pragma GCC optimize("O3")
 
 /* Base.accumulate!(+, dst, src) on Float32: sequential, Float32 arithmetic. */
 void kfb_scan_add_f32_seq(const float* x, float* y, int64_t n) {
@@ -412,11 +416,7 @@ float kfb_sum_f32_par(const float* x, int64_t n, int threads) {
  * combine of the chunk totals and a second pass that re-scans each chunk
  * from its prefix). Element arithmetic throughout (Int32 wraps, Float32 and
  * Float64 stay in their width); sums keep 8 independent partials per
- * thread, as Base's vectorised blocks do. Compiled at -O3 so that the
- * independent partials vectorise. */
-#pragma GCC push_options
-#pragma GCC optimize("O3")
-
+ * thread, as Base's vectorised blocks do. */
 static int clamp_threads(int threads) { return threads < 1 ? 1 : threads > 1024 ? 1024 : threads; }
 
 /* Base.accumulate!(+, dst, src) on Int32 (wrap-around); exclusive shifts
