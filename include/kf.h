@@ -193,11 +193,14 @@ int kf_scan_shaped(kf_op op, kf_map f, kf_post g, kf_dtype dt, int exclusive,
  * buffer), a tile stops after 2^24 lookback polls and raises the give-up
  * flag in the scratch header; every waiting tile of that grid then stops
  * too, no stopped tile stores, and the results are invalid. The flag is
- * sticky: until it is cleared, every later kf_scan on that scratch is a
- * no-op (dst untouched). kf_scan_scratch_status synchronises `stream`,
+ * sticky: until it is cleared, every later kf_scan on that scratch stores
+ * nothing (dst untouched), and each such call is reported like the give-up
+ * itself (kf_async_status). kf_scan_scratch_status synchronises `stream`,
  * sets *gave_up = 1 if the flag is raised and then clears it and moves the
  * buffer's epoch past every descriptor of the failed call, so the buffer is
- * valid again; kf_scratch_reset (a zero fill) also clears it. */
+ * valid again; kf_scratch_reset (a zero fill) also clears it. The status
+ * queries leave the process-wide report alone (it may stand for another
+ * buffer): read it with kf_async_status. */
 int kf_scan_scratch_status(void* scratch, void* stream, int* gave_up);
 
 
