@@ -129,18 +129,19 @@ constexpr int kTierHuge = kTiers + 1;  // UInt8 from kHugeBytes
 template <class T> constexpr bool has_wide_tier() {
   return sizeof(T) == 4 || sizeof(T) == 8 || sizeof(T) == 1 || is_quat<T>;
 }
-// Quaternions take a wide shape of longer lane chunks: QuaternionF32 768
-// threads x 8 units (96 KiB) from kQ32WideBytes, QuaternionF64 512 x 4
-// units (64 KiB, as its 1024 x 2 default) from kWideBytes. More units per
-// lane spread the wave scan's six combines and the prefix combine over more
-// elements (about 2.9 Hamilton products per element at 8 units, 3.75 at 4),
-// and the shorter QuaternionF64 workgroups fit more tiles per CU. Measured
-// on MI355X (HIP graphs, us, default -> wide): QuaternionF32 2^26 588.7 ->
-// 549.3, 2^24 157.7 -> 150.6 (4*10^6: 43.9 -> 45.0, hence the threshold);
-// QuaternionF64 10^6 37.8 -> 36.7, 2^22 123.6 -> 103.6, 2^24 471.9 -> 401.4.
-// (QuaternionF32 at 512 x 8: 639.8 us at 2^26; at 256 x 8: 683.0.)
-constexpr int64_t kQ32WideBytes = 128LL << 20;
-constexpr int kWideBlockQ32 = 768, kWideVQ32 = 8, kWideBlockQ64 = 512, kWideVQ64 = 4;
+// Quaternions take a wide shape of longer lane chunks from kWideBytes on:
+// QuaternionF32 768 threads x 8 units (96 KiB), QuaternionF64 1024 x 4
+// units (128 KiB). More units per lane spread the wave scan's six combines
+// and the prefix combine over more elements (about 2.9 Hamilton products
+// per element at 8 units, 3.75 at 4). Measured on MI355X (HIP graphs, us;
+// tiles through the LDS transpose below): QuaternionF32 at 768 x 8 vs 1024
+// x 4: 2*10^6 18.5 vs 19.6, 4*10^6 32.6 vs 33.6, 2^23 57.3 vs 61.8, 2^24
+// 103.0 vs 115.0, 2^26 377.1 vs 434.7 (512 x 16 378, 768 x 16 402);
+// QuaternionF64 at 1024 x 4 vs 1024 x 2: 10^6 28.4 vs 32.9, 2^22 87.4 vs
+// 114.0, 2^24 335.4 vs 430.9 (512 x 4 349, 768 x 4 346, 512 x 8 341). (Before
+// the transpose, with blocked loads and stores, QuaternionF32 2^26 took
+// 588.7 us at 1024 x 4 and 549.3 at 768 x 8.)
+constexpr int kWideBlockQ32 = 768, kWideVQ32 = 8, kWideBlockQ64 = 1024, kWideVQ64 = 4;
 template <class T> constexpr bool has_huge_tier() { return sizeof(T) == 1; }
 // (Float32 and the 8-byte types measured 0.5-10 % slower at 512 x 12 or 16.)
 constexpr int kWideBlockF32 = 768, kWideVF32 = 8, kWideBlock8 = 768, kWideV8 = 8;
@@ -502,16 +503,76 @@ template <class Op, int V> constexpr bool kLdsRowsFor = __is_same(Op, OpAffine) 
 // holds units l*V .. l*V + V-1 of its wave's chunk, scans them serially in
 // registers, and one wave scan over the lane totals follows. Striped, every
 // 64-element row needed its own 6-step wave scan (6 of the 16-product
-// combines per element); blocked, about 2 to 3.5. The loads of one
-// instruction then stride V units and the V instructions of a lane cover
-// its contiguous chunk, so these accesses go through the cache (temporal
-// loads and stores) and every line is still read from HBM once. Measured
-// (HIP graphs, 2^26 quaternions): QuaternionF32 897 -> 608 us, Float64
-// 1916 -> 1874 us (nontemporal accesses in this layout: 1580 / 2335 us).
-// Both stay bound by their combine chains at one or two workgroups per CU
-// (QuaternionF32 at 8 units per lane, one workgroup per CU: 675 us;
-// Float64 quaternions at 512 threads: 2343 us).
+// combines per element); blocked, about 2 to 3.5 (2^26 quaternions, HIP
+// graphs: QuaternionF32 897 -> 608 us, Float64 1916 -> 1874 us). Full tiles
+// reach that order through LDS (below); the partial tiles read and write
+// their units in place, through the cache (temporal accesses, so that the
+// lines a lane's V instructions share stay cached between them).
 template <class T> constexpr bool kBlockedFor = ScanShape<T>::EPV == 1;
+
+// Full tiles of the blocked layout move through LDS instead: the wave loads
+// its chunk striped (unit j*64 + lane: every instruction one contiguous
+// KiB, nontemporal) and transposes it to the blocked order, and the results
+// go back to the striped order before the stores. A lane's units l*V ..
+// l*V+V-1 are V*16 or V*32 bytes apart from its neighbours', so a blocked
+// access instruction touches 64 cache lines where a striped one touches 8:
+// a copy in the blocked pattern through the cache moves 3.9 TB/s on MI355X
+// (1 GiB), in the striped pattern 5.7-6.6. The transpose runs in two halves
+// (lanes 0-31, then 32-63) through a per-wave buffer of half the chunk, with
+// one 16-byte pad per V units so that the blocked side's stride of V+1
+// granules spreads over the banks.
+template <class T, int V> struct BlockedLds {
+  static constexpr int G = kVecBytes<T> / 16;                  // 16-byte granules per unit
+  static constexpr int HALF = V / 2 * kWave;                     // units per half chunk
+  static constexpr int GRANULES = HALF * G + HALF / V;           // with the pads
+  __device__ static int at(int i) { return i * G + i / V; }     // granule of local unit i
+};
+template <class Vec> __device__ inline void lds_put(uint4* buf, int g, const Vec& v) {
+  __builtin_memcpy(buf + g, &v, sizeof(Vec));
+}
+template <class Vec> __device__ inline void lds_get(const uint4* buf, int g, Vec& v) {
+  __builtin_memcpy(&v, buf + g, sizeof(Vec));
+}
+// striped -> blocked (in place on r); buf: this wave's BlockedLds::GRANULES
+template <class T, int V, class Vec>
+__device__ inline void striped_to_blocked(Vec (&r)[V], uint4* buf, int lane) {
+  using B = BlockedLds<T, V>;
+  Vec b[V];
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int jj = 0; jj < V / 2; ++jj) lds_put(buf, B::at(jj * kWave + lane), r[p * (V / 2) + jj]);
+    __builtin_amdgcn_wave_barrier();
+    if ((lane >> 5) == p) {
+#pragma unroll
+      for (int k = 0; k < V; ++k) lds_get(buf, B::at((lane - 32 * p) * V + k), b[k]);
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int k = 0; k < V; ++k) r[k] = b[k];
+}
+// blocked -> striped (in place on r)
+template <class T, int V, class Vec>
+__device__ inline void blocked_to_striped(Vec (&r)[V], uint4* buf, int lane) {
+  using B = BlockedLds<T, V>;
+  Vec s[V];
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    __builtin_amdgcn_wave_barrier();
+    if ((lane >> 5) == p) {
+#pragma unroll
+      for (int k = 0; k < V; ++k) lds_put(buf, B::at((lane - 32 * p) * V + k), r[k]);
+    }
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int jj = 0; jj < V / 2; ++jj) lds_get(buf, B::at(jj * kWave + lane), s[p * (V / 2) + jj]);
+  }
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int k = 0; k < V; ++k) r[k] = s[k];
+}
 template <class T, int V> __device__ inline int unit_slot(int j, int lane) {
   return kBlockedFor<T> ? lane * V + j : j * kWave + lane;
 }
@@ -545,6 +606,8 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
   __shared__ Vec s_stash[kStashForLookback<T, BLOCK> ? V : 1][kWave];
   __shared__ T s_rowpre[kStashForLookback<T, BLOCK> && !kLdsRows ? V : 1][kWave];
   __shared__ __align__(16) T s_rows[kLdsRows ? kScanWaves : 1][kLdsRows ? V * kWave : 1];
+  constexpr bool kTranspose = kBlockedFor<T> && V >= 2;
+  __shared__ uint4 s_tr[kTranspose ? kScanWaves : 1][kTranspose ? BlockedLds<T, (V >= 2 ? V : 2)>::GRANULES : 1];
 
   const int tid = threadIdx.x;
   const int lane = lane_id();
@@ -580,9 +643,15 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
   Vec r[V];
   if (full) {
     const Vec* g = reinterpret_cast<const Vec*>(srcv + wbase);
+    if constexpr (kTranspose) {
 #pragma unroll
-    for (int j = 0; j < V; ++j)
-      r[j] = kBlockedFor<T> ? ld_unit_cached(g + unit_slot<T, V>(j, lane)) : ld_vec(g + unit_slot<T, V>(j, lane));
+      for (int j = 0; j < V; ++j) r[j] = ld_vec(g + j * kWave + lane);
+      striped_to_blocked<T, V>(r, s_tr[wave], lane);
+    } else {
+#pragma unroll
+      for (int j = 0; j < V; ++j)
+        r[j] = kBlockedFor<T> ? ld_unit_cached(g + unit_slot<T, V>(j, lane)) : ld_vec(g + unit_slot<T, V>(j, lane));
+    }
     if constexpr (!__is_same(Map, MapIdentity)) {
 #pragma unroll
       for (int j = 0; j < V; ++j) {
@@ -770,8 +839,38 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
   }
 
   // ---- apply and store ----------------------------------------------------
+  if constexpr (kTranspose) {
+    if (full) {
+      // the lane's results in the blocked order, then back to striped
+      // through LDS, then 16-byte nontemporal stores of whole KiB rows
+      const T p = Op::combine(prefix, rowpre[0]);
+      Vec ob[V];
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        T x, o;
+        __builtin_memcpy(&x, &r[j], sizeof(T));
+        if constexpr (EXCL) {
+          if (j == 0) {
+            o = (tile == 0 && tid == 0) ? exclusive_first<T, Op>() : p;  // element 0
+          } else {
+            T prev;
+            __builtin_memcpy(&prev, &r[j - 1], sizeof(T));
+            o = Op::combine(p, prev);
+          }
+        } else {
+          o = Op::combine(p, x);
+        }
+        __builtin_memcpy(&ob[j], &o, sizeof(T));
+      }
+      blocked_to_striped<T, V>(ob, s_tr[wave], lane);
+      Vec* gd = reinterpret_cast<Vec*>(dstv + wbase);
+#pragma unroll
+      for (int j = 0; j < V; ++j) st_vec(gd + j * kWave + lane, ob[j]);
+    }
+  }
 #pragma unroll
   for (int j = 0; j < V; ++j) {
+    if (kTranspose && full) break;
     if constexpr (__is_same(T, uint8_t) && __is_same(Op, OpAdd)) {
       // UInt8 +: add the prefix byte to all 16 packed bytes at once (the
       // exclusive result is the inclusive one shifted by a byte; element 0
@@ -857,7 +956,7 @@ template <class T> int scan_tier(int64_t n) {
   const int64_t bytes = n * (int64_t)sizeof(T);
   if (has_huge_tier<T>() && bytes >= kHugeBytes) return kTierHuge;
   if (has_wide_tier<T>() &&
-      bytes >= (sizeof(T) == 1 ? kU8WideBytes : sizeof(T) == 16 ? kQ32WideBytes : kWideBytes))
+      bytes >= (sizeof(T) == 1 ? kU8WideBytes : kWideBytes))
     return kTierWide;
   int t = max_tier<T>();
   while (t > kMinTier<T> && bytes < min_tiles<T>() * (int64_t)scan_block<T>(t) * kTierV[t] * kVecBytes<T>) --t;

@@ -128,14 +128,14 @@ def test_scan_shape_keywords_pick_the_nearest_compiled_shape(kf):
     # Nitem beyond the compiled range clamps to the widest shape
     assert _shape(kf, K.F32, 2**20, 0, 10**6)[1] == 32
     # quaternions: 1024 x 1, 2 or 4 units (QuaternionF64 1 or 2) and the wide
-    # shapes 768 x 8 (QuaternionF32 from 128 MiB) and 512 x 4 (QuaternionF64
-    # from 17 MiB)
-    assert _shape(kf, K.Q64, 100, 1024, 64) == (1024, 2)  # 1024-thread shapes stop at 2 per thread
-    assert _shape(kf, K.Q64, 100, 512, 64) == (512, 4)
-    assert _shape(kf, K.Q64, 100, 0, 64) == (1024, 2)  # a tie in distance goes to the first equal tile
+    # shapes 768 x 8 (QuaternionF32) and 1024 x 4 (QuaternionF64) from 17 MiB
+    assert _shape(kf, K.Q64, 100, 1024, 64) == (1024, 4)  # the widest QuaternionF64 shape
+    assert _shape(kf, K.Q64, 100, 1024, 2) == (1024, 2)
+    assert _shape(kf, K.Q32, 100, 1024, 64) == (768, 8)
     assert _shape(kf, K.Q32, 2**26, 0, 0) == (768, 8)
-    assert _shape(kf, K.Q32, 2**22, 0, 0) == (1024, 4)
-    assert _shape(kf, K.Q64, 10**6, 0, 0) == (512, 4)
+    assert _shape(kf, K.Q32, 2**22, 0, 0) == (768, 8)
+    assert _shape(kf, K.Q32, 10**6, 0, 0) == (1024, 4)
+    assert _shape(kf, K.Q64, 10**6, 0, 0) == (1024, 4)
     assert _shape(kf, K.Q64, 5 * 10**5, 0, 0) == (1024, 2)
     # scratch follows the shape: one 128-byte line per tile + the header
     n = 10**6
