@@ -1041,8 +1041,14 @@ __global__ __launch_bounds__(kDimBlock) void reduce_rows_kernel(
   for (int u = 0; u < kRowVecs; ++u)
 #pragma unroll
     for (int e = 0; e < EPV; ++e) a[u][e] = id;
+  // Vector launches have rows % EPV == 0; the last strip may be partial: its
+  // vectors past the end load nothing and store nothing (the rows beyond the
+  // last column's end may lie past the allocation)
+  bool in_strip[kRowVecs];
+#pragma unroll
+  for (int u = 0; u < kRowVecs; ++u) in_strip[u] = strip + (int64_t)(u * kDimBlock + tid) * EPV < rows;
   if constexpr (VEC && Dot4<T, Op, F>::kind >= 0) {
-    // UInt8 +: packed 16-bit accumulators (whole strips only, as below)
+    // UInt8 +: packed 16-bit accumulators
     constexpr int K = Dot4<T, Op, F>::kind;
     uint32_t ae[kRowVecs][4] = {}, ao[kRowVecs][4] = {};
     const T* p = A + strip;
@@ -1053,7 +1059,8 @@ __global__ __launch_bounds__(kDimBlock) void reduce_rows_kernel(
       for (int q = 0; q < kColUnroll; ++q)
 #pragma unroll
         for (int u = 0; u < kRowVecs; ++u)
-          r[q][u] = ld_stream(reinterpret_cast<const uint4*>(p + (c + q) * col_stride) + u * kDimBlock + tid);
+          r[q][u] = in_strip[u] ? ld_stream(reinterpret_cast<const uint4*>(p + (c + q) * col_stride) + u * kDimBlock + tid)
+                                : uint4{0, 0, 0, 0};
 #pragma unroll
       for (int q = 0; q < kColUnroll; ++q) {
         const uint32_t w16 = F::kHasX ? 0x00010001u * (uint32_t)xv[(c + q) * xs] : 0u;
@@ -1065,7 +1072,9 @@ __global__ __launch_bounds__(kDimBlock) void reduce_rows_kernel(
       const uint32_t w16 = F::kHasX ? 0x00010001u * (uint32_t)xv[c * xs] : 0u;
 #pragma unroll
       for (int u = 0; u < kRowVecs; ++u)
-        pk16_vec<K>(ae[u], ao[u], ld_stream(reinterpret_cast<const uint4*>(p + c * col_stride) + u * kDimBlock + tid),
+        pk16_vec<K>(ae[u], ao[u],
+                    in_strip[u] ? ld_stream(reinterpret_cast<const uint4*>(p + c * col_stride) + u * kDimBlock + tid)
+                                : uint4{0, 0, 0, 0},
                     w16);
     }
 #pragma unroll
@@ -1075,7 +1084,7 @@ __global__ __launch_bounds__(kDimBlock) void reduce_rows_kernel(
       __builtin_memcpy(a[u], wd, sizeof(wd));
     }
   } else if constexpr (VEC) {
-  {  // vector launches cover whole strips only (the host splits off the rest)
+  {
     const T* p = A + strip;
     int64_t c = c0;
     for (; c + kColUnroll <= c1; c += kColUnroll) {
@@ -1084,7 +1093,8 @@ __global__ __launch_bounds__(kDimBlock) void reduce_rows_kernel(
       for (int q = 0; q < kColUnroll; ++q)
 #pragma unroll
         for (int u = 0; u < kRowVecs; ++u)
-          r[q][u] = ld_stream(reinterpret_cast<const uint4*>(p + (c + q) * col_stride) + u * kDimBlock + tid);
+          r[q][u] = in_strip[u] ? ld_stream(reinterpret_cast<const uint4*>(p + (c + q) * col_stride) + u * kDimBlock + tid)
+                                : uint4{0, 0, 0, 0};
 #pragma unroll
       for (int q = 0; q < kColUnroll; ++q) {
         const T w = F::kHasX ? xv[(c + q) * xs] : id;
@@ -1101,7 +1111,8 @@ __global__ __launch_bounds__(kDimBlock) void reduce_rows_kernel(
       const T w = F::kHasX ? xv[c * xs] : id;
 #pragma unroll
       for (int u = 0; u < kRowVecs; ++u) {
-        const uint4 r = ld_stream(reinterpret_cast<const uint4*>(p + c * col_stride) + u * kDimBlock + tid);
+        const uint4 r = in_strip[u] ? ld_stream(reinterpret_cast<const uint4*>(p + c * col_stride) + u * kDimBlock + tid)
+                                    : uint4{0, 0, 0, 0};
         T x[EPV];
         __builtin_memcpy(x, &r, sizeof(x));
 #pragma unroll
@@ -1147,9 +1158,10 @@ __global__ __launch_bounds__(kDimBlock) void reduce_rows_kernel(
 #pragma unroll
   for (int u = 0; u < kRowVecs; ++u) {
     const int64_t r0 = strip + (int64_t)(u * kDimBlock + tid) * EPV;
+    if (r0 >= rows) continue;
     T* o = gridDim.y == 1 ? out + r0 * out_stride : out + (int64_t)s * rows + r0;
     if (VEC && (gridDim.y > 1 || out_stride == 1) && (uintptr_t)o % 16 == 0) {
-      // whole strip, contiguous aligned outputs: one 16-byte store
+      // a whole vector of rows, contiguous aligned outputs: one 16-byte store
       uint4 v;
       __builtin_memcpy(&v, a[u], sizeof(v));
       *reinterpret_cast<uint4*>(o) = v;
@@ -1511,16 +1523,10 @@ inline DimVec dim_vec(const void* A, int64_t rows, int64_t cs, size_t es, int di
   return v;
 }
 
-// A dim-2 vector launch covers whole strips only: rows past the last whole
-// strip go to further launches under the same rule (ending in the narrow
-// kernel). Partial bytes of that decomposition:
+// Partial bytes of a dim-2 vector launch (one launch, the last strip
+// possibly partial).
 inline size_t dim2_vec_need(size_t es, int64_t rows, int64_t cols, int64_t batch) {
-  const DimPlan p = plan_dim(es, rows, cols, 2, true, batch);
-  if (p.narrow) return p.partial_bytes;
-  const int64_t rs = (int64_t)kDimBlock * p.row_vecs * (int64_t)(16 / es);
-  const int64_t whole = rows / rs * rs;
-  if (whole == rows || whole == 0) return p.partial_bytes;
-  return kmax(dim2_vec_need(es, whole, cols, batch), dim2_vec_need(es, rows - whole, cols, batch));
+  return plan_dim(es, rows, cols, 2, true, batch).partial_bytes;
 }
 
 // Partial bytes the launch will use for this alignment (0: no scratch).
@@ -1730,20 +1736,6 @@ int launch_reduce_dim(const void* A, int64_t rows, int64_t cols, int64_t cs, int
     return kf_check_launch("reduce_rows_few_kernel");
   }
   const DimPlan p = plan_dim(sizeof(T), rows, cols, dim, vec, batch);
-  if (dim == 2 && vec && !p.narrow) {
-    // the vector kernel takes whole strips only; the rest is launched under
-    // the same rule (stream order lets the launches share the scratch)
-    const int64_t rs = (int64_t)kDimBlock * p.row_vecs * (int64_t)(16 / sizeof(T));
-    const int64_t whole = rows / rs * rs;
-    if (whole != rows && whole > 0) {
-      int rc = launch_reduce_dim<T, Op, F>(A, whole, cols, cs, 2, dst, ds, scratch, stream, batch, a_bstride, x, xs,
-                                           dst_bstride, false);
-      if (!rc)
-        rc = launch_reduce_dim<T, Op, F>((const T*)A + whole, rows - whole, cols, cs, 2, (T*)dst + whole * ds, ds,
-                                         scratch, stream, batch, a_bstride, x, xs, dst_bstride, false);
-      return rc;
-    }
-  }
   if (dim == 1) {
     if (use_flat_cols_dim1(A, rows, cs, sizeof(T), batch))
       return launch_flat_cols<T, Op, F>((const T*)A, rows, cols, (T*)dst, ds, (const T*)x, xs, stream);

@@ -386,3 +386,33 @@ def test_flat_path_columns_up_to_4k(kf, oracle, dev, dt):
                     got = kf.mapreduce(kf.identity, op, A, dims=1).cpu().numpy().reshape(-1)
                     ref = Mi.astype(np.int64).sum(axis=1).astype(dt) if op == "+" else Mi.max(axis=1)
                     assert np.array_equal(got, ref), (rows, cols, op)
+
+
+@pytest.mark.parametrize("dt", [np.uint8, np.int32, np.int64])
+def test_dims2_partial_last_strip(kf, dev, dt):
+    # dims=2 over tall aligned columns whose row count is not a whole number
+    # of the vector kernel's strips (256 threads x 1-8 vectors): the last
+    # strip is partial, its vectors past the end load and store nothing. The
+    # matrix is a tensor of exactly rows * cols elements, so a load past the
+    # last column's end would leave the allocation. Integers: exact.
+    rng = np.random.default_rng(211)
+    ev = 16 // np.dtype(dt).itemsize
+    for rows, cols in ((10_000, 700), (100_000, 90), (1_000_000, 12), (4096 + ev, 300), (65536 - ev, 64)):
+        a = rng.integers(0, 100, (cols, rows)).astype(dt)       # Julia rows x cols, column-major
+        A = torch.from_numpy(a).to(dev).T
+        x = rng.integers(0, 7, cols).astype(dt)
+        print(f"partial strip {np.dtype(dt).name} {rows}x{cols}", flush=True)
+        got = kf.mapreduce(kf.identity, "+", A, dims=2).cpu().numpy().reshape(-1)
+        a64 = a.astype(np.int64)
+        m = 256 if dt == np.uint8 else 2**32 if dt == np.int32 else None
+        ref = a64.sum(axis=0)
+        if m:
+            assert np.array_equal(got.astype(np.int64) % m, ref % m), (rows, cols)
+        else:
+            assert np.array_equal(got.astype(np.int64), ref), (rows, cols)
+        got = kf.matvec(operator.mul, "+", A, torch.from_numpy(x).to(dev)).cpu().numpy()
+        ref = (a64 * x.astype(np.int64)[:, None]).sum(axis=0)
+        if m:
+            assert np.array_equal(got.astype(np.int64) % m, ref % m), (rows, cols, "matvec")
+        else:
+            assert np.array_equal(got.astype(np.int64), ref), (rows, cols, "matvec")
