@@ -5,7 +5,8 @@
  * Every entry point takes plain device pointers, element counts and strides
  * (in elements), and a hipStream_t (passed as void*; NULL = default stream).
  * Calls are stream-ordered and non-blocking; the library never allocates
- * device memory and never synchronises. Scratch memory is caller-owned:
+ * device memory (its one allocation is a 256-byte pinned host word for
+ * give-up reports, see kf_async_status) and never synchronises. Scratch memory is caller-owned:
  * size it with the matching *_scratch_bytes query and zero-fill it ONCE
  * before its first use (kf_scratch_reset does that on a stream). After that
  * the kernels keep it valid themselves (epoch-tagged tile descriptors and
@@ -128,8 +129,10 @@ int kf_scratch_reset(void* scratch, size_t bytes, void* stream);
  * HIP itself, the report belongs to the process, not to one buffer or
  * stream. The report word is allocated (pinned host memory, 256 bytes,
  * once per process) by kf_init or by the first call of any compute entry
- * point except kf_reduce_noalloc, which never allocates: call kf_init at
- * set-up to have its give-ups reported too. */
+ * point except kf_reduce_noalloc, which never allocates, and never while
+ * the call's stream is being captured into a graph: kernels launched before
+ * the word exists carry none. Call kf_init at set-up to have every kernel,
+ * captured and kf_reduce_noalloc ones included, report. */
 int kf_init(void);
 int kf_async_status(int* gave_up);
 

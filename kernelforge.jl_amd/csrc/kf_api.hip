@@ -84,9 +84,18 @@ bool g_mbox_failed = false;
 
 uint32_t* kf_mailbox_peek() { return g_mbox.load(std::memory_order_acquire); }
 
-uint32_t* kf_mailbox() {
+uint32_t* kf_mailbox(hipStream_t stream) {
   uint32_t* p = g_mbox.load(std::memory_order_acquire);
   if (p) return p;
+  // never allocate while the caller's stream is being captured into a graph
+  // (an allocation there can invalidate the capture): the captured kernels
+  // then carry no report word; kf_init before the capture avoids that
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &cap) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  if (cap != hipStreamCaptureStatusNone) return nullptr;
   std::lock_guard<std::mutex> lock(g_mbox_mu);
   p = g_mbox.load(std::memory_order_relaxed);
   if (p || g_mbox_failed) return p;
@@ -115,7 +124,7 @@ int kf_take_giveup(const char* who) {
 }
 
 extern "C" int kf_init(void) {
-  if (!kf_mailbox()) return kf_set_error(KF_EHIP, "kf_init: could not allocate the pinned give-up report word");
+  if (!kf_mailbox(nullptr)) return kf_set_error(KF_EHIP, "kf_init: could not allocate the pinned give-up report word");
   return KF_OK;
 }
 

@@ -275,9 +275,10 @@ int kf_check_launch(const char* what);
 size_t kf_dtype_size(kf_dtype dt);
 int kf_validate_op(kf_op op, kf_map f, kf_dtype dt, int allow_affine);
 int kf_device_cu_count();
-// Host-mapped give-up report word (allocated on first use; null if that
-// failed). kf_mailbox_peek never allocates (for kf_reduce_noalloc).
-uint32_t* kf_mailbox();
+// Host-mapped give-up report word (allocated on first use outside stream
+// capture; null if that failed or the stream is capturing). kf_mailbox_peek
+// never allocates (for kf_reduce_noalloc).
+uint32_t* kf_mailbox(hipStream_t stream);
 uint32_t* kf_mailbox_peek();
 // KF_EGIVEUP (and clears the report) if a kernel queued by an earlier call
 // has given up since the last report; KF_OK otherwise. Non-blocking.

@@ -26,7 +26,7 @@ extern "C" int kf_reduce_dim_x(kf_op op, kf_map2 f, kf_dtype dt, const void* A, 
                                int64_t dst_stride, void* scratch, size_t scratch_bytes, void* stream) {
   int rc = kf_validate_op(op, KF_MAP_IDENTITY, dt, /*allow_affine=*/0);
   if (rc) return rc;
-  kf_mailbox();
+  kf_mailbox((hipStream_t)stream);
   if ((rc = kf_take_giveup("kf_reduce_dim_x"))) return rc;
   if (f != KF_MAP2_MUL && f != KF_MAP2_SQDIFF)
     return kf_set_error(KF_EINVAL, "kf_reduce_dim_x: map %d is not one of x*y, (x-y)^2", (int)f);

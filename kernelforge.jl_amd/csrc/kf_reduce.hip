@@ -800,7 +800,7 @@ extern "C" int kf_reduce(kf_op op, kf_map f, kf_dtype dt, const void* src, int64
                          void* dst, void* scratch, size_t scratch_bytes, void* stream) {
   int rc = kf_validate_op(op, f, dt, /*allow_affine=*/0);
   if (rc) return rc;
-  kf_mailbox();
+  kf_mailbox((hipStream_t)stream);
   if ((rc = kf_take_giveup("kf_reduce"))) return rc;
   if (n < 0) return kf_set_error(KF_EINVAL, "kf_reduce: n = %lld < 0", (long long)n);
   if (n == 0) return KF_OK;
@@ -843,7 +843,7 @@ extern "C" int kf_reduce2(kf_op op, kf_map2 f, kf_dtype dt, const void* x, int64
                           int64_t y_stride, int64_t n, void* dst, void* scratch, size_t scratch_bytes, void* stream) {
   int rc = kf_validate_op(op, KF_MAP_IDENTITY, dt, /*allow_affine=*/0);
   if (rc) return rc;
-  kf_mailbox();
+  kf_mailbox((hipStream_t)stream);
   if ((rc = kf_take_giveup("kf_reduce2"))) return rc;
   if (f != KF_MAP2_MUL && f != KF_MAP2_SQDIFF && f != KF_MAP2_WSQ && f != KF_MAP2_EXPDIFF)
     return kf_set_error(KF_EINVAL, "kf_reduce2: unknown map %d", (int)f);
@@ -889,7 +889,7 @@ extern "C" int kf_reduce3(kf_op op, kf_map3 f, kf_dtype dt, const void* x, int64
                           size_t scratch_bytes, void* stream) {
   int rc = kf_validate_op(op, KF_MAP_IDENTITY, dt, /*allow_affine=*/0);
   if (rc) return rc;
-  kf_mailbox();
+  kf_mailbox((hipStream_t)stream);
   if ((rc = kf_take_giveup("kf_reduce3"))) return rc;
   if (f != KF_MAP3_MUL) return kf_set_error(KF_EINVAL, "kf_reduce3: unknown map %d", (int)f);
   if (n < 0) return kf_set_error(KF_EINVAL, "kf_reduce3: n = %lld < 0", (long long)n);

@@ -19,7 +19,7 @@ extern "C" int kf_reduce_dim(kf_op op, kf_map f, kf_dtype dt, const void* A, int
                              size_t scratch_bytes, void* stream) {
   int rc = kf_validate_op(op, f, dt, /*allow_affine=*/0);
   if (rc) return rc;
-  kf_mailbox();
+  kf_mailbox((hipStream_t)stream);
   if ((rc = kf_take_giveup("kf_reduce_dim"))) return rc;
   if (dim != 1 && dim != 2) return kf_set_error(KF_EINVAL, "kf_reduce_dim: dim must be 1 or 2 (got %d)", dim);
   if (rows < 0 || cols < 0) return kf_set_error(KF_EINVAL, "kf_reduce_dim: negative shape");
@@ -62,7 +62,7 @@ extern "C" int kf_reduce_dim_batched(kf_op op, kf_map f, kf_dtype dt, const void
                                      int64_t dst_stride, void* scratch, size_t scratch_bytes, void* stream) {
   int rc = kf_validate_op(op, f, dt, /*allow_affine=*/0);
   if (rc) return rc;
-  kf_mailbox();
+  kf_mailbox((hipStream_t)stream);
   if ((rc = kf_take_giveup("kf_reduce_dim_batched"))) return rc;
   if (rows < 0 || cols < 0 || batch < 0) return kf_set_error(KF_EINVAL, "kf_reduce_dim_batched: negative shape");
   if (rows == 0 || batch == 0) return KF_OK;

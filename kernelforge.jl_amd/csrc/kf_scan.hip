@@ -1048,13 +1048,13 @@ void launch_scan_tier(const void* src, int64_t ss, void* dst, int64_t ds, int64_
     hipLaunchKernelGGL(kernel, dim3((unsigned)ntiles), dim3(B), 0, stream, (const T*)src, ss, (T*)dst, ds, n,
                        ntiles, (uint64_t*)scratch, vec, off, look_window(ntiles, resident_tiles<kernel>(B), (int64_t)B * V * kVecBytes<T>, kLookAllFor<T>,
                                    kLookBlockFor<T, B, V>, B), post,
-                       g_spin_limit, g_withhold, kf_mailbox());
+                       g_spin_limit, g_withhold, kf_mailbox(stream));
   } else {
     constexpr auto kernel = scan_kernel<T, Op, Map, false, B, V>;
     hipLaunchKernelGGL(kernel, dim3((unsigned)ntiles), dim3(B), 0, stream, (const T*)src, ss, (T*)dst, ds, n,
                        ntiles, (uint64_t*)scratch, vec, off, look_window(ntiles, resident_tiles<kernel>(B), (int64_t)B * V * kVecBytes<T>, kLookAllFor<T>,
                                    kLookBlockFor<T, B, V>, B), post,
-                       g_spin_limit, g_withhold, kf_mailbox());
+                       g_spin_limit, g_withhold, kf_mailbox(stream));
   }
 }
 

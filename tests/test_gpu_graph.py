@@ -69,3 +69,44 @@ def test_two_streams_concurrently(kf, oracle, dev):
         for i in range(2):
             ref = np.maximum.accumulate(oracle.scan(xs[i], "+"))
             assert np.array_equal(outs[i].cpu().numpy(), ref), (rep, i)
+
+
+_FRESH = r"""
+import sys, ctypes
+sys.path.insert(0, sys.argv[1])
+import torch
+import __graft_entry__
+kf = __graft_entry__.load_package()
+dev = torch.device("cuda:0")
+x = torch.arange(1, 100_001, dtype=torch.int64, device=dev)
+y = torch.empty_like(x)
+tmp = kf.get_allocation(kf.Scan1D, kf.identity, "+", x)
+torch.cuda.synchronize()
+g = torch.cuda.CUDAGraph()
+with torch.cuda.graph(g):          # the library's very first call happens under capture
+    kf.scan_("+", y, x, tmp=tmp)
+for _ in range(3):
+    y.zero_()
+    g.replay()
+    torch.cuda.synchronize()
+    assert int(y[-1]) == 100_000 * 100_001 // 2, int(y[-1])
+kf.scan_("+", y, x, tmp=tmp)       # and eagerly afterwards (the report word is allocated now)
+assert int(y[-1]) == 100_000 * 100_001 // 2
+flag = ctypes.c_int(-1)
+assert kf._lib.lib().kf_async_status(ctypes.byref(flag)) == 0 and flag.value == 0
+print("FRESH_OK")
+"""
+
+
+def test_first_library_call_under_capture(tmp_path):
+    # the give-up report word is allocated on first use, never while the
+    # caller's stream is being captured: a process whose first call is
+    # captured into a graph must capture and replay cleanly
+    import os
+    import subprocess
+    import sys
+    repo = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    script = tmp_path / "fresh.py"
+    script.write_text(_FRESH)
+    r = subprocess.run([sys.executable, str(script), repo], capture_output=True, text=True, timeout=110)
+    assert r.returncode == 0 and "FRESH_OK" in r.stdout, r.stdout[-2000:] + r.stderr[-2000:]
