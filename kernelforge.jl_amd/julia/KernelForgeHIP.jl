@@ -349,6 +349,7 @@ function scan(f::F, op::O, src::AbstractArray; g::G=identity, kwargs...) where {
     dst = similar(src, H, length(src))
     return scan!(f, op, dst, src; g, kwargs...)
 end
+
 function _scan_status(buf::ROCVector{UInt8})
     flag = Ref{Cint}(0)
     rc = ccall((:kf_scan_scratch_status, libkf), Cint, (Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cint}),
