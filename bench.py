@@ -470,7 +470,7 @@ def _host(t, out=False):
     _HOST_USED.add(key)
     if key not in _HOST:
         if out:
-            _HOST[key] = np.empty(tuple(t.shape), dtype=t.cpu()[:0].numpy().dtype)
+            _HOST[key] = np.empty(tuple(t.shape), dtype=torch.empty(0, dtype=t.dtype).numpy().dtype)
         else:
             _HOST[key] = t.contiguous().cpu().numpy()
     return _HOST[key]
