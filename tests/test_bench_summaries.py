@@ -75,3 +75,17 @@ def test_pmc_summary_calibrates_on_the_copy(tmp_path):
     assert r["configs"]["X"]["fetch_bytes"] == 1024 * 1024
     assert r["configs"]["X"]["write_bytes"] == 2048 * 1024
     assert abs(r["configs"]["X"]["ratio"] - 1.0) < 1e-12
+
+
+def test_cpu_row_times_both_thread_counts_and_reports_elements():
+    calls = []
+
+    def prep():
+        return lambda threads: calls.append(threads)
+    row = bench.cpu_row(prep, 2e9, 5e8, 16, budget_s=0.01)
+    assert set(calls) == {16, 1}
+    assert row["kind"] == "port" and row["threads"] == 16
+    # bytes / seconds and elements / seconds of the same timing
+    assert abs(row["gbps"] / row["gelems_per_s"] - 4.0) < 1e-2
+    assert abs(row["single_thread_gbps"] / row["single_thread_gelems_per_s"] - 4.0) < 1e-2
+    assert row["calls"] >= 1 and row["single_thread_calls"] >= 1
