@@ -193,6 +193,26 @@ def test_quaternion_scan_every_compiled_shape(kf, oracle, dev, dt):
                     (threads, items, n, exclusive)
 
 
+@pytest.mark.parametrize("dt", [np.float32, np.float64])
+def test_quaternion_scan_source_off_the_16_byte_grid(kf, oracle, dev, dt):
+    # full tiles load their source striped and transpose it through LDS; a
+    # source one component (4 or 8 bytes) off the 16-byte grid, with an
+    # aligned destination, takes that path with unaligned 16-byte loads.
+    # Exact on the group {+-1, +-i, +-j, +-k}; sizes over several wide tiles.
+    import operator
+    rng = np.random.default_rng(53)
+    for n in (3 * 6144 + 5, 1_500_001):
+        q = q8_sequence(rng, n, dt)
+        flat = torch.zeros(4 * n + 4, dtype=torch.float32 if dt == np.float32 else torch.float64, device=dev)
+        flat[1:1 + 4 * n] = torch.from_numpy(q.reshape(-1)).to(dev)
+        src = flat[1:1 + 4 * n].view(n, 4)
+        assert src.data_ptr() % 16 != 0
+        for exclusive in (False, True):
+            got = kf.scan(operator.mul, src, exclusive=exclusive).cpu().numpy()
+            ref = oracle.scan(q, "*", exclusive=exclusive)
+            assert np.array_equal(got.astype(np.float64), ref), (dt.__name__, n, exclusive)
+
+
 @pytest.mark.parametrize("dt,n", [(np.float64, 10**6), (np.float32, 10**4)])
 def test_quaternion_scan_reference_case(kf, oracle, dev, dt, n):
     # reference test/tests/scan/scan_test.jl:22-33: scan!(identity, *, dst,
