@@ -164,3 +164,29 @@ def test_python_mapreduce_and_scan_raise_and_recover(kf, oracle, dev, D):
         kf.scan_("+", dst, src, tmp=tmp, check=True)
         assert np.array_equal(dst.cpu().numpy(), oracle.scan(x, "+"))
         kf.check_async()
+
+
+def test_noalloc_fold_giveup_is_reported(kf, oracle, dev, D):
+    # kf_reduce_noalloc never allocates: with the report word set up by
+    # kf_init, its fold give-up is reported like any other, dst is left
+    # untouched, and the static scratch serves the next call exactly
+    K = kf._lib
+    assert D.kf_init() == 0
+    n = 10**7
+    x = np.random.default_rng(7).integers(-1000, 1000, n).astype(np.int32)
+    src = torch.from_numpy(x).to(dev)
+    out = torch.full((1,), 12345, dtype=torch.int32, device=dev)
+
+    def red():
+        return D.kf_reduce_noalloc(K.OP_ADD, K.MAP_IDENTITY, K.I32, _p(src), n, 1, _p(out), _stream())
+
+    print("noalloc fold give-up", flush=True)
+    with _hook(D.kf_debug_reduce_giveup, 5):
+        assert red() == K.KF_OK
+        torch.cuda.synchronize()
+    assert int(out.item()) == 12345
+    assert _async(D) == 1
+    for _ in range(2):
+        assert red() == K.KF_OK
+        assert int(out.item()) == int(oracle.reduce(x, "+"))
+    assert _async(D) == 0
