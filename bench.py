@@ -306,19 +306,22 @@ def measure_ceilings(kf, dev, src):
     assert torch.equal(cbuf, src), "copy probe mismatch"
     for name, kind in (("read_kernel_gbps", K.BW_READ), ("read_tiled_gbps", K.BW_READ_TILED)):
         out[name] = nbytes / time_calls(probe(kind, sink), 20) / 1e9
-    # write-only: kf_fill of the same 1 GiB (16-byte stores, nothing read)
+    # write-only: kf_fill of the same 1 GiB (nontemporal 16-byte stores) and
+    # the write probe (plain 16-byte stores, the faster of the two)
     val = ctypes.create_string_buffer(b"\0" * 4, 4)
 
     def fill():
         K.check(L.kf_fill(ctypes.c_void_p(cbuf.data_ptr()), cbuf.numel(), ctypes.cast(val, ctypes.c_void_p), 4,
                           ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)), "kf_fill")
-    out["write_kernel_gbps"] = nbytes / time_calls(fill, 20) / 1e9
+    out["write_fill_gbps"] = nbytes / time_calls(fill, 20) / 1e9
+    out["write_kernel_gbps"] = nbytes / time_calls(probe(K.BW_WRITE, cbuf), 20) / 1e9
     out["copy_ceiling_gbps"] = max(out[k] for k in ("copy_kernel_gbps", "copy_tiled_gbps", "copy_ordered_gbps",
                                                     "hipMemcpyDtoD_gbps"))
     out["read_ceiling_gbps"] = max(out["read_kernel_gbps"], out["read_tiled_gbps"])
     # a copy cannot beat reading its bytes at the best read rate and writing
     # them at the write rate one after the other: bytes/R_read + bytes/R_write
-    out["rw_bound_gbps"] = 2.0 / (1.0 / out["read_ceiling_gbps"] + 1.0 / out["write_kernel_gbps"])
+    out["write_ceiling_gbps"] = max(out["write_kernel_gbps"], out["write_fill_gbps"])
+    out["rw_bound_gbps"] = 2.0 / (1.0 / out["read_ceiling_gbps"] + 1.0 / out["write_ceiling_gbps"])
     del cbuf, scratch
     return out
 

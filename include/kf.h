@@ -351,9 +351,11 @@ int kf_fill(void* dst, int64_t count, const void* value, size_t value_bytes, voi
  * Measurement probes (no counterpart in the reference's library; they play
  * the part of its vendor copy benchmark,
  * perfs/cuda_cpp/cub_nvcc/cub_memcpy_benchmark.cu, bytes = 2N): the copy
- * and read ceilings the scan and reduction kernels are measured against.
- * src, dst and bytes must be multiples of 16. The copies write dst[0:bytes];
- * the reads load src[0:bytes] and use dst only as a 4-byte sink.
+ * and read ceilings the scan and reduction kernels are measured against,
+ * and the write rate of the read+write bound. src, dst and bytes must be
+ * multiples of 16. The copies write dst[0:bytes]; the reads load
+ * src[0:bytes] and use dst only as a 4-byte sink; the write stores to
+ * dst[0:bytes] and reads nothing (src unused).
  * KF_BW_COPY_ORDERED needs kf_bw_probe_scratch_bytes(bytes) of scratch (no
  * zeroing needed; its epoch comes from a host counter, so it must not be
  * captured into a graph). */
@@ -362,7 +364,8 @@ typedef enum {
   KF_BW_COPY_TILED = 1,    /* the scan's tile shape: 768 threads x 8 striped vectors */
   KF_BW_COPY_ORDERED = 2,  /* one vector per lane; tile t stores after tile t-1 loaded */
   KF_BW_READ = 3,          /* read: one vector per lane                            */
-  KF_BW_READ_TILED = 4     /* read: two vectors per lane, 256 apart (reduction level 0) */
+  KF_BW_READ_TILED = 4,    /* read: two vectors per lane, 256 apart (reduction level 0) */
+  KF_BW_WRITE = 5          /* write: one vector per lane, plain (temporal) 16-byte stores */
 } kf_bw_kind;
 
 size_t kf_bw_probe_scratch_bytes(size_t bytes);

@@ -18,7 +18,7 @@ MAP2_MUL, MAP2_SQDIFF, MAP2_WSQ, MAP2_EXPDIFF = 0, 1, 2, 3
 MAP3_MUL = 0
 POST_IDENTITY, POST_SQRT, POST_ABS2 = 0, 1, 2
 F32, F64, I32, I64, U8, F32X2, Q32, Q64 = 0, 1, 2, 3, 4, 5, 6, 7
-BW_COPY, BW_COPY_TILED, BW_COPY_ORDERED, BW_READ, BW_READ_TILED = 0, 1, 2, 3, 4
+BW_COPY, BW_COPY_TILED, BW_COPY_ORDERED, BW_READ, BW_READ_TILED, BW_WRITE = 0, 1, 2, 3, 4, 5
 
 # Every symbol include/kf.h declares, with its ctypes signature.
 _P, _I, _I64, _SZ = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_size_t

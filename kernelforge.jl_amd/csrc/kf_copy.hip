@@ -115,6 +115,15 @@ __global__ __launch_bounds__(256) void read_probe_kernel(const uint4* src, int64
   if (a == 0x9e3779b9u) sink[0] = a;
 }
 
+// Write-only probe: one plain (temporal) 16-byte store per lane. Measured
+// on MI355X, 1-2 GiB: 6.89 TB/s against 6.70 for nontemporal stores
+// (fill_kernel) and 5.6 at 8 vectors per lane; copies keep the nontemporal
+// stores (6.52 against 6.48 TB/s plain).
+__global__ __launch_bounds__(256) void write_probe_kernel(uint4* dst, int64_t nvec) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < nvec) dst[i] = make_uint4((uint32_t)i, (uint32_t)(i >> 32), 0u, 0u);
+}
+
 }  // namespace kf
 
 using namespace kf;
@@ -146,7 +155,7 @@ extern "C" size_t kf_bw_probe_scratch_bytes(size_t bytes) {
 extern "C" int kf_bw_probe(int kind, void* dst, const void* src, size_t bytes, void* scratch, size_t scratch_bytes,
                            void* stream) {
   if (bytes == 0) return KF_OK;
-  if (!dst || !src) return kf_set_error(KF_EINVAL, "kf_bw_probe: null pointer");
+  if (!dst || (!src && kind != KF_BW_WRITE)) return kf_set_error(KF_EINVAL, "kf_bw_probe: null pointer");
   if ((uintptr_t)src % 16 || (uintptr_t)dst % 16 || bytes % 16)
     return kf_set_error(KF_EINVAL, "kf_bw_probe: src, dst and bytes must be multiples of 16");
   hipStream_t s = (hipStream_t)stream;
@@ -177,6 +186,9 @@ extern "C" int kf_bw_probe(int kind, void* dst, const void* src, size_t bytes, v
       hipLaunchKernelGGL((read_probe_kernel<1>), dim3((unsigned)((nvec + 255) / 256)), dim3(256), 0, s, p, nvec,
                          (uint32_t*)dst);
       return kf_check_launch("read_probe_kernel");
+    case KF_BW_WRITE:
+      hipLaunchKernelGGL(write_probe_kernel, dim3((unsigned)((nvec + 255) / 256)), dim3(256), 0, s, d, nvec);
+      return kf_check_launch("write_probe_kernel");
     case KF_BW_READ_TILED:
       hipLaunchKernelGGL((read_probe_kernel<2>), dim3((unsigned)((nvec + 511) / 512)), dim3(256), 0, s, p, nvec,
                          (uint32_t*)dst);

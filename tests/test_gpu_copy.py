@@ -129,3 +129,22 @@ def test_bw_probe_reads_write_nothing_but_their_sink(kf, dev):
                          None, 0, s) == K.KF_ENOSCRATCH
     assert L.kf_bw_probe(99, ctypes.c_void_p(sink.data_ptr()), ctypes.c_void_p(src.data_ptr()), 16, None, 0,
                          s) == K.KF_EINVAL
+
+
+@pytest.mark.parametrize("nbytes", [16, 4096 + 16, 1 << 24])
+def test_bw_probe_write_stores_every_vector_and_nothing_past_it(kf, dev, nbytes):
+    # the write probe stores vector i as (i, i >> 32, 0, 0) over dst[0:bytes]
+    # and reads nothing; the word after the buffer stays untouched
+    import ctypes
+    L, K = kf._lib.lib(), kf._lib
+    n4 = nbytes // 4
+    dst = torch.full((n4 + 4,), -1, dtype=torch.int32, device=dev)
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    rc = L.kf_bw_probe(K.BW_WRITE, ctypes.c_void_p(dst.data_ptr()), None, nbytes, None, 0, s)
+    assert rc == K.KF_OK, L.kf_last_error()
+    torch.cuda.synchronize()
+    v = dst[:n4].view(-1, 4).cpu()
+    nvec = nbytes // 16
+    assert torch.equal(v[:, 0], torch.arange(nvec, dtype=torch.int32))
+    assert bool((v[:, 1:] == 0).all())
+    assert dst[n4:].tolist() == [-1, -1, -1, -1]
