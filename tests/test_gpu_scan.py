@@ -184,7 +184,7 @@ def test_quaternion_scan_every_compiled_shape(kf, oracle, dev, dt):
     rng = np.random.default_rng(47)
     for threads, items in shapes:
         tile = threads * items
-        for n in (tile - 1, tile + 1, 3 * tile + 5, 700 * tile + 7):
+        for n in (tile - 1, tile + 1, 2 * tile, 3 * tile + 5, 700 * tile + 7):
             q = q8_sequence(rng, n, dt)
             t = torch.from_numpy(q).to(dev)
             for exclusive in (False, True):
