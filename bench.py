@@ -667,12 +667,16 @@ def bench_all(kf, dev, ceil, json_path=None, cpu=True):
         with torch.cuda.graph(graph):
             for _ in range(reps):
                 fn()
-        graph.replay()
-        torch.cuda.synchronize()
-        # median of five timed replays: right after the scans of the rows
-        # before it, the first replays of a 4 GiB reduction were seen to run
-        # 4-5 % slower for a few milliseconds, a transient of the device and
-        # not of this configuration (alone it times the same every replay)
+        # replayed for 250 ms before it is timed: in the kernel trace of this
+        # loop the 4 GiB reduction (C3a) ran at 636 us per call for its first
+        # 90 ms and at 606 us from one call to the next after that, on the same
+        # buffer; alone in a process it runs at 608 us from its first call.
+        # The step is a device transient, not a property of the kernel, so
+        # each row is timed in the steady state, as the median of five replays.
+        t_end = time.perf_counter() + 0.25
+        while time.perf_counter() < t_end:
+            graph.replay()
+            torch.cuda.synchronize()
         s = statistics.median(time_calls(graph.replay, 1) for _ in range(5)) / reps
         _mark(kf, dev, False)
         del graph
@@ -777,7 +781,8 @@ def scan_timeline(dev, cases=TIMELINE_CASES):
         last = st.max()
         tile_bytes = 2 * es * n / len(a)
         # no steady window when every tile is resident at once (one generation)
-        steady = ((en >= full) & (en <= last)).sum() * tile_bytes / (last - full) / 1e3 if last > full else None
+        one_generation = len(a) <= active.max() or last <= full
+        steady = None if one_generation else ((en >= full) & (en <= last)).sum() * tile_bytes / (last - full) / 1e3
         row = {"case": label, "us": round(t * 1e6, 1), "gbps": round(2 * es * n / t / 1e9), "tiles": len(a),
                "peak_resident": int(active.max()), "span_us": round(float(en.max()), 1),
                "tile_life_us": round(float(np.median(en - st)), 2), "load_scan_us": round(float(np.median(sc - st)), 2),
