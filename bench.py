@@ -134,9 +134,10 @@ def main():
                     help="the reference's scan/mapreduce size sweep (perfs/julia/benchmarks)")
     ap.add_argument("--sweep-2d", action="store_true",
                     help="the reference's matvec/vecmat shape sweep (perfs/julia/benchmarks)")
-    ap.add_argument("--timeline", nargs="?", const="large", choices=("large", "mid", "reduce"),
+    ap.add_argument("--timeline", nargs="?", const="large", choices=("large", "mid", "quat", "reduce"),
                     help="only the per-tile scan timeline (libkfhip_timeline.so): the large "
-                         "scans (default) or the mid sizes of the reference's sweep")
+                         "scans (default), the mid sizes of the reference's sweep, the "
+                         "quaternion scans, or the reductions' per-workgroup timeline")
     ap.add_argument("--pmc-run", action="store_true",
                     help="only the dispatch sequence for rocprofv3 --pmc (see pmc_run)")
     ap.add_argument("--pmc-summary", nargs=4, metavar=("FETCH_DIR", "WRITE_DIR", "CASES_LOG", "OUT_JSON"),
@@ -166,7 +167,7 @@ def main():
         print(json.dumps({"reduce_timeline": reduce_timeline(dev)}), flush=True)
         return
     if args.timeline:
-        cases = TIMELINE_CASES if args.timeline == "large" else MID_TIMELINE_CASES
+        cases = {"large": TIMELINE_CASES, "mid": MID_TIMELINE_CASES, "quat": QUAT_TIMELINE_CASES}[args.timeline]
         print(json.dumps({"scan_timeline": scan_timeline(dev, cases)}), flush=True)
         return
 
@@ -610,13 +611,15 @@ def config_cases(kf, dev):
         ts = tmp_for(kf.Scan1D, xs)
         yield f"X7-{label}", f"X7 scan F32 incl n={label}", 8 * n, lambda: kf.scan_("+", ys, xs, tmp=ts), 20, n, None
     # the reference's non-commutative test case (test/tests/scan/scan_test.jl:22-33):
-    # QuaternionF64 at its n = 10^6 and QuaternionF32 at 2^26, Hamilton products
-    for n, dt, label in ((10**6, torch.float64, "QuaternionF64 n=10^6"), (2**26, torch.float32, "QuaternionF32 n=2^26")):
+    # QuaternionF64 at its n = 10^6 and 2^24, QuaternionF32 at 2^26, Hamilton products
+    for key, n, dt, label in (("X9-QuaternionF64", 10**6, torch.float64, "QuaternionF64 n=10^6"),
+                              ("X9-QuaternionF64-2^24", 2**24, torch.float64, "QuaternionF64 n=2^24"),
+                              ("X9-QuaternionF32", 2**26, torch.float32, "QuaternionF32 n=2^26")):
         q = torch.randn(n, 4, device=dev, generator=g, dtype=dt)
         q = q / q.norm(dim=1, keepdim=True)
         yq = torch.empty_like(q)
         tq = kf.get_allocation(kf.Scan1D, kf.identity, "*", q)
-        yield f"X9-{label.split()[0]}", f"X9 scan {label}", 2 * q.numel() * q.element_size(), \
+        yield key, f"X9 scan {label}", 2 * q.numel() * q.element_size(), \
             lambda: kf.scan_("*", yq, q, tmp=tq), 20, n, None
         del q, yq
 
@@ -716,6 +719,10 @@ MID_TIMELINE_CASES = (("Float32 n=10^6 (C1)", 0, 10**6), ("UInt8 n=10^7", 4, 10*
                       ("UInt8 n=2^30", 4, 2**30), ("Float32 n=2.5*10^6", 0, 25 * 10**5),
                       ("Float32 n=2.5*10^7", 0, 25 * 10**6), ("Float32 n=10^8", 0, 10**8),
                       ("Float64 n=10^7", 1, 10**7))
+# Quaternion products (unit quaternions): the reference's test size and the
+# large arrays of the wide tiles.
+QUAT_TIMELINE_CASES = (("QuaternionF64 n=10^6", 7, 10**6), ("QuaternionF64 n=2^24", 7, 2**24),
+                       ("QuaternionF32 n=2^24", 6, 2**24), ("QuaternionF32 n=2^26", 6, 2**26))
 
 
 def scan_timeline(dev, cases=TIMELINE_CASES):

@@ -130,18 +130,22 @@ template <class T> constexpr bool has_wide_tier() {
   return sizeof(T) == 4 || sizeof(T) == 8 || sizeof(T) == 1 || is_quat<T>;
 }
 // Quaternions take a wide shape of longer lane chunks from kWideBytes on:
-// QuaternionF32 768 threads x 8 units (96 KiB), QuaternionF64 1024 x 4
-// units (128 KiB). More units per lane spread the wave scan's six combines
+// QuaternionF32 768 threads x 8 units (96 KiB), QuaternionF64 1024 x 8
+// units (256 KiB, one workgroup per CU at 128 VGPRs). More units per lane spread the wave scan's six combines
 // and the prefix combine over more elements (about 2.9 Hamilton products
 // per element at 8 units, 3.75 at 4). Measured on MI355X (HIP graphs, us;
 // tiles through the LDS transpose below): QuaternionF32 at 768 x 8 vs 1024
 // x 4: 2*10^6 18.5 vs 19.6, 4*10^6 32.6 vs 33.6, 2^23 57.3 vs 61.8, 2^24
 // 103.0 vs 115.0, 2^26 377.1 vs 434.7 (512 x 16 378, 768 x 16 402);
 // QuaternionF64 at 1024 x 4 vs 1024 x 2: 10^6 28.4 vs 32.9, 2^22 87.4 vs
-// 114.0, 2^24 335.4 vs 430.9 (512 x 4 349, 768 x 4 346, 512 x 8 341). (Before
+// 114.0, 2^24 335.4 vs 430.9 (512 x 4 349, 768 x 4 346, 512 x 8 341).
+// With granule-striped loads and stores (below), QuaternionF64 at 1024 x 8
+// / 768 x 8 / 1024 x 4 / 512 x 8: 10^6 23.1 / 22.8 / 23.1 / 22.6, 2^22
+// 62.0 / 67.2 / 71.9 / 72.6, 2^24 220.1 / 229.3 / 288.2 / 290.6, 2^25
+// 423.1 / 438.7 / 562.1 / 568.2. (Before
 // the transpose, with blocked loads and stores, QuaternionF32 2^26 took
 // 588.7 us at 1024 x 4 and 549.3 at 768 x 8.)
-constexpr int kWideBlockQ32 = 768, kWideVQ32 = 8, kWideBlockQ64 = 1024, kWideVQ64 = 4;
+constexpr int kWideBlockQ32 = 768, kWideVQ32 = 8, kWideBlockQ64 = 1024, kWideVQ64 = 8;
 template <class T> constexpr bool has_huge_tier() { return sizeof(T) == 1; }
 // (Float32 and the 8-byte types measured 0.5-10 % slower at 512 x 12 or 16.)
 constexpr int kWideBlockF32 = 768, kWideVF32 = 8, kWideBlock8 = 768, kWideV8 = 8;
@@ -533,16 +537,28 @@ template <class Vec> __device__ inline void lds_put(uint4* buf, int g, const Vec
 template <class Vec> __device__ inline void lds_get(const uint4* buf, int g, Vec& v) {
   __builtin_memcpy(&v, buf + g, sizeof(Vec));
 }
+// The striped side works in 16-byte granules: register granule i of a lane
+// (granule i % G of unit i / G in r) is granule i*64 + lane of the wave's
+// chunk, so that every load and store instruction covers one contiguous KiB
+// also for the 32-byte units (QuaternionF64: loading whole units instead,
+// each instruction read every other granule of 2 KiB: 2^24 at 768 x 8
+// took 302.1 us against 229.3, 10^6 27.9 against 22.8).
 // striped -> blocked (in place on r); buf: this wave's BlockedLds::GRANULES
 template <class T, int V, class Vec>
 __device__ inline void striped_to_blocked(Vec (&r)[V], uint4* buf, int lane) {
   using B = BlockedLds<T, V>;
+  constexpr int G = B::G, HG = V * G / 2;  // register granules per half chunk
+  uint4 rg[V * G];
+  __builtin_memcpy(rg, r, sizeof rg);
   Vec b[V];
 #pragma unroll
   for (int p = 0; p < 2; ++p) {
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
-    for (int jj = 0; jj < V / 2; ++jj) lds_put(buf, B::at(jj * kWave + lane), r[p * (V / 2) + jj]);
+    for (int i = 0; i < HG; ++i) {
+      const int q = i * kWave + lane;  // granule of the half chunk
+      buf[B::at(q / G) + q % G] = rg[p * HG + i];
+    }
     __builtin_amdgcn_wave_barrier();
     if ((lane >> 5) == p) {
 #pragma unroll
@@ -557,7 +573,8 @@ __device__ inline void striped_to_blocked(Vec (&r)[V], uint4* buf, int lane) {
 template <class T, int V, class Vec>
 __device__ inline void blocked_to_striped(Vec (&r)[V], uint4* buf, int lane) {
   using B = BlockedLds<T, V>;
-  Vec s[V];
+  constexpr int G = B::G, HG = V * G / 2;
+  uint4 sg[V * G];
 #pragma unroll
   for (int p = 0; p < 2; ++p) {
     __builtin_amdgcn_wave_barrier();
@@ -567,11 +584,13 @@ __device__ inline void blocked_to_striped(Vec (&r)[V], uint4* buf, int lane) {
     }
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
-    for (int jj = 0; jj < V / 2; ++jj) lds_get(buf, B::at(jj * kWave + lane), s[p * (V / 2) + jj]);
+    for (int i = 0; i < HG; ++i) {
+      const int q = i * kWave + lane;
+      sg[p * HG + i] = buf[B::at(q / G) + q % G];
+    }
   }
   __builtin_amdgcn_wave_barrier();
-#pragma unroll
-  for (int k = 0; k < V; ++k) r[k] = s[k];
+  __builtin_memcpy(r, sg, sizeof sg);
 }
 template <class T, int V> __device__ inline int unit_slot(int j, int lane) {
   return kBlockedFor<T> ? lane * V + j : j * kWave + lane;
@@ -644,8 +663,13 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
   if (full) {
     const Vec* g = reinterpret_cast<const Vec*>(srcv + wbase);
     if constexpr (kTranspose) {
+      // granule-striped: register granule i is granule i*64 + lane
+      constexpr int G = kVecBytes<T> / 16;
+      const uint4* gg = reinterpret_cast<const uint4*>(g);
+      uint4 rg[V * G];
 #pragma unroll
-      for (int j = 0; j < V; ++j) r[j] = ld_vec(g + j * kWave + lane);
+      for (int i = 0; i < V * G; ++i) rg[i] = ld_vec(gg + i * kWave + lane);
+      __builtin_memcpy(r, rg, sizeof rg);
       striped_to_blocked<T, V>(r, s_tr[wave], lane);
     } else {
 #pragma unroll
@@ -863,9 +887,12 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
         __builtin_memcpy(&ob[j], &o, sizeof(T));
       }
       blocked_to_striped<T, V>(ob, s_tr[wave], lane);
-      Vec* gd = reinterpret_cast<Vec*>(dstv + wbase);
+      constexpr int G = kVecBytes<T> / 16;
+      uint4 og[V * G];
+      __builtin_memcpy(og, ob, sizeof og);
+      uint4* gd = reinterpret_cast<uint4*>(dstv + wbase);
 #pragma unroll
-      for (int j = 0; j < V; ++j) st_vec(gd + j * kWave + lane, ob[j]);
+      for (int i = 0; i < V * G; ++i) st_vec(gd + i * kWave + lane, og[i]);
     }
   }
 #pragma unroll

@@ -128,14 +128,15 @@ def test_scan_shape_keywords_pick_the_nearest_compiled_shape(kf):
     # Nitem beyond the compiled range clamps to the widest shape
     assert _shape(kf, K.F32, 2**20, 0, 10**6)[1] == 32
     # quaternions: 1024 x 1, 2 or 4 units (QuaternionF64 1 or 2) and the wide
-    # shapes 768 x 8 (QuaternionF32) and 1024 x 4 (QuaternionF64) from 17 MiB
-    assert _shape(kf, K.Q64, 100, 1024, 64) == (1024, 4)  # the widest QuaternionF64 shape
+    # shapes 768 x 8 (QuaternionF32) and 1024 x 8 (QuaternionF64) from 17 MiB
+    assert _shape(kf, K.Q64, 100, 1024, 64) == (1024, 8)  # the widest QuaternionF64 shape
     assert _shape(kf, K.Q64, 100, 1024, 2) == (1024, 2)
+    assert _shape(kf, K.Q64, 100, 1024, 4) == (1024, 2)  # no 1024 x 4 for QuaternionF64
     assert _shape(kf, K.Q32, 100, 1024, 64) == (768, 8)
     assert _shape(kf, K.Q32, 2**26, 0, 0) == (768, 8)
     assert _shape(kf, K.Q32, 2**22, 0, 0) == (768, 8)
     assert _shape(kf, K.Q32, 10**6, 0, 0) == (1024, 4)
-    assert _shape(kf, K.Q64, 10**6, 0, 0) == (1024, 4)
+    assert _shape(kf, K.Q64, 10**6, 0, 0) == (1024, 8)
     assert _shape(kf, K.Q64, 5 * 10**5, 0, 0) == (1024, 2)
     # scratch follows the shape: one 128-byte line per tile + the header
     n = 10**6
