@@ -167,7 +167,7 @@ int kf_scan(kf_op op, kf_map f, kf_post g, kf_dtype dt, int exclusive,
  * compiled for a fixed set of tile shapes (1024 threads x 1, 2, 4 or 8
  * 16-byte vectors per thread, 768 x 8 for 4- and 8-byte elements, 512 x 1,
  * 2, 4, 8, 12 or 16 for UInt8; quaternions 1024 x 1, 2 or 4 units
- * (QuaternionF64: 1 or 2) and 768 x 8 (QuaternionF32) or 512 x 4
+ * (QuaternionF64: 1 or 2) and 768 x 8 (QuaternionF32) or 1024 x 8
  * (QuaternionF64)), so a request takes the nearest shape: the smallest
  * |log2(threads / workgroup)| + |log2(elements per thread / nitem)|, a
  * keyword not given standing for the size-based default shape's value;
