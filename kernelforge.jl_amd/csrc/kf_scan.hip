@@ -98,7 +98,11 @@ constexpr int64_t kMinTiles = 160;
 // UInt8 tiles carry 4x the elements per byte of work: they need more tiles
 // (480) before a larger shape pays (10^7 9.7 us at 480, 10.7 at 240, 18.2
 // at 960).
-template <class T> constexpr int64_t min_tiles() { return sizeof(T) == 1 ? 480 : kMinTiles; }
+// Quaternion tiles carry about three Hamilton products per element of
+// in-tile work, so fewer, longer tiles pay off sooner: QuaternionF32 takes
+// 1024 x 4 from 64 tiles (HIP graphs, us, 1024 x 2 -> 1024 x 4: 4*10^5
+// 12.1 -> 11.4, 6*10^5 13.9 -> 12.4; 2*10^5 9.9 vs 9.8).
+template <class T> constexpr int64_t min_tiles() { return sizeof(T) == 1 ? 480 : is_quat<T> ? 64 : kMinTiles; }
 template <class T> constexpr int kMinTier = sizeof(T) == 1 ? 0 : 1;
 // Arrays of at least kWideBytes take a wider shape: the 4- and 8-byte
 // types 768 threads x 8 vectors (96 KiB); UInt8 (from kU8WideBytes) 512
