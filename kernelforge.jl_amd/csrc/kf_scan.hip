@@ -204,6 +204,9 @@ template <class T> constexpr bool kLookAllFor = sizeof(T) <= 4;
 constexpr int kBlockChunk = 2;
 template <class T, int BLOCK, int VPL>
 constexpr bool kLookBlockFor = sizeof(T) <= 8 && VPL <= (sizeof(T) == 8 ? 4 : 2);
+// For grids of several generations the window code also carries, in its
+// bits from 8 on, the number of tiles resident from the start (the first
+// generation), for the staggered start below.
 inline int look_window(int64_t ntiles, int64_t resident, int64_t tile_bytes, bool look_all, bool look_block,
                        int block) {
   if (ntiles <= resident) {
@@ -211,9 +214,31 @@ inline int look_window(int64_t ntiles, int64_t resident, int64_t tile_bytes, boo
     if (look_block && ntiles <= (int64_t)block * kBlockChunk + 1) return -1;
     return kWave;
   }
-  if (tile_bytes >= (128 << 10) && ntiles > 4 * resident) return 2;
-  if (tile_bytes <= (64 << 10)) return 8;
-  return 4;
+  const int gen1 = (int)kmin<int64_t>(resident, 1 << 22) << 8;
+  if (tile_bytes >= (128 << 10) && ntiles > 4 * resident) return 2 | gen1;
+  if (tile_bytes <= (64 << 10)) return 8 | gen1;
+  return 4 | gen1;
+}
+__device__ inline int window_of(int win) { return win > 0 ? (win & 0xff) : win; }
+
+// Staggered start of the first generation: tile t of the R tiles resident
+// from the start waits t/R x kFirstGenStaggerNs before its loads. All R
+// tiles loading at once finish together, and the PREFIX front then walks
+// through them (a tile of the first generation sees only tile 0's PREFIX
+// and the others' PARTIALs), so the first stores start about one tile life
+// late; spread out, the low tiles finish loading first and the front
+// follows them. Measured on MI355X (median of 9 HIP graphs, us, as before /
+// spread over 3, 4, 6 us): Float32 2^28 320.6 / 319.8 / 319.9 / 319.3,
+// 10^8 124.5 / 123.8 / 123.8 / 123.2, 2.5*10^7 37.0 / 36.2 / 36.1 / 35.9;
+// affine 2^26 167.9 / 167.7 / 167.5 / 167.3; QuaternionF64 2^24 220.4 /
+// 219.1 / 218.0 / 217.0; UInt8 10^8 40.6 / 40.3 / 40.5 / 40.6 (8 us: 42.0).
+constexpr uint64_t kFirstGenStaggerNs = 6000;
+__device__ inline void first_gen_stagger(int win, int64_t tile) {
+  const int64_t gen1 = win > 0 ? (int64_t)(win >> 8) : 0;
+  if (tile >= gen1) return;
+  const uint64_t ticks = (uint64_t)tile * (kFirstGenStaggerNs / 10) / (uint64_t)gen1;  // 100 MHz counter
+  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  while (__builtin_amdgcn_s_memrealtime() - t0 < ticks) __builtin_amdgcn_s_sleep(4);
 }
 
 // The unit a lane loads and stores: 16 bytes, or one element of a wider
@@ -652,6 +677,7 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
   }
   const int64_t tile = blockIdx.x;
   uint64_t* desc = scratch + kScanHeaderBytes / sizeof(uint64_t);
+  first_gen_stagger(win, tile);
 
   const int64_t wbase = tile * S::TILE + (int64_t)wave * S::WAVE_ELEMS;  // this wave's virtual chunk
   const int64_t nv = n + off;
@@ -833,9 +859,9 @@ __global__ __launch_bounds__(BLOCK) void scan_kernel(
     if (tile > 0 && !look_block) {
       if constexpr (kLookAllFor<T>)
         excl = win == 0 ? lookback_all<T, Op, kAllChunk>(desc, tile, epoch30, limit, gave_up)
-                        : lookback<T, Op>(desc, tile, epoch30, win, limit, gave_up);
+                        : lookback<T, Op>(desc, tile, epoch30, window_of(win), limit, gave_up);
       else
-        excl = lookback<T, Op>(desc, tile, epoch30, win, limit, gave_up);
+        excl = lookback<T, Op>(desc, tile, epoch30, window_of(win), limit, gave_up);
     }
     if (tile > 0 && lane == 0 && pub && !gave_up)
       publish(desc, tile, (epoch30 << 2) | kStatePrefix, Op::combine(excl, agg));
