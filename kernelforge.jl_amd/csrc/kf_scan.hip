@@ -232,6 +232,10 @@ __device__ inline int window_of(int win) { return win > 0 ? (win & 0xff) : win; 
 // 10^8 124.5 / 123.8 / 123.8 / 123.2, 2.5*10^7 37.0 / 36.2 / 36.1 / 35.9;
 // affine 2^26 167.9 / 167.7 / 167.5 / 167.3; QuaternionF64 2^24 220.4 /
 // 219.1 / 218.0 / 217.0; UInt8 10^8 40.6 / 40.3 / 40.5 / 40.6 (8 us: 42.0).
+// Grids of a single generation are not staggered: their last tile ends one
+// load, one poll round trip and one store after the last load starts, and
+// any delay adds to it (0.5 / 1 us spread: Float32 10^6 5.05 -> 5.61 / 6.19
+// us, UInt8 10^7 8.41 -> 9.08 / 9.73).
 constexpr uint64_t kFirstGenStaggerNs = 6000;
 __device__ inline void first_gen_stagger(int win, int64_t tile) {
   const int64_t gen1 = win > 0 ? (int64_t)(win >> 8) : 0;
