@@ -483,11 +483,11 @@ struct OnceLevels {
   int u0;
   int64_t count[8];
 };
-inline OnceLevels once_levels(int64_t nvec, int epv, bool adaptive = true) {
+inline OnceLevels once_levels(int64_t nvec, int epv, bool adaptive = true, int max_u = kOnceMaxUnroll) {
   OnceLevels L{};
   L.u0 = kOnceUnroll;
   if (adaptive) {
-    for (int u = kOnceUnroll; u <= kOnceMaxUnroll; u *= 2)
+    for (int u = kOnceUnroll; u <= max_u; u *= 2)
       if ((nvec + (int64_t)kRedBlock * u - 1) / ((int64_t)kRedBlock * u) <= kFoldMax) {
         L.u0 = u;
         break;
@@ -639,7 +639,7 @@ template <class M, class T, int K> __device__ inline T apply_k(const T (&v)[K]) 
 
 // Multi-array reduction, vector path: the one-shot workgroups of
 // reduce_once_kernel, each loading the same 16-byte vectors of all K arrays.
-template <class T, class Op, class M, int K, bool FOLD = false>
+template <class T, class Op, class M, int K, bool FOLD = false, int U = kOnceUnroll>
 __global__ __launch_bounds__(kRedBlock) void reducek_once_kernel(Operands<T, K> a, int64_t n, T* out,
                                                                  uint64_t* fold_hdr, FoldCtl ctl) {
   constexpr int EPV = 16 / (int)sizeof(T);
@@ -648,10 +648,10 @@ __global__ __launch_bounds__(kRedBlock) void reducek_once_kernel(Operands<T, K> 
   const int tid = threadIdx.x;
   const uint32_t hdr0 = FOLD ? fold_epoch(fold_hdr) : 0u;  // fold tag, read ahead of the data
   const int64_t nvec = n / EPV;
-  const int64_t base = (int64_t)blockIdx.x * kOnceVecs + tid;
-  uint4 r[kOnceUnroll][K];
+  const int64_t base = (int64_t)blockIdx.x * (kRedBlock * U) + tid;
+  uint4 r[U][K];
 #pragma unroll
-  for (int u = 0; u < kOnceUnroll; ++u)
+  for (int u = 0; u < U; ++u)
     if (base + u * kRedBlock < nvec) {
 #pragma unroll
       for (int k = 0; k < K; ++k) r[u][k] = ld_stream(reinterpret_cast<const uint4*>(a.p[k]) + base + u * kRedBlock);
@@ -660,7 +660,7 @@ __global__ __launch_bounds__(kRedBlock) void reducek_once_kernel(Operands<T, K> 
 #pragma unroll
   for (int e = 0; e < EPV; ++e) acc_e[e] = id;
 #pragma unroll
-  for (int u = 0; u < kOnceUnroll; ++u)
+  for (int u = 0; u < U; ++u)
     if (base + u * kRedBlock < nvec) {
       T x[K][EPV];
 #pragma unroll
@@ -688,6 +688,73 @@ __global__ __launch_bounds__(kRedBlock) void reducek_once_kernel(Operands<T, K> 
   } else {
     fold_partial<T, Op>(part, out, fold_hdr, s_wave, hdr0, ctl);  // out is the result
   }
+}
+
+// Persistent multi-array reduction for large operands (K x 16-byte vectors
+// of kChunkMinVecs or more): kFoldMax workgroups, workgroup b folding the
+// contiguous chunk [b*chunk, (b+1)*chunk) of vectors of every array with U
+// loads per array in flight per lane, then the in-kernel fold, as
+// reduce_chunk_kernel does for one array. The host makes `chunk` a whole
+// number of U * kRedBlock-vector rounds.
+template <class T, class Op, class M, int K, int U>
+__global__ __launch_bounds__(kRedBlock) void reducek_chunk_kernel(Operands<T, K> a, int64_t n, int64_t chunk, T* out,
+                                                                  uint64_t* fold_hdr, FoldCtl ctl) {
+  constexpr int EPV = 16 / (int)sizeof(T);
+  __shared__ T s_wave[kRedWaves];
+  const T id = Op::template identity<T>();
+  const int tid = threadIdx.x;
+  const uint32_t hdr0 = fold_epoch(fold_hdr);  // fold tag, read ahead of the data
+  const int64_t nvec = n / EPV;
+  const int64_t b0 = (int64_t)blockIdx.x * chunk;
+  const int64_t b1 = kmin<int64_t>(nvec, b0 + chunk);
+  T acc_e[EPV];
+#pragma unroll
+  for (int e = 0; e < EPV; ++e) acc_e[e] = id;
+  auto fold = [&](const uint4 (&rv)[K]) {
+    T x[K][EPV];
+#pragma unroll
+    for (int k = 0; k < K; ++k) __builtin_memcpy(x[k], &rv[k], 16);
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) {
+      T v[K];
+#pragma unroll
+      for (int k = 0; k < K; ++k) v[k] = x[k][e];
+      acc_e[e] = Op::combine(acc_e[e], apply_k<M, T, K>(v));
+    }
+  };
+  int64_t i = b0 + tid;
+  for (; i + (int64_t)(U - 1) * kRedBlock < b1; i += (int64_t)U * kRedBlock) {
+    uint4 r[U][K];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int k = 0; k < K; ++k) r[u][k] = ld_stream(reinterpret_cast<const uint4*>(a.p[k]) + i + u * kRedBlock);
+#pragma unroll
+    for (int u = 0; u < U; ++u) fold(r[u]);
+  }
+  if (i < b1) {  // the partial last round
+    uint4 r[U][K];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (i + u * kRedBlock < b1) {
+#pragma unroll
+        for (int k = 0; k < K; ++k) r[u][k] = ld_stream(reinterpret_cast<const uint4*>(a.p[k]) + i + u * kRedBlock);
+      }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (i + u * kRedBlock < b1) fold(r[u]);
+  }
+  T acc = acc_e[0];
+#pragma unroll
+  for (int e = 1; e < EPV; ++e) acc = Op::combine(acc, acc_e[e]);
+  if (blockIdx.x == 0 && nvec * EPV + tid < n) {
+    T v[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) v[k] = a.p[k][nvec * EPV + tid];
+    acc = Op::combine(acc, apply_k<M, T, K>(v));
+  }
+  const T part = block_reduce<T, Op>(acc, s_wave);
+  fold_partial<T, Op>(part, out, fold_hdr, s_wave, hdr0, ctl);
 }
 
 // Multi-array reduction, strided operands: grid-stride loop.
@@ -721,10 +788,35 @@ int launch_reducek(const Operands<T, K>& a, int64_t n, void* dst, void* scratch_
                          (const T*)scratch, grid, (T*)dst);
     return kf_check_launch("reducek_kernel");
   }
-  const OnceLevels L = once_levels(n / EPV, EPV, /*adaptive=*/false);
+  // Loads in flight per lane and array: 8 for two arrays, 4 for three (the
+  // single-array kernels' 16 over K arrays). From 1 GiB of operands the
+  // persistent chunk kernel, below it the one-shot kernel with the fewest
+  // loads per lane that fold in one launch, else two levels. Measured on
+  // MI355X (HIP graphs, us, two levels -> this): dot products Float32 2^28
+  // 314.9 -> 308.3, Float64 2^27 326.2 -> 320.2; x*y*z Float32 2^28 483.3 ->
+  // 462.9, 10^8 182.0 -> 174.9, Float64 2^27 482.0 -> 461.6 (the Float32 10^8
+  // dot product, 800 MB, stays on two levels: 120.4 against 123.1 chunked).
+  constexpr int KU = K == 2 ? 8 : 4;
+  const int64_t nvec = n / EPV;
+  if (nvec * K >= 4 * kChunkMinVecs) {
+    constexpr int64_t kRound = (int64_t)KU * kRedBlock;
+    const int64_t chunk = ((nvec + kFoldMax - 1) / kFoldMax + kRound - 1) / kRound * kRound;
+    hipLaunchKernelGGL((reducek_chunk_kernel<T, Op, M, K, KU>), dim3(kFoldMax), dim3(kRedBlock), 0, stream, a, n,
+                       chunk, (T*)dst, (uint64_t*)scratch_base, fold_ctl());
+    return kf_check_launch("reducek_chunk_kernel");
+  }
+  const OnceLevels L = once_levels(nvec, EPV, /*adaptive=*/true, KU);
   if (L.nlev == 1 && L.count[0] > 1) {
-    hipLaunchKernelGGL((reducek_once_kernel<T, Op, M, K, true>), dim3((unsigned)L.count[0]), dim3(kRedBlock), 0,
-                       stream, a, n, (T*)dst, (uint64_t*)scratch_base, fold_ctl());
+    const dim3 grid((unsigned)L.count[0]);
+    if (L.u0 == 8)
+      hipLaunchKernelGGL((reducek_once_kernel<T, Op, M, K, true, (KU >= 8 ? 8 : KU)>), grid, dim3(kRedBlock), 0,
+                         stream, a, n, (T*)dst, (uint64_t*)scratch_base, fold_ctl());
+    else if (L.u0 == 4)
+      hipLaunchKernelGGL((reducek_once_kernel<T, Op, M, K, true, 4>), grid, dim3(kRedBlock), 0, stream, a, n,
+                         (T*)dst, (uint64_t*)scratch_base, fold_ctl());
+    else
+      hipLaunchKernelGGL((reducek_once_kernel<T, Op, M, K, true>), grid, dim3(kRedBlock), 0, stream, a, n, (T*)dst,
+                         (uint64_t*)scratch_base, fold_ctl());
     return kf_check_launch("reducek_once_kernel");
   }
   size_t abytes = 0;

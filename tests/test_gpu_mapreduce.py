@@ -734,3 +734,29 @@ def test_lower_level_entry_points(kf, oracle, dev):
     dst = torch.empty(1, 7, 1, dtype=torch.int32, device=dev)
     kf.mapreducedims_(kf.identity, "+", dst, B, (1, 3))
     assert np.array_equal(dst.cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("dt", [np.float32, np.int32])
+def test_multi_array_chunked_large(kf, oracle, dev, dt):
+    # from 1 GiB of operands the multi-array reductions run the persistent
+    # chunk kernel (2048 workgroups over contiguous chunks of every array,
+    # folded in the same launch); ragged lengths leave a scalar tail for
+    # workgroup 0. Exact for integers (wrapping), rtol * sum|f| for floats.
+    import operator
+    rng = np.random.default_rng(67)
+    for k, n in ((2, (1 << 27) + 5), (3, 100_000_003)):
+        arrs = [gen(rng, dt, n) for _ in range(k)]
+        t = tuple(torch.from_numpy(a).to(dev) for a in arrs)
+        for op in ("+", "max"):
+            got = kf.mapreduce(operator.mul if k == 2 else kf.prod3, op, t)
+            ref = oracle.reduce2(arrs[0], arrs[1], op, "mul") if k == 2 else oracle.reduce3(*arrs, op)
+            if dt == np.float32 and op == "+":
+                p = arrs[0].astype(np.float64) * arrs[1]
+                if k == 3:
+                    p = p * arrs[2]
+                assert abs(got - ref) <= 1e-6 * np.sum(np.abs(p)), (k, n, op, got, ref)
+            elif dt == np.float32:
+                assert got == pytest.approx(ref, rel=1e-6), (k, n, op)
+            else:
+                assert got == int(ref), (k, n, op)
+        del t
