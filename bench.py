@@ -496,7 +496,7 @@ def _cpu_prep(make):
 def config_cases(kf, dev):
     """(key, name, algorithmic bytes, fn, reps, elements, cpu prep or None)
     for every BASELINE.json configuration (C1-C5) and the extra rows
-    (X1-X9); each case's inputs are alive until the next case is
+    (X1-X10); each case's inputs are alive until the next case is
     requested."""
     import operator
     g = torch.Generator(device=dev).manual_seed(20261201)
@@ -622,6 +622,17 @@ def config_cases(kf, dev):
         yield key, f"X9 scan {label}", 2 * q.numel() * q.element_size(), \
             lambda: kf.scan_("*", yq, q, tmp=tq), 20, n, None
         del q, yq
+    # multi-array reductions (mapreduce1d!(f, op, dst, (x, y[, z]))): the dot
+    # product and the reference's three-array sum(a .* b .* c)
+    import operator
+    xs = [torch.rand(2**28, device=dev, generator=g) for _ in range(3)]
+    om = torch.empty(1, device=dev)
+    tm = kf.get_allocation(kf.MapReduce1D, kf.prod3, "+", tuple(xs))
+    yield "X10-dot", "X10 mapreduce(*, +, x, y) F32 n=2^28", 8 * 2**28, \
+        lambda: kf.mapreduce1d_(operator.mul, "+", om, (xs[0], xs[1]), tmp=tm), 10, 2**28, None
+    yield "X10-xyz", "X10 mapreduce(a*b*c, +, a, b, c) F32 n=2^28", 12 * 2**28, \
+        lambda: kf.mapreduce1d_(kf.prod3, "+", om, tuple(xs), tmp=tm), 10, 2**28, None
+    del xs
 
 
 def _cpu_seconds(run, budget_s):
