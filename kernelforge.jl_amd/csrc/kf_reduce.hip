@@ -302,10 +302,16 @@ __global__ __launch_bounds__(kRedBlock) void reduce_once_kernel(const T* src, in
 // folding level 1 (eager, us): Float32 2^26 41.0 vs 41.9-43.1, 2^28 154.0
 // vs 156.9, 2^30 606 vs 622; Float64 2^26 79.1 vs 80.9, 2^28 305 vs 318;
 // Int32 2^28 153.7 vs 156.7. At 200 MB (5*10^7 Float32, 1.5 loop
-// iterations per lane) it lost (32.5 vs 31.6), hence the threshold; 8 loads
-// in flight instead of 16 were 1-2 % slower.
+// iterations per lane) it lost (32.5 vs 31.6), hence the threshold. Loads
+// in flight per lane (HIP graphs, median of 7, us, 16 / 8 / 24 / 32 / 48 /
+// 64; 32 loads take 146 VGPRs, three workgroups per CU): Float32 2^28
+// 154.6 / 157.2 / 161.7 / 153.2 / 161.3 / 153.8, 2^30 607.8 / 613.1 / 611.5
+// / 602.5 / 610.9 / 603.2, 10^8 62.1 / 62.2 / 61.7 / 59.2 / 58.9 / 61.5;
+// Float64 2^27 154.8 / 156.3 / 162.6 / 153.9 / 162.7 / 153.3; Int32 2^28
+// 154.4 / 156.5 / 162.5 / 153.5 / 162.8 / 154.0 (24 and 48 do not divide
+// the rounds evenly over the CUs' resident workgroups).
 constexpr int64_t kChunkMinVecs = (int64_t)1 << 24;
-constexpr int kChunkUnroll = 16;
+constexpr int kChunkUnroll = 32;
 template <class T, class Op, class Map, int U>
 __global__ __launch_bounds__(kRedBlock) void reduce_chunk_kernel(const T* src, int64_t n, int64_t head, int64_t nvec,
                                                                  int64_t chunk, T* out, uint64_t* fold_hdr, FoldCtl ctl) {
