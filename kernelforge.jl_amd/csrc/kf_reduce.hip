@@ -794,15 +794,16 @@ int launch_reducek(const Operands<T, K>& a, int64_t n, void* dst, void* scratch_
                          (const T*)scratch, grid, (T*)dst);
     return kf_check_launch("reducek_kernel");
   }
-  // Loads in flight per lane and array: 8 for two arrays, 4 for three (the
-  // single-array kernels' 16 over K arrays). From 1 GiB of operands the
+  // Loads in flight per lane and array: 8 (three arrays at 4 per array:
+  // x*y*z Float64 2^27 464.8 against 460.6 us, Float32 10^7 21.6 against
+  // 20.8; two arrays at 16: no gain). From 1 GiB of operands the
   // persistent chunk kernel, below it the one-shot kernel with the fewest
   // loads per lane that fold in one launch, else two levels. Measured on
   // MI355X (HIP graphs, us, two levels -> this): dot products Float32 2^28
   // 314.9 -> 308.3, Float64 2^27 326.2 -> 320.2; x*y*z Float32 2^28 483.3 ->
   // 462.9, 10^8 182.0 -> 174.9, Float64 2^27 482.0 -> 461.6 (the Float32 10^8
   // dot product, 800 MB, stays on two levels: 120.4 against 123.1 chunked).
-  constexpr int KU = K == 2 ? 8 : 4;
+  constexpr int KU = 8;
   const int64_t nvec = n / EPV;
   if (nvec * K >= 4 * kChunkMinVecs) {
     constexpr int64_t kRound = (int64_t)KU * kRedBlock;
@@ -813,16 +814,20 @@ int launch_reducek(const Operands<T, K>& a, int64_t n, void* dst, void* scratch_
   }
   const OnceLevels L = once_levels(nvec, EPV, /*adaptive=*/true, KU);
   if (L.nlev == 1 && L.count[0] > 1) {
+    // the kernel's loads per lane must be the width the grid was sized for
+    static_assert(KU == 8, "one-shot widths compiled below: 2, 4, 8");
     const dim3 grid((unsigned)L.count[0]);
     if (L.u0 == 8)
-      hipLaunchKernelGGL((reducek_once_kernel<T, Op, M, K, true, (KU >= 8 ? 8 : KU)>), grid, dim3(kRedBlock), 0,
-                         stream, a, n, (T*)dst, (uint64_t*)scratch_base, fold_ctl());
+      hipLaunchKernelGGL((reducek_once_kernel<T, Op, M, K, true, 8>), grid, dim3(kRedBlock), 0, stream, a, n,
+                         (T*)dst, (uint64_t*)scratch_base, fold_ctl());
     else if (L.u0 == 4)
       hipLaunchKernelGGL((reducek_once_kernel<T, Op, M, K, true, 4>), grid, dim3(kRedBlock), 0, stream, a, n,
                          (T*)dst, (uint64_t*)scratch_base, fold_ctl());
+    else if (L.u0 == 2)
+      hipLaunchKernelGGL((reducek_once_kernel<T, Op, M, K, true, 2>), grid, dim3(kRedBlock), 0, stream, a, n,
+                         (T*)dst, (uint64_t*)scratch_base, fold_ctl());
     else
-      hipLaunchKernelGGL((reducek_once_kernel<T, Op, M, K, true>), grid, dim3(kRedBlock), 0, stream, a, n, (T*)dst,
-                         (uint64_t*)scratch_base, fold_ctl());
+      return kf_set_error(KF_EINVAL, "kf_reduce2/3: internal: no kernel of width %d", L.u0);
     return kf_check_launch("reducek_once_kernel");
   }
   size_t abytes = 0;
