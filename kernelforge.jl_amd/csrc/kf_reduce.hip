@@ -291,10 +291,12 @@ __global__ __launch_bounds__(kRedBlock) void reduce_once_kernel(const T* src, in
   }
 }
 
-// Persistent single-launch reduction for arrays of kChunkMinVecs vectors
-// (256 MiB) or more: kFoldMax workgroups, workgroup b streaming the
-// contiguous chunk [b*chunk, (b+1)*chunk) of vectors with U loads in flight
-// per lane, then the fold. The host makes `chunk` a whole number of
+// Single-launch reduction for arrays of kChunkMinVecs vectors (256 MiB) or
+// more: kFoldMax workgroups, workgroup b streaming the contiguous chunk
+// [b*chunk, (b+1)*chunk) of vectors with U loads in flight per lane, then
+// the fold. At 32 loads about three workgroups fit per CU, so the grid runs
+// in rounds; the fold's waiter is the last workgroup, dispatched last, so
+// every workgroup it waits for has started and none of them waits. The host makes `chunk` a whole number of
 // U * kRedBlock-vector rounds, so only the last non-empty chunk ends in a
 // partial round, which is one guarded round with every load in flight (a
 // one-load-per-iteration remainder loop cost 13 serial memory latencies per
