@@ -213,6 +213,32 @@ def test_quaternion_scan_source_off_the_16_byte_grid(kf, oracle, dev, dt):
             assert np.array_equal(got.astype(np.float64), ref), (dt.__name__, n, exclusive)
 
 
+@pytest.mark.parametrize("dt", [np.float32, np.float64])
+def test_quaternion_scan_destination_off_the_16_byte_grid(kf, oracle, dev, dt):
+    # the tiles place 16-byte vectors on dst's grid: a destination one
+    # component off it shifts every tile's virtual range (the first tile
+    # partial), with the source aligned or off the grid by the same amount.
+    # Exact on the group {+-1, +-i, +-j, +-k}; over several wide tiles
+    # (8192-unit QuaternionF64 tiles, 6144-unit QuaternionF32 tiles).
+    import operator
+    tdt = torch.float32 if dt == np.float32 else torch.float64
+    rng = np.random.default_rng(71)
+    for n in (3 * 8192 + 7, 1_200_003):
+        q = q8_sequence(rng, n, dt)
+        for src_off in (0, 1):
+            flat_s = torch.zeros(4 * n + 4, dtype=tdt, device=dev)
+            flat_s[src_off:src_off + 4 * n] = torch.from_numpy(q.reshape(-1)).to(dev)
+            src = flat_s[src_off:src_off + 4 * n].view(n, 4)
+            flat_d = torch.zeros(4 * n + 4, dtype=tdt, device=dev)
+            dst = flat_d[1:1 + 4 * n].view(n, 4)
+            assert dst.data_ptr() % 16 != 0
+            for exclusive in (False, True):
+                kf.scan_(operator.mul, dst, src, exclusive=exclusive)
+                ref = oracle.scan(q, "*", exclusive=exclusive)
+                assert np.array_equal(dst.cpu().numpy().astype(np.float64), ref), (dt.__name__, n, src_off, exclusive)
+                assert flat_d[0].item() == 0 and flat_d[-3:].abs().sum().item() == 0  # nothing stored outside
+
+
 @pytest.mark.parametrize("dt,n", [(np.float64, 10**6), (np.float32, 10**4)])
 def test_quaternion_scan_reference_case(kf, oracle, dev, dt, n):
     # reference test/tests/scan/scan_test.jl:22-33: scan!(identity, *, dst,
